@@ -1,0 +1,180 @@
+/*
+ * mlrs_hip_knn.h -- C ABI of the MI355X (gfx950) brute-force kNN engine.
+ *
+ * Drop-in replacement for the kernel launches behind mlrs-backend's
+ * brute-force kNN / k-means-assignment / pairwise-distance prims.  Every entry
+ * point:
+ *   - takes DEVICE pointers (HIP, owned by the caller) plus each buffer's
+ *     element count, so the geometry checks of the Rust prims can run here;
+ *   - validates everything BEFORE any launch and returns 0 or a negative
+ *     MLRS_ERR_* code; mlrs_last_error() then describes the failure with the
+ *     same fields as mlrs_core::PrimError (crates/mlrs-core/src/error.rs:62);
+ *   - enqueues its work on `stream` (a hipStream_t; NULL = the null stream)
+ *     and returns without synchronizing, except when it must grow its cached
+ *     device workspace;
+ *   - is callable from any thread, one call at a time per process (the
+ *     Rust side serializes through its global pool mutex,
+ *     crates/mlrs-py/src/lib.rs:104-186); calls are serialized internally.
+ * Results equal mlrs's cpu-backend arithmetic bit for bit: the same arm
+ * (direct / metric / host) the cpu dispatch would pick for the shape
+ * (crates/mlrs-algos/src/neighbors/nearest.rs:891-953) is evaluated in the same
+ * operation order, and selection uses the (value, index) order with the lowest
+ * index winning ties.
+ */
+#ifndef MLRS_HIP_KNN_H
+#define MLRS_HIP_KNN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define MLRS_OK 0
+#define MLRS_ERR_SHAPE_MISMATCH (-1) /* PrimError::ShapeMismatch{operand, rows, cols, len} */
+#define MLRS_ERR_DIM_MISMATCH (-2)   /* PrimError::DimMismatch{dim(operand), lhs(rows), rhs(cols)} */
+#define MLRS_ERR_UNSUPPORTED (-3)    /* metric or shape this build does not serve */
+#define MLRS_ERR_NULL_POINTER (-4)   /* a required pointer was NULL */
+#define MLRS_ERR_HIP (-5)            /* a HIP runtime call failed (hip_error holds it) */
+#define MLRS_ERR_ALLOC (-6)          /* device workspace allocation failed */
+
+/* ---- metrics: the Metric enum of crates/mlrs-backend/src/prims/knn_graph.rs:61-75 ---- */
+#define MLRS_METRIC_EUCLIDEAN 0
+#define MLRS_METRIC_COSINE 1
+
+typedef struct mlrs_error_info {
+    int32_t code;        /* the MLRS_ERR_* value returned */
+    char operand[32];    /* PrimError operand / dim name, e.g. "x", "y", "k", "out" */
+    int64_t rows;        /* ShapeMismatch rows   | DimMismatch lhs */
+    int64_t cols;        /* ShapeMismatch cols   | DimMismatch rhs */
+    int64_t len;         /* ShapeMismatch len */
+    int32_t hip_error;   /* hipError_t for MLRS_ERR_HIP / MLRS_ERR_ALLOC */
+    char message[160];   /* human-readable, PrimError's Display text */
+} mlrs_error_info;
+
+/* Details of the calling thread's last failed call. Returns its code. */
+int32_t mlrs_last_error(mlrs_error_info *out);
+/* Static description of a status code. */
+const char *mlrs_status_string(int32_t code);
+/* ABI version of this header (bumped on any signature change). */
+int32_t mlrs_abi_version(void);
+#define MLRS_ABI_VERSION 1
+
+/*
+ * Brute-force k nearest training rows of every query row.
+ *
+ * Replaces: the arm chosen by metric_topk (nearest.rs:891-953) --
+ *   cpu_rows_topk (crates/mlrs-backend/src/prims/knn.rs:491-671),
+ *   cpu_metric_rows_topk (prims/knn.rs:732-898),
+ *   knn_host_topk (crates/mlrs-backend/src/prims/knn_host.rs:210-304),
+ *   fused_distance_topk (prims/knn.rs:1070-1323) and
+ *   tiled_distance_topk / tiled_metric_distance_topk (nearest.rs:1058-1512).
+ * Layout: xq is n_query x n_features, x_train n_train x n_features, both
+ *   row-major; out_dist / out_idx are n_query x k row-major, each row ascending
+ *   by (distance, index).  Distances are TRUE distances (Euclidean: the root of
+ *   the selected squared values; cosine: 1 - cos, clamped to [0, 2]).  A slot
+ *   no admissible (non-NaN) candidate filled holds (+inf, 0).
+ * Errors (checked in this order, before any launch, mirroring
+ *   cpu_metric_rows_topk / knn_host_topk):
+ *   ShapeMismatch "x"        n_query*n_features != xq_len
+ *   ShapeMismatch "y"        n_train*n_features != xt_len
+ *   ShapeMismatch "k"        k < 1 or k > n_train           (rows=1, cols=k, len=n_train)
+ *   ShapeMismatch "features" n_features < 1
+ *   ShapeMismatch "rows"     n_query or n_train > UINT32_MAX
+ *   ShapeMismatch "out"      out_len != n_query*k
+ *   MLRS_ERR_UNSUPPORTED     metric not served, or k above mlrs_knn_max_k()
+ * `p` is the Minkowski exponent and is ignored by the two metrics served.
+ */
+int32_t mlrs_knn_topk_f32(const float *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                          const float *x_train, int64_t xt_len, int64_t n_train, int32_t k,
+                          int32_t metric, double p, float *out_dist, uint32_t *out_idx,
+                          int64_t out_len, void *stream);
+int32_t mlrs_knn_topk_f64(const double *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                          const double *x_train, int64_t xt_len, int64_t n_train, int32_t k,
+                          int32_t metric, double p, double *out_dist, uint32_t *out_idx,
+                          int64_t out_len, void *stream);
+/* Largest k served for (dtype_bytes, n_features, metric). */
+int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric);
+
+/*
+ * Nearest-centre assignment (the k-means assignment step, k = 1 search).
+ *
+ * Replaces: assign_min (crates/mlrs-backend/src/prims/kmeans.rs:635-750) --
+ *   dist_direct_2d_c4 + argmin_dist_rows (crates/mlrs-kernels/src/kmeans.rs:
+ *   206-310) -- without its n x n_centers staging matrix.
+ * Writes labels[i] = argmin_c ||x_i - c||^2 (lowest index on a tie; a NaN
+ *   distance to centre 0 wins with label 0, as argmin_dist_rows seeds from
+ *   centre 0) and sqdist[i] = that SQUARED distance.
+ * Errors (validate_geometry, prims/kmeans.rs:1416-1454, then assign_min):
+ *   ShapeMismatch "x"        n*n_features != x_len
+ *   ShapeMismatch "k"        n_centers < 1 or n_centers > n
+ *   ShapeMismatch "n"/"d"/"k" a dimension > UINT32_MAX
+ *   ShapeMismatch "centers"  n_centers*n_features != centers_len
+ *   ShapeMismatch "labels"   labels_len != n or dist_len != n
+ * The reference's extra guard n*n_centers <= UINT32_MAX existed only for its
+ * staging matrix, which this kernel does not have; it is not enforced.
+ */
+int32_t mlrs_kmeans_assign_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features,
+                               const float *centers, int64_t centers_len, int64_t n_centers,
+                               uint32_t *labels, int64_t labels_len, float *sqdist, int64_t dist_len,
+                               void *stream);
+int32_t mlrs_kmeans_assign_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features,
+                               const double *centers, int64_t centers_len, int64_t n_centers,
+                               uint32_t *labels, int64_t labels_len, double *sqdist, int64_t dist_len,
+                               void *stream);
+
+/*
+ * Full pairwise distance matrix out[i*rows_y + j].
+ *
+ * Replaces: distance_direct (crates/mlrs-backend/src/prims/distance.rs:428-551,
+ *   kernel euclidean_sq_dist, crates/mlrs-kernels/src/distance.rs:411-440) for
+ *   MLRS_METRIC_EUCLIDEAN -- SQUARED distance, with the boundary root of
+ *   sqrt_elem (crates/mlrs-kernels/src/elementwise.rs:131-136) when
+ *   do_sqrt != 0 -- and metric_distance's cosine_dist
+ *   (crates/mlrs-kernels/src/distance.rs:257-310) for MLRS_METRIC_COSINE.
+ * Errors (validate_geometry, prims/distance.rs:260-302):
+ *   ShapeMismatch "x" / "y", DimMismatch "cols", ShapeMismatch "out".
+ */
+int32_t mlrs_pairwise_distance_f32(const float *x, int64_t x_len, int64_t rows_x, int64_t cols,
+                                   const float *y, int64_t y_len, int64_t rows_y, int64_t cols_y,
+                                   int32_t metric, int32_t do_sqrt, float *out, int64_t out_len,
+                                   void *stream);
+int32_t mlrs_pairwise_distance_f64(const double *x, int64_t x_len, int64_t rows_x, int64_t cols,
+                                   const double *y, int64_t y_len, int64_t rows_y, int64_t cols_y,
+                                   int32_t metric, int32_t do_sqrt, double *out, int64_t out_len,
+                                   void *stream);
+
+/*
+ * Per-row squared L2 norms, out[r] = sum_c x[r,c]^2 accumulated in column
+ * order with separate multiply and add.
+ *
+ * Replaces: row_sqnorms (crates/mlrs-backend/src/prims/kmeans.rs:805-832,
+ *   kernel row_sqnorm, crates/mlrs-kernels/src/kmeans.rs:610) and the
+ *   row_sumsq norm feeder (crates/mlrs-kernels/src/knn.rs:2130-2149).
+ * Errors: ShapeMismatch "x" (n*n_features != x_len), ShapeMismatch "out".
+ */
+int32_t mlrs_row_sqnorms_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features, float *out,
+                             int64_t out_len, void *stream);
+int32_t mlrs_row_sqnorms_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features,
+                             double *out, int64_t out_len, void *stream);
+
+/* Release the cached device workspace of the current device. */
+int32_t mlrs_release_workspace(void);
+
+/*
+ * Measurement hook (no counterpart in the reference; for benchmarks).
+ * While enabled, every call records a pair of HIP events on its own stream
+ * around the launch of its dominant kernel (the Gram-MFMA kernel, the low-d
+ * ALU kernel, or the generic path's distance tile).  mlrs_timing_read waits
+ * for the recorded events and returns the summed kernel time, the number of
+ * timed launches and the kernel's name; enabling again clears the records.
+ */
+int32_t mlrs_timing_enable(int32_t on);
+int32_t mlrs_timing_read(double *total_ms, int64_t *launches, char *kernel_name, int32_t name_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLRS_HIP_KNN_H */

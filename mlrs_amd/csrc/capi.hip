@@ -1,0 +1,645 @@
+// C-ABI layer: validation (before any launch), arm selection, workspace and
+// dispatch to the kernels.  See include/mlrs_hip_knn.h for the contract.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/mlrs_hip_knn.h"
+#include "knn_common.hpp"
+#include "knn_kernels.hpp"
+
+using namespace mlrs;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+thread_local mlrs_error_info g_err;
+
+int32_t set_err(int32_t code, const char* operand, int64_t rows, int64_t cols, int64_t len, int hip,
+                const char* fmt, ...) {
+    std::memset(&g_err, 0, sizeof(g_err));
+    g_err.code = code;
+    std::snprintf(g_err.operand, sizeof(g_err.operand), "%s", operand ? operand : "");
+    g_err.rows = rows;
+    g_err.cols = cols;
+    g_err.len = len;
+    g_err.hip_error = hip;
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_err.message, sizeof(g_err.message), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+// PrimError::ShapeMismatch's Display text (crates/mlrs-core/src/error.rs:66-70).
+int32_t shape_err(const char* operand, int64_t rows, int64_t cols, int64_t len) {
+    return set_err(MLRS_ERR_SHAPE_MISMATCH, operand, rows, cols, len, 0,
+                   "primitive '%s' shape mismatch: rows(%lld) * cols(%lld) = %lld != len(%lld)", operand,
+                   (long long)rows, (long long)cols, (long long)(rows * cols), (long long)len);
+}
+
+// PrimError::DimMismatch's Display text (crates/mlrs-core/src/error.rs:76).
+int32_t dim_err(const char* dim, int64_t lhs, int64_t rhs) {
+    return set_err(MLRS_ERR_DIM_MISMATCH, dim, lhs, rhs, 0, 0,
+                   "primitive dimension mismatch (%s): lhs declares %lld, rhs declares %lld", dim,
+                   (long long)lhs, (long long)rhs);
+}
+
+int32_t hip_err(hipError_t e, const char* where) {
+    return set_err(MLRS_ERR_HIP, where, 0, 0, 0, (int)e, "HIP error in %s: %s", where, hipGetErrorString(e));
+}
+
+int32_t ok() {
+    return MLRS_OK;
+}
+
+// rows * cols == len without overflow (checked_mul in the reference).
+bool geom_ok(int64_t rows, int64_t cols, int64_t len) {
+    if (rows < 0 || cols < 0 || len < 0) return false;
+    if (cols != 0 && rows > INT64_MAX / cols) return false;
+    return rows * cols == len;
+}
+
+constexpr int64_t kU32Max = 0xFFFFFFFFll;
+
+// ---------------------------------------------------------------------------
+// per-device cached workspace (the BufferPool role: reuse across calls)
+// ---------------------------------------------------------------------------
+std::mutex g_mu;
+constexpr int kMaxDevices = 64;
+struct Arena {
+    char* base = nullptr;
+    size_t cap = 0;
+    int cus = 0;
+};
+Arena g_arena[kMaxDevices];
+
+struct Carver {
+    char* p;
+    size_t off = 0;
+    explicit Carver(char* b) : p(b) {}
+    template <typename T>
+    T* take(size_t n) {
+        off = (off + 255) & ~(size_t)255;
+        T* r = reinterpret_cast<T*>(p + off);
+        off += n * sizeof(T);
+        return r;
+    }
+};
+
+static size_t aligned_bytes(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_err(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return set_err(MLRS_ERR_UNSUPPORTED, "device", dev, 0, 0, 0, "device ordinal %d out of range", dev);
+    Arena& A = g_arena[dev];
+    if (A.cus == 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return hip_err(e, "hipDeviceGetAttribute");
+        A.cus = n > 0 ? n : 1;
+    }
+    *cus = A.cus;
+    if (bytes == 0) bytes = 256;
+    if (A.cap < bytes) {
+        // Earlier work may still read the old buffer: drain the device first.
+        if (A.base) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
+            (void)hipFree(A.base);
+            A.base = nullptr;
+            A.cap = 0;
+        }
+        size_t want = std::max(bytes + bytes / 4, (size_t)64 << 20);
+        e = hipMalloc((void**)&A.base, want);
+        if (e != hipSuccess) {
+            A.base = nullptr;
+            return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)want, 0, 0, (int)e,
+                           "device workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+        }
+        A.cap = want;
+    }
+    *out = A.base;
+    (void)s;
+    return MLRS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// measurement hook: events around the dominant kernel launch
+// ---------------------------------------------------------------------------
+struct TimedLaunch {
+    hipEvent_t a, b;
+};
+bool g_timing = false;
+std::vector<TimedLaunch> g_timed;
+char g_timed_name[64] = "";
+
+struct KernelTimer {
+    hipStream_t s;
+    TimedLaunch t{nullptr, nullptr};
+    KernelTimer(hipStream_t st, const char* name) : s(st) {
+        if (!g_timing) return;
+        if (hipEventCreate(&t.a) != hipSuccess || hipEventCreate(&t.b) != hipSuccess) {
+            t.a = t.b = nullptr;
+            return;
+        }
+        std::snprintf(g_timed_name, sizeof(g_timed_name), "%s", name);
+        (void)hipEventRecord(t.a, s);
+    }
+    ~KernelTimer() {
+        if (!g_timing || !t.a) return;
+        (void)hipEventRecord(t.b, s);
+        g_timed.push_back(t);
+    }
+};
+
+void clear_timed() {
+    for (auto& t : g_timed) {
+        (void)hipEventDestroy(t.a);
+        (void)hipEventDestroy(t.b);
+    }
+    g_timed.clear();
+}
+
+// ---------------------------------------------------------------------------
+// arm selection: the cpu-backend dispatch of metric_topk
+// ---------------------------------------------------------------------------
+// crates/mlrs-algos/src/neighbors/nearest.rs:910-947 with the caps of
+// cpu_rows_applicable (prims/knn.rs:400-412: d <= 32, k <= 16) and
+// cpu_metric_rows_applicable (prims/knn.rs:703-720: d <= 128, k <= 128).
+int knn_arm(int64_t d, int64_t k, int metric) {
+    const bool metric_family = d >= 1 && d <= 128 && k >= 1 && k <= 128;
+    if (metric == MLRS_METRIC_EUCLIDEAN) return metric_family ? ARM_EUCLID_FMA : ARM_EUCLID_MULADD;
+    return metric_family ? ARM_COS_FOLD : ARM_COS_HOST;
+}
+
+// Split the index axis so the grid has enough workgroups to fill the chip,
+// preferring a total that is a whole number of waves of workgroups.
+int pick_strips(int64_t nblocks, int64_t nt, int64_t slots, int64_t min_rows, int max_strips) {
+    int64_t best_s = 1;
+    double best_cost = 1e300;
+    int64_t s_hi = std::max<int64_t>(1, std::min<int64_t>(max_strips, (nt + min_rows - 1) / min_rows));
+    for (int64_t s = 1; s <= s_hi; ++s) {
+        int64_t wgs = nblocks * s;
+        int64_t rounds = (wgs + slots - 1) / slots;
+        // time ~ rounds * (work per WG) = rounds / s; penalize the merge a little
+        double cost = (double)rounds / (double)s * (1.0 + 0.002 * (double)s);
+        if (cost < best_cost - 1e-12) {
+            best_cost = cost;
+            best_s = s;
+        }
+    }
+    return (int)best_s;
+}
+
+// ---------------------------------------------------------------------------
+// generic exact path: tile of exact pairwise values + per-row selection
+// ---------------------------------------------------------------------------
+template <typename T>
+int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, int k, int arm, int mode,
+                    T* out_v, uint32_t* out_i, hipStream_t s) {
+    if (k > select_rows_max_k())
+        return set_err(MLRS_ERR_UNSUPPORTED, "k", 1, k, nt, 0, "k=%d above the largest k served (%d)", k,
+                       select_rows_max_k());
+    const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
+    const size_t tile_budget = (size_t)256 << 20;
+    int64_t qt = (int64_t)(tile_budget / (sizeof(T) * (size_t)std::max<int64_t>(nt, 1)));
+    qt = std::max<int64_t>(1, std::min<int64_t>(qt, nq));
+    size_t bytes = aligned_bytes(sizeof(T) * (size_t)qt * nt) + 4 * aligned_bytes(sizeof(T) * (nq + nt)) + 4096;
+    char* ws;
+    int cus;
+    int32_t rc = workspace(bytes, s, &ws, &cus);
+    if (rc) return rc;
+    Carver cv(ws);
+    T* dist = cv.take<T>((size_t)qt * nt);
+    T* qa = nullptr;
+    T* xa = nullptr;
+    if (cos) {
+        qa = cv.take<T>(nq);
+        xa = cv.take<T>(nt);
+        hipError_t e;
+        if (arm == ARM_COS_HOST) {
+            // reciprocal norms (row_inv_norm_host), squared norms discarded
+            T* qsq = cv.take<T>(nq);
+            T* xsq = cv.take<T>(nt);
+            e = launch_row_norms<T>(xq, nq, d, qsq, qa, nullptr, nullptr, s);
+            if (e == hipSuccess) e = launch_row_norms<T>(xt, nt, d, xsq, xa, nullptr, nullptr, s);
+        } else {
+            // squared norms (row_sumsq)
+            e = launch_row_norms<T>(xq, nq, d, qa, nullptr, nullptr, nullptr, s);
+            if (e == hipSuccess) e = launch_row_norms<T>(xt, nt, d, xa, nullptr, nullptr, nullptr, s);
+        }
+        if (e != hipSuccess) return hip_err(e, "row_norms");
+    }
+    for (int64_t q0 = 0; q0 < nq; q0 += qt) {
+        int64_t rows = std::min<int64_t>(qt, nq - q0);
+        hipError_t e;
+        {
+            KernelTimer timer(s, "pairwise_tile_kernel");
+            e = launch_pairwise_tile<T>(xq + q0 * d, rows, xt, nt, d, arm, cos ? qa + q0 : nullptr, xa, dist,
+                                        nt, 0, s);
+        }
+        if (e == hipSuccess)
+            e = launch_select_rows<T>(dist, rows, nt, nt, k, mode, out_v + q0 * k, out_i + q0 * k, s);
+        if (e != hipSuccess) return hip_err(e, "generic kNN");
+    }
+    return ok();
+}
+
+template <typename T>
+int32_t kmeans_generic(const T* x, int64_t n, const T* c, int64_t kc, int64_t d, uint32_t* labels, T* dist,
+                       hipStream_t s) {
+    const size_t tile_budget = (size_t)256 << 20;
+    int64_t qt = (int64_t)(tile_budget / (sizeof(T) * (size_t)std::max<int64_t>(kc, 1)));
+    qt = std::max<int64_t>(1, std::min<int64_t>(qt, n));
+    char* ws;
+    int cus;
+    int32_t rc = workspace(aligned_bytes(sizeof(T) * (size_t)qt * kc) + 256, s, &ws, &cus);
+    if (rc) return rc;
+    T* buf = reinterpret_cast<T*>(ws);
+    for (int64_t r0 = 0; r0 < n; r0 += qt) {
+        int64_t rows = std::min<int64_t>(qt, n - r0);
+        hipError_t e = launch_pairwise_tile<T>(x + r0 * d, rows, c, kc, d, ARM_EUCLID_MULADD, nullptr, nullptr,
+                                               buf, kc, 0, s);
+        if (e == hipSuccess) e = launch_argmin_rows<T>(buf, rows, kc, kc, labels + r0, dist + r0, s);
+        if (e != hipSuccess) return hip_err(e, "generic k-means assignment");
+    }
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+// fast paths
+// ---------------------------------------------------------------------------
+int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
+                   int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
+    const bool cos = (arm == ARM_COS_FOLD);
+    const int64_t qpb = gram_f32_queries_per_block();
+    const int64_t nblocks = (nq + qpb - 1) / qpb;
+    // sizes that do not depend on the strip count
+    size_t fixed = aligned_bytes(sizeof(float) * nq) + 2 * aligned_bytes(sizeof(float) * nt) +
+                   aligned_bytes(sizeof(NormStats)) + 1024;
+    char* ws;
+    int cus;
+    int32_t rc = workspace(fixed, s, &ws, &cus);
+    if (rc) return rc;
+    const int64_t slots = cus;  // one 4-wave workgroup per CU (LDS-bound)
+    int nstrips = pick_strips(nblocks, nt, slots, 2048, 64);
+    const int64_t tile = gram_f32_rows_per_tile();
+    int64_t rps = (nt + nstrips - 1) / nstrips;
+    rps = (rps + tile - 1) / tile * tile;
+    nstrips = (int)((nt + rps - 1) / rps);
+    size_t parts = nstrips > 1 ? (size_t)nstrips * nq * k : 0;
+    size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t));
+    rc = workspace(bytes, s, &ws, &cus);
+    if (rc) return rc;
+    Carver cv(ws);
+    GramArgs32 a;
+    std::memset(&a, 0, sizeof(a));
+    float* qsq = cv.take<float>(nq);
+    float* xsq = cv.take<float>(nt);
+    float* xscale = cv.take<float>(nt);
+    NormStats* stats = cv.take<NormStats>(1);
+    hipError_t e = launch_row_norms<float>(xq, nq, d, qsq, nullptr, nullptr, nullptr, s);
+    if (e == hipSuccess)
+        e = launch_row_norms<float>(xt, nt, d, xsq, nullptr, cos ? xscale : nullptr, stats, s);
+    if (e != hipSuccess) return hip_err(e, "row_norms");
+    a.q = xq;
+    a.nq = nq;
+    a.x = xt;
+    a.nt = nt;
+    a.d = d;
+    a.k = k;
+    a.mode = mode;
+    a.qsq = qsq;
+    a.xsq = xsq;
+    a.xscale = xscale;
+    a.stats = stats;
+    // Screen bounds (see knn_gram_f32.hip): with u = 2^-23 (covers any
+    // rounding mode of the matrix core) the expansion's and the reference's
+    // rounding errors together stay below 6(d+3)u(||q||^2 + ||x||^2) for
+    // Euclidean and (4d+11)u for cosine; the bounds used are 8(d+4)u and
+    // (8d+32)u, plus an absolute floor for flushed subnormal products.
+    const double u = std::ldexp(1.0, -23);
+    if (!cos) {
+        a.eps_rel = 8.0 * (double)(d + 4) * u;
+        a.eps_abs = (double)(d + 4) * std::ldexp(1.0, -120);
+    } else {
+        a.eps_rel = 0.0;
+        a.eps_abs = (8.0 * (double)d + 32.0) * u;
+    }
+    a.rows_per_strip = rps;
+    a.nstrips = nstrips;
+    if (nstrips > 1) {
+        a.part_val = cv.take<float>(parts);
+        a.part_idx = cv.take<uint32_t>(parts);
+    }
+    a.out_val = out_v;
+    a.out_idx = out_i;
+    {
+        KernelTimer timer(s, "knn_gram_f32_kernel");
+        e = launch_gram_f32(a, arm, s);
+    }
+    if (e != hipSuccess) return hip_err(e, "knn_gram_f32");
+    return ok();
+}
+
+int32_t knn_lowd32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
+                   int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
+    char* ws;
+    int cus;
+    int32_t rc = workspace(1024, s, &ws, &cus);
+    if (rc) return rc;
+    const int64_t nblocks = (nq + 255) / 256;
+    // ~8 resident 256-lane workgroups per CU
+    int nstrips = pick_strips(nblocks, nt, (int64_t)cus * 8, 4096, 64);
+    int64_t rps = (nt + nstrips - 1) / nstrips;
+    nstrips = (int)((nt + rps - 1) / rps);
+    size_t parts = nstrips > 1 ? (size_t)nstrips * nq * k : 0;
+    if (parts) {
+        rc = workspace(aligned_bytes(parts * 4) * 2 + 1024, s, &ws, &cus);
+        if (rc) return rc;
+    }
+    Carver cv(ws);
+    LowdArgs32 a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = xq;
+    a.nq = nq;
+    a.x = xt;
+    a.nt = nt;
+    a.d = d;
+    a.k = k;
+    a.mode = mode;
+    a.rows_per_strip = rps;
+    a.nstrips = nstrips;
+    if (parts) {
+        a.part_val = cv.take<float>(parts);
+        a.part_idx = cv.take<uint32_t>(parts);
+    }
+    a.out_val = out_v;
+    a.out_idx = out_i;
+    hipError_t e;
+    {
+        KernelTimer timer(s, "knn_lowd_kernel");
+        e = launch_lowd_f32(a, arm, s);
+    }
+    if (e != hipSuccess) return hip_err(e, "knn_lowd_f32");
+    return ok();
+}
+
+template <typename T>
+int32_t validate_knn(const T* xq, int64_t xq_len, int64_t nq, int64_t d, const T* xt, int64_t xt_len,
+                     int64_t nt, int32_t k, int32_t metric, const void* ov, const void* oi, int64_t out_len) {
+    if (!geom_ok(nq, d, xq_len)) return shape_err("x", nq, d, xq_len);
+    if (!geom_ok(nt, d, xt_len)) return shape_err("y", nt, d, xt_len);
+    if (k < 1 || (int64_t)k > nt) return shape_err("k", 1, k, nt);
+    if (d < 1) return shape_err("features", d, 0, 0);
+    if (nq > kU32Max || nt > kU32Max) return shape_err("rows", std::max(nq, nt), 0, kU32Max);
+    if (!geom_ok(nq, k, out_len)) return shape_err("out", nq, k, out_len);
+    if (metric != MLRS_METRIC_EUCLIDEAN && metric != MLRS_METRIC_COSINE)
+        return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0, "metric %d is not served", metric);
+    if (nq > 0 && (!xq || !ov || !oi)) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
+    if (!xt) return set_err(MLRS_ERR_NULL_POINTER, "y", 0, 0, 0, 0, "null pointer");
+    return MLRS_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// exported entry points
+// ===========================================================================
+extern "C" {
+
+int32_t mlrs_abi_version(void) { return MLRS_ABI_VERSION; }
+
+int32_t mlrs_last_error(mlrs_error_info* out) {
+    if (out) *out = g_err;
+    return g_err.code;
+}
+
+const char* mlrs_status_string(int32_t code) {
+    switch (code) {
+    case MLRS_OK: return "ok";
+    case MLRS_ERR_SHAPE_MISMATCH: return "shape mismatch";
+    case MLRS_ERR_DIM_MISMATCH: return "dimension mismatch";
+    case MLRS_ERR_UNSUPPORTED: return "unsupported metric or shape";
+    case MLRS_ERR_NULL_POINTER: return "null pointer";
+    case MLRS_ERR_HIP: return "HIP runtime error";
+    case MLRS_ERR_ALLOC: return "device workspace allocation failed";
+    default: return "unknown status";
+    }
+}
+
+int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric) {
+    (void)dtype_bytes;
+    (void)n_features;
+    (void)metric;
+    return select_rows_max_k();
+}
+
+int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                          const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
+                          double p, float* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
+    (void)p;
+    std::lock_guard<std::mutex> lk(g_mu);
+    int32_t rc = validate_knn<float>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
+                                     out_dist, out_idx, out_len);
+    if (rc) return rc;
+    if (n_query == 0) return MLRS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const int arm = knn_arm(n_features, k, metric);
+    const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
+    if (metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k())
+        return knn_lowd32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+    if (arm != ARM_COS_HOST && n_features <= gram_f32_max_d() && k <= gram_f32_max_k())
+        return knn_gram32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+    return knn_generic<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+}
+
+int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                          const double* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
+                          double p, double* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
+    (void)p;
+    std::lock_guard<std::mutex> lk(g_mu);
+    int32_t rc = validate_knn<double>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
+                                      out_dist, out_idx, out_len);
+    if (rc) return rc;
+    if (n_query == 0) return MLRS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const int arm = knn_arm(n_features, k, metric);
+    const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
+    return knn_generic<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+}
+
+extern "C++" {
+template <typename T>
+static int32_t validate_kmeans(const T* x, int64_t x_len, int64_t n, int64_t d, const T* c, int64_t c_len,
+                               int64_t kc, const void* labels, int64_t labels_len, const void* dist,
+                               int64_t dist_len) {
+    // validate_geometry (prims/kmeans.rs:1416-1440) then assign_min's checks (:646-677)
+    if (!geom_ok(n, d, x_len)) return shape_err("x", n, d, x_len);
+    if (kc < 1 || kc > n) return shape_err("k", 1, kc, n);
+    if (n > kU32Max) return shape_err("n", n, 0, kU32Max);
+    if (d > kU32Max) return shape_err("d", d, 0, kU32Max);
+    if (kc > kU32Max) return shape_err("k", kc, 0, kU32Max);
+    if (!geom_ok(kc, d, c_len)) return shape_err("centers", kc, d, c_len);
+    if (labels_len != n || dist_len != n) return shape_err("labels", n, 1, std::min(labels_len, dist_len));
+    if (d < 1) return shape_err("x", n, d, x_len);
+    if (!x || !c || !labels || !dist) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
+    return MLRS_OK;
+}
+}  // extern "C++"
+
+int32_t mlrs_kmeans_assign_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features, const float* centers,
+                               int64_t centers_len, int64_t n_centers, uint32_t* labels, int64_t labels_len,
+                               float* sqdist, int64_t dist_len, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int32_t rc = validate_kmeans<float>(x, x_len, n, n_features, centers, centers_len, n_centers, labels,
+                                        labels_len, sqdist, dist_len);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (n_features <= gram_f32_max_d())
+        return knn_gram32(x, n, centers, n_centers, n_features, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, sqdist, labels,
+                          s);
+    return kmeans_generic<float>(x, n, centers, n_centers, n_features, labels, sqdist, s);
+}
+
+int32_t mlrs_kmeans_assign_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features,
+                               const double* centers, int64_t centers_len, int64_t n_centers, uint32_t* labels,
+                               int64_t labels_len, double* sqdist, int64_t dist_len, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int32_t rc = validate_kmeans<double>(x, x_len, n, n_features, centers, centers_len, n_centers, labels,
+                                         labels_len, sqdist, dist_len);
+    if (rc) return rc;
+    return kmeans_generic<double>(x, n, centers, n_centers, n_features, labels, sqdist, (hipStream_t)stream);
+}
+
+extern "C++" {
+template <typename T>
+static int32_t pairwise_impl(const T* x, int64_t x_len, int64_t rows_x, int64_t cols, const T* y, int64_t y_len,
+                             int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt, T* out,
+                             int64_t out_len, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!geom_ok(rows_x, cols, x_len)) return shape_err("x", rows_x, cols, x_len);
+    if (!geom_ok(rows_y, cols_y, y_len)) return shape_err("y", rows_y, cols_y, y_len);
+    if (cols != cols_y) return dim_err("cols", cols, cols_y);
+    if (!geom_ok(rows_x, rows_y, out_len)) return shape_err("out", rows_x, rows_y, out_len);
+    if (metric != MLRS_METRIC_EUCLIDEAN && metric != MLRS_METRIC_COSINE)
+        return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0, "metric %d is not served", metric);
+    if (rows_x == 0 || rows_y == 0) return MLRS_OK;
+    if (!x || !y || !out) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    const T* xa = nullptr;
+    const T* ya = nullptr;
+    int arm = ARM_EUCLID_MULADD;
+    if (metric == MLRS_METRIC_COSINE) {
+        arm = ARM_COS_PAIRWISE;
+        char* ws;
+        int cus;
+        int32_t rc = workspace(aligned_bytes(sizeof(T) * rows_x) + aligned_bytes(sizeof(T) * rows_y) + 256, s, &ws,
+                               &cus);
+        if (rc) return rc;
+        Carver cv(ws);
+        T* xn = cv.take<T>(rows_x);
+        T* yn = cv.take<T>(rows_y);
+        hipError_t e = launch_row_norms<T>(x, rows_x, cols, xn, nullptr, nullptr, nullptr, s);
+        if (e == hipSuccess) e = launch_row_norms<T>(y, rows_y, cols, yn, nullptr, nullptr, nullptr, s);
+        if (e != hipSuccess) return hip_err(e, "row_norms");
+        xa = xn;
+        ya = yn;
+    }
+    hipError_t e = launch_pairwise_tile<T>(x, rows_x, y, rows_y, cols, arm, xa, ya, out, rows_y, do_sqrt, s);
+    if (e != hipSuccess) return hip_err(e, "pairwise_tile");
+    return MLRS_OK;
+}
+}  // extern "C++"
+
+int32_t mlrs_pairwise_distance_f32(const float* x, int64_t x_len, int64_t rows_x, int64_t cols, const float* y,
+                                   int64_t y_len, int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt,
+                                   float* out, int64_t out_len, void* stream) {
+    return pairwise_impl<float>(x, x_len, rows_x, cols, y, y_len, rows_y, cols_y, metric, do_sqrt, out, out_len,
+                                stream);
+}
+
+int32_t mlrs_pairwise_distance_f64(const double* x, int64_t x_len, int64_t rows_x, int64_t cols, const double* y,
+                                   int64_t y_len, int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt,
+                                   double* out, int64_t out_len, void* stream) {
+    return pairwise_impl<double>(x, x_len, rows_x, cols, y, y_len, rows_y, cols_y, metric, do_sqrt, out, out_len,
+                                 stream);
+}
+
+extern "C++" {
+template <typename T>
+static int32_t sqnorms_impl(const T* x, int64_t x_len, int64_t n, int64_t d, T* out, int64_t out_len,
+                            void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!geom_ok(n, d, x_len)) return shape_err("x", n, d, x_len);
+    if (out_len != n) return shape_err("out", n, 1, out_len);
+    if (n == 0) return MLRS_OK;
+    if (!x || !out) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
+    hipError_t e = launch_row_norms<T>(x, n, d, out, nullptr, nullptr, nullptr, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_err(e, "row_norms");
+    return MLRS_OK;
+}
+}  // extern "C++"
+
+int32_t mlrs_row_sqnorms_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features, float* out,
+                             int64_t out_len, void* stream) {
+    return sqnorms_impl<float>(x, x_len, n, n_features, out, out_len, stream);
+}
+
+int32_t mlrs_row_sqnorms_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features, double* out,
+                             int64_t out_len, void* stream) {
+    return sqnorms_impl<double>(x, x_len, n, n_features, out, out_len, stream);
+}
+
+int32_t mlrs_timing_enable(int32_t on) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    clear_timed();
+    g_timing = on != 0;
+    g_timed_name[0] = 0;
+    return MLRS_OK;
+}
+
+int32_t mlrs_timing_read(double* total_ms, int64_t* launches, char* kernel_name, int32_t name_len) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    double tot = 0.0;
+    for (auto& t : g_timed) {
+        hipError_t e = hipEventSynchronize(t.b);
+        if (e != hipSuccess) return hip_err(e, "hipEventSynchronize");
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, t.a, t.b);
+        if (e != hipSuccess) return hip_err(e, "hipEventElapsedTime");
+        tot += ms;
+    }
+    if (total_ms) *total_ms = tot;
+    if (launches) *launches = (int64_t)g_timed.size();
+    if (kernel_name && name_len > 0) std::snprintf(kernel_name, (size_t)name_len, "%s", g_timed_name);
+    return MLRS_OK;
+}
+
+int32_t mlrs_release_workspace(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MLRS_OK;
+    Arena& A = g_arena[dev];
+    if (A.base) {
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
+        (void)hipFree(A.base);
+        A.base = nullptr;
+        A.cap = 0;
+    }
+    return MLRS_OK;
+}
+
+}  // extern "C"

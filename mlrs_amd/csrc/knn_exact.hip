@@ -1,0 +1,455 @@
+// Exact building blocks: row norms, the tiled exact pairwise-value kernel and
+// the per-row (value, index) top-k selection over a materialized matrix.
+//
+// Together the last two are the engine's generic path -- any d, any k up to
+// select_rows_max_k(), any arm, f32 or f64 -- the MI355X counterpart of the
+// reference's two-kernel distance_direct -> top_k composition
+// (crates/mlrs-algos/src/neighbors/nearest.rs:1117-1343,
+// crates/mlrs-backend/src/prims/distance.rs:428-551, prims/topk.rs:62-186).
+// The pairwise kernel alone is the pairwise-distance entry point.
+#include "knn_common.hpp"
+#include "knn_kernels.hpp"
+
+namespace mlrs {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row norms (row_sumsq order) + device-side max for the Gram screen bound.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void row_norms_kernel(const T* __restrict__ x, int64_t n, int64_t d, T* __restrict__ sq,
+                                 T* __restrict__ inv, T* __restrict__ neg_inv, NormStats* stats) {
+    int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    T s = T(0);
+    bool valid = r < n;
+    if (valid) {
+        s = row_sumsq<T>(x + r * d, d);
+        sq[r] = s;
+        T iv = (s > T(0)) ? T(1) / FloatTraits<T>::sqrt_(s) : T(0);
+        if (inv) inv[r] = iv;
+        if (neg_inv) neg_inv[r] = -iv;
+    }
+    if (stats) {
+        // Max over non-NaN squared norms; non-negative floats order like their bits.
+        unsigned long long bits = 0;
+        if (valid && !(s != s)) {
+            if (sizeof(T) == 4) {
+                float f = (float)s;
+                bits = (unsigned long long)__float_as_uint(f);
+            } else {
+                bits = (unsigned long long)__double_as_longlong((double)s);
+            }
+        }
+        // Wave-level max first, then one atomic per wave.
+        for (int m = 32; m > 0; m >>= 1) {
+            unsigned long long o = (unsigned long long)__shfl_xor((long long)bits, m, 64);
+            bits = o > bits ? o : bits;
+        }
+        if ((threadIdx.x & 63) == 0 && bits) atomicMax(&stats->xsq_max_bits, bits);
+    }
+}
+
+template <typename T>
+__global__ void stats_reset_kernel(NormStats* stats) {
+    if (threadIdx.x == 0) stats->xsq_max_bits = 0ull;
+}
+
+template <typename T>
+__global__ void stats_finalize_kernel(NormStats* stats) {
+    if (threadIdx.x == 0) {
+        unsigned long long b = stats->xsq_max_bits;
+        if (sizeof(T) == 4) {
+            float f = __uint_as_float((uint32_t)b);
+            stats->xsq_max = f;
+            stats->xsq_max64 = (double)f;
+        } else {
+            double v = __longlong_as_double((long long)b);
+            stats->xsq_max64 = v;
+            stats->xsq_max = (float)v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled exact pairwise values.  A 16x16 thread block computes a 64x64 output
+// tile, 4x4 per thread; 16-column chunks of both operands are staged in LDS.
+// Each pair still accumulates over ascending columns one step at a time, so
+// the value is the arm's exact reference value.
+// ---------------------------------------------------------------------------
+constexpr int PT = 64;   // output tile edge
+constexpr int PC = 16;   // staged columns per chunk
+
+template <typename T, int ARM>
+__global__ __launch_bounds__(256) void pairwise_tile_kernel(const T* __restrict__ x, int64_t nx,
+                                                            const T* __restrict__ y, int64_t ny,
+                                                            int64_t d, const T* __restrict__ xa,
+                                                            const T* __restrict__ ya, T* __restrict__ out,
+                                                            int64_t ldo, int do_sqrt) {
+    using F = FloatTraits<T>;
+    __shared__ T xs[PC][PT + 1];
+    __shared__ T ys[PC][PT + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int64_t i0 = (int64_t)blockIdx.y * PT, j0 = (int64_t)blockIdx.x * PT;
+    T acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = T(0);
+
+    for (int64_t c0 = 0; c0 < d; c0 += PC) {
+        // Stage x[i0..i0+64)[c0..c0+16) and y[j0..)[c0..) transposed.
+        for (int e = threadIdx.x; e < PT * PC; e += 256) {
+            int r = e / PC, c = e % PC;
+            int64_t gi = i0 + r, gj = j0 + r, gc = c0 + c;
+            xs[c][r] = (gi < nx && gc < d) ? x[gi * d + gc] : T(0);
+            ys[c][r] = (gj < ny && gc < d) ? y[gj * d + gc] : T(0);
+        }
+        __syncthreads();
+        int cn = (d - c0) < PC ? (int)(d - c0) : PC;
+        for (int c = 0; c < cn; ++c) {
+            T xv[4], yv[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) xv[a] = xs[c][ty + 16 * a];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) yv[b] = ys[c][tx + 16 * b];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    if (ARM == ARM_EUCLID_FMA) {
+                        T diff = xv[a] - yv[b];
+                        acc[a][b] = F::fma_(diff, diff, acc[a][b]);
+                    } else if (ARM == ARM_EUCLID_MULADD) {
+                        T diff = xv[a] - yv[b];
+                        acc[a][b] = acc[a][b] + diff * diff;
+                    } else if (ARM == ARM_COS_FOLD) {
+                        acc[a][b] = F::fma_(xv[a], yv[b], acc[a][b]);
+                    } else {
+                        acc[a][b] = acc[a][b] + xv[a] * yv[b];
+                    }
+                }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        int64_t gi = i0 + ty + 16 * a;
+        if (gi >= nx) continue;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            int64_t gj = j0 + tx + 16 * b;
+            if (gj >= ny) continue;
+            T v = acc[a][b];
+            if (ARM == ARM_COS_FOLD || ARM == ARM_COS_PAIRWISE) {
+                T denom = F::sqrt_(xa[gi] * ya[gj]);
+                T sim = T(0);
+                if (denom > T(0)) sim = v / denom;
+                v = clamp02<T>(T(1) - sim);
+            } else if (ARM == ARM_COS_HOST) {
+                v = clamp02<T>(T(1) - v * xa[gi] * ya[gj]);
+            } else if (do_sqrt) {
+                v = F::sqrt_(v);
+            }
+            out[gi * ldo + gj] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-row top-k selection by radix select over order-preserving keys.
+// ---------------------------------------------------------------------------
+template <typename T> struct KeyOf;
+template <> struct KeyOf<float> {
+    typedef uint32_t K;
+    static constexpr int BITS = 32;
+    static __device__ __forceinline__ K key(float v) {
+        if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal: one key
+        uint32_t b = __float_as_uint(v);
+        return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    }
+    static __device__ __forceinline__ float val(K k) {
+        uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+        return __uint_as_float(b);
+    }
+};
+template <> struct KeyOf<double> {
+    typedef unsigned long long K;
+    static constexpr int BITS = 64;
+    static __device__ __forceinline__ K key(double v) {
+        if (v == 0.0) v = 0.0;
+        unsigned long long b = (unsigned long long)__double_as_longlong(v);
+        return (b & 0x8000000000000000ull) ? ~b : (b | 0x8000000000000000ull);
+    }
+    static __device__ __forceinline__ double val(K k) {
+        unsigned long long b = (k & 0x8000000000000000ull) ? (k & 0x7FFFFFFFFFFFFFFFull) : ~k;
+        return __longlong_as_double((long long)b);
+    }
+};
+
+constexpr int SEL_MAXK = 256;
+
+template <typename T>
+__global__ __launch_bounds__(256) void select_rows_kernel(const T* __restrict__ dist, int64_t rows,
+                                                          int64_t cols, int64_t ld, int k, int mode,
+                                                          T* __restrict__ out_val,
+                                                          uint32_t* __restrict__ out_idx) {
+    typedef typename KeyOf<T>::K K;
+    __shared__ uint32_t hist[256];
+    __shared__ K skey[SEL_MAXK];
+    __shared__ uint32_t sidx[SEL_MAXK];
+    __shared__ uint32_t s_cnt_less, s_cnt_eq, s_nvalid;
+    __shared__ uint32_t s_wave_eq[4];
+    __shared__ K s_prefix;
+    __shared__ uint32_t s_want;
+
+    const int64_t row = blockIdx.x;
+    if (row >= rows) return;
+    const T* dr = dist + row * ld;
+    const int tid = threadIdx.x;
+
+    // 1. count admissible (non-NaN) values
+    if (tid == 0) s_nvalid = 0;
+    __syncthreads();
+    uint32_t local = 0;
+    for (int64_t c = tid; c < cols; c += 256) {
+        T v = dr[c];
+        local += (v == v) ? 1u : 0u;
+    }
+    atomicAdd(&s_nvalid, local);
+    __syncthreads();
+    const uint32_t nvalid = s_nvalid;
+    const int kk = (int)((uint32_t)k < nvalid ? (uint32_t)k : nvalid);
+
+    if (kk > 0) {
+        // 2. radix select of the kk-th smallest key
+        K prefix = 0, pmask = 0;
+        uint32_t want = (uint32_t)kk;
+        for (int shift = KeyOf<T>::BITS - 8; shift >= 0; shift -= 8) {
+            hist[tid] = 0;
+            __syncthreads();
+            for (int64_t c = tid; c < cols; c += 256) {
+                T v = dr[c];
+                if (v != v) continue;
+                K key = KeyOf<T>::key(v);
+                if ((key & pmask) == prefix) atomicAdd(&hist[(uint32_t)(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t w = want;
+                int b = 0;
+                for (; b < 255; ++b) {
+                    if (hist[b] >= w) break;
+                    w -= hist[b];
+                }
+                s_prefix = prefix | ((K)b << shift);
+                s_want = w;
+            }
+            __syncthreads();
+            prefix = s_prefix;
+            want = s_want;
+            pmask |= ((K)255 << shift);
+            __syncthreads();
+        }
+        // prefix = kk-th smallest key; `want` of its copies are taken, lowest index first.
+        // 3. collect
+        if (tid == 0) {
+            s_cnt_less = 0;
+            s_cnt_eq = 0;
+        }
+        __syncthreads();
+        const uint32_t n_less = (uint32_t)kk - want;
+        for (int64_t base = 0; base < cols; base += 256) {
+            int64_t c = base + tid;
+            bool is_less = false, is_eq = false;
+            K key = 0;
+            if (c < cols) {
+                T v = dr[c];
+                if (v == v) {
+                    key = KeyOf<T>::key(v);
+                    is_less = key < prefix;
+                    is_eq = key == prefix;
+                }
+            }
+            if (is_less) {
+                uint32_t p = atomicAdd(&s_cnt_less, 1u);
+                if (p < n_less) {  // always true; keeps every store inside skey
+                    skey[p] = key;
+                    sidx[p] = (uint32_t)c;
+                }
+            }
+            // index-ordered rank among equal keys in this chunk
+            uint64_t bal = __builtin_amdgcn_ballot_w64(is_eq);
+            int lane = tid & 63, wv = tid >> 6;
+            uint32_t below = (uint32_t)__builtin_popcountll(bal & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+            if (lane == 0) s_wave_eq[wv] = (uint32_t)__builtin_popcountll(bal);
+            __syncthreads();
+            uint32_t before = s_cnt_eq;
+            for (int w2 = 0; w2 < wv; ++w2) before += s_wave_eq[w2];
+            if (is_eq) {
+                uint32_t r = before + below;
+                if (r < want && n_less + r < (uint32_t)kk) {
+                    skey[n_less + r] = key;
+                    sidx[n_less + r] = (uint32_t)c;
+                }
+            }
+            __syncthreads();
+            if (tid == 0) s_cnt_eq += s_wave_eq[0] + s_wave_eq[1] + s_wave_eq[2] + s_wave_eq[3];
+            __syncthreads();
+        }
+        // 4. bitonic sort of the kk kept pairs by (key, index)
+        int n2 = 1;
+        while (n2 < kk) n2 <<= 1;
+        for (int e = kk + tid; e < n2; e += 256) {
+            skey[e] = ~(K)0;
+            sidx[e] = kSentinelIdx;
+        }
+        __syncthreads();
+        for (int size = 2; size <= n2; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int e = tid; e < n2; e += 256) {
+                    int p = e ^ stride;
+                    if (p > e) {
+                        bool up = (e & size) == 0;
+                        K ka = skey[e], kb = skey[p];
+                        uint32_t ia = sidx[e], ib = sidx[p];
+                        bool a_gt = (ka > kb) || (ka == kb && ia > ib);
+                        if (a_gt == up) {
+                            skey[e] = kb;
+                            skey[p] = ka;
+                            sidx[e] = ib;
+                            sidx[p] = ia;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+    }
+    // 5. emit (value recovered from the key: exact, since the key map is a bijection)
+    for (int s = tid; s < k; s += 256) {
+        T v;
+        uint32_t ix;
+        if (s < kk) {
+            v = KeyOf<T>::val(skey[s]);
+            ix = sidx[s];
+        } else {
+            v = FloatTraits<T>::inf();
+            ix = 0;  // sentinel index emitted as 0 (crates/mlrs-kernels/src/knn.rs:2931-2961)
+        }
+        if (mode == EMIT_SQRT) v = FloatTraits<T>::sqrt_(v);
+        out_val[row * k + s] = v;
+        out_idx[row * k + s] = ix;
+    }
+}
+
+// argmin_dist_rows (crates/mlrs-kernels/src/kmeans.rs:284-310) over a
+// materialized rows x cols block: best seeded from column 0, strict `<`
+// afterwards (so a NaN in column 0 wins and NaN elsewhere never does).
+template <typename T>
+__global__ void argmin_rows_kernel(const T* __restrict__ dist, int64_t rows, int64_t cols, int64_t ld,
+                                   uint32_t* __restrict__ labels, T* __restrict__ best_out) {
+    int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const T* dr = dist + r * ld;
+    T best = dr[0];
+    uint32_t bc = 0;
+    for (int64_t c = 1; c < cols; ++c) {
+        T v = dr[c];
+        if (v < best) {
+            best = v;
+            bc = (uint32_t)c;
+        }
+    }
+    labels[r] = bc;
+    best_out[r] = best;
+}
+
+}  // namespace
+
+template <typename T>
+hipError_t launch_argmin_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, uint32_t* labels,
+                              T* best, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL((argmin_rows_kernel<T>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
+                       dist, rows, cols, ld, labels, best);
+    return hipGetLastError();
+}
+template hipError_t launch_argmin_rows<float>(const float*, int64_t, int64_t, int64_t, uint32_t*, float*,
+                                              hipStream_t);
+template hipError_t launch_argmin_rows<double>(const double*, int64_t, int64_t, int64_t, uint32_t*,
+                                               double*, hipStream_t);
+
+template <typename T>
+hipError_t launch_row_norms(const T* x, int64_t n, int64_t d, T* sq, T* inv, T* neg_inv,
+                            NormStats* stats, hipStream_t s) {
+    if (stats) hipLaunchKernelGGL((stats_reset_kernel<T>), dim3(1), dim3(64), 0, s, stats);
+    if (n > 0) {
+        unsigned blocks = (unsigned)((n + 255) / 256);
+        hipLaunchKernelGGL((row_norms_kernel<T>), dim3(blocks), dim3(256), 0, s, x, n, d, sq, inv,
+                           neg_inv, stats);
+    }
+    if (stats) hipLaunchKernelGGL((stats_finalize_kernel<T>), dim3(1), dim3(64), 0, s, stats);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_pairwise_tile(const T* x, int64_t nx, const T* y, int64_t ny, int64_t d, int arm,
+                                const T* xa, const T* ya, T* out, int64_t ldo, int do_sqrt,
+                                hipStream_t s) {
+    if (nx == 0 || ny == 0) return hipSuccess;
+    dim3 grid((unsigned)((ny + PT - 1) / PT), (unsigned)((nx + PT - 1) / PT));
+    switch (arm) {
+    case ARM_EUCLID_FMA:
+        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_EUCLID_FMA>), grid, dim3(256), 0, s, x, nx, y, ny,
+                           d, xa, ya, out, ldo, do_sqrt);
+        break;
+    case ARM_EUCLID_MULADD:
+        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_EUCLID_MULADD>), grid, dim3(256), 0, s, x, nx, y,
+                           ny, d, xa, ya, out, ldo, do_sqrt);
+        break;
+    case ARM_COS_FOLD:
+        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_COS_FOLD>), grid, dim3(256), 0, s, x, nx, y, ny, d,
+                           xa, ya, out, ldo, do_sqrt);
+        break;
+    case ARM_COS_HOST:
+        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_COS_HOST>), grid, dim3(256), 0, s, x, nx, y, ny, d,
+                           xa, ya, out, ldo, do_sqrt);
+        break;
+    case ARM_COS_PAIRWISE:
+        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_COS_PAIRWISE>), grid, dim3(256), 0, s, x, nx, y,
+                           ny, d, xa, ya, out, ldo, do_sqrt);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+int select_rows_max_k() { return SEL_MAXK; }
+
+template <typename T>
+hipError_t launch_select_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, int k, int mode,
+                              T* out_val, uint32_t* out_idx, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (k < 1 || k > SEL_MAXK) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((select_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, s, dist, rows, cols,
+                       ld, k, mode, out_val, out_idx);
+    return hipGetLastError();
+}
+
+template hipError_t launch_row_norms<float>(const float*, int64_t, int64_t, float*, float*, float*,
+                                            NormStats*, hipStream_t);
+template hipError_t launch_row_norms<double>(const double*, int64_t, int64_t, double*, double*, double*,
+                                             NormStats*, hipStream_t);
+template hipError_t launch_pairwise_tile<float>(const float*, int64_t, const float*, int64_t, int64_t, int,
+                                                const float*, const float*, float*, int64_t, int, hipStream_t);
+template hipError_t launch_pairwise_tile<double>(const double*, int64_t, const double*, int64_t, int64_t,
+                                                 int, const double*, const double*, double*, int64_t, int,
+                                                 hipStream_t);
+template hipError_t launch_select_rows<float>(const float*, int64_t, int64_t, int64_t, int, int, float*,
+                                              uint32_t*, hipStream_t);
+template hipError_t launch_select_rows<double>(const double*, int64_t, int64_t, int64_t, int, int, double*,
+                                               uint32_t*, hipStream_t);
+
+}  // namespace mlrs

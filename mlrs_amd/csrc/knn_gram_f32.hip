@@ -1,0 +1,464 @@
+// Fused f32 Gram-MFMA kNN with exact rescoring (gfx950).
+//
+// Replaces the GPU arm euclidean_topk_fused{,_dot,_dot_vec,_dot_vec8}
+// (crates/mlrs-kernels/src/knn.rs:377-2112) and the two-kernel
+// distance_direct -> top_k fallback (crates/mlrs-algos/src/neighbors/
+// nearest.rs:1058-1343) for f32, d <= 128, k <= 64, Euclidean and cosine.
+//
+// Shape of one workgroup: 4 waves x 32 queries = 128 queries, walking one
+// strip of index rows 32 at a time.
+//  * Each wave keeps its 32 query rows in VGPRs as the B operand of
+//    v_mfma_f32_32x32x2f32 (pre-scaled by -2 for Euclidean), loaded once.
+//  * The 32-row index tile is staged in LDS (row stride d_pad+4 floats: rows
+//    land 4 banks apart, so the ds_read_b128 A-operand reads do not conflict),
+//    prefetched into registers one tile ahead.
+//  * Euclidean: the accumulator starts at ||x_t||^2, so after the contraction
+//    acc = ||x_t||^2 - 2 x_t.q_j, the expansion minus the per-query constant.
+//    Cosine: tile rows are pre-scaled by -1/||x_t||, acc = -x_t.q_j/||x_t||.
+//  * Screen: acc is compared against a per-query threshold derived from the
+//    CURRENT exact k-th value plus a rigorous bound on the expansion's rounding
+//    error (plus the reference's own).  A pair that can still enter the exact
+//    top-k always passes; the comparison is !(acc > thr) so NaN passes too.
+//  * Passing (query, row) pairs are queued in LDS.  When a query's queue is
+//    half full the wave evaluates the queued pairs EXACTLY, in the reference
+//    arm's operation order (knn_common.hpp exact_pair), sorts them and merges
+//    them into the query's exact top-k list with the (value, index) order.
+// The kept lists are therefore the reference's own top-k: the full distance
+// matrix never reaches HBM and no tolerance is involved.
+#include "knn_common.hpp"
+#include "knn_kernels.hpp"
+
+namespace mlrs {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kQpw = 32;                 // queries per wave (MFMA N dimension)
+constexpr int kQpb = kWaves * kQpw;      // queries per workgroup
+constexpr int kBn = 32;                  // index rows per tile (MFMA M dimension)
+constexpr int kKcap = 64;                // largest k this kernel keeps
+constexpr int kQcap = 64;                // queued candidates per query
+constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct WaveLds {
+    float lval[kQpw][kKcap];
+    uint32_t lidx[kQpw][kKcap];
+    uint32_t qidx[kQpw][kQcap];
+    uint32_t cnt[kQpw];
+    float thr[kQpw];
+    float qa[kQpw];   // exact arm's query operand (row_sumsq for the fold arm)
+    float qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
+    float eps[kQpw];  // screen error bound
+};
+
+// Smallest float >= t.
+__device__ __forceinline__ float round_up_f(double t) {
+    float f = (float)t;
+    if ((double)f < t) {  // step one ulp towards +inf
+        uint32_t b = __float_as_uint(f);
+        if (f == 0.0f)
+            f = __uint_as_float(1u);
+        else
+            f = __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
+    }
+    return f;
+}
+
+template <bool COS>
+__device__ __forceinline__ float screen_threshold(float R, float qs, float eps) {
+    const float inf = __builtin_huge_valf();
+    if (!(R < inf)) return inf;  // list not yet full of finite values
+    if (!COS) {
+        // exact <= R  =>  ||x||^2 - 2 x.q <= R - ||q||^2 + eps
+        return round_up_f((double)R - (double)qs + (double)eps);
+    } else {
+        // exact <= R  =>  1 + acc/||q|| <= R + eps  =>  acc <= (R + eps - 1)||q||
+        if (qs == 0.0f) return -inf;  // zero query: every value is 1, lowest index kept
+        return round_up_f(((double)R + (double)eps - 1.0) * (double)qs);
+    }
+}
+
+template <int ARM, bool VEC4>
+__device__ __forceinline__ float exact_f32(const float* __restrict__ q, const float* __restrict__ y,
+                                           int64_t d, float qa, float ya) {
+    if (!VEC4) return exact_pair<float, ARM>(q, y, d, qa, ya);
+    // Same ascending-column operation order, 16-byte loads.
+    const float4* q4 = reinterpret_cast<const float4*>(q);
+    const float4* y4 = reinterpret_cast<const float4*>(y);
+    const int64_t n4 = d >> 2;
+    if (ARM == ARM_EUCLID_FMA || ARM == ARM_EUCLID_MULADD) {
+        float acc = 0.0f;
+        for (int64_t c = 0; c < n4; ++c) {
+            float4 a = q4[c], b = y4[c];
+            float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+            if (ARM == ARM_EUCLID_FMA) {
+                acc = __builtin_fmaf(d0, d0, acc);
+                acc = __builtin_fmaf(d1, d1, acc);
+                acc = __builtin_fmaf(d2, d2, acc);
+                acc = __builtin_fmaf(d3, d3, acc);
+            } else {
+                acc = acc + d0 * d0;
+                acc = acc + d1 * d1;
+                acc = acc + d2 * d2;
+                acc = acc + d3 * d3;
+            }
+        }
+        return acc;
+    } else {  // ARM_COS_FOLD
+        float dot = 0.0f;
+        for (int64_t c = 0; c < n4; ++c) {
+            float4 a = q4[c], b = y4[c];
+            dot = __builtin_fmaf(a.x, b.x, dot);
+            dot = __builtin_fmaf(a.y, b.y, dot);
+            dot = __builtin_fmaf(a.z, b.z, dot);
+            dot = __builtin_fmaf(a.w, b.w, dot);
+        }
+        float denom = __builtin_sqrtf(qa * ya);
+        float sim = (denom > 0.0f) ? dot / denom : 0.0f;
+        return clamp02<float>(1.0f - sim);
+    }
+}
+
+// Evaluate query j's queued rows exactly and merge them into its list.
+template <int ARM, bool COS, bool VEC4>
+__device__ __noinline__ void flush_query(WaveLds& L, int j, int lane, const GramArgs32& a,
+                                         int64_t qglob) {
+    const float inf = __builtin_huge_valf();
+    const uint32_t n = L.cnt[j];
+    const float* qp = a.q + qglob * a.d;
+    float e = inf;
+    uint32_t t = kSentinelIdx;
+    if ((uint32_t)lane < n) {
+        t = L.qidx[j][lane];
+        float ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f;
+        e = exact_f32<ARM, VEC4>(qp, a.x + (int64_t)t * a.d, a.d, L.qa[j], ya);
+        if (e != e) {  // NaN is never admitted
+            e = inf;
+            t = kSentinelIdx;
+        }
+    }
+    wave_sort64<float>(e, t, lane);
+    const int k = a.k;
+    float lv = (lane < k) ? L.lval[j][lane] : inf;
+    uint32_t li = (lane < k) ? L.lidx[j][lane] : kSentinelIdx;
+    wave_merge64<float>(lv, li, e, t, lane);
+    if (lane < k) {
+        L.lval[j][lane] = lv;
+        L.lidx[j][lane] = li;
+    }
+    float R = shfl_f(lv, k - 1);
+    if (lane == 0) {
+        L.cnt[j] = 0;
+        L.thr[j] = screen_threshold<COS>(R, L.qs[j], L.eps[j]);
+    }
+}
+
+template <int NG, int ARM, bool COS, bool VEC4>
+__global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
+    constexpr int DP = NG * 8;        // padded feature count
+    constexpr int STRIDE = DP + 4;    // LDS row stride (floats)
+    constexpr int TILE_F4 = kBn * DP / 4;
+    constexpr int PF = (TILE_F4 + 255) / 256;
+
+    __shared__ __attribute__((aligned(16))) float tile[2][kBn][STRIDE];
+    __shared__ __attribute__((aligned(16))) float tnorm[2][kBn];
+    __shared__ WaveLds wl[kWaves];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int h = lane >> 5;
+    const int jl = lane & 31;
+    WaveLds& L = wl[w];
+    const float inf = __builtin_huge_valf();
+
+    const int64_t qwave = (int64_t)blockIdx.x * kQpb + w * kQpw;  // first query of this wave
+    const int64_t qmine = qwave + jl;
+    const bool qvalid = qmine < a.nq;
+    const int64_t t_begin = (int64_t)blockIdx.y * a.rows_per_strip;
+    int64_t t_end = t_begin + a.rows_per_strip;
+    if (t_end > a.nt) t_end = a.nt;
+    const int64_t d = a.d;
+
+    // ---- per-query constants, lists, queues ----
+    if (lane < kQpw) {
+        float qsq = qvalid ? a.qsq[qmine] : 0.0f;
+        L.cnt[lane] = 0;
+        L.thr[lane] = qvalid ? inf : -inf;
+        if (!COS) {
+            L.qs[lane] = qsq;
+            L.qa[lane] = 0.0f;
+            L.eps[lane] = (float)(a.eps_rel * ((double)qsq + (double)a.stats->xsq_max) + a.eps_abs);
+        } else {
+            L.qs[lane] = __builtin_sqrtf(qsq);
+            L.qa[lane] = qsq;
+            L.eps[lane] = (float)a.eps_abs;
+        }
+    }
+    for (int i = lane; i < kQpw * kKcap; i += 64) {
+        (&L.lval[0][0])[i] = inf;
+        (&L.lidx[0][0])[i] = kSentinelIdx;
+    }
+
+    // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3] ----
+    float4 qreg[NG];
+    {
+        const float scale = COS ? 1.0f : -2.0f;
+        const float* qp = a.q + qmine * d;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                int64_t c = 8 * g + 4 * h + e;
+                v[e] = (qvalid && c < d) ? qp[c] * scale : 0.0f;
+            }
+            qreg[g] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+
+    // ---- tile prefetch into registers ----
+    float4 pf[PF];
+    float pfn = 0.0f;
+    auto prefetch = [&](int64_t t0) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            int f = tid + 256 * p;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (f < TILE_F4) {
+                int r = f / (DP / 4);
+                int c4 = f % (DP / 4);
+                int64_t t = t0 + r;
+                if (t < t_end) {
+                    const float* src = a.x + t * d + 4 * c4;
+                    if (VEC4) {
+                        if (4 * c4 < d) v = *reinterpret_cast<const float4*>(src);
+                    } else {
+                        float e4[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) e4[e] = (4 * c4 + e < d) ? src[e] : 0.0f;
+                        v = make_float4(e4[0], e4[1], e4[2], e4[3]);
+                    }
+                    if (COS) {
+                        float s = a.xscale[t];
+                        v.x *= s; v.y *= s; v.z *= s; v.w *= s;
+                    }
+                }
+            }
+            pf[p] = v;
+        }
+        if (!COS && tid < kBn) {
+            int64_t t = t0 + tid;
+            pfn = (t < t_end) ? a.xsq[t] : 0.0f;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            int f = tid + 256 * p;
+            if (f < TILE_F4) {
+                int r = f / (DP / 4);
+                int c4 = f % (DP / 4);
+                *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = pf[p];
+            }
+        }
+        if (!COS && tid < kBn) tnorm[buf][tid] = pfn;
+    };
+
+    if (t_begin < t_end) prefetch(t_begin);
+    __syncthreads();  // per-wave LDS init visible to the wave (and tile buffers free)
+
+    float thr = L.thr[jl];
+    int buf = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn) {
+        store_tile(buf);
+        __syncthreads();
+        if (t0 + kBn < t_end) prefetch(t0 + kBn);
+
+        f32x16 acc;
+        if (!COS) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                float4 n4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                acc[4 * g4 + 0] = n4.x;
+                acc[4 * g4 + 1] = n4.y;
+                acc[4 * g4 + 2] = n4.z;
+                acc[4 * g4 + 3] = n4.w;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            float4 av = *reinterpret_cast<const float4*>(&tile[buf][jl][8 * g + 4 * h]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qreg[g].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qreg[g].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qreg[g].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
+        }
+
+        // ---- screen: lane holds rows 8*(r/4) + 4h + (r%4) of the tile, query jl ----
+        bool hit = false;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) hit |= !(acc[r] > thr);
+        if (__builtin_amdgcn_ballot_w64(hit)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int64_t t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (qvalid && t < t_end && !(acc[r] > thr)) {
+                    uint32_t pos = atomicAdd(&L.cnt[jl], 1u);
+                    L.qidx[jl][pos] = (uint32_t)t;
+                }
+            }
+        }
+        // ---- flush queries whose queue could overflow on the next tile ----
+        bool need = (lane < kQpw) && (L.cnt[lane] > (uint32_t)kFlushAt);
+        uint64_t mask = __builtin_amdgcn_ballot_w64(need);
+        if (mask) {
+            while (mask) {
+                int j = __builtin_ctzll(mask);
+                mask &= mask - 1;
+                flush_query<ARM, COS, VEC4>(L, j, lane, a, qwave + j);
+            }
+            thr = L.thr[jl];
+        }
+        buf ^= 1;
+    }
+
+    // ---- final flush of every non-empty queue ----
+    {
+        bool need = (lane < kQpw) && (L.cnt[lane] > 0u);
+        uint64_t mask = __builtin_amdgcn_ballot_w64(need);
+        while (mask) {
+            int j = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            flush_query<ARM, COS, VEC4>(L, j, lane, a, qwave + j);
+        }
+    }
+
+    // ---- emit ----
+    const int k = a.k;
+    for (int j = 0; j < kQpw; ++j) {
+        int64_t qg = qwave + j;
+        if (qg >= a.nq) break;
+        if (lane < k) {
+            float v = L.lval[j][lane];
+            uint32_t ix = L.lidx[j][lane];
+            if (a.nstrips > 1) {
+                int64_t o = ((int64_t)blockIdx.y * a.nq + qg) * k + lane;
+                a.part_val[o] = v;
+                a.part_idx[o] = ix;
+            } else {
+                emit_one_f32(a.mode, a, qg, lane, v, ix);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+// Output transform shared with the strip merge: the boundary root of
+// prims/knn.rs:877-883 (Euclidean), identity (cosine), or the k-means
+// (label, squared distance) pair with argmin_dist_rows' centre-0 seeding
+// (crates/mlrs-kernels/src/kmeans.rs:284-310).
+__device__ void emit_one_f32(int mode, const GramArgs32& a, int64_t qg, int slot, float v, uint32_t ix) {
+    int64_t o = qg * a.k + slot;
+    if (mode == EMIT_KMEANS) {
+        // argmin_dist_rows seeds `best` from centre 0 unconditionally, so a NaN
+        // distance to centre 0 wins with label 0.  That distance can only be
+        // NaN when a norm is non-finite; check those rows exactly.
+        float q0 = a.qsq[qg];
+        float c0 = a.xsq[0];
+        if (!(q0 < __builtin_huge_valf()) || !(c0 < __builtin_huge_valf())) {
+            float e0 = exact_pair<float, ARM_EUCLID_MULADD>(a.q + qg * a.d, a.x, a.d, 0.0f, 0.0f);
+            if (e0 != e0) {
+                v = e0;
+                ix = 0;
+            }
+        }
+        a.out_val[o] = v;
+        a.out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
+        return;
+    }
+    a.out_val[o] = (mode == EMIT_SQRT) ? __builtin_sqrtf(v) : v;
+    a.out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
+}
+
+// Merge the per-strip exact lists of one query per wave (the strip merge of
+// select_k_onepass_indexed, crates/mlrs-kernels/src/topk.rs:612-758, here a
+// wave-wide bitonic merge of sorted lists).
+__global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (qg >= a.nq) return;
+    const int k = a.k;
+    const float inf = __builtin_huge_valf();
+    float lv = inf;
+    uint32_t li = kSentinelIdx;
+    if (lane < k) {
+        lv = a.part_val[qg * k + lane];
+        li = a.part_idx[qg * k + lane];
+    }
+    for (int s = 1; s < a.nstrips; ++s) {
+        float v = inf;
+        uint32_t ix = kSentinelIdx;
+        if (lane < k) {
+            int64_t o = ((int64_t)s * a.nq + qg) * k + lane;
+            v = a.part_val[o];
+            ix = a.part_idx[o];
+        }
+        wave_merge64<float>(lv, li, v, ix, lane);
+    }
+    if (lane < k) emit_one_f32(a.mode, a, qg, lane, lv, li);
+}
+
+template <int NG, int ARM, bool COS, bool VEC4>
+static hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
+    dim3 grid((unsigned)nblocks, (unsigned)a.nstrips);
+    hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int ARM, bool COS, bool VEC4>
+static hipError_t launch_arm(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
+    int ng = (int)((a.d + 7) / 8);
+    if (ng <= 2) return launch_ng<2, ARM, COS, VEC4>(a, nblocks, s);
+    if (ng <= 4) return launch_ng<4, ARM, COS, VEC4>(a, nblocks, s);
+    if (ng <= 8) return launch_ng<8, ARM, COS, VEC4>(a, nblocks, s);
+    if (ng <= 12) return launch_ng<12, ARM, COS, VEC4>(a, nblocks, s);
+    return launch_ng<16, ARM, COS, VEC4>(a, nblocks, s);
+}
+
+int gram_f32_max_k() { return kKcap; }
+int gram_f32_max_d() { return 128; }
+int gram_f32_queries_per_block() { return kQpb; }
+int gram_f32_rows_per_tile() { return kBn; }
+
+hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
+    const int64_t nblocks = (a.nq + kQpb - 1) / kQpb;
+    const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    hipError_t e;
+    if (arm == ARM_EUCLID_FMA)
+        e = vec4 ? launch_arm<ARM_EUCLID_FMA, false, true>(a, nblocks, s)
+                 : launch_arm<ARM_EUCLID_FMA, false, false>(a, nblocks, s);
+    else if (arm == ARM_EUCLID_MULADD)
+        e = vec4 ? launch_arm<ARM_EUCLID_MULADD, false, true>(a, nblocks, s)
+                 : launch_arm<ARM_EUCLID_MULADD, false, false>(a, nblocks, s);
+    else if (arm == ARM_COS_FOLD)
+        e = vec4 ? launch_arm<ARM_COS_FOLD, true, true>(a, nblocks, s)
+                 : launch_arm<ARM_COS_FOLD, true, false>(a, nblocks, s);
+    else
+        return hipErrorInvalidValue;
+    if (e != hipSuccess) return e;
+    if (a.nstrips > 1) {
+        hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+}  // namespace mlrs

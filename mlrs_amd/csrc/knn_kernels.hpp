@@ -1,0 +1,97 @@
+// Launch-side declarations shared by the kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlrs {
+
+enum EmitMode : int {
+    EMIT_SQRT = 0,      // Euclidean kNN: boundary sqrt of the k kept squared values
+    EMIT_IDENTITY = 1,  // cosine kNN: values as kept
+    EMIT_KMEANS = 2,    // k-means assignment: squared value + argmin centre-0 rule
+};
+
+// Device-resident summary of the index rows' squared norms, written by the
+// norm kernel and read by the Gram kernels' screen bound (no host sync).
+struct NormStats {
+    unsigned long long xsq_max_bits;  // max finite-or-inf squared norm (NaN rows ignored), as bits
+    float xsq_max;                    // f32 view filled by the finalize kernel
+    double xsq_max64;                 // f64 view
+};
+
+struct GramArgs32 {
+    const float* q;
+    int64_t nq;
+    const float* x;
+    int64_t nt;
+    int64_t d;
+    int k;
+    int mode;          // EmitMode
+    const float* qsq;  // query row_sumsq
+    const float* xsq;  // index row_sumsq
+    const float* xscale;  // cosine: -1/||x_t|| (0 for zero rows)
+    const NormStats* stats;
+    double eps_rel;    // Euclidean screen bound: eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
+    double eps_abs;    // cosine screen bound (absolute)
+    int64_t rows_per_strip;
+    int nstrips;
+    float* part_val;   // [nstrips][nq][k] when nstrips > 1
+    uint32_t* part_idx;
+    float* out_val;    // [nq][k]
+    uint32_t* out_idx;
+};
+
+__device__ void emit_one_f32(int mode, const GramArgs32& a, int64_t qg, int slot, float v, uint32_t ix);
+
+hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
+int gram_f32_max_k();
+int gram_f32_max_d();
+int gram_f32_queries_per_block();
+int gram_f32_rows_per_tile();
+
+// Row norms: sq[r] = row_sumsq (separate multiply/add, ascending column),
+// optional inv[r] = (sq > 0) ? 1/sqrt(sq) : 0 and optional neg-inverse scale.
+template <typename T>
+hipError_t launch_row_norms(const T* x, int64_t n, int64_t d, T* sq, T* inv, T* neg_inv,
+                            NormStats* stats, hipStream_t s);
+
+// Generic exact path: tiled exact pairwise values under one arm.
+template <typename T>
+hipError_t launch_pairwise_tile(const T* x, int64_t nx, const T* y, int64_t ny, int64_t d, int arm,
+                                const T* xa, const T* ya, T* out, int64_t ldo, int do_sqrt,
+                                hipStream_t s);
+
+// Generic exact path: per-row (value, index) top-k over a materialized
+// rows x cols matrix, NaN never admitted, sentinel-padded.
+template <typename T>
+hipError_t launch_select_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, int k,
+                              int mode, T* out_val, uint32_t* out_idx, hipStream_t s);
+int select_rows_max_k();
+
+// argmin_dist_rows semantics over a materialized block (generic k-means path).
+template <typename T>
+hipError_t launch_argmin_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, uint32_t* labels,
+                              T* best, hipStream_t s);
+
+// Low-dimension ALU path (exact, lane per query).
+struct LowdArgs32 {
+    const float* q;
+    int64_t nq;
+    const float* x;
+    int64_t nt;
+    int64_t d;
+    int k;
+    int mode;
+    int64_t rows_per_strip;
+    int nstrips;
+    float* part_val;
+    uint32_t* part_idx;
+    float* out_val;
+    uint32_t* out_idx;
+};
+hipError_t launch_lowd_f32(const LowdArgs32& a, int arm, hipStream_t s);
+int lowd_max_d();
+int lowd_max_k();
+
+}  // namespace mlrs

@@ -1,0 +1,144 @@
+"""CPU oracle for the brute-force kNN path -- TEST INFRASTRUCTURE ONLY.
+
+A ctypes front for ``ref_cpu.c`` (the plain-C restatement of mlrs's cpu-backend
+kNN, k-means assignment and pairwise-distance arithmetic; see that file's header
+for the reference citations).  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s CPU-baseline leg may import this package, and only as the
+checker or the timed CPU baseline -- never as part of the product path.
+
+Parity status of each function (how it is pinned) is listed in
+``tests/test_oracle.py``; every function here is pinned by at least one of: the
+reference's sklearn fixtures, an exact-arithmetic brute force on small inputs,
+or a known-answer invariant from the reference's own tests.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libmlrs_oracle.so")
+
+METRIC_EUCLIDEAN = 0
+METRIC_COSINE = 1
+METRICS = {"euclidean": METRIC_EUCLIDEAN, "cosine": METRIC_COSINE}
+
+ARM_DIRECT = 0
+ARM_METRIC = 1
+ARM_HOST = 2
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        from . import build as _build  # noqa: F401  (oracle/build.py)
+        _build.build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+    lib.orc_knn_arm.argtypes = [i64, i64, i32]
+    lib.orc_knn_arm.restype = i32
+    lib.orc_max_threads.argtypes = []
+    lib.orc_max_threads.restype = i32
+    for s in ("f32", "f64"):
+        f = getattr(lib, "orc_knn_topk_" + s)
+        f.argtypes = [vp, i64, vp, i64, i64, i64, i32, vp, vp, i32]
+        f.restype = i32
+        f = getattr(lib, "orc_kmeans_assign_" + s)
+        f.argtypes = [vp, i64, vp, i64, i64, vp, vp, i32]
+        f.restype = i32
+        f = getattr(lib, "orc_pairwise_" + s)
+        f.argtypes = [vp, i64, vp, i64, i64, i32, i32, vp, i32]
+        f.restype = i32
+        f = getattr(lib, "orc_row_sqnorms_" + s)
+        f.argtypes = [vp, i64, i64, vp]
+        f.restype = None
+    _lib = lib
+    return lib
+
+
+def _suffix(dtype):
+    if dtype == np.float32:
+        return "f32"
+    if dtype == np.float64:
+        return "f64"
+    raise TypeError("oracle supports float32/float64, got %s" % dtype)
+
+
+def _metric_id(metric):
+    if isinstance(metric, str):
+        return METRICS[metric]
+    return int(metric)
+
+
+def knn_arm(d, k, metric="euclidean"):
+    """Which reference cpu arm serves (d, k, metric): ARM_DIRECT/METRIC/HOST."""
+    return _load().orc_knn_arm(int(d), int(k), _metric_id(metric))
+
+
+def max_threads():
+    return _load().orc_max_threads()
+
+
+def knn_topk(xq, xt, k, metric="euclidean", nthreads=0):
+    """(distances, uint32 indices), each (n_query, k), ascending (value, index)."""
+    lib = _load()
+    xq = np.ascontiguousarray(xq)
+    xt = np.ascontiguousarray(xt, dtype=xq.dtype)
+    nq, d = xq.shape
+    nt, d2 = xt.shape
+    assert d == d2
+    s = _suffix(xq.dtype)
+    out_v = np.empty((nq, k), dtype=xq.dtype)
+    out_i = np.empty((nq, k), dtype=np.uint32)
+    rc = getattr(lib, "orc_knn_topk_" + s)(
+        xq.ctypes.data, nq, xt.ctypes.data, nt, d, int(k), _metric_id(metric),
+        out_v.ctypes.data, out_i.ctypes.data, int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle knn_topk rejected k=%d for n_train=%d" % (k, nt))
+    return out_v, out_i
+
+
+def kmeans_assign(x, centers, nthreads=0):
+    """(uint32 labels, squared distances) of the nearest centre per row."""
+    lib = _load()
+    x = np.ascontiguousarray(x)
+    centers = np.ascontiguousarray(centers, dtype=x.dtype)
+    n, d = x.shape
+    kc = centers.shape[0]
+    s = _suffix(x.dtype)
+    labels = np.empty(n, dtype=np.uint32)
+    dist = np.empty(n, dtype=x.dtype)
+    rc = getattr(lib, "orc_kmeans_assign_" + s)(
+        x.ctypes.data, n, centers.ctypes.data, kc, d, labels.ctypes.data,
+        dist.ctypes.data, int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle kmeans_assign rejected k=%d for n=%d" % (kc, n))
+    return labels, dist
+
+
+def pairwise(x, y, metric="euclidean", sqrt=False, nthreads=0):
+    lib = _load()
+    x = np.ascontiguousarray(x)
+    y = np.ascontiguousarray(y, dtype=x.dtype)
+    nx, d = x.shape
+    ny = y.shape[0]
+    out = np.empty((nx, ny), dtype=x.dtype)
+    rc = getattr(lib, "orc_pairwise_" + _suffix(x.dtype))(
+        x.ctypes.data, nx, y.ctypes.data, ny, d, _metric_id(metric), int(bool(sqrt)),
+        out.ctypes.data, int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle pairwise rejected d=%d" % d)
+    return out
+
+
+def row_sqnorms(x):
+    lib = _load()
+    x = np.ascontiguousarray(x)
+    n, d = x.shape
+    out = np.empty(n, dtype=x.dtype)
+    getattr(lib, "orc_row_sqnorms_" + _suffix(x.dtype))(x.ctypes.data, n, d, out.ctypes.data)
+    return out

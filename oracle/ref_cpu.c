@@ -1,0 +1,370 @@
+/*
+ * oracle/ref_cpu.c -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+ *
+ * A plain-C restatement of the arithmetic and selection rules of mlrs's
+ * cpu-backend brute-force kNN, k-means assignment and pairwise-distance paths.
+ * It exists to check the HIP engine (tests/, __graft_entry__.smoke) and to be
+ * timed as the CPU baseline (bench.py's cpu_baseline leg).  Nothing in the
+ * product (mlrs_amd/) may link, load or call it.
+ *
+ * Build: oracle/build.py (gcc -O3 -march=native -ffp-contract=off -fopenmp).
+ * -ffp-contract=off is load-bearing: every multiply and add below rounds
+ * separately, and a fused multiply-add appears ONLY where the reference writes
+ * one (`fma(...)`), exactly as in the Rust/CubeCL sources cited per function.
+ *
+ * Arm dispatch (which arithmetic serves which shape) follows
+ * crates/mlrs-algos/src/neighbors/nearest.rs:891-953 (`metric_topk`) on the cpu
+ * backend with Device::Auto:
+ *   1. Euclidean, d <= 32 and k <= 16  -> euclidean_topk_rows_cpu_direct
+ *      (crates/mlrs-backend/src/prims/knn.rs:400-412 cpu_rows_applicable,
+ *       crates/mlrs-kernels/src/knn.rs:2968-3227): acc = fma(x-y, x-y, acc).
+ *   2. else d <= 128 and k <= 128      -> *_topk_rows_cpu_metric
+ *      (prims/knn.rs:703-720, kernels/knn.rs:3265-3375, 3646-3661):
+ *      Euclidean fma(x-y, x-y, acc); cosine fma(x, y, dot) folded by
+ *      cosine_fold with row_sumsq squared norms.
+ *   3. else                             -> knn_host_topk
+ *      (crates/mlrs-backend/src/prims/knn_host.rs:418-851): Euclidean
+ *      acc + diff*diff; cosine acc + x*y with reciprocal norms.
+ * Selection is THE admission rule of kernels/knn.rs:2655-2706 (`insert_lane`)
+ * and knn_host.rs:777-810 (`insert`): (value, index) order, lowest index wins a
+ * tie, NaN is never admitted, lists are prefilled with (+inf, UINT32_MAX) and
+ * a surviving sentinel index is emitted as 0 (kernels/knn.rs:2931-2961).
+ * Because that order is total on admitted pairs, the k kept pairs do not
+ * depend on the order candidates are offered, so this file is free to walk
+ * query blocks in parallel (the reference makes the same argument,
+ * crates/mlrs-backend/tests/knn_test.rs:881-884).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_METRIC_EUCLIDEAN 0
+#define ORC_METRIC_COSINE 1
+
+#define ORC_ARM_DIRECT 0
+#define ORC_ARM_METRIC 1
+#define ORC_ARM_HOST 2
+
+#define ORC_QB 32
+
+/* Which cpu arm the reference dispatch picks for this shape
+ * (nearest.rs:910-947; caps CPU_MAX_COLS=32 / CPU_K_CAP=16 at
+ * kernels/knn.rs:2206-2210, CPU_METRIC_MAX_COLS=128 / CPU_METRIC_K_CAP=128 at
+ * kernels/knn.rs:3240-3257). */
+int orc_knn_arm(int64_t d, int64_t k, int metric)
+{
+    if (metric == ORC_METRIC_EUCLIDEAN && d >= 1 && d <= 32 && k >= 1 && k <= 16)
+        return ORC_ARM_DIRECT;
+    if (d >= 1 && d <= 128 && k >= 1 && k <= 128)
+        return ORC_ARM_METRIC;
+    return ORC_ARM_HOST;
+}
+
+static void set_threads(int nthreads)
+{
+#ifdef _OPENMP
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+}
+
+int orc_max_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/*
+ * The template below is instantiated for float and double.  T is the element
+ * type, S the symbol suffix, FMA/SQRT the matching libm routines.
+ */
+#define ORC_DEFINE(T, S, FMA, SQRT)                                                        \
+                                                                                           \
+/* row_sumsq / row_sqnorm: acc += v*v over ascending c (kernels/knn.rs:2130-2149,         \
+ * kernels/kmeans.rs:610). */                                                              \
+void orc_row_sqnorms_##S(const T *x, int64_t n, int64_t d, T *out)                         \
+{                                                                                          \
+    for (int64_t r = 0; r < n; r++) {                                                      \
+        T acc = (T)0;                                                                      \
+        const T *row = x + r * d;                                                          \
+        for (int64_t c = 0; c < d; c++) {                                                  \
+            T v = row[c];                                                                  \
+            acc = acc + v * v;                                                             \
+        }                                                                                  \
+        out[r] = acc;                                                                      \
+    }                                                                                      \
+}                                                                                          \
+                                                                                           \
+/* row_inv_norm_host (knn_host.rs:382-397): 1/sqrt(sum v*v), 0 for a zero row. */          \
+static void inv_norms_##S(const T *x, int64_t n, int64_t d, T *out)                        \
+{                                                                                          \
+    for (int64_t r = 0; r < n; r++) {                                                      \
+        T acc = (T)0;                                                                      \
+        const T *row = x + r * d;                                                          \
+        for (int64_t c = 0; c < d; c++)                                                    \
+            acc = acc + row[c] * row[c];                                                   \
+        out[r] = (acc > (T)0) ? (T)1 / SQRT(acc) : (T)0;                                   \
+    }                                                                                      \
+}                                                                                          \
+                                                                                           \
+/* insert_lane / insert: fold (v, t) into a sorted k-list or reject it. */                 \
+static inline void insert_##S(T *lval, uint32_t *lidx, int64_t k, T v, uint32_t t)         \
+{                                                                                          \
+    T w = lval[k - 1];                                                                     \
+    if (!(v < w || (v == w && t < lidx[k - 1])))                                           \
+        return;                                                                            \
+    T cav = v;                                                                             \
+    uint32_t cai = t;                                                                      \
+    for (int64_t j = 0; j < k; j++) {                                                      \
+        T jv = lval[j];                                                                    \
+        uint32_t ji = lidx[j];                                                             \
+        if (cav < jv || (cav == jv && cai < ji)) {                                         \
+            lval[j] = cav;                                                                 \
+            lidx[j] = cai;                                                                 \
+            cav = jv;                                                                      \
+            cai = ji;                                                                      \
+        }                                                                                  \
+    }                                                                                      \
+}                                                                                          \
+                                                                                           \
+/* One 32-query block against every training row, under `arm`/`metric`.                 \
+ * xt is the transposed tile xt[c*QB + a]; lanes >= active stage zeros and are            \
+ * never emitted.  qn / yn are the cosine norm operands of the arm (squared              \
+ * norms for the metric family, reciprocal norms for the host arm). */                     \
+static void scan_block_##S(const T *xt, int64_t active, const T *xtrain, int64_t nt,       \
+                           int64_t d, int64_t k, int metric, int arm, const T *qn,         \
+                           const T *yn, T *lval, uint32_t *lidx)                           \
+{                                                                                          \
+    T acc[ORC_QB];                                                                         \
+    T worst[ORC_QB];                                                                       \
+    for (int a = 0; a < ORC_QB; a++)                                                       \
+        worst[a] = (a < active) ? (T)INFINITY : (T)-INFINITY;                              \
+    for (int64_t t = 0; t < nt; t++) {                                                     \
+        const T *y = xtrain + t * d;                                                       \
+        for (int a = 0; a < ORC_QB; a++)                                                   \
+            acc[a] = (T)0;                                                                 \
+        if (metric == ORC_METRIC_EUCLIDEAN) {                                              \
+            if (arm == ORC_ARM_HOST) {                                                     \
+                for (int64_t c = 0; c < d; c++) {                                          \
+                    T yc = y[c];                                                           \
+                    const T *xc = xt + c * ORC_QB;                                         \
+                    for (int a = 0; a < ORC_QB; a++) {                                     \
+                        T diff = xc[a] - yc;                                               \
+                        acc[a] = acc[a] + diff * diff;                                     \
+                    }                                                                      \
+                }                                                                          \
+            } else {                                                                       \
+                for (int64_t c = 0; c < d; c++) {                                          \
+                    T yc = y[c];                                                           \
+                    const T *xc = xt + c * ORC_QB;                                         \
+                    for (int a = 0; a < ORC_QB; a++) {                                     \
+                        T diff = xc[a] - yc;                                               \
+                        acc[a] = FMA(diff, diff, acc[a]);                                  \
+                    }                                                                      \
+                }                                                                          \
+            }                                                                              \
+        } else {                                                                           \
+            if (arm == ORC_ARM_HOST) {                                                     \
+                for (int64_t c = 0; c < d; c++) {                                          \
+                    T yc = y[c];                                                           \
+                    const T *xc = xt + c * ORC_QB;                                         \
+                    for (int a = 0; a < ORC_QB; a++)                                       \
+                        acc[a] = acc[a] + xc[a] * yc;                                      \
+                }                                                                          \
+                T iy = yn[t];                                                              \
+                for (int a = 0; a < ORC_QB; a++) {                                         \
+                    T dv = (T)1 - acc[a] * qn[a] * iy;                                     \
+                    dv = (dv < (T)0) ? (T)0 : dv;                                          \
+                    dv = (dv > (T)2) ? (T)2 : dv;                                          \
+                    acc[a] = dv;                                                           \
+                }                                                                          \
+            } else {                                                                       \
+                for (int64_t c = 0; c < d; c++) {                                          \
+                    T yc = y[c];                                                           \
+                    const T *xc = xt + c * ORC_QB;                                         \
+                    for (int a = 0; a < ORC_QB; a++)                                       \
+                        acc[a] = FMA(xc[a], yc, acc[a]);                                   \
+                }                                                                          \
+                T ynt = yn[t];                                                             \
+                for (int a = 0; a < ORC_QB; a++) {                                         \
+                    T denom = SQRT(qn[a] * ynt);                                           \
+                    T sim = (denom > (T)0) ? acc[a] / denom : (T)0;                        \
+                    T dv = (T)1 - sim;                                                     \
+                    dv = (dv < (T)0) ? (T)0 : dv;                                          \
+                    dv = (dv > (T)2) ? (T)2 : dv;                                          \
+                    acc[a] = dv;                                                           \
+                }                                                                          \
+            }                                                                              \
+        }                                                                                  \
+        int hit = 0;                                                                       \
+        for (int a = 0; a < ORC_QB; a++)                                                   \
+            hit |= (acc[a] <= worst[a]);                                                   \
+        if (hit) {                                                                         \
+            for (int a = 0; a < active; a++) {                                             \
+                insert_##S(lval + a * k, lidx + a * k, k, acc[a], (uint32_t)t);            \
+                worst[a] = lval[a * k + k - 1];                                            \
+            }                                                                              \
+        }                                                                                  \
+    }                                                                                      \
+}                                                                                          \
+                                                                                           \
+/* Brute-force kNN under the reference's cpu dispatch.  Returns true distances            \
+ * (sqrt applied to the k selected Euclidean values, prims/knn.rs:877-883 and            \
+ * knn_host.rs:826-851), indices as uint32 with the sentinel clamped to 0.               \
+ * Returns 0, or -1 for a k outside [1, nt]. */                                            \
+int orc_knn_topk_##S(const T *xq, int64_t nq, const T *xtrain, int64_t nt, int64_t d,      \
+                     int64_t k, int metric, T *out_val, uint32_t *out_idx, int nthreads)   \
+{                                                                                          \
+    if (k < 1 || k > nt || nq < 0 || d < 1)                                                \
+        return -1;                                                                         \
+    int arm = orc_knn_arm(d, k, metric);                                                   \
+    T *qn = NULL, *yn = NULL;                                                              \
+    if (metric == ORC_METRIC_COSINE) {                                                     \
+        qn = (T *)malloc(sizeof(T) * (size_t)(nq > 0 ? nq : 1));                           \
+        yn = (T *)malloc(sizeof(T) * (size_t)nt);                                          \
+        if (arm == ORC_ARM_HOST) {                                                         \
+            inv_norms_##S(xq, nq, d, qn);                                                  \
+            inv_norms_##S(xtrain, nt, d, yn);                                              \
+        } else {                                                                           \
+            orc_row_sqnorms_##S(xq, nq, d, qn);                                            \
+            orc_row_sqnorms_##S(xtrain, nt, d, yn);                                        \
+        }                                                                                  \
+    }                                                                                      \
+    int64_t nblocks = (nq + ORC_QB - 1) / ORC_QB;                                          \
+    set_threads(nthreads);                                                                 \
+    _Pragma("omp parallel")                                                                \
+    {                                                                                      \
+        T *xt = (T *)malloc(sizeof(T) * (size_t)(d * ORC_QB));                             \
+        T *lval = (T *)malloc(sizeof(T) * (size_t)(k * ORC_QB));                           \
+        uint32_t *lidx = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)(k * ORC_QB));      \
+        T qblk[ORC_QB];                                                                    \
+        _Pragma("omp for schedule(dynamic, 1)")                                            \
+        for (int64_t b = 0; b < nblocks; b++) {                                            \
+            int64_t q0 = b * ORC_QB;                                                       \
+            int64_t active = nq - q0 < ORC_QB ? nq - q0 : ORC_QB;                          \
+            for (int64_t c = 0; c < d; c++)                                                \
+                for (int a = 0; a < ORC_QB; a++)                                           \
+                    xt[c * ORC_QB + a] = (a < active) ? xq[(q0 + a) * d + c] : (T)0;       \
+            for (int a = 0; a < ORC_QB; a++)                                               \
+                qblk[a] = (qn && a < active) ? qn[q0 + a] : (T)0;                          \
+            for (int64_t j = 0; j < k * ORC_QB; j++) {                                     \
+                lval[j] = (T)INFINITY;                                                     \
+                lidx[j] = UINT32_MAX;                                                      \
+            }                                                                              \
+            scan_block_##S(xt, active, xtrain, nt, d, k, metric, arm, qblk, yn, lval,      \
+                           lidx);                                                          \
+            for (int64_t a = 0; a < active; a++)                                           \
+                for (int64_t j = 0; j < k; j++) {                                          \
+                    T v = lval[a * k + j];                                                 \
+                    uint32_t ix = lidx[a * k + j];                                         \
+                    out_val[(q0 + a) * k + j] =                                            \
+                        (metric == ORC_METRIC_EUCLIDEAN) ? SQRT(v) : v;                    \
+                    out_idx[(q0 + a) * k + j] = (ix == UINT32_MAX) ? 0u : ix;              \
+                }                                                                          \
+        }                                                                                  \
+        free(xt);                                                                          \
+        free(lval);                                                                        \
+        free(lidx);                                                                        \
+    }                                                                                      \
+    free(qn);                                                                              \
+    free(yn);                                                                              \
+    return 0;                                                                              \
+}                                                                                          \
+                                                                                           \
+/* k-means assignment (prims/kmeans.rs:635-750): dist_direct_2d_c4                        \
+ * (kernels/kmeans.rs:206-274, a += d*d) then argmin_dist_rows (:284-310): best           \
+ * seeded from centre 0, strict `<` afterwards. Writes squared distances. */               \
+int orc_kmeans_assign_##S(const T *x, int64_t n, const T *centers, int64_t kc, int64_t d,  \
+                          uint32_t *labels, T *dist, int nthreads)                         \
+{                                                                                          \
+    if (kc < 1 || kc > n || d < 1)                                                         \
+        return -1;                                                                         \
+    set_threads(nthreads);                                                                 \
+    _Pragma("omp parallel for schedule(static)")                                           \
+    for (int64_t i = 0; i < n; i++) {                                                      \
+        const T *xr = x + i * d;                                                           \
+        T best = (T)0;                                                                     \
+        uint32_t best_c = 0;                                                               \
+        for (int64_t c = 0; c < kc; c++) {                                                 \
+            const T *cr = centers + c * d;                                                 \
+            T acc = (T)0;                                                                  \
+            for (int64_t j = 0; j < d; j++) {                                              \
+                T diff = xr[j] - cr[j];                                                    \
+                acc = acc + diff * diff;                                                   \
+            }                                                                              \
+            if (c == 0) {                                                                  \
+                best = acc;                                                                \
+            } else if (acc < best) {                                                       \
+                best = acc;                                                                \
+                best_c = (uint32_t)c;                                                      \
+            }                                                                              \
+        }                                                                                  \
+        labels[i] = best_c;                                                                \
+        dist[i] = best;                                                                    \
+    }                                                                                      \
+    return 0;                                                                              \
+}                                                                                          \
+                                                                                           \
+/* Pairwise distance matrix.  Euclidean = distance_direct / euclidean_sq_dist             \
+ * (prims/distance.rs:428-551, kernels/distance.rs:411-440: acc += diff*diff),            \
+ * optional boundary sqrt (sqrt_elem, kernels/elementwise.rs:131-136).                    \
+ * Cosine = metric_distance / cosine_dist (kernels/distance.rs:257-310):                  \
+ * dot += x*y, denom = sqrt(xn*yn) over row_sumsq norms, sim = dot/denom when             \
+ * denom > 0 else 0, then the [0, 2] clamp. */                                             \
+int orc_pairwise_##S(const T *x, int64_t nx, const T *y, int64_t ny, int64_t d,            \
+                     int metric, int do_sqrt, T *out, int nthreads)                        \
+{                                                                                          \
+    if (d < 1)                                                                             \
+        return -1;                                                                         \
+    T *xn = NULL, *yn = NULL;                                                              \
+    if (metric == ORC_METRIC_COSINE) {                                                     \
+        xn = (T *)malloc(sizeof(T) * (size_t)(nx > 0 ? nx : 1));                           \
+        yn = (T *)malloc(sizeof(T) * (size_t)(ny > 0 ? ny : 1));                           \
+        orc_row_sqnorms_##S(x, nx, d, xn);                                                 \
+        orc_row_sqnorms_##S(y, ny, d, yn);                                                 \
+    }                                                                                      \
+    set_threads(nthreads);                                                                 \
+    _Pragma("omp parallel for schedule(static)")                                           \
+    for (int64_t i = 0; i < nx; i++) {                                                     \
+        const T *xr = x + i * d;                                                           \
+        for (int64_t j = 0; j < ny; j++) {                                                 \
+            const T *yr = y + j * d;                                                       \
+            T acc = (T)0;                                                                  \
+            if (metric == ORC_METRIC_EUCLIDEAN) {                                          \
+                for (int64_t c = 0; c < d; c++) {                                          \
+                    T diff = xr[c] - yr[c];                                                \
+                    acc = acc + diff * diff;                                               \
+                }                                                                          \
+                out[i * ny + j] = do_sqrt ? SQRT(acc) : acc;                               \
+            } else {                                                                       \
+                for (int64_t c = 0; c < d; c++)                                            \
+                    acc = acc + xr[c] * yr[c];                                             \
+                T denom = SQRT(xn[i] * yn[j]);                                             \
+                T sim = (T)0;                                                              \
+                if (denom > (T)0)                                                          \
+                    sim = acc / denom;                                                     \
+                T dv = (T)1 - sim;                                                         \
+                if (dv < (T)0)                                                             \
+                    dv = (T)0;                                                             \
+                if (dv > (T)2)                                                             \
+                    dv = (T)2;                                                             \
+                out[i * ny + j] = dv;                                                      \
+            }                                                                              \
+        }                                                                                  \
+    }                                                                                      \
+    free(xn);                                                                              \
+    free(yn);                                                                              \
+    return 0;                                                                              \
+}
+
+ORC_DEFINE(float, f32, fmaf, sqrtf)
+ORC_DEFINE(double, f64, fma, sqrt)

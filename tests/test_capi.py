@@ -1,0 +1,139 @@
+"""The C-ABI library loads, exports every declared symbol, and rejects bad
+geometry before touching the GPU -- CPU only (no compute calls)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from mlrs_amd import _lib
+
+HEADER = os.path.join(ROOT, "include", "mlrs_hip_knn.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|const char \*)\s*\*?\s*(mlrs_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    syms = declared_symbols()
+    for s in ("mlrs_knn_topk_f32", "mlrs_knn_topk_f64", "mlrs_kmeans_assign_f32", "mlrs_kmeans_assign_f64",
+              "mlrs_pairwise_distance_f32", "mlrs_pairwise_distance_f64", "mlrs_row_sqnorms_f32",
+              "mlrs_row_sqnorms_f64", "mlrs_last_error", "mlrs_status_string"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+        assert s in _lib.SIGNATURES, "binding missing for " + s
+
+
+def test_abi_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.mlrs_abi_version() == 1
+    assert lib.mlrs_status_string(0) == b"ok"
+    assert lib.mlrs_status_string(-1) == b"shape mismatch"
+    assert lib.mlrs_status_string(-2) == b"dimension mismatch"
+
+
+# Dummy non-null "device" pointers: validation fails before any dereference or launch.
+P = ctypes.c_void_p(0x1000)
+
+
+def _knn32(xq_len, nq, d, xt_len, nt, k, metric=0, out_len=None):
+    lib = _lib.load()
+    out_len = nq * k if out_len is None else out_len
+    return lib.mlrs_knn_topk_f32(P, xq_len, nq, d, P, xt_len, nt, k, metric, 2.0, P, P, out_len, None)
+
+
+def _info():
+    e = _lib.ErrorInfo()
+    _lib.load().mlrs_last_error(ctypes.byref(e))
+    return e
+
+
+@pytest.mark.parametrize("args,operand,fields", [
+    ((10 * 4 - 1, 10, 4, 20 * 4, 20, 3), "x", (10, 4, 39)),
+    ((10 * 4, 10, 4, 20 * 4 + 1, 20, 3), "y", (20, 4, 81)),
+    ((10 * 4, 10, 4, 20 * 4, 20, 0), "k", (1, 0, 20)),
+    ((10 * 4, 10, 4, 20 * 4, 20, 21), "k", (1, 21, 20)),
+    ((0, 10, 0, 0, 20, 3), "features", (0, 0, 0)),
+])
+def test_knn_validation_is_prim_error(args, operand, fields):
+    rc = _knn32(*args)
+    assert rc == _lib.MLRS_ERR_SHAPE_MISMATCH
+    e = _info()
+    assert e.operand.decode() == operand
+    assert (e.rows, e.cols, e.len) == fields
+    assert b"shape mismatch" in e.message
+
+
+def test_knn_out_and_metric_validation():
+    assert _knn32(40, 10, 4, 80, 20, 3, out_len=29) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"out"
+    assert _knn32(40, 10, 4, 80, 20, 3, metric=7) == _lib.MLRS_ERR_UNSUPPORTED
+
+
+def test_kmeans_validation():
+    lib = _lib.load()
+    f = lib.mlrs_kmeans_assign_f32
+    assert f(P, 99, 10, 10, P, 30, 3, P, 10, P, 10, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"x"
+    assert f(P, 100, 10, 10, P, 110, 11, P, 10, P, 10, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"k"
+    assert f(P, 100, 10, 10, P, 29, 3, P, 10, P, 10, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"centers"
+    assert f(P, 100, 10, 10, P, 30, 3, P, 9, P, 10, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"labels"
+
+
+def test_pairwise_validation():
+    lib = _lib.load()
+    f = lib.mlrs_pairwise_distance_f64
+    assert f(P, 14, 5, 3, P, 12, 4, 3, 0, 0, P, 20, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert (_info().operand, _info().len) == (b"x", 14)
+    assert f(P, 15, 5, 3, P, 13, 4, 3, 0, 0, P, 20, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"y"
+
+
+def test_pairwise_dim_mismatch_and_out():
+    lib = _lib.load()
+    f = lib.mlrs_pairwise_distance_f32
+    assert f(P, 15, 5, 3, P, 16, 4, 4, 0, 0, P, 20, None) == _lib.MLRS_ERR_DIM_MISMATCH
+    e = _info()
+    assert (e.operand, e.rows, e.cols) == (b"cols", 3, 4)
+    assert f(P, 15, 5, 3, P, 12, 4, 3, 0, 0, P, 19, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"out"
+
+
+def test_python_error_mapping():
+    with pytest.raises(_lib.ShapeMismatch) as ei:
+        _lib.check(_knn32(39, 10, 4, 80, 20, 3))
+    assert ei.value.operand == "x" and ei.value.len == 39
+
+
+def test_estimator_parameter_validation_needs_no_gpu():
+    from mlrs_amd.neighbors import NearestNeighbors, _resolve_metric
+    with pytest.raises(ValueError, match="Algorithm is not supported"):
+        NearestNeighbors(algorithm="lsh").fit(np.zeros((3, 2)))
+    with pytest.raises(ValueError, match="Metric 'cosine' not valid"):
+        NearestNeighbors(algorithm="kd_tree", metric="cosine").fit(np.zeros((3, 2)))
+    with pytest.raises(ValueError, match="p must be greater or equal to one"):
+        NearestNeighbors(p=0.5).fit(np.zeros((3, 2)))
+    assert _resolve_metric("minkowski", 2, None)[0] == "euclidean"
+    assert _resolve_metric("minkowski", 1, None)[0] == "manhattan"
+    assert _resolve_metric("minkowski", float("inf"), None)[0] == "chebyshev"
+
+
+def test_self_drop_by_index_identity():
+    from mlrs_amd.neighbors import _drop_self_column
+    dist = np.array([[0.0, 0.0, 1.0], [0.0, 0.0, 2.0], [0.5, 0.7, 0.9]])
+    idx = np.array([[1, 0, 2], [0, 1, 2], [0, 1, 3]])
+    d, i = _drop_self_column(dist, idx, 2)
+    assert i.tolist() == [[1, 2], [0, 2], [0, 1]]
+    assert d.tolist() == [[0.0, 1.0], [0.0, 2.0], [0.5, 0.7]]

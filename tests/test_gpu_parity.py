@@ -1,0 +1,284 @@
+"""GPU parity: the HIP engine against the CPU oracle, bit for bit.
+
+Every case compares the C-ABI results (through mlrs_amd.prims) with
+oracle/ (the restatement of the mlrs cpu-backend arithmetic) on the same
+seeded inputs.  The bar is exact equality of distances and indices: the engine
+evaluates every kept pair in the reference arm's own operation order, so no
+tolerance is needed.  Shapes are chosen to reach every dispatch path: the
+low-d ALU kernel, the f32 Gram-MFMA kernel (single- and multi-strip), and the
+generic exact path (large k, large d, f64).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_topk_matches, load_golden
+from mlrs_amd import prims
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def gpu_knn(xq, xt, k, metric="euclidean"):
+    d, i = prims.knn_topk(_t(xq), _t(xt), k, metric)
+    torch.cuda.synchronize()
+    return d.cpu().numpy(), i.cpu().numpy()
+
+
+def assert_same(got_d, got_i, want_d, want_i, label=""):
+    bad = np.argwhere(got_i != want_i.astype(np.int64))
+    assert bad.size == 0, "%s: %d index mismatches, first %s got %s want %s" % (
+        label, len(bad), bad[:3].tolist(), got_i[tuple(bad[0])], want_i[tuple(bad[0])])
+    same = (got_d == want_d) | (np.isnan(got_d) & np.isnan(want_d))
+    assert same.all(), "%s: distance bits differ at %s" % (label, np.argwhere(~same)[:3].tolist())
+
+
+def check_knn(xq, xt, k, metric="euclidean", label=""):
+    gd, gi = gpu_knn(xq, xt, k, metric)
+    wd, wi = oracle.knn_topk(xq, xt, k, metric)
+    assert_same(gd, gi, wd, wi, label)
+    return gd, gi
+
+
+def _data(seed, nq, nt, d, dtype=np.float32, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return ((rng.standard_normal((nq, d)) * scale).astype(dtype),
+            (rng.standard_normal((nt, d)) * scale).astype(dtype))
+
+
+# (nq, nt, d, k): low-d ALU path (d <= 16, k <= 32)
+LOWD = [(300, 2000, 3, 8), (257, 1000, 1, 1), (100, 3000, 16, 32), (1000, 5000, 7, 16), (64, 20, 2, 20)]
+# Gram-MFMA path (f32, 16 < d <= 128, k <= 64)
+GRAM = [(300, 3000, 64, 10), (129, 1000, 17, 5), (500, 4000, 128, 32), (77, 600, 100, 64),
+        (1000, 70000, 128, 32), (5, 100, 33, 1), (200, 2048, 24, 20), (1, 31, 40, 31), (130, 5000, 96, 7)]
+# generic exact path (k > 64, d > 128)
+GENERIC = [(50, 500, 64, 100), (20, 300, 64, 200), (30, 400, 200, 10)]
+
+
+@pytest.mark.parametrize("case", LOWD + GRAM + GENERIC)
+def test_f32_euclidean_bitwise(case):
+    nq, nt, d, k = case
+    xq, xt = _data(100 + d, nq, nt, d)
+    check_knn(xq, xt, k, "euclidean", str(case))
+
+
+@pytest.mark.parametrize("case", [(300, 3000, 64, 10), (100, 2000, 5, 7), (50, 500, 130, 8), (40, 400, 64, 80),
+                                  (600, 20000, 128, 32)])
+def test_f32_cosine_bitwise(case):
+    nq, nt, d, k = case
+    xq, xt = _data(200 + d, nq, nt, d)
+    xq += 0.3  # keep similarities away from the all-zero-mean regime
+    check_knn(xq, xt, k, "cosine", str(case))
+
+
+@pytest.mark.parametrize("case,metric", [((100, 2000, 64, 10), "euclidean"), ((50, 1000, 3, 8), "euclidean"),
+                                         ((64, 2000, 256, 16), "cosine"), ((40, 700, 20, 5), "cosine")])
+def test_f64_bitwise(case, metric):
+    nq, nt, d, k = case
+    rng = np.random.default_rng(300 + d)
+    xq = rng.random((nq, d))
+    xt = rng.random((nt, d))
+    check_knn(xq, xt, k, metric, str(case))
+
+
+@pytest.mark.parametrize("d", [3, 64])
+def test_duplicates_and_boundary_ties(d):
+    """100 identical rows around the k-th slot: membership and order are
+    decided by index alone (knn_metric_kernel_test.rs:269-289)."""
+    rng = np.random.default_rng(5)
+    xt = rng.standard_normal((3000, d)).astype(np.float32)
+    xt[500:600] = xt[7]            # 101 copies of row 7
+    xq = np.concatenate([xt[7:8], xt[:50], rng.standard_normal((20, d)).astype(np.float32)])
+    gd, gi = check_knn(xq, xt, 32, "euclidean", "dups d=%d" % d)
+    assert gi[0].tolist() == [7] + list(range(500, 531))
+    assert np.all(gd[0] == 0)
+
+
+@pytest.mark.parametrize("d,k", [(3, 8), (48, 24)])
+def test_quantized_data_many_ties(d, k):
+    rng = np.random.default_rng(6)
+    xt = rng.integers(-3, 4, size=(4000, d)).astype(np.float32)
+    xq = rng.integers(-3, 4, size=(300, d)).astype(np.float32)
+    check_knn(xq, xt, k, "euclidean", "quantized")
+    check_knn(xq, xt, k, "cosine", "quantized cosine")
+
+
+@pytest.mark.parametrize("d", [4, 64])
+def test_nan_rows(d):
+    xq, xt = _data(8, 200, 1500, d)
+    xt[[3, 700, 1499]] = np.nan
+    xt[10, 1] = np.nan
+    xq[[0, 57]] = np.nan
+    check_knn(xq, xt, 12, "euclidean", "nan")
+    # fewer admissible rows than k -> sentinel (+inf, 0) slots
+    small = xt[:8].copy()
+    small[2] = np.nan
+    check_knn(xq[:20], small, 8, "euclidean", "nan sentinel")
+
+
+def test_cosine_zero_rows():
+    xq, xt = _data(9, 100, 1000, 40)
+    xt[[0, 5, 999]] = 0.0
+    xq[3] = 0.0
+    check_knn(xq, xt, 10, "cosine", "zero rows")
+
+
+def test_huge_values_overflow_norms():
+    """Squared norms overflow f32: the screen bound becomes infinite and every
+    row is evaluated exactly; results still match the reference arithmetic."""
+    xq, xt = _data(10, 40, 500, 64, scale=1e18)
+    xt[:5] *= 1e2
+    check_knn(xq, xt, 6, "euclidean", "huge")
+
+
+def test_k_equals_n_train_and_tiny_index():
+    xq, xt = _data(11, 33, 40, 50)
+    check_knn(xq, xt, 40, "euclidean", "k=n")
+    check_knn(xq, xt[:1], 1, "euclidean", "n_train=1")
+
+
+def test_nonaligned_pointer_and_odd_d():
+    xq, xt = _data(12, 70, 900, 37)
+    tq = _t(np.concatenate([np.zeros((1, 37), np.float32), xq]))[1:]  # 148-byte offset -> not 16-aligned
+    tq = tq.contiguous()
+    d_, i_ = prims.knn_topk(tq, _t(xt), 9)
+    torch.cuda.synchronize()
+    wd, wi = oracle.knn_topk(xq, xt, 9)
+    assert_same(d_.cpu().numpy(), i_.cpu().numpy(), wd, wi, "offset")
+
+
+def test_side_stream():
+    xq, xt = _data(13, 256, 4096, 64)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        tq, tt = _t(xq), _t(xt)
+        d_, i_ = prims.knn_topk(tq, tt, 16)
+    s.synchronize()
+    wd, wi = oracle.knn_topk(xq, xt, 16)
+    assert_same(d_.cpu().numpy(), i_.cpu().numpy(), wd, wi, "side stream")
+
+
+# ---------------------------------------------------------------------------
+# k-means assignment, pairwise distance, row norms
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,kc,d,dtype", [(5000, 100, 64, np.float32), (3000, 7, 3, np.float32),
+                                         (2000, 50, 200, np.float32), (1500, 40, 32, np.float64),
+                                         (20000, 1024, 64, np.float32)])
+def test_kmeans_assign_bitwise(n, kc, d, dtype):
+    rng = np.random.default_rng(kc + d)
+    c = rng.standard_normal((kc, d)).astype(dtype) * 3
+    x = (c[rng.integers(0, kc, n)] + rng.standard_normal((n, d))).astype(dtype)
+    lab, sq = prims.kmeans_assign(_t(x), _t(c))
+    torch.cuda.synchronize()
+    wl, ws = oracle.kmeans_assign(x, c)
+    assert np.array_equal(lab.cpu().numpy(), wl.astype(np.int64))
+    assert np.array_equal(sq.cpu().numpy(), ws)
+
+
+@pytest.mark.parametrize("d", [4, 64])
+def test_kmeans_ties_and_nan(d):
+    rng = np.random.default_rng(14)
+    c = rng.standard_normal((10, d)).astype(np.float32)
+    c[6] = c[2]                       # exact duplicate centre: ties go to 2
+    x = rng.standard_normal((500, d)).astype(np.float32)
+    x[:20] = c[2]
+    x[30] = np.nan                    # NaN distance to centre 0 wins with label 0
+    lab, sq = prims.kmeans_assign(_t(x), _t(c))
+    torch.cuda.synchronize()
+    wl, ws = oracle.kmeans_assign(x, c)
+    assert np.array_equal(lab.cpu().numpy(), wl.astype(np.int64))
+    assert np.array_equal(sq.cpu().numpy(), ws, equal_nan=True)
+    assert lab[30].item() == 0 and np.isnan(sq[30].item())
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("metric,sqrt", [("euclidean", False), ("euclidean", True), ("cosine", False)])
+def test_pairwise_bitwise(dtype, metric, sqrt):
+    x, y = _data(15, 65, 130, 7, dtype)
+    got = prims.pairwise_distance(_t(x), _t(y), metric, sqrt)
+    torch.cuda.synchronize()
+    want = oracle.pairwise(x, y, metric, sqrt)
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_row_sqnorms_bitwise(dtype):
+    x, _ = _data(16, 1000, 1, 77, dtype)
+    got = prims.row_sqnorms(_t(x))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.row_sqnorms(x))
+
+
+def test_prim_error_on_device():
+    with pytest.raises(Exception) as ei:
+        prims.knn_topk(_t(np.zeros((4, 3), np.float32)), _t(np.zeros((5, 3), np.float32)), 6)
+    assert getattr(ei.value, "operand", None) == "k"
+
+
+# ---------------------------------------------------------------------------
+# estimator replays of the reference fixtures
+# ---------------------------------------------------------------------------
+def _brute(xq, xt, metric):
+    q, t = xq.astype(np.float64), xt.astype(np.float64)
+    if metric == "euclidean":
+        return lambda r, j: float(np.sqrt(np.sum((q[r] - t[j]) ** 2)))
+    return lambda r, j: float(1.0 - np.dot(q[r], t[j]) / (np.linalg.norm(q[r]) * np.linalg.norm(t[j])))
+
+
+@pytest.mark.parametrize("s", ["f32", "f64"])
+def test_estimator_knn_fixture(s):
+    from mlrs_amd.neighbors import NearestNeighbors
+    z = load_golden("knn_%s_seed42" % s)
+    k = int(z["k"][0])
+    nn = NearestNeighbors(n_neighbors=k).fit(z["X"])
+    d, i = nn.kneighbors(z["Xq"])
+    assert i.dtype == np.int32
+    assert np.all(np.abs(d - z["distances"]) <= 1e-5 * np.maximum(np.abs(z["distances"]), 1.0))
+    assert np.array_equal(i, z["indices"].astype(np.int32))
+
+
+@pytest.mark.parametrize("s", ["f32", "f64"])
+@pytest.mark.parametrize("metric", ["euclidean", "l2", "minkowski", "cosine"])
+def test_estimator_nn_params_fixture(s, metric):
+    from mlrs_amd.neighbors import NearestNeighbors
+    z = load_golden("nn_params_%s_seed42" % s)
+    k = int(z["k"][0])
+    nn = NearestNeighbors(n_neighbors=k, metric=metric, p=2).fit(z["X"])
+    d, i = nn.kneighbors(z["Xq"])
+    base = "cosine" if metric == "cosine" else "euclidean"
+    assert_topk_matches(d, i, z["distances_" + base], z["indices_" + base].astype(np.int64),
+                        _brute(z["Xq"], z["X"], base))
+
+
+@pytest.mark.parametrize("s", ["f32", "f64"])
+@pytest.mark.parametrize("metric", ["euclidean", "cosine"])
+def test_estimator_self_query_drops_self_by_identity(s, metric):
+    from mlrs_amd.neighbors import NearestNeighbors
+    z = load_golden("knn_%s_%s_seed42" % (metric, s))
+    k = int(z["k"][0])
+    nn = NearestNeighbors(n_neighbors=k, metric=metric).fit(z["X"])
+    d, i = nn.kneighbors()                    # X=None: k+1 search, self dropped
+    want_d, want_i = z["distances"], z["indices"].astype(np.int64)
+    rows = np.arange(len(want_i))
+    keep = want_i != rows[:, None]
+    # reference self-drop of the sklearn k+1 result
+    wd = np.stack([want_d[r][keep[r]][:k] for r in rows])
+    wi = np.stack([want_i[r][keep[r]][:k] for r in rows])
+    assert_topk_matches(d, i, wd, wi, _brute(z["X"], z["X"], metric))
+    a, b = int(z["dup_row_a"][0]), int(z["dup_row_b"][0])
+    assert i[a, 0] == b and i[b, 0] == a and d[a, 0] == 0 and d[b, 0] == 0
+
+
+def test_kmeans_estimator_fixture():
+    from mlrs_amd.cluster import KMeans
+    for s in ("f32", "f64"):
+        z = load_golden("kmeans_%s_seed42" % s)
+        km = KMeans(cluster_centers=z["centers"])
+        assert np.array_equal(km.predict(z["X"]), z["labels"].astype(np.int32))
+        inertia = float(np.sum(km.transform_min_sqdist(z["X"]).astype(np.float64)))
+        assert abs(inertia - float(z["inertia"][0])) <= 1e-5 * max(1.0, abs(float(z["inertia"][0])))
