@@ -299,7 +299,8 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     rps = (rps + tile - 1) / tile * tile;
     nstrips = (int)((nt + rps - 1) / rps);
     size_t parts = nstrips > 1 ? (size_t)nstrips * nq * k : 0;
-    size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t));
+    size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
+                   aligned_bytes(sizeof(unsigned int) * nq);
     rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
@@ -342,6 +343,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     if (nstrips > 1) {
         a.part_val = cv.take<float>(parts);
         a.part_idx = cv.take<uint32_t>(parts);
+        a.shared_r = cv.take<unsigned int>(nq);
     }
     a.out_val = out_v;
     a.out_idx = out_i;

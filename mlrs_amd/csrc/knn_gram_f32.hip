@@ -11,18 +11,21 @@
 //    v_mfma_f32_32x32x2f32 (pre-scaled by -2 for Euclidean), loaded once.
 //  * The 32-row index tile is staged in LDS (row stride d_pad+4 floats: rows
 //    land 4 banks apart, so the ds_read_b128 A-operand reads do not conflict),
-//    prefetched into registers one tile ahead.
+//    double-buffered and prefetched into registers one tile ahead.
 //  * Euclidean: the accumulator starts at ||x_t||^2, so after the contraction
 //    acc = ||x_t||^2 - 2 x_t.q_j, the expansion minus the per-query constant.
 //    Cosine: tile rows are pre-scaled by -1/||x_t||, acc = -x_t.q_j/||x_t||.
 //  * Screen: acc is compared against a per-query threshold derived from the
-//    CURRENT exact k-th value plus a rigorous bound on the expansion's rounding
-//    error (plus the reference's own).  A pair that can still enter the exact
-//    top-k always passes; the comparison is !(acc > thr) so NaN passes too.
+//    best exact k-th value known for the query (its own list, or any strip's,
+//    shared through a per-query word in global memory) plus a rigorous bound
+//    on the expansion's rounding error and the reference's own.  A pair that
+//    can still enter the exact top-k always passes; the comparison is
+//    !(acc > thr), so NaN passes too.  For k = 1 the bound is tightened every
+//    tile with the tile's smallest expansion value.
 //  * Passing (query, row) pairs are queued in LDS.  When a query's queue is
 //    half full the wave evaluates the queued pairs EXACTLY, in the reference
-//    arm's operation order (knn_common.hpp exact_pair), sorts them and merges
-//    them into the query's exact top-k list with the (value, index) order.
+//    arm's operation order, sorts them and merges them into the query's exact
+//    top-k list with the (value, index) order.
 // The kept lists are therefore the reference's own top-k: the full distance
 // matrix never reaches HBM and no tolerance is involved.
 #include "knn_common.hpp"
@@ -39,6 +42,7 @@ constexpr int kBn = 32;                  // index rows per tile (MFMA M dimensio
 constexpr int kKcap = 64;                // largest k this kernel keeps
 constexpr int kQcap = 64;                // queued candidates per query
 constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
+constexpr int kShareEvery = 32;          // tiles between reads of the shared thresholds
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -69,7 +73,7 @@ __device__ __forceinline__ float round_up_f(double t) {
 template <bool COS>
 __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) {
     const float inf = __builtin_huge_valf();
-    if (!(R < inf)) return inf;  // list not yet full of finite values
+    if (!(R < inf)) return inf;  // no finite k-th value known yet
     if (!COS) {
         // exact <= R  =>  ||x||^2 - 2 x.q <= R - ||q||^2 + eps
         return round_up_f((double)R - (double)qs + (double)eps);
@@ -80,79 +84,100 @@ __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) 
     }
 }
 
+// Exact value of one (query, row) pair in the arm's operation order, loads
+// issued eight 16-byte chunks at a time.
 template <int ARM, bool VEC4>
 __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const float* __restrict__ y,
                                            int64_t d, float qa, float ya) {
     if (!VEC4) return exact_pair<float, ARM>(q, y, d, qa, ya);
-    // Same ascending-column operation order, 16-byte loads.
     const float4* q4 = reinterpret_cast<const float4*>(q);
     const float4* y4 = reinterpret_cast<const float4*>(y);
-    const int64_t n4 = d >> 2;
-    if (ARM == ARM_EUCLID_FMA || ARM == ARM_EUCLID_MULADD) {
-        float acc = 0.0f;
-        for (int64_t c = 0; c < n4; ++c) {
-            float4 a = q4[c], b = y4[c];
-            float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+    const int n4 = (int)(d >> 2);
+    float acc = 0.0f;
+    int c = 0;
+    for (; c + 8 <= n4; c += 8) {
+        float4 a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a[u] = q4[c + u];
+            b[u] = y4[c + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
             if (ARM == ARM_EUCLID_FMA) {
+                float d0 = a[u].x - b[u].x, d1 = a[u].y - b[u].y, d2 = a[u].z - b[u].z, d3 = a[u].w - b[u].w;
                 acc = __builtin_fmaf(d0, d0, acc);
                 acc = __builtin_fmaf(d1, d1, acc);
                 acc = __builtin_fmaf(d2, d2, acc);
                 acc = __builtin_fmaf(d3, d3, acc);
-            } else {
+            } else if (ARM == ARM_EUCLID_MULADD) {
+                float d0 = a[u].x - b[u].x, d1 = a[u].y - b[u].y, d2 = a[u].z - b[u].z, d3 = a[u].w - b[u].w;
                 acc = acc + d0 * d0;
                 acc = acc + d1 * d1;
                 acc = acc + d2 * d2;
                 acc = acc + d3 * d3;
+            } else {  // ARM_COS_FOLD: fma dot
+                acc = __builtin_fmaf(a[u].x, b[u].x, acc);
+                acc = __builtin_fmaf(a[u].y, b[u].y, acc);
+                acc = __builtin_fmaf(a[u].z, b[u].z, acc);
+                acc = __builtin_fmaf(a[u].w, b[u].w, acc);
             }
         }
-        return acc;
-    } else {  // ARM_COS_FOLD
-        float dot = 0.0f;
-        for (int64_t c = 0; c < n4; ++c) {
-            float4 a = q4[c], b = y4[c];
-            dot = __builtin_fmaf(a.x, b.x, dot);
-            dot = __builtin_fmaf(a.y, b.y, dot);
-            dot = __builtin_fmaf(a.z, b.z, dot);
-            dot = __builtin_fmaf(a.w, b.w, dot);
+    }
+    for (; c < n4; ++c) {
+        float4 a = q4[c], b = y4[c];
+        if (ARM == ARM_EUCLID_FMA) {
+            float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+            acc = __builtin_fmaf(d0, d0, acc);
+            acc = __builtin_fmaf(d1, d1, acc);
+            acc = __builtin_fmaf(d2, d2, acc);
+            acc = __builtin_fmaf(d3, d3, acc);
+        } else if (ARM == ARM_EUCLID_MULADD) {
+            float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+            acc = acc + d0 * d0;
+            acc = acc + d1 * d1;
+            acc = acc + d2 * d2;
+            acc = acc + d3 * d3;
+        } else {
+            acc = __builtin_fmaf(a.x, b.x, acc);
+            acc = __builtin_fmaf(a.y, b.y, acc);
+            acc = __builtin_fmaf(a.z, b.z, acc);
+            acc = __builtin_fmaf(a.w, b.w, acc);
         }
+    }
+    if (ARM == ARM_COS_FOLD) {
         float denom = __builtin_sqrtf(qa * ya);
-        float sim = (denom > 0.0f) ? dot / denom : 0.0f;
+        float sim = (denom > 0.0f) ? acc / denom : 0.0f;
         return clamp02<float>(1.0f - sim);
     }
+    return acc;
 }
 
-// Evaluate query j's queued rows exactly and merge them into its list.
-template <int ARM, bool COS, bool VEC4>
-__device__ __noinline__ void flush_query(WaveLds& L, int j, int lane, const GramArgs32& a,
-                                         int64_t qglob) {
-    const float inf = __builtin_huge_valf();
-    const uint32_t n = L.cnt[j];
-    const float* qp = a.q + qglob * a.d;
-    float e = inf;
-    uint32_t t = kSentinelIdx;
-    if ((uint32_t)lane < n) {
-        t = L.qidx[j][lane];
-        float ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f;
-        e = exact_f32<ARM, VEC4>(qp, a.x + (int64_t)t * a.d, a.d, L.qa[j], ya);
-        if (e != e) {  // NaN is never admitted
-            e = inf;
-            t = kSentinelIdx;
+// Output transform: the boundary root of prims/knn.rs:877-883 (Euclidean),
+// identity (cosine), or the k-means (label, squared distance) pair with
+// argmin_dist_rows' centre-0 seeding (crates/mlrs-kernels/src/kmeans.rs:284-310).
+__device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q, const float* __restrict__ X,
+                                          const float* __restrict__ qsq, const float* __restrict__ xsq, int64_t d,
+                                          int k, int64_t qg, int slot, float v, uint32_t ix,
+                                          float* __restrict__ out_val, uint32_t* __restrict__ out_idx) {
+    const int64_t o = qg * k + slot;
+    if (mode == EMIT_KMEANS) {
+        // argmin_dist_rows seeds `best` from centre 0 unconditionally, so a NaN
+        // distance to centre 0 wins with label 0.  That distance can only be
+        // NaN when a norm is non-finite; check those rows exactly.
+        const float inf = __builtin_huge_valf();
+        if (!(qsq[qg] < inf) || !(xsq[0] < inf)) {
+            float e0 = exact_pair<float, ARM_EUCLID_MULADD>(Q + qg * d, X, d, 0.0f, 0.0f);
+            if (e0 != e0) {
+                v = e0;
+                ix = 0;
+            }
         }
+        out_val[o] = v;
+    } else {
+        out_val[o] = (mode == EMIT_SQRT) ? __builtin_sqrtf(v) : v;
     }
-    wave_sort64<float>(e, t, lane);
-    const int k = a.k;
-    float lv = (lane < k) ? L.lval[j][lane] : inf;
-    uint32_t li = (lane < k) ? L.lidx[j][lane] : kSentinelIdx;
-    wave_merge64<float>(lv, li, e, t, lane);
-    if (lane < k) {
-        L.lval[j][lane] = lv;
-        L.lidx[j][lane] = li;
-    }
-    float R = shfl_f(lv, k - 1);
-    if (lane == 0) {
-        L.cnt[j] = 0;
-        L.thr[j] = screen_threshold<COS>(R, L.qs[j], L.eps[j]);
-    }
+    out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
 }
 
 template <int NG, int ARM, bool COS, bool VEC4>
@@ -166,6 +191,16 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
     __shared__ __attribute__((aligned(16))) float tnorm[2][kBn];
     __shared__ WaveLds wl[kWaves];
 
+    // Kernel arguments as locals: they stay in SGPRs.
+    const float* __restrict__ Q = a.q;
+    const float* __restrict__ X = a.x;
+    const float* __restrict__ QSQ = a.qsq;
+    const float* __restrict__ XSQ = a.xsq;
+    const float* __restrict__ XSCALE = a.xscale;
+    unsigned int* __restrict__ SHARED_R = a.shared_r;
+    const int64_t nq = a.nq, nt = a.nt, d = a.d;
+    const int k = a.k;
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -176,15 +211,14 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
 
     const int64_t qwave = (int64_t)blockIdx.x * kQpb + w * kQpw;  // first query of this wave
     const int64_t qmine = qwave + jl;
-    const bool qvalid = qmine < a.nq;
+    const bool qvalid = qmine < nq;
     const int64_t t_begin = (int64_t)blockIdx.y * a.rows_per_strip;
     int64_t t_end = t_begin + a.rows_per_strip;
-    if (t_end > a.nt) t_end = a.nt;
-    const int64_t d = a.d;
+    if (t_end > nt) t_end = nt;
 
     // ---- per-query constants, lists, queues ----
     if (lane < kQpw) {
-        float qsq = qvalid ? a.qsq[qmine] : 0.0f;
+        float qsq = qvalid ? QSQ[qmine] : 0.0f;
         L.cnt[lane] = 0;
         L.thr[lane] = qvalid ? inf : -inf;
         if (!COS) {
@@ -206,7 +240,7 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
     float4 qreg[NG];
     {
         const float scale = COS ? 1.0f : -2.0f;
-        const float* qp = a.q + qmine * d;
+        const float* qp = Q + qmine * d;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             float v[4];
@@ -219,63 +253,102 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         }
     }
 
-    // ---- tile prefetch into registers ----
+    // ---- tile prefetch into registers (rows past the strip: zeros, norm +inf) ----
     float4 pf[PF];
     float pfn = 0.0f;
-    auto prefetch = [&](int64_t t0) {
+#define MLRS_PREFETCH(T0)                                                                    \
+    do {                                                                                     \
+        const int64_t t0_ = (T0);                                                            \
+        _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
+            const int f = tid + 256 * p;                                                     \
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);                                      \
+            if (f < TILE_F4) {                                                               \
+                const int r = f / (DP / 4);                                                  \
+                const int c4 = f % (DP / 4);                                                 \
+                const int64_t t = t0_ + r;                                                   \
+                if (t < t_end) {                                                             \
+                    const float* src = X + t * d + 4 * c4;                                   \
+                    if (VEC4) {                                                              \
+                        if (4 * c4 < d) v = *reinterpret_cast<const float4*>(src);           \
+                    } else {                                                                 \
+                        float e4[4];                                                         \
+                        _Pragma("unroll") for (int e = 0; e < 4; ++e) e4[e] =                \
+                            (4 * c4 + e < d) ? src[e] : 0.0f;                                \
+                        v = make_float4(e4[0], e4[1], e4[2], e4[3]);                         \
+                    }                                                                        \
+                    if (COS) {                                                               \
+                        const float s_ = XSCALE[t];                                          \
+                        v.x *= s_;                                                           \
+                        v.y *= s_;                                                           \
+                        v.z *= s_;                                                           \
+                        v.w *= s_;                                                           \
+                    }                                                                        \
+                }                                                                            \
+            }                                                                                \
+            pf[p] = v;                                                                       \
+        }                                                                                    \
+        if (!COS && tid < kBn) {                                                             \
+            const int64_t t = t0_ + tid;                                                     \
+            pfn = (t < t_end) ? XSQ[t] : inf;                                                \
+        }                                                                                    \
+    } while (0)
+
+    // ---- flush: exact evaluation of one query's queue, sort, merge ----
+#define MLRS_FLUSH(J)                                                                        \
+    do {                                                                                     \
+        const int j_ = (J);                                                                  \
+        const int64_t qg_ = qwave + j_;                                                      \
+        const uint32_t n_ = L.cnt[j_];                                                       \
+        float e_ = inf;                                                                      \
+        uint32_t t_ = kSentinelIdx;                                                          \
+        if ((uint32_t)lane < n_) {                                                           \
+            t_ = L.qidx[j_][lane];                                                           \
+            const float ya_ = (ARM == ARM_COS_FOLD) ? XSQ[t_] : 0.0f;                        \
+            e_ = exact_f32<ARM, VEC4>(Q + qg_ * d, X + (int64_t)t_ * d, d, L.qa[j_], ya_);   \
+            if (e_ != e_) { /* NaN is never admitted */                                      \
+                e_ = inf;                                                                    \
+                t_ = kSentinelIdx;                                                           \
+            }                                                                                \
+        }                                                                                    \
+        wave_sort64<float>(e_, t_, lane);                                                    \
+        float lv_ = (lane < k) ? L.lval[j_][lane] : inf;                                     \
+        uint32_t li_ = (lane < k) ? L.lidx[j_][lane] : kSentinelIdx;                         \
+        wave_merge64<float>(lv_, li_, e_, t_, lane);                                         \
+        if (lane < k) {                                                                      \
+            L.lval[j_][lane] = lv_;                                                          \
+            L.lidx[j_][lane] = li_;                                                          \
+        }                                                                                    \
+        float R_ = shfl_f(lv_, k - 1);                                                       \
+        if (lane == 0) {                                                                     \
+            if (SHARED_R && R_ < inf) {                                                      \
+                unsigned int old_ = atomicMin(&SHARED_R[qg_], __float_as_uint(R_));          \
+                R_ = fminf(R_, __uint_as_float(old_));                                       \
+            }                                                                                \
+            L.cnt[j_] = 0;                                                                   \
+            L.thr[j_] = fminf(L.thr[j_], screen_threshold<COS>(R_, L.qs[j_], L.eps[j_]));    \
+        }                                                                                    \
+    } while (0)
+
+    if (t_begin < t_end) MLRS_PREFETCH(t_begin);
+    __syncthreads();  // per-wave LDS init visible to the wave
+
+    float thr = L.thr[jl];
+    int buf = 0;
+    int tiles = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, ++tiles) {
+        // publish the prefetched tile
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
-            int f = tid + 256 * p;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            const int f = tid + 256 * p;
             if (f < TILE_F4) {
-                int r = f / (DP / 4);
-                int c4 = f % (DP / 4);
-                int64_t t = t0 + r;
-                if (t < t_end) {
-                    const float* src = a.x + t * d + 4 * c4;
-                    if (VEC4) {
-                        if (4 * c4 < d) v = *reinterpret_cast<const float4*>(src);
-                    } else {
-                        float e4[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) e4[e] = (4 * c4 + e < d) ? src[e] : 0.0f;
-                        v = make_float4(e4[0], e4[1], e4[2], e4[3]);
-                    }
-                    if (COS) {
-                        float s = a.xscale[t];
-                        v.x *= s; v.y *= s; v.z *= s; v.w *= s;
-                    }
-                }
-            }
-            pf[p] = v;
-        }
-        if (!COS && tid < kBn) {
-            int64_t t = t0 + tid;
-            pfn = (t < t_end) ? a.xsq[t] : 0.0f;
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            int f = tid + 256 * p;
-            if (f < TILE_F4) {
-                int r = f / (DP / 4);
-                int c4 = f % (DP / 4);
+                const int r = f / (DP / 4);
+                const int c4 = f % (DP / 4);
                 *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = pf[p];
             }
         }
         if (!COS && tid < kBn) tnorm[buf][tid] = pfn;
-    };
-
-    if (t_begin < t_end) prefetch(t_begin);
-    __syncthreads();  // per-wave LDS init visible to the wave (and tile buffers free)
-
-    float thr = L.thr[jl];
-    int buf = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn) {
-        store_tile(buf);
         __syncthreads();
-        if (t0 + kBn < t_end) prefetch(t0 + kBn);
+        if (t0 + kBn < t_end) MLRS_PREFETCH(t0 + kBn);
 
         f32x16 acc;
         if (!COS) {
@@ -291,13 +364,27 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
         }
+        // A operands double-buffered: the next group's LDS read is in flight
+        // while the current group's four MFMAs run.
+        const float* arow = &tile[buf][jl][4 * h];
+        float4 av = *reinterpret_cast<const float4*>(arow);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            float4 av = *reinterpret_cast<const float4*>(&tile[buf][jl][8 * g + 4 * h]);
+            float4 an = (g + 1 < NG) ? *reinterpret_cast<const float4*>(arow + 8 * (g + 1)) : av;
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qreg[g].x, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qreg[g].y, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qreg[g].z, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
+            av = an;
+        }
+
+        // ---- k = 1: tighten with this tile's smallest expansion value ----
+        if (!COS && k == 1) {
+            float m = inf;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) m = fminf(m, acc[r]);  // NaN ignored; past-end rows are +inf
+            m = fminf(m, shfl_xor_f(m, 32));
+            if (m < inf) thr = fminf(thr, round_up_f((double)m + 2.0 * (double)L.eps[jl]));
         }
 
         // ---- screen: lane holds rows 8*(r/4) + 4h + (r%4) of the tile, query jl ----
@@ -307,7 +394,7 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         if (__builtin_amdgcn_ballot_w64(hit)) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                int64_t t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int64_t t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (qvalid && t < t_end && !(acc[r] > thr)) {
                     uint32_t pos = atomicAdd(&L.cnt[jl], 1u);
                     L.qidx[jl][pos] = (uint32_t)t;
@@ -318,10 +405,19 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         bool need = (lane < kQpw) && (L.cnt[lane] > (uint32_t)kFlushAt);
         uint64_t mask = __builtin_amdgcn_ballot_w64(need);
         if (mask) {
+            if (lane < kQpw) L.thr[lane] = fminf(L.thr[lane], thr);
             while (mask) {
-                int j = __builtin_ctzll(mask);
+                const int j = __builtin_ctzll(mask);
                 mask &= mask - 1;
-                flush_query<ARM, COS, VEC4>(L, j, lane, a, qwave + j);
+                MLRS_FLUSH(j);
+            }
+            thr = L.thr[jl];
+        }
+        // ---- pick up thresholds tightened by other strips of these queries ----
+        if (SHARED_R && (tiles % kShareEvery) == kShareEvery - 1) {
+            if (lane < kQpw && qvalid) {
+                float R = __uint_as_float(SHARED_R[qmine]);
+                L.thr[lane] = fminf(fminf(L.thr[lane], thr), screen_threshold<COS>(R, L.qs[lane], L.eps[lane]));
             }
             thr = L.thr[jl];
         }
@@ -333,58 +429,30 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         bool need = (lane < kQpw) && (L.cnt[lane] > 0u);
         uint64_t mask = __builtin_amdgcn_ballot_w64(need);
         while (mask) {
-            int j = __builtin_ctzll(mask);
+            const int j = __builtin_ctzll(mask);
             mask &= mask - 1;
-            flush_query<ARM, COS, VEC4>(L, j, lane, a, qwave + j);
+            MLRS_FLUSH(j);
         }
     }
+#undef MLRS_FLUSH
+#undef MLRS_PREFETCH
 
     // ---- emit ----
-    const int k = a.k;
     for (int j = 0; j < kQpw; ++j) {
-        int64_t qg = qwave + j;
-        if (qg >= a.nq) break;
+        const int64_t qg = qwave + j;
+        if (qg >= nq) break;
         if (lane < k) {
-            float v = L.lval[j][lane];
-            uint32_t ix = L.lidx[j][lane];
+            const float v = L.lval[j][lane];
+            const uint32_t ix = L.lidx[j][lane];
             if (a.nstrips > 1) {
-                int64_t o = ((int64_t)blockIdx.y * a.nq + qg) * k + lane;
+                const int64_t o = ((int64_t)blockIdx.y * nq + qg) * k + lane;
                 a.part_val[o] = v;
                 a.part_idx[o] = ix;
             } else {
-                emit_one_f32(a.mode, a, qg, lane, v, ix);
+                emit_pair(a.mode, Q, X, QSQ, XSQ, d, k, qg, lane, v, ix, a.out_val, a.out_idx);
             }
         }
     }
-}
-
-}  // namespace
-
-// Output transform shared with the strip merge: the boundary root of
-// prims/knn.rs:877-883 (Euclidean), identity (cosine), or the k-means
-// (label, squared distance) pair with argmin_dist_rows' centre-0 seeding
-// (crates/mlrs-kernels/src/kmeans.rs:284-310).
-__device__ void emit_one_f32(int mode, const GramArgs32& a, int64_t qg, int slot, float v, uint32_t ix) {
-    int64_t o = qg * a.k + slot;
-    if (mode == EMIT_KMEANS) {
-        // argmin_dist_rows seeds `best` from centre 0 unconditionally, so a NaN
-        // distance to centre 0 wins with label 0.  That distance can only be
-        // NaN when a norm is non-finite; check those rows exactly.
-        float q0 = a.qsq[qg];
-        float c0 = a.xsq[0];
-        if (!(q0 < __builtin_huge_valf()) || !(c0 < __builtin_huge_valf())) {
-            float e0 = exact_pair<float, ARM_EUCLID_MULADD>(a.q + qg * a.d, a.x, a.d, 0.0f, 0.0f);
-            if (e0 != e0) {
-                v = e0;
-                ix = 0;
-            }
-        }
-        a.out_val[o] = v;
-        a.out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
-        return;
-    }
-    a.out_val[o] = (mode == EMIT_SQRT) ? __builtin_sqrtf(v) : v;
-    a.out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
 }
 
 // Merge the per-strip exact lists of one query per wave (the strip merge of
@@ -406,31 +474,39 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
         float v = inf;
         uint32_t ix = kSentinelIdx;
         if (lane < k) {
-            int64_t o = ((int64_t)s * a.nq + qg) * k + lane;
+            const int64_t o = ((int64_t)s * a.nq + qg) * k + lane;
             v = a.part_val[o];
             ix = a.part_idx[o];
         }
         wave_merge64<float>(lv, li, v, ix, lane);
     }
-    if (lane < k) emit_one_f32(a.mode, a, qg, lane, lv, li);
+    if (lane < k) emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, k, qg, lane, lv, li, a.out_val, a.out_idx);
+}
+
+// The shared per-query threshold words start at +inf (as float bits).
+__global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0x7F800000u;
 }
 
 template <int NG, int ARM, bool COS, bool VEC4>
-static hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
+hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     dim3 grid((unsigned)nblocks, (unsigned)a.nstrips);
     hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 template <int ARM, bool COS, bool VEC4>
-static hipError_t launch_arm(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
-    int ng = (int)((a.d + 7) / 8);
+hipError_t launch_arm(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
+    const int ng = (int)((a.d + 7) / 8);
     if (ng <= 2) return launch_ng<2, ARM, COS, VEC4>(a, nblocks, s);
     if (ng <= 4) return launch_ng<4, ARM, COS, VEC4>(a, nblocks, s);
     if (ng <= 8) return launch_ng<8, ARM, COS, VEC4>(a, nblocks, s);
     if (ng <= 12) return launch_ng<12, ARM, COS, VEC4>(a, nblocks, s);
     return launch_ng<16, ARM, COS, VEC4>(a, nblocks, s);
 }
+
+}  // namespace
 
 int gram_f32_max_k() { return kKcap; }
 int gram_f32_max_d() { return 128; }
@@ -441,6 +517,10 @@ hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
     const int64_t nblocks = (a.nq + kQpb - 1) / kQpb;
     const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    if (a.shared_r) {
+        hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s,
+                           a.shared_r, a.nq);
+    }
     hipError_t e;
     if (arm == ARM_EUCLID_FMA)
         e = vec4 ? launch_arm<ARM_EUCLID_FMA, false, true>(a, nblocks, s)

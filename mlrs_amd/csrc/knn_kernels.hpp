@@ -40,9 +40,8 @@ struct GramArgs32 {
     uint32_t* part_idx;
     float* out_val;    // [nq][k]
     uint32_t* out_idx;
+    unsigned int* shared_r;  // [nq] best known exact k-th value per query (float bits), or null
 };
-
-__device__ void emit_one_f32(int mode, const GramArgs32& a, int64_t qg, int slot, float v, uint32_t ix);
 
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
 int gram_f32_max_k();
