@@ -17,14 +17,40 @@ namespace {
 // ---------------------------------------------------------------------------
 // Row norms (row_sumsq order) + device-side max for the Gram screen bound.
 // ---------------------------------------------------------------------------
+// 256 rows per block.  Each 32-element (f32) / 16-element (f64) column chunk
+// of the block's rows is staged in LDS with coalesced loads (consecutive
+// threads read consecutive columns of one row), then each thread continues
+// its own row's sum over the chunk in column order -- the row_sumsq order.
 template <typename T>
-__global__ void row_norms_kernel(const T* __restrict__ x, int64_t n, int64_t d, T* __restrict__ sq,
-                                 T* __restrict__ inv, T* __restrict__ neg_inv, NormStats* stats) {
-    int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void row_norms_kernel(const T* __restrict__ x, int64_t n, int64_t d,
+                                                        T* __restrict__ sq, T* __restrict__ inv,
+                                                        T* __restrict__ neg_inv, NormStats* stats) {
+    constexpr int CW = 128 / sizeof(T);  // columns per chunk: one 128-byte segment per row
+    __shared__ T stage[256][CW + 1];
+    const int tid = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * 256;
+    const int64_t r = r0 + tid;
+    const bool valid = r < n;
     T s = T(0);
-    bool valid = r < n;
+    for (int64_t c0 = 0; c0 < d; c0 += CW) {
+        const int cw = (d - c0) < CW ? (int)(d - c0) : CW;
+#pragma unroll 4
+        for (int m = 0; m < CW; ++m) {
+            const int e = tid + 256 * m;  // element of the 256 x CW chunk
+            const int rr = e / CW, cc = e % CW;
+            const int64_t gr = r0 + rr;
+            if (cc < cw && gr < n) stage[rr][cc] = x[gr * d + c0 + cc];
+        }
+        __syncthreads();
+        if (valid) {
+            for (int cc = 0; cc < cw; ++cc) {
+                T v = stage[tid][cc];
+                s = s + v * v;
+            }
+        }
+        __syncthreads();
+    }
     if (valid) {
-        s = row_sumsq<T>(x + r * d, d);
         sq[r] = s;
         T iv = (s > T(0)) ? T(1) / FloatTraits<T>::sqrt_(s) : T(0);
         if (inv) inv[r] = iv;
@@ -46,7 +72,7 @@ __global__ void row_norms_kernel(const T* __restrict__ x, int64_t n, int64_t d, 
             unsigned long long o = (unsigned long long)__shfl_xor((long long)bits, m, 64);
             bits = o > bits ? o : bits;
         }
-        if ((threadIdx.x & 63) == 0 && bits) atomicMax(&stats->xsq_max_bits, bits);
+        if ((tid & 63) == 0 && bits) atomicMax(&stats->xsq_max_bits, bits);
     }
 }
 

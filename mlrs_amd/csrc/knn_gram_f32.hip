@@ -55,7 +55,13 @@ struct WaveLds {
     float qa[kQpw];   // exact arm's query operand (row_sumsq for the fold arm)
     float qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
     float eps[kQpw];  // screen error bound
+    uint32_t off[kQpw];                 // k = 1: queue offsets of the batched flush
+    unsigned long long best[kQpw];      // k = 1: (value bits << 32 | index) of the kept pair
 };
+
+// (value, index) packed so that unsigned order is the (value, index) order
+// for the non-negative values every served arm produces.
+constexpr unsigned long long kBestEmpty = (0x7F800000ull << 32) | 0xFFFFFFFFull;
 
 // Smallest float >= t.
 __device__ __forceinline__ float round_up_f(double t) {
@@ -180,7 +186,7 @@ __device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q,
     out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
 }
 
-template <int NG, int ARM, bool COS, bool VEC4>
+template <int NG, int ARM, bool COS, bool VEC4, bool K1>
 __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
     constexpr int DP = NG * 8;        // padded feature count
     constexpr int STRIDE = DP + 4;    // LDS row stride (floats)
@@ -231,9 +237,18 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
             L.eps[lane] = (float)a.eps_abs;
         }
     }
-    for (int i = lane; i < kQpw * kKcap; i += 64) {
-        (&L.lval[0][0])[i] = inf;
-        (&L.lidx[0][0])[i] = kSentinelIdx;
+    if (K1) {
+        if (lane < kQpw) L.best[lane] = kBestEmpty;
+    } else {
+        for (int i = lane; i < kQpw * kKcap; i += 64) {
+            (&L.lval[0][0])[i] = inf;
+            (&L.lidx[0][0])[i] = kSentinelIdx;
+        }
+    }
+    // Strips that start late begin from the bound earlier strips have reached.
+    if (SHARED_R && lane < kQpw && qvalid) {
+        const float R0 = __uint_as_float(SHARED_R[qmine]);
+        L.thr[lane] = fminf(L.thr[lane], screen_threshold<COS>(R0, L.qs[lane], L.eps[lane]));
     }
 
     // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3] ----
@@ -329,6 +344,43 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         }                                                                                    \
     } while (0)
 
+    // ---- k = 1: every queued pair of the wave evaluated in lane-parallel
+    //      batches, kept with a 64-bit LDS atomicMin on (value, index) ----
+#define MLRS_FLUSH_K1()                                                                      \
+    do {                                                                                     \
+        const uint32_t c_ = (lane < kQpw) ? L.cnt[lane] : 0u;                                \
+        uint32_t incl_ = c_;                                                                 \
+        _Pragma("unroll") for (int m_ = 1; m_ < kQpw; m_ <<= 1) {                            \
+            const uint32_t o_ = (uint32_t)__shfl_up((int)incl_, m_, 64);                     \
+            if ((lane & 31) >= m_) incl_ += o_;                                              \
+        }                                                                                    \
+        const uint32_t total_ = (uint32_t)__shfl((int)incl_, kQpw - 1, 64);                  \
+        if (lane < kQpw) L.off[lane] = incl_ - c_;                                           \
+        for (uint32_t base_ = 0; base_ < total_; base_ += 64) {                              \
+            const uint32_t e_ = base_ + (uint32_t)lane;                                      \
+            if (e_ < total_) {                                                               \
+                int j_ = 0;                                                                  \
+                _Pragma("unroll") for (int m_ = 16; m_ >= 1; m_ >>= 1) if (L.off[j_ + m_] <= e_) \
+                    j_ += m_;                                                                \
+                const uint32_t t_ = L.qidx[j_][e_ - L.off[j_]];                              \
+                const float ya_ = (ARM == ARM_COS_FOLD) ? XSQ[t_] : 0.0f;                    \
+                const float v_ = exact_f32<ARM, VEC4>(Q + (qwave + j_) * d, X + (int64_t)t_ * d, d, \
+                                                       L.qa[j_], ya_);                       \
+                if (v_ == v_)                                                                \
+                    atomicMin(&L.best[j_], ((unsigned long long)__float_as_uint(v_) << 32) | t_); \
+            }                                                                                \
+        }                                                                                    \
+        if (lane < kQpw) {                                                                   \
+            L.cnt[lane] = 0u;                                                                \
+            float R_ = __uint_as_float((uint32_t)(L.best[lane] >> 32));                      \
+            if (SHARED_R && qvalid && R_ < inf) {                                            \
+                const unsigned int old_ = atomicMin(&SHARED_R[qmine], __float_as_uint(R_));  \
+                R_ = fminf(R_, __uint_as_float(old_));                                       \
+            }                                                                                \
+            L.thr[lane] = fminf(L.thr[lane], screen_threshold<COS>(R_, L.qs[lane], L.eps[lane])); \
+        }                                                                                    \
+    } while (0)
+
     if (t_begin < t_end) MLRS_PREFETCH(t_begin);
     __syncthreads();  // per-wave LDS init visible to the wave
 
@@ -406,10 +458,14 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         uint64_t mask = __builtin_amdgcn_ballot_w64(need);
         if (mask) {
             if (lane < kQpw) L.thr[lane] = fminf(L.thr[lane], thr);
-            while (mask) {
-                const int j = __builtin_ctzll(mask);
-                mask &= mask - 1;
-                MLRS_FLUSH(j);
+            if (K1) {
+                MLRS_FLUSH_K1();
+            } else {
+                while (mask) {
+                    const int j = __builtin_ctzll(mask);
+                    mask &= mask - 1;
+                    MLRS_FLUSH(j);
+                }
             }
             thr = L.thr[jl];
         }
@@ -428,12 +484,17 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
     {
         bool need = (lane < kQpw) && (L.cnt[lane] > 0u);
         uint64_t mask = __builtin_amdgcn_ballot_w64(need);
-        while (mask) {
-            const int j = __builtin_ctzll(mask);
-            mask &= mask - 1;
-            MLRS_FLUSH(j);
+        if (K1) {
+            if (mask) MLRS_FLUSH_K1();
+        } else {
+            while (mask) {
+                const int j = __builtin_ctzll(mask);
+                mask &= mask - 1;
+                MLRS_FLUSH(j);
+            }
         }
     }
+#undef MLRS_FLUSH_K1
 #undef MLRS_FLUSH
 #undef MLRS_PREFETCH
 
@@ -442,8 +503,16 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         const int64_t qg = qwave + j;
         if (qg >= nq) break;
         if (lane < k) {
-            const float v = L.lval[j][lane];
-            const uint32_t ix = L.lidx[j][lane];
+            float v;
+            uint32_t ix;
+            if (K1) {
+                const unsigned long long b = L.best[j];
+                v = __uint_as_float((uint32_t)(b >> 32));
+                ix = (uint32_t)b;
+            } else {
+                v = L.lval[j][lane];
+                ix = L.lidx[j][lane];
+            }
             if (a.nstrips > 1) {
                 const int64_t o = ((int64_t)blockIdx.y * nq + qg) * k + lane;
                 a.part_val[o] = v;
@@ -492,7 +561,10 @@ __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
 template <int NG, int ARM, bool COS, bool VEC4>
 hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     dim3 grid((unsigned)nblocks, (unsigned)a.nstrips);
-    hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4>), grid, dim3(256), 0, s, a);
+    if (a.k == 1)
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
