@@ -292,13 +292,14 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     int cus;
     int32_t rc = workspace(fixed, s, &ws, &cus);
     if (rc) return rc;
-    const int64_t slots = cus;  // one 4-wave workgroup per CU (LDS-bound)
+    const int64_t slots = 2 * (int64_t)cus;  // two 4-wave workgroups per CU (LDS-bound)
     int nstrips = pick_strips(nblocks, nt, slots, 2048, 64);
     const int64_t tile = gram_f32_rows_per_tile();
     int64_t rps = (nt + nstrips - 1) / nstrips;
     rps = (rps + tile - 1) / tile * tile;
     nstrips = (int)((nt + rps - 1) / rps);
-    size_t parts = nstrips > 1 ? (size_t)nstrips * nq * k : 0;
+    // per-(strip, query) exact lists: the kernel's top-k state, merged at the end
+    size_t parts = (size_t)nstrips * nq * k;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
                    aligned_bytes(sizeof(unsigned int) * nq);
     rc = workspace(bytes, s, &ws, &cus);
@@ -340,11 +341,9 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     }
     a.rows_per_strip = rps;
     a.nstrips = nstrips;
-    if (nstrips > 1) {
-        a.part_val = cv.take<float>(parts);
-        a.part_idx = cv.take<uint32_t>(parts);
-        a.shared_r = cv.take<unsigned int>(nq);
-    }
+    a.part_val = cv.take<float>(parts);
+    a.part_idx = cv.take<uint32_t>(parts);
+    if (nstrips > 1) a.shared_r = cv.take<unsigned int>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
     {

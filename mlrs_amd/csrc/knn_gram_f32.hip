@@ -25,7 +25,10 @@
 //  * Passing (query, row) pairs are queued in LDS.  When a query's queue is
 //    half full the wave evaluates the queued pairs EXACTLY, in the reference
 //    arm's operation order, sorts them and merges them into the query's exact
-//    top-k list with the (value, index) order.
+//    top-k list with the (value, index) order.  The lists live in global
+//    memory (one per query and strip): keeping only the queues in LDS (~70 KB
+//    per workgroup) lets two workgroups share a CU, so one workgroup's
+//    selection work overlaps the other's MFMAs.
 // The kept lists are therefore the reference's own top-k: the full distance
 // matrix never reaches HBM and no tolerance is involved.
 #include "knn_common.hpp"
@@ -47,8 +50,6 @@ constexpr int kShareEvery = 32;          // tiles between reads of the shared th
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct WaveLds {
-    float lval[kQpw][kKcap];
-    uint32_t lidx[kQpw][kKcap];
     uint32_t qidx[kQpw][kQcap];
     uint32_t cnt[kQpw];
     float thr[kQpw];
@@ -187,7 +188,7 @@ __device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q,
 }
 
 template <int NG, int ARM, bool COS, bool VEC4, bool K1>
-__global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
+__global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     constexpr int DP = NG * 8;        // padded feature count
     constexpr int STRIDE = DP + 4;    // LDS row stride (floats)
     constexpr int TILE_F4 = kBn * DP / 4;
@@ -206,6 +207,10 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
     unsigned int* __restrict__ SHARED_R = a.shared_r;
     const int64_t nq = a.nq, nt = a.nt, d = a.d;
     const int k = a.k;
+    // This strip's exact top-k lists, [nstrips][nq][k] in global memory: they
+    // are only touched when a query's queue is flushed.
+    float* __restrict__ LV = a.part_val + (int64_t)blockIdx.y * nq * k;
+    uint32_t* __restrict__ LI = a.part_idx + (int64_t)blockIdx.y * nq * k;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -240,9 +245,12 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
     if (K1) {
         if (lane < kQpw) L.best[lane] = kBestEmpty;
     } else {
-        for (int i = lane; i < kQpw * kKcap; i += 64) {
-            (&L.lval[0][0])[i] = inf;
-            (&L.lidx[0][0])[i] = kSentinelIdx;
+        for (int j = 0; j < kQpw; ++j) {
+            const int64_t qg = qwave + j;
+            if (qg < nq && lane < k) {
+                LV[qg * k + lane] = inf;
+                LI[qg * k + lane] = kSentinelIdx;
+            }
         }
     }
     // Strips that start late begin from the bound earlier strips have reached.
@@ -314,6 +322,8 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
         const int j_ = (J);                                                                  \
         const int64_t qg_ = qwave + j_;                                                      \
         const uint32_t n_ = L.cnt[j_];                                                       \
+        float lv_ = (lane < k) ? LV[qg_ * k + lane] : inf;                                   \
+        uint32_t li_ = (lane < k) ? LI[qg_ * k + lane] : kSentinelIdx;                       \
         float e_ = inf;                                                                      \
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
@@ -326,12 +336,10 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
             }                                                                                \
         }                                                                                    \
         wave_sort64<float>(e_, t_, lane);                                                    \
-        float lv_ = (lane < k) ? L.lval[j_][lane] : inf;                                     \
-        uint32_t li_ = (lane < k) ? L.lidx[j_][lane] : kSentinelIdx;                         \
         wave_merge64<float>(lv_, li_, e_, t_, lane);                                         \
         if (lane < k) {                                                                      \
-            L.lval[j_][lane] = lv_;                                                          \
-            L.lidx[j_][lane] = li_;                                                          \
+            LV[qg_ * k + lane] = lv_;                                                        \
+            LI[qg_ * k + lane] = li_;                                                        \
         }                                                                                    \
         float R_ = shfl_f(lv_, k - 1);                                                       \
         if (lane == 0) {                                                                     \
@@ -498,35 +506,17 @@ __global__ __launch_bounds__(256, 1) void knn_gram_f32_kernel(GramArgs32 a) {
 #undef MLRS_FLUSH
 #undef MLRS_PREFETCH
 
-    // ---- emit ----
-    for (int j = 0; j < kQpw; ++j) {
-        const int64_t qg = qwave + j;
-        if (qg >= nq) break;
-        if (lane < k) {
-            float v;
-            uint32_t ix;
-            if (K1) {
-                const unsigned long long b = L.best[j];
-                v = __uint_as_float((uint32_t)(b >> 32));
-                ix = (uint32_t)b;
-            } else {
-                v = L.lval[j][lane];
-                ix = L.lidx[j][lane];
-            }
-            if (a.nstrips > 1) {
-                const int64_t o = ((int64_t)blockIdx.y * nq + qg) * k + lane;
-                a.part_val[o] = v;
-                a.part_idx[o] = ix;
-            } else {
-                emit_pair(a.mode, Q, X, QSQ, XSQ, d, k, qg, lane, v, ix, a.out_val, a.out_idx);
-            }
-        }
+    // ---- k = 1: the kept pair becomes this strip's one-entry list ----
+    if (K1 && lane < kQpw && qvalid) {
+        const unsigned long long b = L.best[lane];
+        LV[qmine] = __uint_as_float((uint32_t)(b >> 32));
+        LI[qmine] = (uint32_t)b;
     }
 }
 
 // Merge the per-strip exact lists of one query per wave (the strip merge of
 // select_k_onepass_indexed, crates/mlrs-kernels/src/topk.rs:612-758, here a
-// wave-wide bitonic merge of sorted lists).
+// wave-wide bitonic merge of sorted lists) and emit the output transform.
 __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
     const int lane = threadIdx.x & 63;
     const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -606,11 +596,8 @@ hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
     else
         return hipErrorInvalidValue;
     if (e != hipSuccess) return e;
-    if (a.nstrips > 1) {
-        hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
-        e = hipGetLastError();
-    }
-    return e;
+    hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace mlrs
