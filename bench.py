@@ -41,6 +41,9 @@ def main():
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel "
+                         "of known traffic, the scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -91,6 +94,16 @@ def main():
     kern_ms = tot_ms.value / max(1, launches.value)
     log("timed %d steps: %.3f ms/step, %s avg %.3f ms over %d launches"
         % (args.steps, ms_per_step, name.value.decode(), kern_ms, launches.value))
+
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: %d MiB read + %d MiB written" % (args.calib_copy_mib, args.calib_copy_mib))
+        del src, dst
 
     # ---- parity of the measured run against the committed golden subset ----
     g = np.load(os.path.join(ROOT, "tests", "golden", "%s_golden.npz" % args.config))

@@ -202,6 +202,25 @@ int pick_strips(int64_t nblocks, int64_t nt, int64_t slots, int64_t min_rows, in
     return (int)best_s;
 }
 
+// The Gram kernel gives each XCD an equal contiguous range of the strip-major
+// work items, so the balance that matters is per XCD: ceil(s*nblocks/8)
+// workgroups over the XCD's slots.
+int pick_strips_xcd(int64_t nblocks, int64_t nt, int64_t slots_per_xcd, int64_t min_rows, int max_strips) {
+    int64_t best_s = 1;
+    double best_cost = 1e300;
+    int64_t s_hi = std::max<int64_t>(1, std::min<int64_t>(max_strips, (nt + min_rows - 1) / min_rows));
+    for (int64_t s = 1; s <= s_hi; ++s) {
+        int64_t per_xcd = (s * nblocks + 7) / 8;
+        int64_t rounds = (per_xcd + slots_per_xcd - 1) / slots_per_xcd;
+        double cost = (double)rounds / (double)s * (1.0 + 0.002 * (double)s);
+        if (cost < best_cost - 1e-12) {
+            best_cost = cost;
+            best_s = s;
+        }
+    }
+    return (int)best_s;
+}
+
 // ---------------------------------------------------------------------------
 // generic exact path: tile of exact pairwise values + per-row selection
 // ---------------------------------------------------------------------------
@@ -292,8 +311,8 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     int cus;
     int32_t rc = workspace(fixed, s, &ws, &cus);
     if (rc) return rc;
-    const int64_t slots = 2 * (int64_t)cus;  // two 4-wave workgroups per CU (LDS-bound)
-    int nstrips = pick_strips(nblocks, nt, slots, 2048, 64);
+    const int64_t slots_per_xcd = 2 * std::max<int64_t>(1, cus / 8);  // two 4-wave workgroups per CU
+    int nstrips = pick_strips_xcd(nblocks, nt, slots_per_xcd, 2048, 64);
     const int64_t tile = gram_f32_rows_per_tile();
     int64_t rps = (nt + nstrips - 1) / nstrips;
     rps = (rps + tile - 1) / tile * tile;
@@ -346,10 +365,12 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     if (nstrips > 1) a.shared_r = cv.take<unsigned int>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
-    {
+    e = launch_gram_f32_prep(a, s);
+    if (e == hipSuccess) {
         KernelTimer timer(s, "knn_gram_f32_kernel");
         e = launch_gram_f32(a, arm, s);
     }
+    if (e == hipSuccess) e = launch_gram_f32_merge(a, s);
     if (e != hipSuccess) return hip_err(e, "knn_gram_f32");
     return ok();
 }

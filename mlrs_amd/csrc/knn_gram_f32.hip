@@ -46,6 +46,7 @@ constexpr int kKcap = 64;                // largest k this kernel keeps
 constexpr int kQcap = 64;                // queued candidates per query
 constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
 constexpr int kShareEvery = 32;          // tiles between reads of the shared thresholds
+constexpr int kXcds = 8;                 // XCDs of an MI355X
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -92,7 +93,7 @@ __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) 
 }
 
 // Exact value of one (query, row) pair in the arm's operation order, loads
-// issued eight 16-byte chunks at a time.
+// issued four 16-byte chunks at a time.
 template <int ARM, bool VEC4>
 __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const float* __restrict__ y,
                                            int64_t d, float qa, float ya) {
@@ -102,15 +103,16 @@ __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const fl
     const int n4 = (int)(d >> 2);
     float acc = 0.0f;
     int c = 0;
-    for (; c + 8 <= n4; c += 8) {
-        float4 a[8], b[8];
+    constexpr int U = 4;
+    for (; c + U <= n4; c += U) {
+        float4 a[U], b[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < U; ++u) {
             a[u] = q4[c + u];
             b[u] = y4[c + u];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < U; ++u) {
             if (ARM == ARM_EUCLID_FMA) {
                 float d0 = a[u].x - b[u].x, d1 = a[u].y - b[u].y, d2 = a[u].z - b[u].z, d3 = a[u].w - b[u].w;
                 acc = __builtin_fmaf(d0, d0, acc);
@@ -209,8 +211,20 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     const int k = a.k;
     // This strip's exact top-k lists, [nstrips][nq][k] in global memory: they
     // are only touched when a query's queue is flushed.
-    float* __restrict__ LV = a.part_val + (int64_t)blockIdx.y * nq * k;
-    uint32_t* __restrict__ LI = a.part_idx + (int64_t)blockIdx.y * nq * k;
+    // Workgroups are dispatched round-robin over the 8 XCDs (physical id p runs
+    // on XCD p % 8).  The (strip, query block) work items, strip-major, are cut
+    // into 8 equal contiguous ranges and XCD x runs range x in order, so the
+    // workgroups streaming one strip's index rows sit behind the same L2.
+    const int64_t nqb = (nq + kQpb - 1) / kQpb;
+    const int64_t n_items = (int64_t)a.nstrips * nqb;
+    const int64_t per_xcd = (n_items + kXcds - 1) / kXcds;
+    const int64_t p_ = blockIdx.x;
+    const int64_t item = (p_ % kXcds) * per_xcd + p_ / kXcds;
+    if (item >= n_items) return;  // padding of the last range
+    const int64_t strip = item / nqb;
+    const int64_t qblock = item % nqb;
+    float* __restrict__ LV = a.part_val + strip * nq * k;
+    uint32_t* __restrict__ LI = a.part_idx + strip * nq * k;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -220,10 +234,10 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     WaveLds& L = wl[w];
     const float inf = __builtin_huge_valf();
 
-    const int64_t qwave = (int64_t)blockIdx.x * kQpb + w * kQpw;  // first query of this wave
+    const int64_t qwave = qblock * kQpb + w * kQpw;  // first query of this wave
     const int64_t qmine = qwave + jl;
     const bool qvalid = qmine < nq;
-    const int64_t t_begin = (int64_t)blockIdx.y * a.rows_per_strip;
+    const int64_t t_begin = strip * a.rows_per_strip;
     int64_t t_end = t_begin + a.rows_per_strip;
     if (t_end > nt) t_end = nt;
 
@@ -277,42 +291,51 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     }
 
     // ---- tile prefetch into registers (rows past the strip: zeros, norm +inf) ----
-    float4 pf[PF];
-    float pfn = 0.0f;
+    // Each thread owns PF fixed 16-byte chunks of the tile: row pf_r[p], column
+    // chunk pf_c[p]; its source pointer walks down one tile (kBn rows) per step.
+    const uint32_t t_end32 = (uint32_t)t_end;
+    int pf_r[PF];
+    bool pf_on[PF];
+    const float* pf_src[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+        const int f = tid + 256 * p;
+        pf_r[p] = f / (DP / 4);
+        const int c4 = f % (DP / 4);
+        pf_on[p] = (f < TILE_F4) && (VEC4 ? (4 * c4 < d) : (4 * c4 < d));
+        pf_src[p] = X + (t_begin + pf_r[p]) * d + 4 * c4;
+    }
 #define MLRS_PREFETCH(T0)                                                                    \
     do {                                                                                     \
-        const int64_t t0_ = (T0);                                                            \
+        const uint32_t t0_ = (uint32_t)(T0);                                                 \
         _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
-            const int f = tid + 256 * p;                                                     \
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);                                      \
-            if (f < TILE_F4) {                                                               \
-                const int r = f / (DP / 4);                                                  \
-                const int c4 = f % (DP / 4);                                                 \
-                const int64_t t = t0_ + r;                                                   \
-                if (t < t_end) {                                                             \
-                    const float* src = X + t * d + 4 * c4;                                   \
-                    if (VEC4) {                                                              \
-                        if (4 * c4 < d) v = *reinterpret_cast<const float4*>(src);           \
-                    } else {                                                                 \
-                        float e4[4];                                                         \
-                        _Pragma("unroll") for (int e = 0; e < 4; ++e) e4[e] =                \
-                            (4 * c4 + e < d) ? src[e] : 0.0f;                                \
-                        v = make_float4(e4[0], e4[1], e4[2], e4[3]);                         \
-                    }                                                                        \
-                    if (COS) {                                                               \
-                        const float s_ = XSCALE[t];                                          \
-                        v.x *= s_;                                                           \
-                        v.y *= s_;                                                           \
-                        v.z *= s_;                                                           \
-                        v.w *= s_;                                                           \
-                    }                                                                        \
+            const uint32_t t = t0_ + (uint32_t)pf_r[p];                                      \
+            if (pf_on[p] && t < t_end32) {                                                   \
+                const float* src = pf_src[p];                                                \
+                if (VEC4) {                                                                  \
+                    v = *reinterpret_cast<const float4*>(src);                               \
+                } else {                                                                     \
+                    const int c0_ = (int)((tid + 256 * p) % (DP / 4)) * 4;                   \
+                    float e4[4];                                                             \
+                    _Pragma("unroll") for (int e = 0; e < 4; ++e) e4[e] =                    \
+                        (c0_ + e < d) ? src[e] : 0.0f;                                       \
+                    v = make_float4(e4[0], e4[1], e4[2], e4[3]);                             \
+                }                                                                            \
+                if (COS) {                                                                   \
+                    const float s_ = XSCALE[t];                                              \
+                    v.x *= s_;                                                               \
+                    v.y *= s_;                                                               \
+                    v.z *= s_;                                                               \
+                    v.w *= s_;                                                               \
                 }                                                                            \
             }                                                                                \
             pf[p] = v;                                                                       \
+            pf_src[p] += kBn * d;                                                            \
         }                                                                                    \
         if (!COS && tid < kBn) {                                                             \
-            const int64_t t = t0_ + tid;                                                     \
-            pfn = (t < t_end) ? XSQ[t] : inf;                                                \
+            const uint32_t t = t0_ + (uint32_t)tid;                                          \
+            pfn = (t < t_end32) ? XSQ[t] : inf;                                              \
         }                                                                                    \
     } while (0)
 
@@ -389,13 +412,15 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         }                                                                                    \
     } while (0)
 
+    float4 pf[PF];
+    float pfn = 0.0f;
     if (t_begin < t_end) MLRS_PREFETCH(t_begin);
     __syncthreads();  // per-wave LDS init visible to the wave
 
     float thr = L.thr[jl];
     int buf = 0;
     int tiles = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, ++tiles) {
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, buf ^= 1) {
         // publish the prefetched tile
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
@@ -424,17 +449,21 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
         }
-        // A operands double-buffered: the next group's LDS read is in flight
-        // while the current group's four MFMAs run.
+        // A operands double-buffered: the next group's LDS read is issued
+        // before the current group's four MFMAs (the scheduling barriers keep
+        // that order), so its latency hides under ~256 MFMA cycles.
         const float* arow = &tile[buf][jl][4 * h];
         float4 av = *reinterpret_cast<const float4*>(arow);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            float4 an = (g + 1 < NG) ? *reinterpret_cast<const float4*>(arow + 8 * (g + 1)) : av;
+            float4 an = av;
+            if (g + 1 < NG) an = *reinterpret_cast<const float4*>(arow + 8 * (g + 1));
+            __builtin_amdgcn_sched_barrier(0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qreg[g].x, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qreg[g].y, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qreg[g].z, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
             av = an;
         }
 
@@ -454,10 +483,10 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         if (__builtin_amdgcn_ballot_w64(hit)) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int64_t t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (qvalid && t < t_end && !(acc[r] > thr)) {
+                const uint32_t t = (uint32_t)t0 + (uint32_t)(8 * (r >> 2) + 4 * h + (r & 3));
+                if (qvalid && t < t_end32 && !(acc[r] > thr)) {
                     uint32_t pos = atomicAdd(&L.cnt[jl], 1u);
-                    L.qidx[jl][pos] = (uint32_t)t;
+                    L.qidx[jl][pos] = t;
                 }
             }
         }
@@ -478,14 +507,13 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             thr = L.thr[jl];
         }
         // ---- pick up thresholds tightened by other strips of these queries ----
-        if (SHARED_R && (tiles % kShareEvery) == kShareEvery - 1) {
+        if (SHARED_R && (++tiles % kShareEvery) == 0) {
             if (lane < kQpw && qvalid) {
                 float R = __uint_as_float(SHARED_R[qmine]);
                 L.thr[lane] = fminf(fminf(L.thr[lane], thr), screen_threshold<COS>(R, L.qs[lane], L.eps[lane]));
             }
             thr = L.thr[jl];
         }
-        buf ^= 1;
     }
 
     // ---- final flush of every non-empty queue ----
@@ -550,7 +578,9 @@ __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
 
 template <int NG, int ARM, bool COS, bool VEC4>
 hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
-    dim3 grid((unsigned)nblocks, (unsigned)a.nstrips);
+    // 1-D grid: kXcds equal ranges of the strip-major work items
+    const int64_t per_xcd = ((int64_t)a.nstrips * nblocks + kXcds - 1) / kXcds;
+    dim3 grid((unsigned)(kXcds * per_xcd));
     if (a.k == 1)
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true>), grid, dim3(256), 0, s, a);
     else
@@ -575,14 +605,23 @@ int gram_f32_max_d() { return 128; }
 int gram_f32_queries_per_block() { return kQpb; }
 int gram_f32_rows_per_tile() { return kBn; }
 
-hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
-    const int64_t nblocks = (a.nq + kQpb - 1) / kQpb;
-    const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+hipError_t launch_gram_f32_prep(const GramArgs32& a, hipStream_t s) {
     if (a.shared_r) {
         hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s,
                            a.shared_r, a.nq);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_gram_f32_merge(const GramArgs32& a, hipStream_t s) {
+    hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
+    const int64_t nblocks = (a.nq + kQpb - 1) / kQpb;
+    const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
     hipError_t e;
     if (arm == ARM_EUCLID_FMA)
         e = vec4 ? launch_arm<ARM_EUCLID_FMA, false, true>(a, nblocks, s)
@@ -595,9 +634,7 @@ hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
                  : launch_arm<ARM_COS_FOLD, true, false>(a, nblocks, s);
     else
         return hipErrorInvalidValue;
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
-    return hipGetLastError();
+    return e;
 }
 
 }  // namespace mlrs

@@ -43,7 +43,11 @@ struct GramArgs32 {
     unsigned int* shared_r;  // [nq] best known exact k-th value per query (float bits), or null
 };
 
+// Three launches per search: prep (shared-bound reset), the Gram kernel, the
+// strip merge + output transform.
+hipError_t launch_gram_f32_prep(const GramArgs32& a, hipStream_t s);
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
+hipError_t launch_gram_f32_merge(const GramArgs32& a, hipStream_t s);
 int gram_f32_max_k();
 int gram_f32_max_d();
 int gram_f32_queries_per_block();
