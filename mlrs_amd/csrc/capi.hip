@@ -311,14 +311,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     int cus;
     int32_t rc = workspace(fixed, s, &ws, &cus);
     if (rc) return rc;
-    const int64_t slots_per_xcd = 2 * std::max<int64_t>(1, cus / 8);  // two 4-wave workgroups per CU
-    int nstrips = pick_strips_xcd(nblocks, nt, slots_per_xcd, 2048, 64);
-    const int64_t tile = gram_f32_rows_per_tile();
-    int64_t rps = (nt + nstrips - 1) / nstrips;
-    rps = (rps + tile - 1) / tile * tile;
-    nstrips = (int)((nt + rps - 1) / rps);
-    // per-(strip, query) exact lists: the kernel's top-k state, merged at the end
-    size_t parts = (size_t)nstrips * nq * k;
+    int64_t grid_wgs = 1;
+    int nslots = 1;
+    gram_f32_split(nq, nt, cus, &grid_wgs, &nslots);
+    // per-(segment slot, query) exact lists: the kernel's top-k state, merged at the end
+    size_t parts = (size_t)nslots * nq * k;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
                    aligned_bytes(sizeof(unsigned int) * nq);
     rc = workspace(bytes, s, &ws, &cus);
@@ -358,11 +355,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
         a.eps_rel = 0.0;
         a.eps_abs = (8.0 * (double)d + 32.0) * u;
     }
-    a.rows_per_strip = rps;
-    a.nstrips = nstrips;
+    a.grid_wgs = grid_wgs;
+    a.nslots = nslots;
     a.part_val = cv.take<float>(parts);
     a.part_idx = cv.take<uint32_t>(parts);
-    if (nstrips > 1) a.shared_r = cv.take<unsigned int>(nq);
+    if (nslots > 1) a.shared_r = cv.take<unsigned int>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
     e = launch_gram_f32_prep(a, s);

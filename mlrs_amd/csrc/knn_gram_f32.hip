@@ -87,7 +87,11 @@ __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) 
         return round_up_f((double)R - (double)qs + (double)eps);
     } else {
         // exact <= R  =>  1 + acc/||q|| <= R + eps  =>  acc <= (R + eps - 1)||q||
-        if (qs == 0.0f) return -inf;  // zero query: every value is 1, lowest index kept
+        // A zero query scores exactly 1 against every row: all rows tie, and a
+        // bound published by another segment cannot tell which of them win
+        // (lower indices may lie in a segment that has not run yet), so such a
+        // query is never screened.
+        if (qs == 0.0f) return inf;
         return round_up_f(((double)R + (double)eps - 1.0) * (double)qs);
     }
 }
@@ -209,23 +213,6 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     unsigned int* __restrict__ SHARED_R = a.shared_r;
     const int64_t nq = a.nq, nt = a.nt, d = a.d;
     const int k = a.k;
-    // This strip's exact top-k lists, [nstrips][nq][k] in global memory: they
-    // are only touched when a query's queue is flushed.
-    // Workgroups are dispatched round-robin over the 8 XCDs (physical id p runs
-    // on XCD p % 8).  The (strip, query block) work items, strip-major, are cut
-    // into 8 equal contiguous ranges and XCD x runs range x in order, so the
-    // workgroups streaming one strip's index rows sit behind the same L2.
-    const int64_t nqb = (nq + kQpb - 1) / kQpb;
-    const int64_t n_items = (int64_t)a.nstrips * nqb;
-    const int64_t per_xcd = (n_items + kXcds - 1) / kXcds;
-    const int64_t p_ = blockIdx.x;
-    const int64_t item = (p_ % kXcds) * per_xcd + p_ / kXcds;
-    if (item >= n_items) return;  // padding of the last range
-    const int64_t strip = item / nqb;
-    const int64_t qblock = item % nqb;
-    float* __restrict__ LV = a.part_val + strip * nq * k;
-    uint32_t* __restrict__ LI = a.part_idx + strip * nq * k;
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -234,11 +221,32 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     WaveLds& L = wl[w];
     const float inf = __builtin_huge_valf();
 
+    // ---- stream-K split: the (query block, tile) units, query-block-major,
+    //      cut into gridDim.x equal contiguous ranges, one per workgroup; a
+    //      range crossing a query-block boundary becomes several segments.
+    //      Each segment keeps its own exact lists [segment slot][nq][k], merged
+    //      at the end by knn_merge_f32_kernel. ----
+    const int64_t nqb = (nq + kQpb - 1) / kQpb;
+    const int64_t ntiles = (nt + kBn - 1) / kBn;
+    const int64_t T = nqb * ntiles;
+    const int64_t G = gridDim.x;
+    const int64_t wg = blockIdx.x;
+    const int64_t u_hi = ((wg + 1) * T) / G;
+    for (int64_t u = (wg * T) / G; u < u_hi;) {
+    const int64_t qblock = u / ntiles;
+    const int64_t tile0 = u % ntiles;
+    const int64_t tile1 = (ntiles - tile0 < u_hi - u) ? ntiles : tile0 + (u_hi - u);
+    // slot = this workgroup's position among the workgroups covering qblock
+    const int64_t first_wg = ((qblock * ntiles + 1) * G + T - 1) / T - 1;
+    const int64_t slot = wg - first_wg;
+    float* __restrict__ LV = a.part_val + slot * nq * k;
+    uint32_t* __restrict__ LI = a.part_idx + slot * nq * k;
+
     const int64_t qwave = qblock * kQpb + w * kQpw;  // first query of this wave
     const int64_t qmine = qwave + jl;
     const bool qvalid = qmine < nq;
-    const int64_t t_begin = strip * a.rows_per_strip;
-    int64_t t_end = t_begin + a.rows_per_strip;
+    const int64_t t_begin = tile0 * kBn;
+    int64_t t_end = tile1 * kBn;
     if (t_end > nt) t_end = nt;
 
     // ---- per-query constants, lists, queues ----
@@ -534,11 +542,14 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
 #undef MLRS_FLUSH
 #undef MLRS_PREFETCH
 
-    // ---- k = 1: the kept pair becomes this strip's one-entry list ----
+    // ---- k = 1: the kept pair becomes this segment's one-entry list ----
     if (K1 && lane < kQpw && qvalid) {
         const unsigned long long b = L.best[lane];
         LV[qmine] = __uint_as_float((uint32_t)(b >> 32));
         LI[qmine] = (uint32_t)b;
+    }
+    u += tile1 - tile0;
+    __syncthreads();  // LDS state and tile buffers are reused by the next segment
     }
 }
 
@@ -557,11 +568,19 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
         lv = a.part_val[qg * k + lane];
         li = a.part_idx[qg * k + lane];
     }
-    for (int s = 1; s < a.nstrips; ++s) {
+    // the workgroups whose stream-K ranges cover this query's block
+    const int64_t nqb = (a.nq + kQpb - 1) / kQpb;
+    const int64_t ntiles = (a.nt + kBn - 1) / kBn;
+    const int64_t T = nqb * ntiles;
+    const int64_t G = a.grid_wgs;
+    const int64_t b = qg / kQpb;
+    const int64_t first_wg = ((b * ntiles + 1) * G + T - 1) / T - 1;
+    const int64_t last_wg = (((b + 1) * ntiles) * G + T - 1) / T - 1;
+    for (int64_t s = 1; s <= last_wg - first_wg; ++s) {
         float v = inf;
         uint32_t ix = kSentinelIdx;
         if (lane < k) {
-            const int64_t o = ((int64_t)s * a.nq + qg) * k + lane;
+            const int64_t o = (s * a.nq + qg) * k + lane;
             v = a.part_val[o];
             ix = a.part_idx[o];
         }
@@ -578,9 +597,8 @@ __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
 
 template <int NG, int ARM, bool COS, bool VEC4>
 hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
-    // 1-D grid: kXcds equal ranges of the strip-major work items
-    const int64_t per_xcd = ((int64_t)a.nstrips * nblocks + kXcds - 1) / kXcds;
-    dim3 grid((unsigned)(kXcds * per_xcd));
+    dim3 grid((unsigned)a.grid_wgs);
+    (void)nblocks;
     if (a.k == 1)
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true>), grid, dim3(256), 0, s, a);
     else
@@ -599,6 +617,19 @@ hipError_t launch_arm(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
 }
 
 }  // namespace
+
+void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots) {
+    const int64_t nqb = (nq + kQpb - 1) / kQpb;
+    const int64_t ntiles = (nt + kBn - 1) / kBn;
+    const int64_t T = nqb * ntiles;
+    // one resident round (two workgroups per CU), but at least 16 tiles each
+    int64_t G = 2 * (int64_t)(cus > 0 ? cus : 1);
+    if (G > T / 16) G = T / 16;
+    if (G < 1) G = 1;
+    *grid_wgs = G;
+    // a query block's ntiles units span at most ceil(ntiles*G/T) + 1 ranges
+    *nslots = (int)((ntiles * G + T - 1) / T + 1);
+}
 
 int gram_f32_max_k() { return kKcap; }
 int gram_f32_max_d() { return 128; }

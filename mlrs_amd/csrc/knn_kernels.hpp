@@ -34,14 +34,17 @@ struct GramArgs32 {
     const NormStats* stats;
     double eps_rel;    // Euclidean screen bound: eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
     double eps_abs;    // cosine screen bound (absolute)
-    int64_t rows_per_strip;
-    int nstrips;
-    float* part_val;   // [nstrips][nq][k] when nstrips > 1
+    int64_t grid_wgs;  // workgroups of the stream-K split (one resident round)
+    int nslots;        // list slots per query: most workgroups any query block is split over
+    float* part_val;   // [nslots][nq][k] exact lists, one per (segment, query)
     uint32_t* part_idx;
     float* out_val;    // [nq][k]
     uint32_t* out_idx;
     unsigned int* shared_r;  // [nq] best known exact k-th value per query (float bits), or null
 };
+
+// Workgroups and per-query list slots of the Gram kernel's stream-K split.
+void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
 
 // Three launches per search: prep (shared-bound reset), the Gram kernel, the
 // strip merge + output transform.
