@@ -359,10 +359,10 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     a.nslots = nslots;
     a.part_val = cv.take<float>(parts);
     a.part_idx = cv.take<uint32_t>(parts);
-    if (nslots > 1) a.shared_r = cv.take<unsigned int>(nq);
+    if (nslots > 1 || k > 1) a.shared_r = cv.take<unsigned int>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
-    e = launch_gram_f32_prep(a, s);
+    e = launch_gram_f32_prep(a, arm, s);
     if (e == hipSuccess) {
         KernelTimer timer(s, "knn_gram_f32_kernel");
         e = launch_gram_f32(a, arm, s);

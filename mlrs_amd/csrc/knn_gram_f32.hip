@@ -22,8 +22,12 @@
 //    can still enter the exact top-k always passes; the comparison is
 //    !(acc > thr), so NaN passes too.  For k = 1 the bound is tightened every
 //    tile with the tile's smallest expansion value.
-//  * Passing (query, row) pairs are queued in LDS.  When a query's queue is
-//    half full the wave evaluates the queued pairs EXACTLY, in the reference
+//  * For k > 1 the per-query bound starts from a prep launch: the k-th
+//    smallest exact value over an evenly spaced sample of index rows.
+//  * Passing (query, row) pairs are queued in LDS (queue lengths live in
+//    registers; a lane pair appends with a popcount prefix, no atomics).
+//    When a query's queue is half full the wave evaluates the queued pairs
+//    EXACTLY, in the reference
 //    arm's operation order, sorts them and merges them into the query's exact
 //    top-k list with the (value, index) order.  The lists live in global
 //    memory (one per query and strip): keeping only the queues in LDS (~70 KB
@@ -46,13 +50,15 @@ constexpr int kKcap = 64;                // largest k this kernel keeps
 constexpr int kQcap = 64;                // queued candidates per query
 constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
 constexpr int kShareEvery = 32;          // tiles between reads of the shared thresholds
-constexpr int kXcds = 8;                 // XCDs of an MI355X
+#ifndef MLRS_SEED_ROWS
+#define MLRS_SEED_ROWS 2048
+#endif
+constexpr int64_t kSeedRows = MLRS_SEED_ROWS;  // index rows sampled for the initial bound (k > 1)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct WaveLds {
     uint32_t qidx[kQpw][kQcap];
-    uint32_t cnt[kQpw];
     float thr[kQpw];
     float qa[kQpw];   // exact arm's query operand (row_sumsq for the fold arm)
     float qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
@@ -97,8 +103,8 @@ __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) 
 }
 
 // Exact value of one (query, row) pair in the arm's operation order, loads
-// issued four 16-byte chunks at a time.
-template <int ARM, bool VEC4>
+// issued U 16-byte chunks at a time.
+template <int ARM, bool VEC4, int U = 4>
 __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const float* __restrict__ y,
                                            int64_t d, float qa, float ya) {
     if (!VEC4) return exact_pair<float, ARM>(q, y, d, qa, ya);
@@ -107,7 +113,6 @@ __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const fl
     const int n4 = (int)(d >> 2);
     float acc = 0.0f;
     int c = 0;
-    constexpr int U = 4;
     for (; c + U <= n4; c += U) {
         float4 a[U], b[U];
 #pragma unroll
@@ -250,9 +255,9 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     if (t_end > nt) t_end = nt;
 
     // ---- per-query constants, lists, queues ----
+    uint32_t cntr = 0u;  // queued candidates of query jl
     if (lane < kQpw) {
         float qsq = qvalid ? QSQ[qmine] : 0.0f;
-        L.cnt[lane] = 0;
         L.thr[lane] = qvalid ? inf : -inf;
         if (!COS) {
             L.qs[lane] = qsq;
@@ -352,7 +357,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     do {                                                                                     \
         const int j_ = (J);                                                                  \
         const int64_t qg_ = qwave + j_;                                                      \
-        const uint32_t n_ = L.cnt[j_];                                                       \
+        const uint32_t n_ = shfl_u(cntr, j_);                                                \
         float lv_ = (lane < k) ? LV[qg_ * k + lane] : inf;                                   \
         uint32_t li_ = (lane < k) ? LI[qg_ * k + lane] : kSentinelIdx;                       \
         float e_ = inf;                                                                      \
@@ -378,16 +383,16 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
                 unsigned int old_ = atomicMin(&SHARED_R[qg_], __float_as_uint(R_));          \
                 R_ = fminf(R_, __uint_as_float(old_));                                       \
             }                                                                                \
-            L.cnt[j_] = 0;                                                                   \
             L.thr[j_] = fminf(L.thr[j_], screen_threshold<COS>(R_, L.qs[j_], L.eps[j_]));    \
         }                                                                                    \
+        if (jl == j_) cntr = 0u;                                                             \
     } while (0)
 
     // ---- k = 1: every queued pair of the wave evaluated in lane-parallel
     //      batches, kept with a 64-bit LDS atomicMin on (value, index) ----
 #define MLRS_FLUSH_K1()                                                                      \
     do {                                                                                     \
-        const uint32_t c_ = (lane < kQpw) ? L.cnt[lane] : 0u;                                \
+        const uint32_t c_ = (lane < kQpw) ? cntr : 0u;                                       \
         uint32_t incl_ = c_;                                                                 \
         _Pragma("unroll") for (int m_ = 1; m_ < kQpw; m_ <<= 1) {                            \
             const uint32_t o_ = (uint32_t)__shfl_up((int)incl_, m_, 64);                     \
@@ -409,8 +414,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
                     atomicMin(&L.best[j_], ((unsigned long long)__float_as_uint(v_) << 32) | t_); \
             }                                                                                \
         }                                                                                    \
+        cntr = 0u;                                                                           \
         if (lane < kQpw) {                                                                   \
-            L.cnt[lane] = 0u;                                                                \
             float R_ = __uint_as_float((uint32_t)(L.best[lane] >> 32));                      \
             if (SHARED_R && qvalid && R_ < inf) {                                            \
                 const unsigned int old_ = atomicMin(&SHARED_R[qmine], __float_as_uint(R_));  \
@@ -484,23 +489,33 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             if (m < inf) thr = fminf(thr, round_up_f((double)m + 2.0 * (double)L.eps[jl]));
         }
 
-        // ---- screen: lane holds rows 8*(r/4) + 4h + (r%4) of the tile, query jl ----
-        bool hit = false;
+        // ---- screen: lane (jl, h) holds rows 8*(r/4) + 4h + (r%4) of the tile
+        //      for query jl.  Passing rows are appended to the query's queue at
+        //      cntr (kept in registers, equal in lanes jl and jl + 32); the h = 1
+        //      lane writes after the h = 0 lane's entries. ----
+        uint32_t m = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) hit |= !(acc[r] > thr);
-        if (__builtin_amdgcn_ballot_w64(hit)) {
+        for (int r = 0; r < 16; ++r) m |= (uint32_t)!(acc[r] > thr) << r;
+        if (!qvalid) m = 0;
+        if (t0 + kBn > t_end) {  // partial tile: rows past the segment are not candidates
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t t = (uint32_t)t0 + (uint32_t)(8 * (r >> 2) + 4 * h + (r & 3));
-                if (qvalid && t < t_end32 && !(acc[r] > thr)) {
-                    uint32_t pos = atomicAdd(&L.cnt[jl], 1u);
-                    L.qidx[jl][pos] = t;
-                }
+            for (int r = 0; r < 16; ++r)
+                if ((uint32_t)t0 + (uint32_t)(8 * (r >> 2) + 4 * h + (r & 3)) >= t_end32) m &= ~(1u << r);
+        }
+        if (__builtin_amdgcn_ballot_w64(m != 0)) {
+            const uint32_t c = (uint32_t)__builtin_popcount(m);
+            const uint32_t co = shfl_xor_u(c, 32);
+            uint32_t pos = cntr + (h ? co : 0u);
+            const uint32_t tb = (uint32_t)t0 + 4u * (uint32_t)h;
+            while (m) {
+                const int r = __builtin_ctz(m);
+                m &= m - 1;
+                L.qidx[jl][pos++] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
             }
+            cntr += c + co;
         }
         // ---- flush queries whose queue could overflow on the next tile ----
-        bool need = (lane < kQpw) && (L.cnt[lane] > (uint32_t)kFlushAt);
-        uint64_t mask = __builtin_amdgcn_ballot_w64(need);
+        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > (uint32_t)kFlushAt);
         if (mask) {
             if (lane < kQpw) L.thr[lane] = fminf(L.thr[lane], thr);
             if (K1) {
@@ -526,8 +541,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
 
     // ---- final flush of every non-empty queue ----
     {
-        bool need = (lane < kQpw) && (L.cnt[lane] > 0u);
-        uint64_t mask = __builtin_amdgcn_ballot_w64(need);
+        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > 0u);
         if (K1) {
             if (mask) MLRS_FLUSH_K1();
         } else {
@@ -551,6 +565,38 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     u += tile1 - tile0;
     __syncthreads();  // LDS state and tile buffers are reused by the next segment
     }
+}
+
+// Initial per-query bound: the k-th smallest exact value over an evenly
+// spaced sample of index rows.  Any k distinct rows bound the final k-th
+// value from above, so the screen starts tight instead of at +inf.
+template <int ARM, bool VEC4>
+__global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t nsamp) {
+    const int lane = threadIdx.x & 63;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (qg >= a.nq) return;
+    const int64_t d = a.d;
+    const float inf = __builtin_huge_valf();
+    const float qa = (ARM == ARM_COS_FOLD) ? a.qsq[qg] : 0.0f;
+    float lv = inf;
+    uint32_t li = kSentinelIdx;
+    for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
+        const int64_t s = s0 + lane;
+        float e = inf;
+        uint32_t t = kSentinelIdx;
+        if (s < nsamp) {
+            t = (uint32_t)((s * a.nt) / nsamp);
+            const float ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f;
+            e = exact_f32<ARM, VEC4>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
+            if (e != e) {
+                e = inf;
+                t = kSentinelIdx;
+            }
+        }
+        wave_sort64<float>(e, t, lane);
+        wave_merge64<float>(lv, li, e, t, lane);
+    }
+    if (lane == a.k - 1) a.shared_r[qg] = __float_as_uint(lv);
 }
 
 // Merge the per-strip exact lists of one query per wave (the strip merge of
@@ -616,6 +662,13 @@ hipError_t launch_arm(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     return launch_ng<16, ARM, COS, VEC4>(a, nblocks, s);
 }
 
+template <int ARM, bool VEC4>
+hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
+    hipLaunchKernelGGL((knn_seed_f32_kernel<ARM, VEC4>), dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a,
+                       nsamp);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots) {
@@ -636,11 +689,22 @@ int gram_f32_max_d() { return 128; }
 int gram_f32_queries_per_block() { return kQpb; }
 int gram_f32_rows_per_tile() { return kBn; }
 
-hipError_t launch_gram_f32_prep(const GramArgs32& a, hipStream_t s) {
-    if (a.shared_r) {
-        hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s,
-                           a.shared_r, a.nq);
+hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
+    if (!a.shared_r) return hipSuccess;
+    if (a.k > 1 && kSeedRows > 0) {
+        const int64_t nsamp = a.nt < kSeedRows ? a.nt : kSeedRows;
+        const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                          ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+        if (arm == ARM_EUCLID_FMA)
+            return vec4 ? launch_seed<ARM_EUCLID_FMA, true>(a, nsamp, s) : launch_seed<ARM_EUCLID_FMA, false>(a, nsamp, s);
+        if (arm == ARM_EUCLID_MULADD)
+            return vec4 ? launch_seed<ARM_EUCLID_MULADD, true>(a, nsamp, s)
+                        : launch_seed<ARM_EUCLID_MULADD, false>(a, nsamp, s);
+        if (arm == ARM_COS_FOLD)
+            return vec4 ? launch_seed<ARM_COS_FOLD, true>(a, nsamp, s) : launch_seed<ARM_COS_FOLD, false>(a, nsamp, s);
+        return hipErrorInvalidValue;
     }
+    hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r, a.nq);
     return hipGetLastError();
 }
 

@@ -46,9 +46,10 @@ struct GramArgs32 {
 // Workgroups and per-query list slots of the Gram kernel's stream-K split.
 void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
 
-// Three launches per search: prep (shared-bound reset), the Gram kernel, the
-// strip merge + output transform.
-hipError_t launch_gram_f32_prep(const GramArgs32& a, hipStream_t s);
+// Three launches per search: prep (the shared per-query bound: seeded from a
+// row sample for k > 1, else reset), the Gram kernel, the strip merge +
+// output transform.
+hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s);
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
 hipError_t launch_gram_f32_merge(const GramArgs32& a, hipStream_t s);
 int gram_f32_max_k();
