@@ -372,6 +372,76 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     return ok();
 }
 
+int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, int64_t d, int k, int arm,
+                   int mode, double* out_v, uint32_t* out_i, hipStream_t s) {
+    const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
+    size_t fixed = 2 * aligned_bytes(sizeof(double) * nq) + 3 * aligned_bytes(sizeof(double) * nt) +
+                   aligned_bytes(sizeof(NormStats)) + 1024;
+    char* ws;
+    int cus;
+    int32_t rc = workspace(fixed, s, &ws, &cus);
+    if (rc) return rc;
+    int64_t grid_wgs = 1;
+    int nslots = 1;
+    gram_f64_split(nq, nt, cus, &grid_wgs, &nslots);
+    size_t parts = (size_t)nslots * nq * k;
+    size_t bytes = fixed + aligned_bytes(parts * sizeof(double)) + aligned_bytes(parts * sizeof(uint32_t)) +
+                   aligned_bytes(sizeof(unsigned long long) * nq);
+    rc = workspace(bytes, s, &ws, &cus);
+    if (rc) return rc;
+    Carver cv(ws);
+    GramArgs64 a;
+    std::memset(&a, 0, sizeof(a));
+    double* qsq = cv.take<double>(nq);
+    double* qinv = cv.take<double>(nq);
+    double* xsq = cv.take<double>(nt);
+    double* xinv = cv.take<double>(nt);
+    double* xscale = cv.take<double>(nt);
+    NormStats* stats = cv.take<NormStats>(1);
+    hipError_t e = launch_row_norms<double>(xq, nq, d, qsq, qinv, nullptr, nullptr, s);
+    if (e == hipSuccess) e = launch_row_norms<double>(xt, nt, d, xsq, xinv, xscale, stats, s);
+    if (e != hipSuccess) return hip_err(e, "row_norms");
+    a.q = xq;
+    a.nq = nq;
+    a.x = xt;
+    a.nt = nt;
+    a.d = d;
+    a.k = k;
+    a.mode = mode;
+    a.qsq = qsq;
+    a.xsq = xsq;
+    a.qinv = qinv;
+    a.xinv = xinv;
+    a.xscale = xscale;
+    a.stats = stats;
+    // Screen bounds as for f32 with u = 2^-52, plus 16u (Euclidean, relative)
+    // and 16u (cosine, absolute) for the rounding of the threshold arithmetic
+    // itself, which the f64 kernel does in double.
+    const double u = std::ldexp(1.0, -52);
+    if (!cos) {
+        a.eps_rel = (8.0 * (double)(d + 4) + 16.0) * u;
+        a.eps_abs = (double)(d + 4) * std::ldexp(1.0, -1000);
+    } else {
+        a.eps_rel = 0.0;
+        a.eps_abs = (8.0 * (double)d + 48.0) * u;
+    }
+    a.grid_wgs = grid_wgs;
+    a.nslots = nslots;
+    a.part_val = cv.take<double>(parts);
+    a.part_idx = cv.take<uint32_t>(parts);
+    a.shared_r = cv.take<unsigned long long>(nq);
+    a.out_val = out_v;
+    a.out_idx = out_i;
+    e = launch_gram_f64_prep(a, s);
+    if (e == hipSuccess) {
+        KernelTimer timer(s, "knn_gram_f64_kernel");
+        e = launch_gram_f64(a, arm, s);
+    }
+    if (e == hipSuccess) e = launch_gram_f64_merge(a, s);
+    if (e != hipSuccess) return hip_err(e, "knn_gram_f64");
+    return ok();
+}
+
 int32_t knn_lowd32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
                    int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
     char* ws;
@@ -496,6 +566,8 @@ int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int
     hipStream_t s = (hipStream_t)stream;
     const int arm = knn_arm(n_features, k, metric);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
+    if (n_features <= gram_f64_max_d() && k <= gram_f64_max_k())
+        return knn_gram64(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     return knn_generic<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
 }
 
@@ -539,6 +611,9 @@ int32_t mlrs_kmeans_assign_f64(const double* x, int64_t x_len, int64_t n, int64_
     int32_t rc = validate_kmeans<double>(x, x_len, n, n_features, centers, centers_len, n_centers, labels,
                                          labels_len, sqdist, dist_len);
     if (rc) return rc;
+    if (n_features <= gram_f64_max_d())
+        return knn_gram64(x, n, centers, n_centers, n_features, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, sqdist, labels,
+                          (hipStream_t)stream);
     return kmeans_generic<double>(x, n, centers, n_centers, n_features, labels, sqdist, (hipStream_t)stream);
 }
 

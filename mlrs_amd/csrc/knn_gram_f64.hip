@@ -1,0 +1,502 @@
+// Fused f64 Gram-MFMA kNN with exact rescoring (gfx950).
+//
+// The f64 counterpart of knn_gram_f32.hip: serves every cpu arm
+// (direct / metric / knn_host, Euclidean and cosine) for d <= 256, k <= 64,
+// replacing the materialized-matrix paths tiled_distance_topk /
+// tiled_metric_distance_topk (crates/mlrs-algos/src/neighbors/nearest.rs:
+// 1058-1512) and the host scan of knn_host_topk (crates/mlrs-backend/src/
+// prims/knn_host.rs:418-851) for f64.
+//
+// Shape of one workgroup: 4 waves x 16 queries = 64 queries, walking one
+// segment of index rows 16 at a time with v_mfma_f64_16x16x4f64.
+//  * Lane l of a wave owns query l%16 and lane group g = l/16.  The K
+//    dimension is split into four contiguous quarters of NS columns: at
+//    k-step s, group g supplies column g*NS + s of both operands, so each
+//    lane's A operand is a contiguous run of its tile row (ds_read_b128
+//    feeds two k-steps) and its B operand (the query, pre-scaled by -2 for
+//    Euclidean) is held in VGPRs for the whole segment.
+//  * The MFMA result layout is D[l/16 + 4r][l%16], r = 0..3: lane l scores
+//    tile rows g, g+4, g+8, g+12 against its query.
+//  * The screen, the per-query queues, the exact rescoring in the reference
+//    arm's operation order, the (value, index) lists and the stream-K split
+//    with a shared per-query bound are those of the f32 kernel, in double.
+// The thresholds are computed in double with a margin for their own
+// rounding folded into the error bound (the f32 kernel rounds up in double
+// instead).
+#include "knn_common.hpp"
+#include "knn_kernels.hpp"
+
+namespace mlrs {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kQpw = 16;               // queries per wave (MFMA N dimension)
+constexpr int kQpb = kWaves * kQpw;    // queries per workgroup
+constexpr int kBn = 16;                // index rows per tile (MFMA M dimension)
+constexpr int kKcap = 64;              // largest k kept
+constexpr int kQcap = 32;              // queued candidates per query
+constexpr int kFlushAt = kQcap - kBn;  // flush when a queue may overflow on the next tile
+constexpr int kShareEvery = 32;        // tiles between reads of the shared bound
+constexpr int kMaxD = 256;
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+struct WaveLds64 {
+    uint32_t qidx[kQpw][kQcap];
+    double thr[kQpw];
+    double qa[kQpw];   // exact arm's query operand (squared or reciprocal norm)
+    double qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
+    double eps[kQpw];  // screen error bound
+};
+
+constexpr unsigned long long kInfBits64 = 0x7FF0000000000000ull;
+
+template <bool COS>
+__device__ __forceinline__ double screen_threshold64(double R, double qs, double eps) {
+    const double inf = __builtin_huge_val();
+    if (!(R < inf)) return inf;
+    if (!COS) return (R - qs) + eps;
+    if (qs == 0.0) return inf;  // a zero query ties every row: never screened
+    return ((R + eps) - 1.0) * qs;
+}
+
+// Exact value of one (query, row) pair in the arm's operation order; loads
+// issued two 16-byte pairs at a time when rows are 16-byte aligned.
+template <int ARM, bool VEC2>
+__device__ __forceinline__ double exact_f64(const double* __restrict__ q, const double* __restrict__ y,
+                                            int64_t d, double qa, double ya) {
+    if (!VEC2) return exact_pair<double, ARM>(q, y, d, qa, ya);
+    const double2* q2 = reinterpret_cast<const double2*>(q);
+    const double2* y2 = reinterpret_cast<const double2*>(y);
+    const int n2 = (int)(d >> 1);
+    double acc = 0.0;
+    constexpr int U = 2;
+    int c = 0;
+    for (; c < n2; c += U) {
+        double2 a[U], b[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c + u < n2) {
+                a[u] = q2[c + u];
+                b[u] = y2[c + u];
+            } else {
+                a[u] = make_double2(0.0, 0.0);
+                b[u] = make_double2(0.0, 0.0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c + u >= n2) break;
+            const double e0a = a[u].x, e1a = a[u].y, e0b = b[u].x, e1b = b[u].y;
+            if (ARM == ARM_EUCLID_FMA) {
+                const double d0 = e0a - e0b, d1 = e1a - e1b;
+                acc = __builtin_fma(d0, d0, acc);
+                acc = __builtin_fma(d1, d1, acc);
+            } else if (ARM == ARM_EUCLID_MULADD) {
+                const double d0 = e0a - e0b, d1 = e1a - e1b;
+                acc = acc + d0 * d0;
+                acc = acc + d1 * d1;
+            } else if (ARM == ARM_COS_FOLD) {
+                acc = __builtin_fma(e0a, e0b, acc);
+                acc = __builtin_fma(e1a, e1b, acc);
+            } else {  // ARM_COS_HOST: mul + add
+                acc = acc + e0a * e0b;
+                acc = acc + e1a * e1b;
+            }
+        }
+    }
+    if (ARM == ARM_COS_FOLD) {
+        const double denom = __builtin_sqrt(qa * ya);
+        const double sim = (denom > 0.0) ? acc / denom : 0.0;
+        return clamp02<double>(1.0 - sim);
+    }
+    if (ARM == ARM_COS_HOST) return clamp02<double>(1.0 - acc * qa * ya);
+    return acc;
+}
+
+template <int NS, int ARM, bool COS, bool VEC2>
+__global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
+    constexpr int DP = 4 * NS;             // padded feature count
+    constexpr int STRIDE = DP + 2;         // LDS row stride (doubles): rows 16 bytes apart in the banks
+    constexpr int CPT = DP / 2;            // 16-byte column pairs per tile row
+    constexpr int RPG = 256 / CPT;         // tile rows one pass of the workgroup loads
+    constexpr int PF = kBn / RPG;          // passes per tile
+    static_assert(RPG >= 1 && kBn % RPG == 0, "tile fill shape");
+
+    __shared__ __attribute__((aligned(16))) double tile[2][kBn][STRIDE];
+    __shared__ __attribute__((aligned(16))) double tnorm[2][kBn];
+    __shared__ WaveLds64 wl[kWaves];
+
+    const double* __restrict__ Q = a.q;
+    const double* __restrict__ X = a.x;
+    const double* __restrict__ QSQ = a.qsq;
+    const double* __restrict__ XSQ = a.xsq;
+    const double* __restrict__ QINV = a.qinv;
+    const double* __restrict__ XINV = a.xinv;
+    const double* __restrict__ XSCALE = a.xscale;
+    unsigned long long* __restrict__ SHARED_R = a.shared_r;
+    const int64_t nq = a.nq, nt = a.nt, d = a.d;
+    const int k = a.k;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int g = lane >> 4;   // lane group: K quarter / first tile row of the lane
+    const int jl = lane & 15;  // query of the lane within the wave
+    WaveLds64& L = wl[w];
+    const double inf = __builtin_huge_val();
+
+    // ---- stream-K split over (query block, tile) units, as in the f32 kernel ----
+    const int64_t nqb = (nq + kQpb - 1) / kQpb;
+    const int64_t ntiles = (nt + kBn - 1) / kBn;
+    const int64_t T = nqb * ntiles;
+    const int64_t G = gridDim.x;
+    const int64_t wg = blockIdx.x;
+    const int64_t u_hi = ((wg + 1) * T) / G;
+    for (int64_t u = (wg * T) / G; u < u_hi;) {
+    const int64_t qblock = u / ntiles;
+    const int64_t tile0 = u % ntiles;
+    const int64_t tile1 = (ntiles - tile0 < u_hi - u) ? ntiles : tile0 + (u_hi - u);
+    const int64_t first_wg = ((qblock * ntiles + 1) * G + T - 1) / T - 1;
+    const int64_t slot = wg - first_wg;
+    double* __restrict__ LV = a.part_val + slot * nq * k;
+    uint32_t* __restrict__ LI = a.part_idx + slot * nq * k;
+
+    const int64_t qwave = qblock * kQpb + w * kQpw;
+    const int64_t qmine = qwave + jl;
+    const bool qvalid = qmine < nq;
+    const int64_t t_begin = tile0 * kBn;
+    int64_t t_end = tile1 * kBn;
+    if (t_end > nt) t_end = nt;
+    const uint32_t t_end32 = (uint32_t)t_end;
+
+    uint32_t cntr = 0u;  // queued candidates of query jl (equal in the four lanes of the query)
+    if (lane < kQpw) {
+        const double qsq = qvalid ? QSQ[qmine] : 0.0;
+        L.thr[lane] = qvalid ? inf : -inf;
+        if (!COS) {
+            L.qs[lane] = qsq;
+            L.qa[lane] = 0.0;
+            L.eps[lane] = a.eps_rel * (qsq + a.stats->xsq_max64) + a.eps_abs;
+        } else {
+            L.qs[lane] = __builtin_sqrt(qsq);
+            L.qa[lane] = (ARM == ARM_COS_HOST) ? (qvalid ? QINV[qmine] : 0.0) : qsq;
+            L.eps[lane] = a.eps_abs;
+        }
+    }
+    for (int j = 0; j < kQpw; ++j) {
+        const int64_t qg = qwave + j;
+        if (qg < nq && lane < k) {
+            LV[qg * k + lane] = inf;
+            LI[qg * k + lane] = kSentinelIdx;
+        }
+    }
+    if (SHARED_R && lane < kQpw && qvalid) {
+        const double R0 = __longlong_as_double((long long)SHARED_R[qmine]);
+        L.thr[lane] = fmin(L.thr[lane], screen_threshold64<COS>(R0, L.qs[lane], L.eps[lane]));
+    }
+
+    // ---- query operand: qreg[s] = scale * q[g*NS + s] ----
+    double qreg[NS];
+    {
+        const double scale = COS ? 1.0 : -2.0;
+        const double* qp = Q + qmine * d;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int64_t c = (int64_t)g * NS + s;
+            qreg[s] = (qvalid && c < d) ? qp[c] * scale : 0.0;
+        }
+    }
+
+    // ---- tile prefetch into registers.  Thread tid owns column pair c2 =
+    //      tid % CPT of rows r0 + RPG*p (r0 = tid / CPT), p < PF: one walking
+    //      row pointer, constant row and LDS offsets. ----
+    const int pc2 = tid % CPT;
+    const int pr0 = tid / CPT;
+    const bool pon = (pr0 < RPG) && (2 * pc2 < d);
+    const double* pfp = X + (t_begin + pr0) * d + 2 * pc2;
+    const int64_t prow = (int64_t)RPG * d;  // elements between a thread's rows
+    double2 pf[PF];
+    double pfn = 0.0;
+#define MLRS_PREFETCH64(T0)                                                                  \
+    do {                                                                                     \
+        const uint32_t t0_ = (uint32_t)(T0);                                                 \
+        _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
+            double2 v = make_double2(0.0, 0.0);                                              \
+            const uint32_t t = t0_ + (uint32_t)(pr0 + RPG * p);                              \
+            if (pon && t < t_end32) {                                                        \
+                const double* src = pfp + p * prow;                                          \
+                if (VEC2) {                                                                  \
+                    v = *reinterpret_cast<const double2*>(src);                              \
+                } else {                                                                     \
+                    v.x = src[0];                                                            \
+                    v.y = (2 * pc2 + 1 < d) ? src[1] : 0.0;                                  \
+                }                                                                            \
+                if (COS) {                                                                   \
+                    const double s_ = XSCALE[t];                                             \
+                    v.x *= s_;                                                               \
+                    v.y *= s_;                                                               \
+                }                                                                            \
+            }                                                                                \
+            pf[p] = v;                                                                       \
+        }                                                                                    \
+        pfp += kBn * d;                                                                      \
+        if (!COS && tid < kBn) {                                                             \
+            const uint32_t t = t0_ + (uint32_t)tid;                                          \
+            pfn = (t < t_end32) ? XSQ[t] : inf;                                              \
+        }                                                                                    \
+    } while (0)
+
+#define MLRS_FLUSH64(J)                                                                      \
+    do {                                                                                     \
+        const int j_ = (J);                                                                  \
+        const int64_t qg_ = qwave + j_;                                                      \
+        const uint32_t n_ = shfl_u(cntr, j_);                                                \
+        double lv_ = (lane < k) ? LV[qg_ * k + lane] : inf;                                  \
+        uint32_t li_ = (lane < k) ? LI[qg_ * k + lane] : kSentinelIdx;                       \
+        double e_ = inf;                                                                     \
+        uint32_t t_ = kSentinelIdx;                                                          \
+        if ((uint32_t)lane < n_) {                                                           \
+            t_ = L.qidx[j_][lane];                                                           \
+            const double ya_ = (ARM == ARM_COS_FOLD) ? XSQ[t_] : (ARM == ARM_COS_HOST) ? XINV[t_] : 0.0; \
+            e_ = exact_f64<ARM, VEC2>(Q + qg_ * d, X + (int64_t)t_ * d, d, L.qa[j_], ya_);  \
+            if (e_ != e_) {                                                                  \
+                e_ = inf;                                                                    \
+                t_ = kSentinelIdx;                                                           \
+            }                                                                                \
+        }                                                                                    \
+        wave_sort64<double>(e_, t_, lane);                                                   \
+        wave_merge64<double>(lv_, li_, e_, t_, lane);                                        \
+        if (lane < k) {                                                                      \
+            LV[qg_ * k + lane] = lv_;                                                        \
+            LI[qg_ * k + lane] = li_;                                                        \
+        }                                                                                    \
+        double R_ = shfl_f(lv_, k - 1);                                                      \
+        if (lane == 0) {                                                                     \
+            if (SHARED_R && R_ < inf && R_ >= 0.0) {                                         \
+                const unsigned long long old_ =                                              \
+                    atomicMin(&SHARED_R[qg_], (unsigned long long)__double_as_longlong(R_)); \
+                R_ = fmin(R_, __longlong_as_double((long long)old_));                        \
+            }                                                                                \
+            L.thr[j_] = fmin(L.thr[j_], screen_threshold64<COS>(R_, L.qs[j_], L.eps[j_]));   \
+        }                                                                                    \
+        if (jl == j_) cntr = 0u;                                                             \
+    } while (0)
+
+#define MLRS_STORE64(B)                                                                      \
+    do {                                                                                     \
+        if (pr0 < RPG) {                                                                     \
+            double* dst_ = &tile[(B)][pr0][2 * pc2];                                         \
+            _Pragma("unroll") for (int p = 0; p < PF; ++p)                                   \
+                *reinterpret_cast<double2*>(dst_ + p * RPG * STRIDE) = pf[p];                \
+        }                                                                                    \
+        if (!COS && tid < kBn) tnorm[(B)][tid] = pfn;                                        \
+    } while (0)
+
+    // The next tile is loaded into registers before this tile's MFMAs and
+    // stored into the other LDS buffer right after them, so the prefetch
+    // registers are free again during the screen and the rescoring.
+    if (t_begin < t_end) {
+        MLRS_PREFETCH64(t_begin);
+        MLRS_STORE64(0);
+    }
+
+    double thr = L.thr[jl];
+    int buf = 0;
+    int tiles = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, buf ^= 1) {
+        __syncthreads();  // tile[buf] written; every wave is done with tile[buf ^ 1]
+        const bool more = t0 + kBn < t_end;
+        if (more) MLRS_PREFETCH64(t0 + kBn);
+
+        f64x4 acc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = COS ? 0.0 : tnorm[buf][g + 4 * r];
+        // A operand: this lane's tile row jl, columns g*NS + s; one 16-byte
+        // read feeds two k-steps, the next pair is read one step ahead.
+        const double* arow = &tile[buf][jl][g * NS];
+        double2 av = *reinterpret_cast<const double2*>(arow);
+#pragma unroll
+        for (int p = 0; p < NS / 2; ++p) {
+            double2 an = av;
+            if (p + 1 < NS / 2) an = *reinterpret_cast<const double2*>(arow + 2 * (p + 1));
+            __builtin_amdgcn_sched_barrier(0);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av.x, qreg[2 * p], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av.y, qreg[2 * p + 1], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            av = an;
+        }
+        if (more) MLRS_STORE64(buf ^ 1);
+
+        // ---- screen: lane holds tile rows g + 4r for query jl ----
+        uint32_t m = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m |= (uint32_t)!(acc[r] > thr) << r;
+        if (!qvalid) m = 0;
+        if (t0 + kBn > t_end) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if ((uint32_t)t0 + (uint32_t)(g + 4 * r) >= t_end32) m &= ~(1u << r);
+        }
+        if (__builtin_amdgcn_ballot_w64(m != 0)) {
+            // the query's four lanes (groups 0..3) append in group order
+            const uint32_t c = (uint32_t)__builtin_popcount(m);
+            const uint32_t c0 = shfl_u(c, jl), c1 = shfl_u(c, jl + 16), c2 = shfl_u(c, jl + 32),
+                           c3 = shfl_u(c, jl + 48);
+            uint32_t pos = cntr + (g > 0 ? c0 : 0u) + (g > 1 ? c1 : 0u) + (g > 2 ? c2 : 0u);
+            while (m) {
+                const int r = __builtin_ctz(m);
+                m &= m - 1;
+                L.qidx[jl][pos++] = (uint32_t)t0 + (uint32_t)(g + 4 * r);
+            }
+            cntr += c0 + c1 + c2 + c3;
+        }
+        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > (uint32_t)kFlushAt);
+        if (mask) {
+            if (lane < kQpw) L.thr[lane] = fmin(L.thr[lane], thr);
+            while (mask) {
+                const int j = __builtin_ctzll(mask);
+                mask &= mask - 1;
+                MLRS_FLUSH64(j);
+            }
+            thr = L.thr[jl];
+        }
+        if (SHARED_R && (++tiles % kShareEvery) == 0) {
+            if (lane < kQpw && qvalid) {
+                const double R = __longlong_as_double((long long)SHARED_R[qmine]);
+                L.thr[lane] = fmin(fmin(L.thr[lane], thr), screen_threshold64<COS>(R, L.qs[lane], L.eps[lane]));
+            }
+            thr = L.thr[jl];
+        }
+    }
+    {
+        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > 0u);
+        while (mask) {
+            const int j = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            MLRS_FLUSH64(j);
+        }
+    }
+#undef MLRS_FLUSH64
+#undef MLRS_STORE64
+#undef MLRS_PREFETCH64
+    u += tile1 - tile0;
+    __syncthreads();  // LDS state and tile buffers are reused by the next segment
+    }
+}
+
+// Merge the per-segment exact lists of one query per wave and emit the output
+// transform (boundary sqrt, identity, or the k-means pair with the centre-0
+// NaN rule of argmin_dist_rows, crates/mlrs-kernels/src/kmeans.rs:284-310).
+__global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (qg >= a.nq) return;
+    const int k = a.k;
+    const double inf = __builtin_huge_val();
+    double lv = inf;
+    uint32_t li = kSentinelIdx;
+    if (lane < k) {
+        lv = a.part_val[qg * k + lane];
+        li = a.part_idx[qg * k + lane];
+    }
+    const int64_t nqb = (a.nq + kQpb - 1) / kQpb;
+    const int64_t ntiles = (a.nt + kBn - 1) / kBn;
+    const int64_t T = nqb * ntiles;
+    const int64_t G = a.grid_wgs;
+    const int64_t b = qg / kQpb;
+    const int64_t first_wg = ((b * ntiles + 1) * G + T - 1) / T - 1;
+    const int64_t last_wg = (((b + 1) * ntiles) * G + T - 1) / T - 1;
+    for (int64_t s = 1; s <= last_wg - first_wg; ++s) {
+        double v = inf;
+        uint32_t ix = kSentinelIdx;
+        if (lane < k) {
+            const int64_t o = (s * a.nq + qg) * k + lane;
+            v = a.part_val[o];
+            ix = a.part_idx[o];
+        }
+        wave_merge64<double>(lv, li, v, ix, lane);
+    }
+    if (lane < k) {
+        const int64_t o = qg * k + lane;
+        if (a.mode == EMIT_KMEANS) {
+            if (!(a.qsq[qg] < inf) || !(a.xsq[0] < inf)) {
+                const double e0 = exact_pair<double, ARM_EUCLID_MULADD>(a.q + qg * a.d, a.x, a.d, 0.0, 0.0);
+                if (e0 != e0) {
+                    lv = e0;
+                    li = 0;
+                }
+            }
+            a.out_val[o] = lv;
+        } else {
+            a.out_val[o] = (a.mode == EMIT_SQRT) ? __builtin_sqrt(lv) : lv;
+        }
+        a.out_idx[o] = (li == kSentinelIdx) ? 0u : li;
+    }
+}
+
+__global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+template <int NS, int ARM, bool COS>
+hipError_t launch_ns(const GramArgs64& a, bool vec2, hipStream_t s) {
+    dim3 grid((unsigned)a.grid_wgs);
+    if (vec2)
+        hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, false>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int ARM, bool COS>
+hipError_t launch_arm64(const GramArgs64& a, bool vec2, hipStream_t s) {
+    // k-steps per lane group, even (one 16-byte LDS read feeds two)
+    const int64_t ns = ((a.d + 3) / 4 + 1) / 2 * 2;
+    if (ns <= 8) return launch_ns<8, ARM, COS>(a, vec2, s);
+    if (ns <= 16) return launch_ns<16, ARM, COS>(a, vec2, s);
+    if (ns <= 32) return launch_ns<32, ARM, COS>(a, vec2, s);
+    if (ns <= 48) return launch_ns<48, ARM, COS>(a, vec2, s);
+    return launch_ns<64, ARM, COS>(a, vec2, s);
+}
+
+}  // namespace
+
+void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots) {
+    const int64_t nqb = (nq + kQpb - 1) / kQpb;
+    const int64_t ntiles = (nt + kBn - 1) / kBn;
+    const int64_t T = nqb * ntiles;
+    int64_t G = 2 * (int64_t)(cus > 0 ? cus : 1);
+    if (G > T / 16) G = T / 16;
+    if (G < 1) G = 1;
+    *grid_wgs = G;
+    *nslots = (int)((ntiles * G + T - 1) / T + 1);
+}
+
+int gram_f64_max_k() { return kKcap; }
+int gram_f64_max_d() { return kMaxD; }
+
+hipError_t launch_gram_f64_prep(const GramArgs64& a, hipStream_t s) {
+    if (!a.shared_r) return hipSuccess;
+    hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r, a.nq,
+                       kInfBits64);
+    return hipGetLastError();
+}
+
+hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s) {
+    const bool vec2 = (a.d % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    if (arm == ARM_EUCLID_FMA) return launch_arm64<ARM_EUCLID_FMA, false>(a, vec2, s);
+    if (arm == ARM_EUCLID_MULADD) return launch_arm64<ARM_EUCLID_MULADD, false>(a, vec2, s);
+    if (arm == ARM_COS_FOLD) return launch_arm64<ARM_COS_FOLD, true>(a, vec2, s);
+    if (arm == ARM_COS_HOST) return launch_arm64<ARM_COS_HOST, true>(a, vec2, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gram_f64_merge(const GramArgs64& a, hipStream_t s) {
+    hipLaunchKernelGGL(knn_merge_f64_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace mlrs

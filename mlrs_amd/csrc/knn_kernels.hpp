@@ -57,6 +57,38 @@ int gram_f32_max_d();
 int gram_f32_queries_per_block();
 int gram_f32_rows_per_tile();
 
+struct GramArgs64 {
+    const double* q;
+    int64_t nq;
+    const double* x;
+    int64_t nt;
+    int64_t d;
+    int k;
+    int mode;             // EmitMode
+    const double* qsq;    // query row_sumsq
+    const double* xsq;    // index row_sumsq
+    const double* qinv;   // knn_host cosine: query reciprocal norms
+    const double* xinv;   // knn_host cosine: index reciprocal norms
+    const double* xscale; // cosine: -1/||x_t|| (0 for zero rows)
+    const NormStats* stats;
+    double eps_rel;       // Euclidean screen bound: eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
+    double eps_abs;       // cosine screen bound (absolute)
+    int64_t grid_wgs;
+    int nslots;
+    double* part_val;     // [nslots][nq][k]
+    uint32_t* part_idx;
+    double* out_val;      // [nq][k]
+    uint32_t* out_idx;
+    unsigned long long* shared_r;  // [nq] best known exact k-th value per query (double bits)
+};
+
+void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
+hipError_t launch_gram_f64_prep(const GramArgs64& a, hipStream_t s);
+hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s);
+hipError_t launch_gram_f64_merge(const GramArgs64& a, hipStream_t s);
+int gram_f64_max_k();
+int gram_f64_max_d();
+
 // Row norms: sq[r] = row_sumsq (separate multiply/add, ascending column),
 // optional inv[r] = (sq > 0) ? 1/sqrt(sq) : 0 and optional neg-inverse scale.
 template <typename T>

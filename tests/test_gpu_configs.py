@@ -7,8 +7,9 @@ subsets; the engine then answers the WHOLE query set and
 * the golden subset (CPU-oracle answers against the full index, written by
   tests/golden/gen_golden.py) must match bit for bit, and
 * every row must satisfy the size-independent properties of the reference's
-  output contract: ascending (value, index) order, indices in range and
-  distinct per row, finite values; self-kNN rows start at distance 0; k-means
+  output contract: ascending values (index order on equal cosine values),
+  indices in range and distinct per row, finite values; self-kNN rows start
+  at distance 0; k-means
   labels in range with the label's squared distance the row minimum over a
   sampled recomputation.
 """
@@ -29,18 +30,23 @@ pytestmark = pytest.mark.gpu
 
 
 def _fingerprint_ok(z, key, arr):
+    # a drift detector for the generator: the float64 dot products behind the
+    # fingerprint may sum in another order on another host's BLAS
     from gen_golden import fingerprint
-    np.testing.assert_array_equal(fingerprint(arr), z[key])
+    np.testing.assert_allclose(fingerprint(arr), z[key], rtol=1e-12, atol=0)
 
 
-def _row_properties(dist, idx, n_index):
+def _row_properties(dist, idx, n_index, ordered_by_output):
     assert np.all(np.isfinite(dist))
     assert np.all((idx >= 0) & (idx < n_index))
-    # ascending by (value, index)
     dv = np.diff(dist, axis=1)
     assert np.all(dv >= 0)
-    ties = dv == 0
-    assert np.all(np.diff(idx, axis=1)[ties] > 0)
+    if ordered_by_output:
+        # cosine emits the selected values themselves: equal values are in index
+        # order.  (Euclidean rows are ordered by the squared values; two of those
+        # can share one rounded root, so there the root ties carry no order.)
+        ties = dv == 0
+        assert np.all(np.diff(idx, axis=1)[ties] > 0)
     # distinct neighbours per row
     s = np.sort(idx, axis=1)
     assert np.all(np.diff(s, axis=1) != 0)
@@ -63,7 +69,7 @@ def test_config_knn_full_size(cfg):
     sub = z["subset"]
     np.testing.assert_array_equal(idx[sub], z["idx"].astype(np.int64))
     np.testing.assert_array_equal(dist[sub], z["dist"])
-    _row_properties(dist, idx, b.shape[0])
+    _row_properties(dist, idx, b.shape[0], c["metric"] == "cosine")
     if cfg == "c4":  # self-kNN: every point finds itself (or an exact duplicate) at distance 0
         assert np.all(dist[:, 0] == 0)
 

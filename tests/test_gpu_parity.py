@@ -76,8 +76,15 @@ def test_f32_cosine_bitwise(case):
     check_knn(xq, xt, k, "cosine", str(case))
 
 
-@pytest.mark.parametrize("case,metric", [((100, 2000, 64, 10), "euclidean"), ((50, 1000, 3, 8), "euclidean"),
-                                         ((64, 2000, 256, 16), "cosine"), ((40, 700, 20, 5), "cosine")])
+# f64: Gram-MFMA path for d <= 256, k <= 64 (direct, metric and knn_host arms),
+# generic exact path beyond
+F64 = [((100, 2000, 64, 10), "euclidean"), ((50, 1000, 3, 8), "euclidean"), ((64, 2000, 256, 16), "cosine"),
+       ((40, 700, 20, 5), "cosine"), ((300, 30000, 256, 16), "cosine"), ((200, 5000, 200, 12), "euclidean"),
+       ((77, 3000, 129, 64), "euclidean"), ((65, 2500, 33, 1), "cosine"), ((129, 4000, 128, 40), "cosine"),
+       ((10, 400, 300, 7), "euclidean"), ((33, 900, 255, 3), "cosine"), ((1, 17, 17, 17), "euclidean")]
+
+
+@pytest.mark.parametrize("case,metric", F64)
 def test_f64_bitwise(case, metric):
     nq, nt, d, k = case
     rng = np.random.default_rng(300 + d)
@@ -128,6 +135,33 @@ def test_cosine_zero_rows():
     check_knn(xq, xt, 10, "cosine", "zero rows")
 
 
+@pytest.mark.parametrize("d", [5, 200])
+def test_f64_nan_zero_rows_and_ties(d):
+    rng = np.random.default_rng(15 + d)
+    xt = rng.integers(-2, 3, size=(3000, d)).astype(np.float64)
+    xq = rng.integers(-2, 3, size=(150, d)).astype(np.float64)
+    xt[[4, 1500]] = np.nan
+    xt[[9, 2999]] = 0.0
+    xq[[1, 77]] = 0.0
+    xq[5] = np.nan
+    xt[100:140] = xt[3]                   # duplicates around the k-th slot
+    xq[10] = xt[3]
+    check_knn(xq, xt, 24, "euclidean", "f64 ties/nan")
+    check_knn(xq, xt, 24, "cosine", "f64 cosine ties/nan/zero")
+
+
+def test_f64_nonaligned_pointer():
+    rng = np.random.default_rng(16)
+    xq, xt = rng.random((60, 64)), rng.random((800, 64))
+    flat = np.concatenate([np.zeros(1), xq.ravel()])
+    tq = _t(flat)[1:].view(60, 64)  # 8-byte offset: not 16-byte aligned
+    assert tq.data_ptr() % 16 == 8
+    d_, i_ = prims.knn_topk(tq, _t(xt), 9, "cosine")
+    torch.cuda.synchronize()
+    wd, wi = oracle.knn_topk(xq, xt, 9, "cosine")
+    assert_same(d_.cpu().numpy(), i_.cpu().numpy(), wd, wi, "f64 offset")
+
+
 def test_huge_values_overflow_norms():
     """Squared norms overflow f32: the screen bound becomes infinite and every
     row is evaluated exactly; results still match the reference arithmetic."""
@@ -168,7 +202,8 @@ def test_side_stream():
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("n,kc,d,dtype", [(5000, 100, 64, np.float32), (3000, 7, 3, np.float32),
                                          (2000, 50, 200, np.float32), (1500, 40, 32, np.float64),
-                                         (20000, 1024, 64, np.float32)])
+                                         (20000, 1024, 64, np.float32), (4000, 300, 200, np.float64),
+                                         (3000, 20, 7, np.float64)])
 def test_kmeans_assign_bitwise(n, kc, d, dtype):
     rng = np.random.default_rng(kc + d)
     c = rng.standard_normal((kc, d)).astype(dtype) * 3
