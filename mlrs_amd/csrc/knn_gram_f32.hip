@@ -27,12 +27,13 @@
 //  * Passing (query, row) pairs are queued in LDS (queue lengths live in
 //    registers; a lane pair appends with a popcount prefix, no atomics).
 //    When a query's queue is half full the wave evaluates the queued pairs
-//    EXACTLY, in the reference
-//    arm's operation order, sorts them and merges them into the query's exact
-//    top-k list with the (value, index) order.  The lists live in global
-//    memory (one per query and strip): keeping only the queues in LDS (~70 KB
-//    per workgroup) lets two workgroups share a CU, so one workgroup's
-//    selection work overlaps the other's MFMAs.
+//    EXACTLY, in the reference arm's operation order, sorts them and merges
+//    them into the query's exact top-k list with the (value, index) order.
+//    The lists live in global memory (one per query and segment): keeping
+//    only the queues in LDS (~70 KB per workgroup) lets two workgroups share
+//    a CU, so one workgroup's selection work overlaps the other's MFMAs.
+//  * Work split: StreamSplit (knn_kernels.hpp), panel-major, so the
+//    workgroups on one index panel stream its rows in lockstep.
 // The kept lists are therefore the reference's own top-k: the full distance
 // matrix never reaches HBM and no tolerance is involved.
 #include "knn_common.hpp"
@@ -226,24 +227,18 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     WaveLds& L = wl[w];
     const float inf = __builtin_huge_valf();
 
-    // ---- stream-K split: the (query block, tile) units, query-block-major,
-    //      cut into gridDim.x equal contiguous ranges, one per workgroup; a
-    //      range crossing a query-block boundary becomes several segments.
-    //      Each segment keeps its own exact lists [segment slot][nq][k], merged
-    //      at the end by knn_merge_f32_kernel. ----
-    const int64_t nqb = (nq + kQpb - 1) / kQpb;
-    const int64_t ntiles = (nt + kBn - 1) / kBn;
-    const int64_t T = nqb * ntiles;
-    const int64_t G = gridDim.x;
+    // ---- work split (StreamSplit): this workgroup's range of (query block,
+    //      tile) units, panel-major; each piece of a job in the range is a
+    //      segment with its own exact lists [slot][nq][k], merged at the end
+    //      by knn_merge_f32_kernel. ----
+    const StreamSplit sp(nq, nt, kQpb, kBn, a.grid_wgs);
     const int64_t wg = blockIdx.x;
-    const int64_t u_hi = ((wg + 1) * T) / G;
-    for (int64_t u = (wg * T) / G; u < u_hi;) {
-    const int64_t qblock = u / ntiles;
-    const int64_t tile0 = u % ntiles;
-    const int64_t tile1 = (ntiles - tile0 < u_hi - u) ? ntiles : tile0 + (u_hi - u);
-    // slot = this workgroup's position among the workgroups covering qblock
-    const int64_t first_wg = ((qblock * ntiles + 1) * G + T - 1) / T - 1;
-    const int64_t slot = wg - first_wg;
+    const int64_t u_hi = ((wg + 1) * sp.P < sp.T) ? (wg + 1) * sp.P : sp.T;
+    for (int64_t u = wg * sp.P; u < u_hi;) {
+    int64_t panel, qblock, tile0, left;
+    sp.decode(u, panel, qblock, tile0, left);
+    const int64_t tile1 = tile0 + ((left < u_hi - u) ? left : (u_hi - u));
+    const int64_t slot = sp.slot(wg, panel, qblock);
     float* __restrict__ LV = a.part_val + slot * nq * k;
     uint32_t* __restrict__ LI = a.part_idx + slot * nq * k;
 
@@ -614,15 +609,10 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
         lv = a.part_val[qg * k + lane];
         li = a.part_idx[qg * k + lane];
     }
-    // the workgroups whose stream-K ranges cover this query's block
-    const int64_t nqb = (a.nq + kQpb - 1) / kQpb;
-    const int64_t ntiles = (a.nt + kBn - 1) / kBn;
-    const int64_t T = nqb * ntiles;
-    const int64_t G = a.grid_wgs;
-    const int64_t b = qg / kQpb;
-    const int64_t first_wg = ((b * ntiles + 1) * G + T - 1) / T - 1;
-    const int64_t last_wg = (((b + 1) * ntiles) * G + T - 1) / T - 1;
-    for (int64_t s = 1; s <= last_wg - first_wg; ++s) {
+    // the list slots of this query's block
+    const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / kQpb);
+    for (int64_t s = 1; s < nsl; ++s) {
         float v = inf;
         uint32_t ix = kSentinelIdx;
         if (lane < k) {
@@ -643,7 +633,7 @@ __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
 
 template <int NG, int ARM, bool COS, bool VEC4>
 hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
-    dim3 grid((unsigned)a.grid_wgs);
+    dim3 grid((unsigned)StreamSplit(a.nq, a.nt, kQpb, kBn, a.grid_wgs).G);
     (void)nblocks;
     if (a.k == 1)
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true>), grid, dim3(256), 0, s, a);
@@ -672,16 +662,13 @@ hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
 }  // namespace
 
 void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots) {
-    const int64_t nqb = (nq + kQpb - 1) / kQpb;
-    const int64_t ntiles = (nt + kBn - 1) / kBn;
-    const int64_t T = nqb * ntiles;
+    const StreamSplit full(nq, nt, kQpb, kBn, 1);
     // one resident round (two workgroups per CU), but at least 16 tiles each
-    int64_t G = 2 * (int64_t)(cus > 0 ? cus : 1);
-    if (G > T / 16) G = T / 16;
-    if (G < 1) G = 1;
-    *grid_wgs = G;
-    // a query block's ntiles units span at most ceil(ntiles*G/T) + 1 ranges
-    *nslots = (int)((ntiles * G + T - 1) / T + 1);
+    int64_t g0 = 2 * (int64_t)(cus > 0 ? cus : 1);
+    if (g0 > full.T / 16) g0 = full.T / 16;
+    if (g0 < 1) g0 = 1;
+    *grid_wgs = g0;
+    *nslots = (int)StreamSplit(nq, nt, kQpb, kBn, g0).nslots();
 }
 
 int gram_f32_max_k() { return kKcap; }

@@ -62,7 +62,9 @@ __device__ __forceinline__ double screen_threshold64(double R, double qs, double
 }
 
 // Exact value of one (query, row) pair in the arm's operation order; loads
-// issued two 16-byte pairs at a time when rows are 16-byte aligned.
+// issued two 16-byte pairs at a time when rows are 16-byte aligned (the
+// d = 256 kernel holds 128 VGPRs of query operand, which leaves room for no
+// more in flight).
 template <int ARM, bool VEC2>
 __device__ __forceinline__ double exact_f64(const double* __restrict__ q, const double* __restrict__ y,
                                             int64_t d, double qa, double ya) {
@@ -146,19 +148,15 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     WaveLds64& L = wl[w];
     const double inf = __builtin_huge_val();
 
-    // ---- stream-K split over (query block, tile) units, as in the f32 kernel ----
-    const int64_t nqb = (nq + kQpb - 1) / kQpb;
-    const int64_t ntiles = (nt + kBn - 1) / kBn;
-    const int64_t T = nqb * ntiles;
-    const int64_t G = gridDim.x;
+    // ---- work split (StreamSplit), as in the f32 kernel ----
+    const StreamSplit sp(nq, nt, kQpb, kBn, a.grid_wgs);
     const int64_t wg = blockIdx.x;
-    const int64_t u_hi = ((wg + 1) * T) / G;
-    for (int64_t u = (wg * T) / G; u < u_hi;) {
-    const int64_t qblock = u / ntiles;
-    const int64_t tile0 = u % ntiles;
-    const int64_t tile1 = (ntiles - tile0 < u_hi - u) ? ntiles : tile0 + (u_hi - u);
-    const int64_t first_wg = ((qblock * ntiles + 1) * G + T - 1) / T - 1;
-    const int64_t slot = wg - first_wg;
+    const int64_t u_hi = ((wg + 1) * sp.P < sp.T) ? (wg + 1) * sp.P : sp.T;
+    for (int64_t u = wg * sp.P; u < u_hi;) {
+    int64_t panel, qblock, tile0, left;
+    sp.decode(u, panel, qblock, tile0, left);
+    const int64_t tile1 = tile0 + ((left < u_hi - u) ? left : (u_hi - u));
+    const int64_t slot = sp.slot(wg, panel, qblock);
     double* __restrict__ LV = a.part_val + slot * nq * k;
     uint32_t* __restrict__ LI = a.part_idx + slot * nq * k;
 
@@ -400,14 +398,9 @@ __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
         lv = a.part_val[qg * k + lane];
         li = a.part_idx[qg * k + lane];
     }
-    const int64_t nqb = (a.nq + kQpb - 1) / kQpb;
-    const int64_t ntiles = (a.nt + kBn - 1) / kBn;
-    const int64_t T = nqb * ntiles;
-    const int64_t G = a.grid_wgs;
-    const int64_t b = qg / kQpb;
-    const int64_t first_wg = ((b * ntiles + 1) * G + T - 1) / T - 1;
-    const int64_t last_wg = (((b + 1) * ntiles) * G + T - 1) / T - 1;
-    for (int64_t s = 1; s <= last_wg - first_wg; ++s) {
+    const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / kQpb);
+    for (int64_t s = 1; s < nsl; ++s) {
         double v = inf;
         uint32_t ix = kSentinelIdx;
         if (lane < k) {
@@ -442,7 +435,7 @@ __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long 
 
 template <int NS, int ARM, bool COS>
 hipError_t launch_ns(const GramArgs64& a, bool vec2, hipStream_t s) {
-    dim3 grid((unsigned)a.grid_wgs);
+    dim3 grid((unsigned)StreamSplit(a.nq, a.nt, kQpb, kBn, a.grid_wgs).G);
     if (vec2)
         hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, true>), grid, dim3(256), 0, s, a);
     else
@@ -464,14 +457,13 @@ hipError_t launch_arm64(const GramArgs64& a, bool vec2, hipStream_t s) {
 }  // namespace
 
 void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots) {
-    const int64_t nqb = (nq + kQpb - 1) / kQpb;
-    const int64_t ntiles = (nt + kBn - 1) / kBn;
-    const int64_t T = nqb * ntiles;
-    int64_t G = 2 * (int64_t)(cus > 0 ? cus : 1);
-    if (G > T / 16) G = T / 16;
-    if (G < 1) G = 1;
-    *grid_wgs = G;
-    *nslots = (int)((ntiles * G + T - 1) / T + 1);
+    const StreamSplit full(nq, nt, kQpb, kBn, 1);
+    // one resident round (two workgroups per CU), but at least 16 tiles each
+    int64_t g0 = 2 * (int64_t)(cus > 0 ? cus : 1);
+    if (g0 > full.T / 16) g0 = full.T / 16;
+    if (g0 < 1) g0 = 1;
+    *grid_wgs = g0;
+    *nslots = (int)StreamSplit(nq, nt, kQpb, kBn, g0).nslots();
 }
 
 int gram_f64_max_k() { return kKcap; }

@@ -20,6 +20,61 @@ struct NormStats {
     double xsq_max64;                 // f64 view
 };
 
+// Work split of the Gram kernels.  The (query block b, index tile t) units
+// are ordered panel-major: the index is cut into S panels of P tiles (the
+// last one L tiles), and the units run panel by panel, query block by query
+// block, tile by tile.  Workgroup w takes units [w*P, (w+1)*P): in every
+// panel but the last that is exactly one (panel, query block) job, so the
+// workgroups of one panel start on the same tile and stream the same index
+// rows together (one L2 fill serves all of them on an XCD).  In the last
+// panel a range may hold pieces of several jobs and a job may be split in
+// two.  Each piece keeps its own exact lists in list slot slot(w, j, b);
+// a query block has slots_of(b) <= S + 1 of them.  With many query blocks
+// S = 1 and this is a plain balanced split over query blocks.
+struct StreamSplit {
+    int64_t nqb, ntiles, T, P, S, L, G;
+    __host__ __device__ StreamSplit(int64_t nq, int64_t nt, int64_t qpb, int64_t bn, int64_t g0) {
+        nqb = (nq + qpb - 1) / qpb;
+        ntiles = (nt + bn - 1) / bn;
+        T = nqb * ntiles;
+        if (g0 < 1) g0 = 1;
+        P = (T + g0 - 1) / g0;
+        S = (ntiles + P - 1) / P;
+        L = ntiles - (S - 1) * P;
+        G = (T + P - 1) / P;
+    }
+    // unit u -> panel j, query block b, tile t, units left in its job from u
+    __host__ __device__ void decode(int64_t u, int64_t& j, int64_t& b, int64_t& t, int64_t& left) const {
+        const int64_t full = (S - 1) * nqb * P;
+        if (u < full) {
+            j = u / (nqb * P);
+            const int64_t r = u - j * nqb * P;
+            b = r / P;
+            const int64_t o = r - b * P;
+            t = j * P + o;
+            left = P - o;
+        } else {
+            j = S - 1;
+            const int64_t r = u - full;
+            b = r / L;
+            const int64_t o = r - b * L;
+            t = j * P + o;
+            left = L - o;
+        }
+    }
+    __host__ __device__ int64_t slot(int64_t w, int64_t j, int64_t b) const {
+        if (j < S - 1) return j;
+        const int64_t u0 = (S - 1) * nqb * P + b * L;
+        return (S - 1) + (w - u0 / P);
+    }
+    __host__ __device__ int64_t slots_of(int64_t b) const {
+        const int64_t u0 = (S - 1) * nqb * P + b * L;
+        const int64_t u1 = u0 + L;
+        return (S - 1) + ((u1 - 1) / P - u0 / P + 1);
+    }
+    __host__ __device__ int64_t nslots() const { return S + 1; }
+};
+
 struct GramArgs32 {
     const float* q;
     int64_t nq;
@@ -34,8 +89,8 @@ struct GramArgs32 {
     const NormStats* stats;
     double eps_rel;    // Euclidean screen bound: eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
     double eps_abs;    // cosine screen bound (absolute)
-    int64_t grid_wgs;  // workgroups of the stream-K split (one resident round)
-    int nslots;        // list slots per query: most workgroups any query block is split over
+    int64_t grid_wgs;  // the G0 the StreamSplit is built from (<= one resident round)
+    int nslots;        // list slots per query (StreamSplit::nslots)
     float* part_val;   // [nslots][nq][k] exact lists, one per (segment, query)
     uint32_t* part_idx;
     float* out_val;    // [nq][k]
@@ -43,7 +98,7 @@ struct GramArgs32 {
     unsigned int* shared_r;  // [nq] best known exact k-th value per query (float bits), or null
 };
 
-// Workgroups and per-query list slots of the Gram kernel's stream-K split.
+// G0, launched workgroups and per-query list slots of the Gram kernel's split.
 void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
 
 // Three launches per search: prep (the shared per-query bound: seeded from a
