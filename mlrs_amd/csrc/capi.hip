@@ -444,23 +444,31 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
 
 int32_t knn_lowd32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
                    int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
+    const size_t fixed = aligned_bytes(sizeof(float) * nq) + aligned_bytes(sizeof(float) * nt) +
+                         aligned_bytes(sizeof(NormStats)) + 1024;
     char* ws;
     int cus;
-    int32_t rc = workspace(1024, s, &ws, &cus);
+    int32_t rc = workspace(fixed, s, &ws, &cus);
     if (rc) return rc;
-    const int64_t nblocks = (nq + 255) / 256;
-    // ~8 resident 256-lane workgroups per CU
-    int nstrips = pick_strips(nblocks, nt, (int64_t)cus * 8, 4096, 64);
+    const int64_t nblocks = (nq + lowd_queries_per_block(k) - 1) / lowd_queries_per_block(k);
+    // ~3 resident 256-lane workgroups per CU (the k <= 8 kernel holds ~150 VGPRs)
+    int nstrips = pick_strips(nblocks, nt, (int64_t)cus * 3, 4096, 64);
     int64_t rps = (nt + nstrips - 1) / nstrips;
     nstrips = (int)((nt + rps - 1) / rps);
     size_t parts = nstrips > 1 ? (size_t)nstrips * nq * k : 0;
     if (parts) {
-        rc = workspace(aligned_bytes(parts * 4) * 2 + 1024, s, &ws, &cus);
+        rc = workspace(fixed + aligned_bytes(parts * 4) * 2 + aligned_bytes(sizeof(unsigned int) * nq), s, &ws, &cus);
         if (rc) return rc;
     }
     Carver cv(ws);
     LowdArgs32 a;
     std::memset(&a, 0, sizeof(a));
+    float* qsq = cv.take<float>(nq);
+    float* xsq = cv.take<float>(nt);
+    NormStats* stats = cv.take<NormStats>(1);
+    hipError_t e = launch_row_norms<float>(xq, nq, d, qsq, nullptr, nullptr, nullptr, s);
+    if (e == hipSuccess) e = launch_row_norms<float>(xt, nt, d, xsq, nullptr, nullptr, stats, s);
+    if (e != hipSuccess) return hip_err(e, "row_norms");
     a.q = xq;
     a.nq = nq;
     a.x = xt;
@@ -468,15 +476,22 @@ int32_t knn_lowd32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     a.d = d;
     a.k = k;
     a.mode = mode;
+    a.qsq = qsq;
+    a.xsq = xsq;
+    a.stats = stats;
+    // the Gram kernels' Euclidean screen bound (knn_gram32)
+    const double u = std::ldexp(1.0, -23);
+    a.eps_rel = 8.0 * (double)(d + 4) * u;
+    a.eps_abs = (double)(d + 4) * std::ldexp(1.0, -120);
     a.rows_per_strip = rps;
     a.nstrips = nstrips;
     if (parts) {
         a.part_val = cv.take<float>(parts);
         a.part_idx = cv.take<uint32_t>(parts);
+        a.shared_r = cv.take<unsigned int>(nq);
     }
     a.out_val = out_v;
     a.out_idx = out_i;
-    hipError_t e;
     {
         KernelTimer timer(s, "knn_lowd_kernel");
         e = launch_lowd_f32(a, arm, s);

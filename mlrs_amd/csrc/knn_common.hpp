@@ -117,6 +117,19 @@ __device__ __forceinline__ T exact_pair(const T* __restrict__ q, const T* __rest
     }
 }
 
+// Smallest float >= t (screen thresholds are rounded up, never down).
+__device__ __forceinline__ float round_up_f(double t) {
+    float f = (float)t;
+    if ((double)f < t) {  // step one ulp towards +inf
+        uint32_t b = __float_as_uint(f);
+        if (f == 0.0f)
+            f = __uint_as_float(1u);
+        else
+            f = __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
+    }
+    return f;
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 bitonic machinery over (value, index) pairs, one pair per lane.
 // ---------------------------------------------------------------------------

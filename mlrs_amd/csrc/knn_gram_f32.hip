@@ -72,19 +72,6 @@ struct WaveLds {
 // for the non-negative values every served arm produces.
 constexpr unsigned long long kBestEmpty = (0x7F800000ull << 32) | 0xFFFFFFFFull;
 
-// Smallest float >= t.
-__device__ __forceinline__ float round_up_f(double t) {
-    float f = (float)t;
-    if ((double)f < t) {  // step one ulp towards +inf
-        uint32_t b = __float_as_uint(f);
-        if (f == 0.0f)
-            f = __uint_as_float(1u);
-        else
-            f = __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
-    }
-    return f;
-}
-
 template <bool COS>
 __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) {
     const float inf = __builtin_huge_valf();

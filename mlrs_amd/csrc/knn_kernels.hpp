@@ -177,13 +177,25 @@ struct LowdArgs32 {
     int64_t d;
     int k;
     int mode;
+    const float* qsq;       // query row_sumsq
+    const float* xsq;       // index row_sumsq
+    const NormStats* stats; // max index row_sumsq (screen bound)
+    double eps_rel;         // screen bound eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
+    double eps_abs;
     int64_t rows_per_strip;
     int nstrips;
+    unsigned int* shared_r;  // [nq] k-th value reached by finished strips (float bits), or null
     float* part_val;
     uint32_t* part_idx;
     float* out_val;
     uint32_t* out_idx;
 };
+// Queries per lane of the low-d kernel for a list capacity K.
+#ifndef MLRS_LOWD_QL_SMALL_K
+#define MLRS_LOWD_QL_SMALL_K 2
+#endif
+constexpr int lowd_queries_per_lane(int K) { return K <= 8 ? MLRS_LOWD_QL_SMALL_K : (K <= 16 ? 2 : 1); }
+int lowd_queries_per_block(int k);
 hipError_t launch_lowd_f32(const LowdArgs32& a, int arm, hipStream_t s);
 int lowd_max_d();
 int lowd_max_k();

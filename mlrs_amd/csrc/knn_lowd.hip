@@ -1,18 +1,22 @@
-// Low-dimension kNN on the vector ALUs (d <= 16), exact direct form.
+// Low-dimension kNN on the vector ALUs (d <= 16), no MFMA.
 //
 // The MI355X counterpart of euclidean_topk_rows_cpu_direct
-// (crates/mlrs-kernels/src/knn.rs:2968-3227): one lane owns one query row,
-// keeps its sorted k-list in VGPRs and walks every index row of its strip,
-// accumulating fma(x-y, x-y, acc) (or acc + d*d for the host arm) over
-// ascending columns.  At d <= 16 a Gram tile would spend as many VALU cycles
-// in its epilogue as the direct form spends on the whole pair, and the direct
-// form is exact by construction (duplicates score exactly 0), so this path
-// uses no MFMA.
+// (crates/mlrs-kernels/src/knn.rs:2968-3227).  Each lane owns QL query rows
+// (QL = 4 for k <= 8, 2 for k <= 16, 1 above), keeps their sorted k-lists in
+// VGPRs and walks every index row of its strip.  Per (query, row) pair the
+// screen costs d FMAs: the expansion ||x||^2 - 2 x.q accumulated from the
+// row's precomputed squared norm, against the threshold derived from the
+// query's exact k-th value (the same rigorous rounding bound as the Gram
+// kernels).  A pair that passes is evaluated exactly, right there, in the
+// reference arm's order -- fma(q-x, q-x, acc) (or acc + d*d for the host
+// arm) over ascending columns, from the query in registers and the row in
+// LDS -- and offered to the list with insert_lane's rule (knn.rs:2655-2706):
+// (value, index) order, NaN never admitted.  The exact direct form is what
+// the list holds, so results are the reference's bit for bit.
 //
-// Index rows are staged through LDS (4-float padded rows); every lane of a
-// wave reads the same row at the same time, so the reads are LDS broadcasts.
-// Admission is insert_lane's rule (knn.rs:2655-2706): reject with one compare
-// against the kept worst, else a shift-insertion by (value, index).
+// Index rows are staged through LDS with their norm appended ((d+1) floats
+// padded to a multiple of 4); every lane of a wave reads the same row at the
+// same time, so the reads are LDS broadcasts.
 #include "knn_common.hpp"
 #include "knn_kernels.hpp"
 
@@ -24,96 +28,176 @@ constexpr int kRt = 512;        // index rows per LDS tile
 constexpr int kMaxD = 16;
 constexpr int kMaxK = 32;
 
-template <int D, int K, int ARM>
+template <int D, int K, int QL, int ARM>
 __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
-    constexpr int DP = (D + 3) & ~3;  // padded row length in LDS
-    __shared__ __attribute__((aligned(16))) float tile[kRt * DP];
+    constexpr int DPN = (D + 1 + 3) & ~3;  // row + norm, padded to float4
+    constexpr int RU = DPN <= 4 ? 8 : (DPN <= 8 ? 4 : 2);  // rows per screening step
+    __shared__ __attribute__((aligned(16))) float tile[kRt * DPN];
 
     const int tid = threadIdx.x;
-    const int64_t q = (int64_t)blockIdx.x * 256 + tid;
-    const bool qvalid = q < a.nq;
+    const int64_t qbase = (int64_t)blockIdx.x * (256 * QL) + tid;
     const int64_t t_begin = (int64_t)blockIdx.y * a.rows_per_strip;
     int64_t t_end = t_begin + a.rows_per_strip;
     if (t_end > a.nt) t_end = a.nt;
     const int k = a.k;
     const float inf = __builtin_huge_valf();
+    const float* __restrict__ X = a.x;
+    const float* __restrict__ XSQ = a.xsq;
 
-    float qv[D];
+    float qv[QL][D];    // the queries
+    float qm2[QL][D];   // -2 * the queries (exact scaling) for the screen
+    float qsq[QL], eps[QL], thr[QL], worst[QL];
+    uint32_t worst_i[QL];
+    float lv[QL][K];
+    uint32_t li[QL][K];
+    const double xmax = (double)a.stats->xsq_max;
 #pragma unroll
-    for (int c = 0; c < D; ++c) qv[c] = qvalid ? a.q[q * D + c] : 0.0f;
-
-    float lv[K];
-    uint32_t li[K];
+    for (int i = 0; i < QL; ++i) {
+        const int64_t q = qbase + 256 * i;
+        const bool ok = q < a.nq;
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-        lv[j] = inf;
-        li[j] = kSentinelIdx;
+        for (int c = 0; c < D; ++c) {
+            qv[i][c] = ok ? a.q[q * D + c] : 0.0f;
+            qm2[i][c] = -2.0f * qv[i][c];
+        }
+        qsq[i] = ok ? a.qsq[q] : 0.0f;
+        eps[i] = (float)(a.eps_rel * ((double)qsq[i] + xmax) + a.eps_abs);
+        // An inactive lane can never admit (prefill_lists' -inf bound, knn.rs:2875-2905).
+        worst[i] = ok ? inf : -inf;
+        thr[i] = ok ? inf : -inf;
+        worst_i[i] = kSentinelIdx;
+        // A later strip starts from the k-th value the earlier strips of this
+        // query reached (strips are dispatched in order, so the first strips
+        // have usually finished by then); any k real rows bound the answer.
+        if (ok && a.shared_r && blockIdx.y > 0) {
+            const float R0 = __uint_as_float(__hip_atomic_load(&a.shared_r[q], __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT));
+            if (R0 < inf) thr[i] = round_up_f((double)R0 - (double)qsq[i] + (double)eps[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            lv[i][j] = inf;
+            li[i][j] = kSentinelIdx;
+        }
     }
-    // An inactive lane can never admit (prefill_lists' -inf bound, knn.rs:2875-2905).
-    float worst = qvalid ? inf : -inf;
-    uint32_t worst_i = kSentinelIdx;
 
     for (int64_t t0 = t_begin; t0 < t_end; t0 += kRt) {
         const int nrows = (int)((t_end - t0) < kRt ? (t_end - t0) : kRt);
         __syncthreads();
-        for (int e = tid; e < kRt * DP; e += 256) {
-            int r = e / DP, c = e % DP;
-            tile[e] = (r < nrows && c < D) ? a.x[(t0 + r) * D + c] : 0.0f;
+        for (int e = tid; e < kRt * DPN; e += 256) {
+            const int r = e / DPN, c = e % DPN;
+            float v = 0.0f;
+            if (r < nrows) {
+                if (c < D)
+                    v = X[(t0 + r) * D + c];
+                else if (c == D)
+                    v = XSQ[t0 + r];
+            }
+            tile[e] = v;
         }
         __syncthreads();
-        for (int r = 0; r < nrows; ++r) {
-            const float* yr = &tile[r * DP];
-            float acc = 0.0f;
+        // RU rows per step: their LDS reads are issued together, so one
+        // LDS latency is paid per RU rows, not per row.
+        for (int r0 = 0; r0 < nrows; r0 += RU) {
+            float row[RU][DPN];
 #pragma unroll
-            for (int c = 0; c < D; ++c) {
-                float diff = qv[c] - yr[c];
-                if (ARM == ARM_EUCLID_FMA)
-                    acc = __builtin_fmaf(diff, diff, acc);
-                else
-                    acc = acc + diff * diff;
-            }
-            const uint32_t t = (uint32_t)(t0 + r);
-            if (acc <= worst) {
-                if (acc < worst || t < worst_i) {
-                    float cav = acc;
+            for (int rr = 0; rr < RU; ++rr)
+#pragma unroll
+                for (int c4 = 0; c4 < DPN / 4; ++c4) {
+                    const float4 v = *reinterpret_cast<const float4*>(&tile[(r0 + rr) * DPN + 4 * c4]);
+                    row[rr][4 * c4 + 0] = v.x;
+                    row[rr][4 * c4 + 1] = v.y;
+                    row[rr][4 * c4 + 2] = v.z;
+                    row[rr][4 * c4 + 3] = v.w;
+                }
+            // screen: acc = ||x||^2 - 2 x.q; NaN passes (!(acc > thr)).
+            bool any = false;
+#pragma unroll
+            for (int i = 0; i < QL; ++i)
+#pragma unroll
+                for (int rr = 0; rr < RU; ++rr) {
+                    float s_ = row[rr][D];
+#pragma unroll
+                    for (int c = 0; c < D; ++c) s_ = __builtin_fmaf(qm2[i][c], row[rr][c], s_);
+                    any |= !(s_ > thr[i]);
+                }
+            if (!any) continue;
+            // exact rescoring of the passing pairs (rare after the lists fill):
+            // the screen is redone from the row registers into a bit mask,
+            // and only the passing rows are read back from LDS
+            const int rmax = (nrows - r0) < RU ? (nrows - r0) : RU;  // padding rows of the last step
+#pragma unroll
+            for (int i = 0; i < QL; ++i) {
+                uint32_t m = 0;
+#pragma unroll
+                for (int rr = 0; rr < RU; ++rr) {
+                    float s_ = row[rr][D];
+#pragma unroll
+                    for (int c = 0; c < D; ++c) s_ = __builtin_fmaf(qm2[i][c], row[rr][c], s_);
+                    m |= (uint32_t)!(s_ > thr[i]) << rr;
+                }
+                m &= (rmax >= 32) ? 0xFFFFFFFFu : ((1u << rmax) - 1u);
+                while (m) {
+                    const int rr = __builtin_ctz(m);
+                    m &= m - 1;
+                    const float* yr = &tile[(r0 + rr) * DPN];
+                    const uint32_t t = (uint32_t)(t0 + r0 + rr);
+                    float e = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < D; ++c) {
+                        const float diff = qv[i][c] - yr[c];
+                        if (ARM == ARM_EUCLID_FMA)
+                            e = __builtin_fmaf(diff, diff, e);
+                        else
+                            e = e + diff * diff;
+                    }
+                    if (!(e <= worst[i]) || (e == worst[i] && t > worst_i[i])) continue;
+                    float cav = e;
                     uint32_t cai = t;
+                    // positions k..K-1 only ever receive pairs pushed out of the
+                    // first k, so they never influence the kept ones
 #pragma unroll
                     for (int j = 0; j < K; ++j) {
-                        if (j < k) {
-                            float jv = lv[j];
-                            uint32_t ji = li[j];
-                            if (cav < jv || (cav == jv && cai < ji)) {
-                                lv[j] = cav;
-                                li[j] = cai;
-                                cav = jv;
-                                cai = ji;
-                            }
+                        const float jv = lv[i][j];
+                        const uint32_t ji = li[i][j];
+                        if (cav < jv || (cav == jv && cai < ji)) {
+                            lv[i][j] = cav;
+                            li[i][j] = cai;
+                            cav = jv;
+                            cai = ji;
                         }
                     }
-                    // the new worst kept pair is slot k-1
 #pragma unroll
                     for (int j = 0; j < K; ++j)
                         if (j == k - 1) {
-                            worst = lv[j];
-                            worst_i = li[j];
+                            worst[i] = lv[i][j];
+                            worst_i[i] = li[i][j];
                         }
+                    // exact <= R  =>  ||x||^2 - 2 x.q <= R - ||q||^2 + eps
+                    if (worst[i] < inf)
+                        thr[i] = round_up_f((double)worst[i] - (double)qsq[i] + (double)eps[i]);
                 }
             }
         }
     }
 
-    if (!qvalid) return;
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-        if (j < k) {
-            if (a.nstrips > 1) {
-                int64_t o = ((int64_t)blockIdx.y * a.nq + q) * k + j;
-                a.part_val[o] = lv[j];
-                a.part_idx[o] = li[j];
-            } else {
-                int64_t o = q * k + j;
-                a.out_val[o] = (a.mode == EMIT_SQRT) ? __builtin_sqrtf(lv[j]) : lv[j];
-                a.out_idx[o] = (li[j] == kSentinelIdx) ? 0u : li[j];
+    for (int i = 0; i < QL; ++i) {
+        const int64_t q = qbase + 256 * i;
+        if (q >= a.nq) continue;
+        if (a.shared_r && worst[i] < inf) atomicMin(&a.shared_r[q], __float_as_uint(worst[i]));
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            if (j < k) {
+                if (a.nstrips > 1) {
+                    const int64_t o = ((int64_t)blockIdx.y * a.nq + q) * k + j;
+                    a.part_val[o] = lv[i][j];
+                    a.part_idx[o] = li[i][j];
+                } else {
+                    const int64_t o = q * k + j;
+                    a.out_val[o] = (a.mode == EMIT_SQRT) ? __builtin_sqrtf(lv[i][j]) : lv[i][j];
+                    a.out_idx[o] = (li[i][j] == kSentinelIdx) ? 0u : li[i][j];
+                }
             }
         }
     }
@@ -148,10 +232,16 @@ __global__ __launch_bounds__(256) void lowd_merge_kernel(LowdArgs32 a) {
     }
 }
 
+__global__ void lowd_fill_inf_kernel(unsigned int* p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0x7F800000u;
+}
+
 template <int D, int K, int ARM>
 hipError_t launch3(const LowdArgs32& a, hipStream_t s) {
-    dim3 grid((unsigned)((a.nq + 255) / 256), (unsigned)a.nstrips);
-    hipLaunchKernelGGL((knn_lowd_kernel<D, K, ARM>), grid, dim3(256), 0, s, a);
+    constexpr int QL = lowd_queries_per_lane(K);
+    dim3 grid((unsigned)((a.nq + 256 * QL - 1) / (256 * QL)), (unsigned)a.nstrips);
+    hipLaunchKernelGGL((knn_lowd_kernel<D, K, QL, ARM>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -190,10 +280,16 @@ hipError_t launch_d(const LowdArgs32& a, hipStream_t s) {
 }  // namespace
 
 int lowd_max_d() { return kMaxD; }
+int lowd_queries_per_block(int k) { return 256 * lowd_queries_per_lane(k <= 1 ? 1 : k <= 4 ? 4 : k <= 8 ? 8 : k <= 16 ? 16 : 32); }
 int lowd_max_k() { return kMaxK; }
 
 hipError_t launch_lowd_f32(const LowdArgs32& a, int arm, hipStream_t s) {
     if (a.d < 1 || a.d > kMaxD || a.k < 1 || a.k > kMaxK) return hipErrorInvalidValue;
+    if (a.shared_r) {
+        hipLaunchKernelGGL(lowd_fill_inf_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r,
+                           a.nq);
+        if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+    }
     hipError_t e;
     if (arm == ARM_EUCLID_FMA)
         e = launch_d<ARM_EUCLID_FMA>(a, s);
