@@ -173,6 +173,22 @@ int32_t mlrs_release_workspace(void);
 int32_t mlrs_timing_enable(int32_t on);
 int32_t mlrs_timing_read(double *total_ms, int64_t *launches, char *kernel_name, int32_t name_len);
 
+/*
+ * Kernel-family override (no counterpart in the reference; for tests and
+ * benchmarks).  Every family returns the same bits, so this only changes
+ * speed: 0 = automatic choice (default); 1 = the fused Gram-MFMA kernels
+ * wherever they serve the shape (f32: d <= 128, k <= 64, not the knn_host
+ * cosine arm; f64: d <= 256, k <= 64; k-means: d <= 128 / 256); 2 = the
+ * low-d ALU kernel wherever it serves the shape (f32 Euclidean, d <= 16,
+ * k <= 32); 3 = the generic exact-tile path.  A family that does not serve
+ * a shape falls back to the automatic choice.  Process-wide.
+ */
+#define MLRS_PATH_AUTO 0
+#define MLRS_PATH_FUSED 1
+#define MLRS_PATH_LOWD 2
+#define MLRS_PATH_GENERIC 3
+int32_t mlrs_force_path(int32_t path);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,7 @@ SIGNATURES = {
     "mlrs_row_sqnorms_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "mlrs_release_workspace": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
+    "mlrs_force_path": (_i32, [_i32]),
     "mlrs_timing_read": (_i32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, _i32]),
 }
 

@@ -299,6 +299,24 @@ int32_t kmeans_generic(const T* x, int64_t n, const T* c, int64_t kc, int64_t d,
 // ---------------------------------------------------------------------------
 // fast paths
 // ---------------------------------------------------------------------------
+// Below about 4e9 multiply-adds the whole exact distance matrix is cheaper
+// than the fused kernel's fixed costs (a few flush round trips per segment
+// and query): c1's 1k x 10k x 64 search takes 0.05 ms of exact tiles against
+// 0.5 ms fused on an MI355X.
+static bool small_search(int64_t nq, int64_t nt, int64_t d) {
+    return (double)nq * (double)nt * (double)d <= 4294967296.0;
+}
+
+// Process-wide kernel-family override (mlrs_force_path); a family that does
+// not serve the shape yields the automatic choice.
+static int g_force_path = MLRS_PATH_AUTO;
+static int pick_path(bool lowd_ok, bool gram_ok) {
+    if (g_force_path == MLRS_PATH_FUSED && gram_ok) return MLRS_PATH_FUSED;
+    if (g_force_path == MLRS_PATH_LOWD && lowd_ok) return MLRS_PATH_LOWD;
+    if (g_force_path == MLRS_PATH_GENERIC) return MLRS_PATH_GENERIC;
+    return MLRS_PATH_AUTO;
+}
+
 int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
                    int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
     const bool cos = (arm == ARM_COS_FOLD);
@@ -562,9 +580,15 @@ int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int6
     hipStream_t s = (hipStream_t)stream;
     const int arm = knn_arm(n_features, k, metric);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
-    if (metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k())
+    const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
+    const bool gram_ok = arm != ARM_COS_HOST && n_features <= gram_f32_max_d() && k <= gram_f32_max_k();
+    int path = pick_path(lowd_ok, gram_ok);
+    if (path == MLRS_PATH_AUTO)
+        path = lowd_ok ? MLRS_PATH_LOWD
+                       : (gram_ok && !small_search(n_query, n_train, n_features)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+    if (path == MLRS_PATH_LOWD)
         return knn_lowd32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
-    if (arm != ARM_COS_HOST && n_features <= gram_f32_max_d() && k <= gram_f32_max_k())
+    if (path == MLRS_PATH_FUSED)
         return knn_gram32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     return knn_generic<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
 }
@@ -581,7 +605,11 @@ int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int
     hipStream_t s = (hipStream_t)stream;
     const int arm = knn_arm(n_features, k, metric);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
-    if (n_features <= gram_f64_max_d() && k <= gram_f64_max_k())
+    const bool gram_ok = n_features <= gram_f64_max_d() && k <= gram_f64_max_k();
+    int path = pick_path(false, gram_ok);
+    if (path == MLRS_PATH_AUTO)
+        path = (gram_ok && !small_search(n_query, n_train, n_features)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+    if (path == MLRS_PATH_FUSED)
         return knn_gram64(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     return knn_generic<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
 }
@@ -613,7 +641,7 @@ int32_t mlrs_kmeans_assign_f32(const float* x, int64_t x_len, int64_t n, int64_t
                                         labels_len, sqdist, dist_len);
     if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;
-    if (n_features <= gram_f32_max_d())
+    if (n_features <= gram_f32_max_d() && pick_path(false, true) != MLRS_PATH_GENERIC)
         return knn_gram32(x, n, centers, n_centers, n_features, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, sqdist, labels,
                           s);
     return kmeans_generic<float>(x, n, centers, n_centers, n_features, labels, sqdist, s);
@@ -626,7 +654,7 @@ int32_t mlrs_kmeans_assign_f64(const double* x, int64_t x_len, int64_t n, int64_
     int32_t rc = validate_kmeans<double>(x, x_len, n, n_features, centers, centers_len, n_centers, labels,
                                          labels_len, sqdist, dist_len);
     if (rc) return rc;
-    if (n_features <= gram_f64_max_d())
+    if (n_features <= gram_f64_max_d() && pick_path(false, true) != MLRS_PATH_GENERIC)
         return knn_gram64(x, n, centers, n_centers, n_features, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, sqdist, labels,
                           (hipStream_t)stream);
     return kmeans_generic<double>(x, n, centers, n_centers, n_features, labels, sqdist, (hipStream_t)stream);
@@ -709,6 +737,14 @@ int32_t mlrs_row_sqnorms_f32(const float* x, int64_t x_len, int64_t n, int64_t n
 int32_t mlrs_row_sqnorms_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features, double* out,
                              int64_t out_len, void* stream) {
     return sqnorms_impl<double>(x, x_len, n, n_features, out, out_len, stream);
+}
+
+int32_t mlrs_force_path(int32_t path) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (path < MLRS_PATH_AUTO || path > MLRS_PATH_GENERIC)
+        return set_err(MLRS_ERR_UNSUPPORTED, "path", path, 0, 0, 0, "unknown kernel family %d", (int)path);
+    g_force_path = path;
+    return ok();
 }
 
 int32_t mlrs_timing_enable(int32_t on) {

@@ -21,11 +21,17 @@ namespace {
 // of the block's rows is staged in LDS with coalesced loads (consecutive
 // threads read consecutive columns of one row), then each thread continues
 // its own row's sum over the chunk in column order -- the row_sumsq order.
-template <typename T>
+// VEC: rows 16-byte aligned with d a multiple of the 16-byte vector; each
+// thread then issues all eight of its 16-byte loads of a chunk before the
+// barrier, so a block keeps 32 KB in flight.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void row_norms_kernel(const T* __restrict__ x, int64_t n, int64_t d,
                                                         T* __restrict__ sq, T* __restrict__ inv,
                                                         T* __restrict__ neg_inv, NormStats* stats) {
     constexpr int CW = 128 / sizeof(T);  // columns per chunk: one 128-byte segment per row
+    constexpr int V = 16 / sizeof(T);    // elements per 16-byte vector
+    constexpr int VPR = CW / V;          // vectors per row chunk (8)
+    constexpr int RPP = 256 / VPR;       // rows per load pass (32)
     __shared__ T stage[256][CW + 1];
     const int tid = threadIdx.x;
     const int64_t r0 = (int64_t)blockIdx.x * 256;
@@ -34,12 +40,42 @@ __global__ __launch_bounds__(256) void row_norms_kernel(const T* __restrict__ x,
     T s = T(0);
     for (int64_t c0 = 0; c0 < d; c0 += CW) {
         const int cw = (d - c0) < CW ? (int)(d - c0) : CW;
+        if (VEC) {
+            const int vr = tid / VPR, vc = tid % VPR;
+            T buf[256 / RPP][V];
+#pragma unroll
+            for (int p = 0; p < 256 / RPP; ++p) {
+                const int64_t gr = r0 + vr + RPP * p;
+#pragma unroll
+                for (int e = 0; e < V; ++e) buf[p][e] = T(0);
+                if (gr < n && vc * V < cw) {
+                    if (sizeof(T) == 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(x + gr * d + c0 + vc * V);
+                        buf[p][0] = (T)v.x;
+                        buf[p][1] = (T)v.y;
+                        if (V > 2) {
+                            buf[p][V > 2 ? 2 : 0] = (T)v.z;
+                            buf[p][V > 2 ? 3 : 0] = (T)v.w;
+                        }
+                    } else {
+                        const double2 v = *reinterpret_cast<const double2*>(x + gr * d + c0 + vc * V);
+                        buf[p][0] = (T)v.x;
+                        buf[p][1] = (T)v.y;
+                    }
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < 256 / RPP; ++p)
+#pragma unroll
+                for (int e = 0; e < V; ++e) stage[vr + RPP * p][vc * V + e] = buf[p][e];
+        } else {
 #pragma unroll 4
-        for (int m = 0; m < CW; ++m) {
-            const int e = tid + 256 * m;  // element of the 256 x CW chunk
-            const int rr = e / CW, cc = e % CW;
-            const int64_t gr = r0 + rr;
-            if (cc < cw && gr < n) stage[rr][cc] = x[gr * d + c0 + cc];
+            for (int m = 0; m < CW; ++m) {
+                const int e = tid + 256 * m;  // element of the 256 x CW chunk
+                const int rr = e / CW, cc = e % CW;
+                const int64_t gr = r0 + rr;
+                if (cc < cw && gr < n) stage[rr][cc] = x[gr * d + c0 + cc];
+            }
         }
         __syncthreads();
         if (valid) {
@@ -412,8 +448,13 @@ hipError_t launch_row_norms(const T* x, int64_t n, int64_t d, T* sq, T* inv, T* 
     if (stats) hipLaunchKernelGGL((stats_reset_kernel<T>), dim3(1), dim3(64), 0, s, stats);
     if (n > 0) {
         unsigned blocks = (unsigned)((n + 255) / 256);
-        hipLaunchKernelGGL((row_norms_kernel<T>), dim3(blocks), dim3(256), 0, s, x, n, d, sq, inv,
-                           neg_inv, stats);
+        const int vec = 16 / (int)sizeof(T);
+        if (d % vec == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
+            hipLaunchKernelGGL((row_norms_kernel<T, true>), dim3(blocks), dim3(256), 0, s, x, n, d, sq, inv,
+                               neg_inv, stats);
+        else
+            hipLaunchKernelGGL((row_norms_kernel<T, false>), dim3(blocks), dim3(256), 0, s, x, n, d, sq, inv,
+                               neg_inv, stats);
     }
     if (stats) hipLaunchKernelGGL((stats_finalize_kernel<T>), dim3(1), dim3(64), 0, s, stats);
     return hipGetLastError();

@@ -52,7 +52,7 @@ constexpr int kQcap = 64;                // queued candidates per query
 constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
 constexpr int kShareEvery = 32;          // tiles between reads of the shared thresholds
 #ifndef MLRS_SEED_ROWS
-#define MLRS_SEED_ROWS 2048
+#define MLRS_SEED_ROWS 512
 #endif
 constexpr int64_t kSeedRows = MLRS_SEED_ROWS;  // index rows sampled for the initial bound (k > 1)
 
@@ -612,6 +612,26 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
     if (lane < k) emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, k, qg, lane, lv, li, a.out_val, a.out_idx);
 }
 
+// k = 1: the same merge with one lane per query (the segment lists are one
+// pair each, so the merge is a (value, index) minimum).
+__global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
+    const int64_t qg = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (qg >= a.nq) return;
+    float lv = a.part_val[qg];
+    uint32_t li = a.part_idx[qg];
+    const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / kQpb);
+    for (int64_t s = 1; s < nsl; ++s) {
+        const float v = a.part_val[s * a.nq + qg];
+        const uint32_t ix = a.part_idx[s * a.nq + qg];
+        if (pair_less<float>(v, ix, lv, li)) {
+            lv = v;
+            li = ix;
+        }
+    }
+    emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, 1, qg, 0, lv, li, a.out_val, a.out_idx);
+}
+
 // The shared per-query threshold words start at +inf (as float bits).
 __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -683,7 +703,10 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
 }
 
 hipError_t launch_gram_f32_merge(const GramArgs32& a, hipStream_t s) {
-    hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+    if (a.k == 1)
+        hipLaunchKernelGGL(knn_merge1_f32_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -31,7 +31,10 @@ constexpr int kMaxK = 32;
 template <int D, int K, int QL, int ARM>
 __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
     constexpr int DPN = (D + 1 + 3) & ~3;  // row + norm, padded to float4
-    constexpr int RU = DPN <= 4 ? 8 : (DPN <= 8 ? 4 : 2);  // rows per screening step
+#ifndef MLRS_LOWD_RU4
+#define MLRS_LOWD_RU4 8
+#endif
+    constexpr int RU = DPN <= 4 ? MLRS_LOWD_RU4 : (DPN <= 8 ? 4 : 2);  // rows per screening step
     __shared__ __attribute__((aligned(16))) float tile[kRt * DPN];
 
     const int tid = threadIdx.x;

@@ -54,6 +54,18 @@ def _dev_check(*ts):
             raise ValueError("mlrs_amd prims take contiguous row-major tensors")
 
 
+_PATHS = {"auto": 0, "fused": 1, "lowd": 2, "generic": 3}
+
+
+def force_path(name):
+    """Kernel-family override for tests and benchmarks (mlrs_force_path):
+    "auto" (default), "fused" (Gram-MFMA), "lowd" (low-d ALU) or "generic"
+    (exact tiles + selection).  Every family returns the same bits."""
+    if name not in _PATHS:
+        raise ValueError("unknown kernel family %r (expected one of %s)" % (name, sorted(_PATHS)))
+    _lib.check(_lib.load().mlrs_force_path(_PATHS[name]))
+
+
 def knn_topk(xq, x_train, k, metric="euclidean", p=2.0, out=None):
     """k nearest rows of ``x_train`` for every row of ``xq``.
 

@@ -137,3 +137,14 @@ def test_self_drop_by_index_identity():
     d, i = _drop_self_column(dist, idx, 2)
     assert i.tolist() == [[1, 2], [0, 2], [0, 1]]
     assert d.tolist() == [[0.0, 1.0], [0.0, 2.0], [0.5, 0.7]]
+
+
+def test_force_path_validation():
+    """The kernel-family override validates its argument without touching a GPU."""
+    from mlrs_amd import _lib, prims
+    lib = _lib.load()
+    assert lib.mlrs_force_path(7) == -3
+    assert lib.mlrs_force_path(0) == 0
+    with pytest.raises(ValueError):
+        prims.force_path("mfma")
+    prims.force_path("auto")

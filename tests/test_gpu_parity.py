@@ -4,9 +4,10 @@ Every case compares the C-ABI results (through mlrs_amd.prims) with
 oracle/ (the restatement of the mlrs cpu-backend arithmetic) on the same
 seeded inputs.  The bar is exact equality of distances and indices: the engine
 evaluates every kept pair in the reference arm's own operation order, so no
-tolerance is needed.  Shapes are chosen to reach every dispatch path: the
-low-d ALU kernel, the f32 Gram-MFMA kernel (single- and multi-strip), and the
-generic exact path (large k, large d, f64).
+tolerance is needed.  Every test runs twice: with the automatic kernel choice
+(small searches take the exact-tile path, d <= 16 the low-d ALU kernel) and
+with the fused Gram-MFMA kernels forced wherever they serve the shape, so the
+edge cases below reach the fused kernels too.
 """
 import numpy as np
 import pytest
@@ -18,6 +19,13 @@ from mlrs_amd import prims
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True, params=["auto", "fused"])
+def kernel_family(request):
+    prims.force_path(request.param)
+    yield request.param
+    prims.force_path("auto")
 
 
 def _t(a):
