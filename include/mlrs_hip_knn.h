@@ -159,6 +159,62 @@ int32_t mlrs_row_sqnorms_f32(const float *x, int64_t x_len, int64_t n, int64_t n
 int32_t mlrs_row_sqnorms_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features,
                              double *out, int64_t out_len, void *stream);
 
+/*
+ * kNN regressor prediction from a neighbour set (device-resident predict).
+ *
+ * Replaces: knn_regress_mean_gather (crates/mlrs-backend/src/prims/knn.rs:59-
+ *   150, kernel knn_regress_mean, crates/mlrs-kernels/src/knn.rs:95-147) for
+ *   weighted == 0 and n_outputs == 1, and knn_regress_gather_weighted
+ *   (prims/knn.rs:151-323, kernel knn_regress_gather, knn.rs:197-316)
+ *   otherwise.
+ * Layout: y_train is n_train x n_outputs row-major; idx / dist are the
+ *   n_query x k neighbour indices and TRUE distances of a search (dist is read
+ *   only when weighted != 0 and may be NULL otherwise); out is n_query x
+ *   n_outputs.  out = sum_j w_j y[idx_j] / sum_j w_j with w = 1 (uniform) or
+ *   1/d (weighted; a row with a zero distance weighs its zero-distance
+ *   neighbours 1 and the rest 0), both sums Neumaier-compensated.
+ * Errors, before any launch: ShapeMismatch "k" (k < 1, n_query < 1,
+ *   n_outputs < 1 or n_train < 1), "idx", "dist", "y_train", "n_query" /
+ *   "n_train" / "n_outputs" (> UINT32_MAX), "out".  After the gather (the call
+ *   synchronizes on `stream` to check): ShapeMismatch "knn.train_idx"
+ *   {rows = first query row holding an index >= n_train, cols = k,
+ *   len = n_train}; such an index contributes nothing.
+ */
+int32_t mlrs_knn_regress_f32(const float *y_train, int64_t y_len, int64_t n_train, int64_t n_outputs,
+                             const uint32_t *idx, int64_t idx_len, const float *dist, int64_t dist_len,
+                             int64_t n_query, int32_t k, int32_t weighted, float *out, int64_t out_len,
+                             void *stream);
+int32_t mlrs_knn_regress_f64(const double *y_train, int64_t y_len, int64_t n_train, int64_t n_outputs,
+                             const uint32_t *idx, int64_t idx_len, const double *dist, int64_t dist_len,
+                             int64_t n_query, int32_t k, int32_t weighted, double *out, int64_t out_len,
+                             void *stream);
+
+/*
+ * kNN classifier vote from a neighbour set (device-resident predict).
+ *
+ * Replaces: KNeighborsClassifier::predict_proba_host / predict_labels_host
+ *   (crates/mlrs-algos/src/neighbors/classifier.rs:782-930), the host f64
+ *   vote after the search.
+ * y_class holds each training row's DENSE class index (0..n_classes-1).
+ *   proba (n_query x n_classes) = per-class sums of the f64 weights (1, or 1/d
+ *   with the zero-distance indicator rule), divided by the row total (an
+ *   all-zero row is left at zero), cast to F; labels (n_query) = the argmax
+ *   over the F probabilities, lowest class index on a tie.
+ * Errors, before any launch: ShapeMismatch "k", "idx", "dist", "n_classes",
+ *   "proba", "labels".  After the vote (synchronizes on `stream`): the first
+ *   bad neighbour in row-major order gives ShapeMismatch "knn.train_idx"
+ *   {rows = the index, cols = 1, len = n_train} or "knn.class_id" {rows =
+ *   max(class, 0), cols = 1, len = n_classes}.
+ */
+int32_t mlrs_knn_classify_f32(const int32_t *y_class, int64_t n_train, int32_t n_classes, const uint32_t *idx,
+                              int64_t idx_len, const float *dist, int64_t dist_len, int64_t n_query, int32_t k,
+                              int32_t weighted, float *proba, int64_t proba_len, int32_t *labels,
+                              int64_t labels_len, void *stream);
+int32_t mlrs_knn_classify_f64(const int32_t *y_class, int64_t n_train, int32_t n_classes, const uint32_t *idx,
+                              int64_t idx_len, const double *dist, int64_t dist_len, int64_t n_query, int32_t k,
+                              int32_t weighted, double *proba, int64_t proba_len, int32_t *labels,
+                              int64_t labels_len, void *stream);
+
 /* Release the cached device workspace of the current device. */
 int32_t mlrs_release_workspace(void);
 

@@ -76,6 +76,12 @@ SIGNATURES = {
     "mlrs_pairwise_distance_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
     "mlrs_row_sqnorms_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "mlrs_row_sqnorms_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "mlrs_knn_regress_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
+    "mlrs_knn_regress_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
+    "mlrs_knn_classify_f32": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _i64,
+                                     _vp]),
+    "mlrs_knn_classify_f64": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _i64,
+                                     _vp]),
     "mlrs_release_workspace": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
     "mlrs_force_path": (_i32, [_i32]),

@@ -739,6 +739,131 @@ int32_t mlrs_row_sqnorms_f64(const double* x, int64_t x_len, int64_t n, int64_t 
     return sqnorms_impl<double>(x, x_len, n, n_features, out, out_len, stream);
 }
 
+// ---------------------------------------------------------------------------
+// kNN consumers: regressor gathers and classifier vote
+// ---------------------------------------------------------------------------
+extern "C++" {
+// Read back the lowest flagged row (UINT64_MAX when none) -- a synchronous
+// point, as in the reference, whose host raises right after its gather.
+static int32_t read_first_bad(const unsigned long long* dev_word, hipStream_t s, int64_t* row) {
+    unsigned long long h = ~0ull;
+    hipError_t e = hipMemcpyAsync(&h, dev_word, sizeof(h), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_err(e, "first_bad read-back");
+    *row = (h == ~0ull) ? -1 : (int64_t)h;
+    return MLRS_OK;
+}
+
+template <typename T>
+static int32_t regress_impl(const T* y, int64_t y_len, int64_t n_train, int64_t n_out, const uint32_t* idx,
+                            int64_t idx_len, const T* dist, int64_t dist_len, int64_t nq, int32_t k,
+                            int32_t weighted, T* out, int64_t out_len, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    // knn_regress_gather_weighted / knn_regress_mean_gather's checks
+    // (crates/mlrs-backend/src/prims/knn.rs:59-323)
+    if (k < 1 || nq < 1 || n_out < 1 || n_train < 1) return shape_err("k", nq, k, idx_len);
+    if (!geom_ok(nq, k, idx_len)) return shape_err("idx", nq, k, idx_len);
+    const bool general = weighted || n_out != 1;
+    if (general && dist_len != idx_len) return shape_err("dist", nq, k, dist_len);
+    if (!geom_ok(n_train, n_out, y_len)) return shape_err("y_train", n_train, n_out, y_len);
+    if (nq > kU32Max) return shape_err("n_query", nq, 0, kU32Max);
+    if (n_train > kU32Max) return shape_err("n_train", n_train, 0, kU32Max);
+    if (n_out > kU32Max) return shape_err("n_outputs", n_out, 0, kU32Max);
+    if (!geom_ok(nq, n_out, out_len)) return shape_err("out", nq, n_out, out_len);
+    if (!y || !idx || !out || (weighted && !dist)) return set_err(MLRS_ERR_NULL_POINTER, "ptr", 0, 0, 0, 0,
+                                                                 "a required pointer is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    char* ws;
+    int cus;
+    int32_t rc = workspace(256, s, &ws, &cus);
+    if (rc) return rc;
+    unsigned long long* first_bad = reinterpret_cast<unsigned long long*>(ws);
+    hipError_t e = launch_first_bad_reset(first_bad, s);
+    if (e == hipSuccess) e = launch_knn_regress<T>(y, n_train, n_out, idx, dist, nq, k, weighted, out, first_bad, s);
+    if (e != hipSuccess) return hip_err(e, "knn_regress");
+    int64_t row;
+    rc = read_first_bad(first_bad, s, &row);
+    if (rc) return rc;
+    if (row >= 0) return shape_err("knn.train_idx", row, k, n_train);
+    return ok();
+}
+
+template <typename T>
+static int32_t classify_impl(const int32_t* y_class, int64_t n_train, int32_t n_classes, const uint32_t* idx,
+                             int64_t idx_len, const T* dist, int64_t dist_len, int64_t nq, int32_t k,
+                             int32_t weighted, T* proba, int64_t proba_len, int32_t* labels, int64_t labels_len,
+                             void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (k < 1 || nq < 1 || n_train < 1) return shape_err("k", nq, k, idx_len);
+    if (!geom_ok(nq, k, idx_len)) return shape_err("idx", nq, k, idx_len);
+    if (weighted && dist_len != idx_len) return shape_err("dist", nq, k, dist_len);
+    if (n_classes < 1) return shape_err("n_classes", n_classes, 1, 0);
+    if (!geom_ok(nq, n_classes, proba_len)) return shape_err("proba", nq, n_classes, proba_len);
+    if (labels_len != nq) return shape_err("labels", nq, 1, labels_len);
+    if (!y_class || !idx || !proba || !labels || (weighted && !dist))
+        return set_err(MLRS_ERR_NULL_POINTER, "ptr", 0, 0, 0, 0, "a required pointer is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    // f64 class sums for a chunk of queries (<= 64 MB) + per-row error records
+    const int64_t chunk = std::max<int64_t>(256, std::min<int64_t>(nq, ((int64_t)64 << 20) / (8 * (int64_t)n_classes)));
+    const size_t bytes = aligned_bytes(sizeof(double) * (size_t)chunk * n_classes) +
+                         aligned_bytes(sizeof(int64_t) * 3 * (size_t)nq) + 512;
+    char* ws;
+    int cus;
+    int32_t rc = workspace(bytes, s, &ws, &cus);
+    if (rc) return rc;
+    Carver cv(ws);
+    unsigned long long* first_bad = cv.take<unsigned long long>(1);
+    double* acc = cv.take<double>((size_t)chunk * n_classes);
+    int64_t* err = cv.take<int64_t>(3 * (size_t)nq);
+    hipError_t e = launch_first_bad_reset(first_bad, s);
+    for (int64_t q0 = 0; e == hipSuccess && q0 < nq; q0 += chunk)
+        e = launch_knn_classify<T>(y_class, n_train, n_classes, idx, dist, q0, std::min(chunk, nq - q0), nq, k,
+                                   weighted, proba, labels, acc, err, first_bad, s);
+    if (e != hipSuccess) return hip_err(e, "knn_classify");
+    int64_t row;
+    rc = read_first_bad(first_bad, s, &row);
+    if (rc) return rc;
+    if (row >= 0) {
+        int64_t rec[3] = {0, 0, 0};
+        e = hipMemcpy(rec, err + 3 * row, sizeof(rec), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_err(e, "knn_classify error read-back");
+        // classifier.rs:850-875: the first bad (query, neighbour) in row order
+        if (rec[0] == 1) return shape_err("knn.train_idx", rec[1], 1, n_train);
+        return shape_err("knn.class_id", std::max<int64_t>(rec[1], 0), 1, n_classes);
+    }
+    return ok();
+}
+}  // extern "C++"
+
+int32_t mlrs_knn_regress_f32(const float* y_train, int64_t y_len, int64_t n_train, int64_t n_outputs,
+                             const uint32_t* idx, int64_t idx_len, const float* dist, int64_t dist_len,
+                             int64_t n_query, int32_t k, int32_t weighted, float* out, int64_t out_len,
+                             void* stream) {
+    return regress_impl<float>(y_train, y_len, n_train, n_outputs, idx, idx_len, dist, dist_len, n_query, k,
+                               weighted, out, out_len, stream);
+}
+int32_t mlrs_knn_regress_f64(const double* y_train, int64_t y_len, int64_t n_train, int64_t n_outputs,
+                             const uint32_t* idx, int64_t idx_len, const double* dist, int64_t dist_len,
+                             int64_t n_query, int32_t k, int32_t weighted, double* out, int64_t out_len,
+                             void* stream) {
+    return regress_impl<double>(y_train, y_len, n_train, n_outputs, idx, idx_len, dist, dist_len, n_query, k,
+                                weighted, out, out_len, stream);
+}
+int32_t mlrs_knn_classify_f32(const int32_t* y_class, int64_t n_train, int32_t n_classes, const uint32_t* idx,
+                              int64_t idx_len, const float* dist, int64_t dist_len, int64_t n_query, int32_t k,
+                              int32_t weighted, float* proba, int64_t proba_len, int32_t* labels,
+                              int64_t labels_len, void* stream) {
+    return classify_impl<float>(y_class, n_train, n_classes, idx, idx_len, dist, dist_len, n_query, k, weighted,
+                                proba, proba_len, labels, labels_len, stream);
+}
+int32_t mlrs_knn_classify_f64(const int32_t* y_class, int64_t n_train, int32_t n_classes, const uint32_t* idx,
+                              int64_t idx_len, const double* dist, int64_t dist_len, int64_t n_query, int32_t k,
+                              int32_t weighted, double* proba, int64_t proba_len, int32_t* labels,
+                              int64_t labels_len, void* stream) {
+    return classify_impl<double>(y_class, n_train, n_classes, idx, idx_len, dist, dist_len, n_query, k, weighted,
+                                 proba, proba_len, labels, labels_len, stream);
+}
+
 int32_t mlrs_force_path(int32_t path) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (path < MLRS_PATH_AUTO || path > MLRS_PATH_GENERIC)

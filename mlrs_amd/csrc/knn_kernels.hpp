@@ -200,4 +200,16 @@ hipError_t launch_lowd_f32(const LowdArgs32& a, int arm, hipStream_t s);
 int lowd_max_d();
 int lowd_max_k();
 
+// kNN consumers (knn_consumers.hip).
+hipError_t launch_first_bad_reset(unsigned long long* first_bad, hipStream_t s);
+template <typename T>
+hipError_t launch_knn_regress(const T* y, int64_t n_train, int64_t n_out, const uint32_t* idx, const T* dist,
+                              int64_t nq, int64_t k, int weighted, T* out, unsigned long long* first_bad,
+                              hipStream_t s);
+template <typename T>
+hipError_t launch_knn_classify(const int32_t* y_class, int64_t n_train, int64_t n_classes, const uint32_t* idx,
+                               const T* dist, int64_t q0, int64_t rows, int64_t nq, int64_t k, int weighted,
+                               T* proba, int32_t* labels, double* acc, int64_t* err, unsigned long long* first_bad,
+                               hipStream_t s);
+
 }  // namespace mlrs

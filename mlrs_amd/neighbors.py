@@ -1,5 +1,6 @@
-"""``NearestNeighbors`` over the HIP engine -- the brute-force kNN estimator
-surface of ``mlrs.neighbors`` (crates/mlrs-py/python/mlrs/neighbors.py).
+"""``NearestNeighbors``, ``KNeighborsRegressor`` and ``KNeighborsClassifier``
+over the HIP engine -- the brute-force kNN estimator surface of
+``mlrs.neighbors`` (crates/mlrs-py/python/mlrs/neighbors.py).
 
 Same parameter names, metric resolution, validation order and error messages
 as the reference shim for the metrics the engine serves (Euclidean and its
@@ -10,6 +11,13 @@ drops each row's own index by identity, not by position or distance
 Inputs may be numpy arrays or torch tensors; the training matrix is uploaded
 once at ``fit`` and stays resident in HBM.  Results come back as numpy arrays
 for numpy input and as device tensors for tensor input.
+
+The regressor and classifier predict on the device end to end: the search,
+then the neighbour-target gather (knn_regress_mean / knn_regress_gather) or
+the class vote (the reference's host f64 vote, restated as a kernel).  A
+callable ``weights`` and a multi-output classification target are served on
+the host from the same neighbour set, as the reference shim does
+(neighbors.py:914-1036).
 """
 import warnings
 
@@ -105,21 +113,10 @@ def _check_finite(t):
                          % str(t.dtype).replace("torch.", ""))
 
 
-class NearestNeighbors:
-    """Brute-force neighbour search (mlrs.neighbors.NearestNeighbors)."""
+class _NeighborsBase:
+    """Shared fit / kneighbors machinery (neighbors.py:241-688)."""
 
-    def __init__(self, n_neighbors=5, output_type="input", *, radius=1.0, algorithm="auto", leaf_size=30,
-                 metric="minkowski", p=2, metric_params=None, n_jobs=None, device="auto"):
-        self.n_neighbors = n_neighbors
-        self.output_type = output_type
-        self.radius = radius
-        self.algorithm = algorithm
-        self.leaf_size = leaf_size
-        self.metric = metric
-        self.p = p
-        self.metric_params = metric_params
-        self.n_jobs = n_jobs
-        self.device = device
+    radius = 1.0
 
     # -- validation (neighbors.py:285-338) --
     def _validate_params_for_fit(self):
@@ -142,7 +139,7 @@ class NearestNeighbors:
         if not isinstance(self.radius, (int, float, np.integer, np.floating)) or self.radius < 0:
             raise ValueError("radius must be non-negative, got %r" % (self.radius,))
 
-    def fit(self, X, y=None):
+    def _fit_X_only(self, X):
         self._validate_params_for_fit()
         eff, params, eff_p = _resolve_metric(self.metric, self.p, self.metric_params)
         engine_metric = _ENGINE_METRIC.get(eff)
@@ -156,12 +153,12 @@ class NearestNeighbors:
         self.n_samples_fit_ = t.shape[0]
         self.effective_metric_ = eff
         self.effective_metric_params_ = params
-        return self
+        return t
 
     def _check_fitted(self):
         if not hasattr(self, "_fit_X_dev"):
-            raise ValueError("This NearestNeighbors instance is not fitted yet. Call 'fit' with "
-                             "appropriate arguments before using this estimator.")
+            raise ValueError("This %s instance is not fitted yet. Call 'fit' with "
+                             "appropriate arguments before using this estimator." % type(self).__name__)
 
     @property
     def _fit_X(self):
@@ -183,6 +180,19 @@ class NearestNeighbors:
         dist, idx = prims.knn_topk(Xq, self._fit_X_dev, k, self._engine_metric)
         return dist, idx.to(torch.int32)
 
+    def _check_query(self, q):
+        if q.shape[1] != self.n_features_in_:
+            raise ValueError("X has %d features, but %s is expecting %d features as input"
+                             % (q.shape[1], type(self).__name__, self.n_features_in_))
+        _check_finite(q)
+
+    def _query(self, X):
+        """(device query matrix, was_numpy) for a predict call."""
+        self._check_fitted()
+        q, was_numpy = _as_device_matrix(X, dtype=self._fit_X_dev.dtype, device=self._fit_X_dev.device)
+        self._check_query(q)
+        return q, was_numpy
+
     def kneighbors(self, X=None, n_neighbors=None, return_distance=True):
         self._check_fitted()
         query_is_train = X is None
@@ -191,10 +201,7 @@ class NearestNeighbors:
             q, was_numpy = self._fit_X_dev, True
         else:
             q, was_numpy = _as_device_matrix(X, dtype=self._fit_X_dev.dtype, device=self._fit_X_dev.device)
-            if q.shape[1] != self.n_features_in_:
-                raise ValueError("X has %d features, but NearestNeighbors is expecting %d features as input"
-                                 % (q.shape[1], self.n_features_in_))
-            _check_finite(q)
+            self._check_query(q)
         dist, idx = self._raw_kneighbors(q, k_query)
         if query_is_train or was_numpy:
             dist_np = dist.cpu().numpy()
@@ -207,6 +214,216 @@ class NearestNeighbors:
         if not return_distance:
             return idx
         return dist, idx
+
+
+class NearestNeighbors(_NeighborsBase):
+    """Brute-force neighbour search (mlrs.neighbors.NearestNeighbors)."""
+
+    def __init__(self, n_neighbors=5, output_type="input", *, radius=1.0, algorithm="auto", leaf_size=30,
+                 metric="minkowski", p=2, metric_params=None, n_jobs=None, device="auto"):
+        self.n_neighbors = n_neighbors
+        self.output_type = output_type
+        self.radius = radius
+        self.algorithm = algorithm
+        self.leaf_size = leaf_size
+        self.metric = metric
+        self.p = p
+        self.metric_params = metric_params
+        self.n_jobs = n_jobs
+        self.device = device
+
+    def fit(self, X, y=None):
+        self._fit_X_only(X)
+        return self
+
+
+def _get_weights(dist, weights):
+    """sklearn ``_get_weights`` on host arrays (neighbors.py:174-199): None for
+    uniform, 1/d with the coincident-row indicator rule, or the callable's."""
+    if weights == "uniform":
+        return None
+    if weights == "distance":
+        with np.errstate(divide="ignore"):
+            w = 1.0 / dist
+        inf_mask = np.isinf(w)
+        inf_row = np.any(inf_mask, axis=1)
+        w[inf_row] = inf_mask[inf_row]
+        return w
+    return weights(dist)
+
+
+def _check_weights(weights):
+    if weights in ("uniform", "distance") or callable(weights):
+        return weights
+    raise ValueError("weights not recognized: should be 'uniform', 'distance', or a callable function")
+
+
+def _out(t, was_numpy):
+    return t.cpu().numpy() if was_numpy else t
+
+
+class KNeighborsRegressor(_NeighborsBase):
+    """k-NN regression (mlrs.neighbors.KNeighborsRegressor, neighbors.py:1036-1156):
+    the weighted mean of each query's k neighbour targets, formed on the device."""
+
+    def __init__(self, n_neighbors=5, output_type="input", *, weights="uniform", algorithm="auto", leaf_size=30,
+                 p=2, metric="minkowski", metric_params=None, n_jobs=None, device="auto"):
+        self.n_neighbors = n_neighbors
+        self.output_type = output_type
+        self.weights = weights
+        self.algorithm = algorithm
+        self.leaf_size = leaf_size
+        self.p = p
+        self.metric = metric
+        self.metric_params = metric_params
+        self.n_jobs = n_jobs
+        self.device = device
+
+    def fit(self, X, y):
+        _check_weights(self.weights)
+        t = self._fit_X_only(X)
+        yt = y if isinstance(y, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(np.asarray(y)))
+        if yt.dim() == 2 and yt.shape[1] == 1:
+            yt = yt.reshape(-1)
+        if yt.dim() not in (1, 2) or yt.shape[0] != t.shape[0]:
+            raise ValueError("Found input variables with inconsistent numbers of samples: [%d, %d]"
+                             % (t.shape[0], yt.shape[0]))
+        self._y_dev = yt.to(device=t.device, dtype=t.dtype).contiguous()
+        _check_finite(self._y_dev.reshape(-1, 1))
+        return self
+
+    @property
+    def _y(self):
+        self._check_fitted()
+        return self._y_dev.cpu().numpy()
+
+    def predict(self, X):
+        q, was_numpy = self._query(X)
+        k = int(self.n_neighbors)
+        if k > self.n_samples_fit_:
+            raise ValueError("Expected n_neighbors <= n_samples_fit, but n_neighbors = %d, n_samples_fit = %d"
+                             % (k, self.n_samples_fit_))
+        dist, idx = self._raw_kneighbors(q, k)
+        if callable(self.weights):
+            d = dist.double().cpu().numpy()
+            i = (idx.to(torch.int64) & 0xFFFFFFFF).cpu().numpy()
+            w = _get_weights(d, self.weights)
+            yn = self._y[i]
+            if w is None:
+                pred = np.mean(yn, axis=1)
+            elif yn.ndim == 3:
+                pred = np.sum(yn * w[:, :, None], axis=1) / np.sum(w, axis=1)[:, None]
+            else:
+                pred = np.sum(yn * w, axis=1) / np.sum(w, axis=1)
+            pred = torch.from_numpy(np.ascontiguousarray(pred.astype(self._y.dtype))).to(q.device)
+        else:
+            pred = prims.knn_regress(self._y_dev, idx, dist, weighted=self.weights == "distance")
+        return _out(pred, was_numpy)
+
+
+class KNeighborsClassifier(_NeighborsBase):
+    """k-NN classification (mlrs.neighbors.KNeighborsClassifier, neighbors.py:767-1033):
+    labels are encoded to dense codes here (np.unique), the vote runs on the
+    device and the argmax code is mapped back through ``classes_``."""
+
+    def __init__(self, n_neighbors=5, output_type="input", *, weights="uniform", algorithm="auto", leaf_size=30,
+                 p=2, metric="minkowski", metric_params=None, n_jobs=None, device="auto"):
+        self.n_neighbors = n_neighbors
+        self.output_type = output_type
+        self.weights = weights
+        self.algorithm = algorithm
+        self.leaf_size = leaf_size
+        self.p = p
+        self.metric = metric
+        self.metric_params = metric_params
+        self.n_jobs = n_jobs
+        self.device = device
+
+    def fit(self, X, y):
+        _check_weights(self.weights)
+        t = self._fit_X_only(X)
+        y = np.asarray(y.cpu().numpy() if isinstance(y, torch.Tensor) else y)
+        if y.ndim == 2 and y.shape[1] == 1:
+            warnings.warn("A column-vector y was passed when a 1d array was expected. Please change the shape "
+                          "of y to (n_samples,), for example using ravel().", UserWarning, stacklevel=2)
+            y = y.ravel()
+        if y.shape[0] != t.shape[0]:
+            raise ValueError("Found input variables with inconsistent numbers of samples: [%d, %d]"
+                             % (t.shape[0], y.shape[0]))
+        self.outputs_2d_ = y.ndim == 2
+        y2 = y.reshape(-1, 1) if not self.outputs_2d_ else y
+        classes, codes = [], np.empty(y2.shape, dtype=np.int64)
+        for col in range(y2.shape[1]):
+            cls, inv = np.unique(y2[:, col], return_inverse=True)
+            classes.append(cls)
+            codes[:, col] = np.asarray(inv).ravel()
+        self.classes_ = classes if self.outputs_2d_ else classes[0]
+        self._codes = codes if self.outputs_2d_ else codes.ravel()
+        self._codes_dev = torch.from_numpy(np.ascontiguousarray(codes[:, 0].astype(np.int32))).to(t.device)
+        return self
+
+    @property
+    def _y(self):
+        self._check_fitted()
+        return self._codes
+
+    def _neighbours(self, q):
+        k = int(self.n_neighbors)
+        if k > self.n_samples_fit_:
+            raise ValueError("Expected n_neighbors <= n_samples_fit, but n_neighbors = %d, n_samples_fit = %d"
+                             % (k, self.n_samples_fit_))
+        return self._raw_kneighbors(q, k)
+
+    def _host_proba(self, dist, idx):
+        """sklearn's predict_proba body on host arrays (neighbors.py:914-955)."""
+        d = dist.double().cpu().numpy()
+        i = (idx.to(torch.int64) & 0xFFFFFFFF).cpu().numpy()
+        w = _get_weights(d, self.weights)
+        if w is None:
+            w = np.ones_like(i, dtype=np.float64)
+        elif np.any(np.all(w == 0, axis=1)):
+            raise ValueError("All neighbors of some sample is getting zero weights. "
+                             "Please modify 'weights' to avoid this case.")
+        classes_ = self.classes_ if self.outputs_2d_ else [self.classes_]
+        codes = self._codes if self.outputs_2d_ else self._codes.reshape(-1, 1)
+        rows = np.arange(i.shape[0])
+        out = []
+        for kk, classes_k in enumerate(classes_):
+            lab = codes[:, kk][i]
+            proba = np.zeros((i.shape[0], classes_k.size), dtype=np.float64)
+            for j, col in enumerate(lab.T):
+                proba[rows, col] += w[:, j]
+            norm = proba.sum(axis=1)[:, None]
+            norm[norm == 0.0] = 1.0
+            out.append(proba / norm)
+        return out
+
+    def _needs_host_vote(self):
+        return self.outputs_2d_ or callable(self.weights)
+
+    def predict(self, X):
+        q, was_numpy = self._query(X)
+        dist, idx = self._neighbours(q)
+        if self._needs_host_vote():
+            probas = self._host_proba(dist, idx)
+            classes_ = self.classes_ if self.outputs_2d_ else [self.classes_]
+            out = np.stack([c.take(np.argmax(pk, axis=1)) for c, pk in zip(classes_, probas)], axis=1)
+            return out if self.outputs_2d_ else out.ravel()
+        _, labels = prims.knn_classify(self._codes_dev, len(self.classes_), idx, dist,
+                                       weighted=self.weights == "distance", dtype=q.dtype)
+        return self.classes_.take(labels.cpu().numpy())
+
+    def predict_proba(self, X):
+        q, was_numpy = self._query(X)
+        dist, idx = self._neighbours(q)
+        if self._needs_host_vote():
+            probas = self._host_proba(dist, idx)
+            if self.outputs_2d_:
+                return probas
+            return probas[0].astype(np.float32 if q.dtype == torch.float32 else np.float64)
+        proba, _ = prims.knn_classify(self._codes_dev, len(self.classes_), idx, dist,
+                                      weighted=self.weights == "distance", dtype=q.dtype)
+        return _out(proba, was_numpy)
 
 
 def kneighbors(X_train, X_query, k, metric="euclidean"):

@@ -142,3 +142,63 @@ def row_sqnorms(x, out=None):
                                                _stream(x.device))
     _lib.check(rc)
     return o
+
+
+def _as_u32_idx(idx):
+    """Neighbour indices as a contiguous int32 tensor holding the uint32 bits."""
+    if idx.dtype == torch.int32:
+        return idx.contiguous()
+    if idx.dtype == torch.int64:
+        return (idx & 0xFFFFFFFF).to(torch.int32).contiguous() if idx.numel() else idx.to(torch.int32)
+    raise TypeError("neighbour indices must be int32 or int64, got %s" % idx.dtype)
+
+
+def knn_regress(y_train, idx, dist=None, weighted=False):
+    """Neighbour-target prediction on the device (mlrs_knn_regress_*).
+
+    ``y_train``: (n_train,) or (n_train, n_outputs); ``idx``/``dist``: the
+    (n_query, k) indices and true distances of a search (``dist`` needed only
+    when ``weighted``).  Returns (n_query,) or (n_query, n_outputs)."""
+    _dev_check(y_train)
+    s = _suffix(y_train)
+    multi = y_train.dim() == 2
+    n_train = y_train.shape[0]
+    n_out = y_train.shape[1] if multi else 1
+    idx32 = _as_u32_idx(idx)
+    nq, k = idx32.shape
+    d = None
+    if dist is not None:
+        d = dist.to(y_train.dtype).contiguous()
+        _dev_check(d)
+    out = torch.empty((nq, n_out) if multi else (nq,), dtype=y_train.dtype, device=y_train.device)
+    lib = _lib.load()
+    rc = getattr(lib, "mlrs_knn_regress_" + s)(
+        _ptr(y_train), y_train.numel(), n_train, n_out, _ptr(idx32), idx32.numel(), _ptr(d),
+        d.numel() if d is not None else 0, nq, int(k), int(bool(weighted)), _ptr(out), out.numel(),
+        _stream(y_train.device))
+    _lib.check(rc)
+    return out
+
+
+def knn_classify(y_class, n_classes, idx, dist=None, weighted=False, dtype=torch.float32):
+    """The classifier vote on the device (mlrs_knn_classify_*): ``y_class``
+    holds each training row's dense class index; returns
+    ``(proba (n_query, n_classes) in dtype, dense labels int64)``."""
+    yc = y_class.to(torch.int32).contiguous()
+    _dev_check(yc)
+    idx32 = _as_u32_idx(idx)
+    nq, k = idx32.shape
+    d = None
+    if dist is not None:
+        d = dist.to(dtype).contiguous()
+        _dev_check(d)
+    proba = torch.empty((nq, int(n_classes)), dtype=dtype, device=yc.device)
+    labels = torch.empty(nq, dtype=torch.int32, device=yc.device)
+    s = "f32" if dtype == torch.float32 else "f64"
+    lib = _lib.load()
+    rc = getattr(lib, "mlrs_knn_classify_" + s)(
+        _ptr(yc), yc.numel(), int(n_classes), _ptr(idx32), idx32.numel(), _ptr(d),
+        d.numel() if d is not None else 0, nq, int(k), int(bool(weighted)), _ptr(proba), proba.numel(),
+        _ptr(labels), labels.numel(), _stream(yc.device))
+    _lib.check(rc)
+    return proba, labels.to(torch.int64)

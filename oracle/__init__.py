@@ -56,6 +56,15 @@ def _load():
         f = getattr(lib, "orc_row_sqnorms_" + s)
         f.argtypes = [vp, i64, i64, vp]
         f.restype = None
+        f = getattr(lib, "orc_knn_regress_mean_" + s)
+        f.argtypes = [vp, i64, vp, i64, i64, vp, vp]
+        f.restype = None
+        f = getattr(lib, "orc_knn_regress_gather_" + s)
+        f.argtypes = [vp, i64, i64, vp, vp, i64, i64, i32, vp, vp]
+        f.restype = None
+        f = getattr(lib, "orc_knn_classify_" + s)
+        f.argtypes = [vp, i64, i64, vp, vp, i64, i64, i32, vp, vp, vp, vp, vp]
+        f.restype = i32
     _lib = lib
     return lib
 
@@ -142,3 +151,56 @@ def row_sqnorms(x):
     out = np.empty(n, dtype=x.dtype)
     getattr(lib, "orc_row_sqnorms_" + _suffix(x.dtype))(x.ctypes.data, n, d, out.ctypes.data)
     return out
+
+
+def _sfx(dtype):
+    return "f32" if np.dtype(dtype) == np.float32 else "f64"
+
+
+def knn_regress(y_train, idx, dist=None, weighted=False):
+    """Neighbour-target prediction (knn_regress_mean for the uniform
+    single-output case, knn_regress_gather otherwise).  ``y_train`` is
+    (n_train,) or (n_train, n_outputs); ``idx``/``dist`` are (n_query, k).
+    Returns (prediction, oob_flags)."""
+    lib = _load()
+    y = np.ascontiguousarray(y_train)
+    multi = y.ndim == 2
+    n_train = y.shape[0]
+    n_out = y.shape[1] if multi else 1
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    nq, k = idx.shape
+    out = np.empty((nq, n_out), dtype=y.dtype)
+    oob = np.empty(nq, dtype=np.uint32)
+    s = _sfx(y.dtype)
+    if not weighted and not multi:
+        getattr(lib, "orc_knn_regress_mean_" + s)(y.ctypes.data, n_train, idx.ctypes.data, nq, k,
+                                                  out.ctypes.data, oob.ctypes.data)
+    else:
+        d = None if dist is None else np.ascontiguousarray(dist, dtype=y.dtype)
+        getattr(lib, "orc_knn_regress_gather_" + s)(y.ctypes.data, n_train, n_out, idx.ctypes.data,
+                                                    None if d is None else d.ctypes.data, nq, k,
+                                                    int(bool(weighted)), out.ctypes.data, oob.ctypes.data)
+    return (out if multi else out.ravel()), oob
+
+
+def knn_classify(y_class, n_classes, idx, dist=None, weighted=False, dtype=np.float32):
+    """The classifier vote: (proba (n_query, n_classes) in ``dtype``, dense
+    labels (n_query,) int32).  Raises IndexError on a bad neighbour index or
+    class id, naming (kind, value, query, slot)."""
+    lib = _load()
+    yc = np.ascontiguousarray(y_class, dtype=np.int32)
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    nq, k = idx.shape
+    proba = np.empty((nq, n_classes), dtype=dtype)
+    labels = np.empty(nq, dtype=np.int32)
+    acc = np.empty(max(n_classes, 1), dtype=np.float64)
+    w = np.empty(max(k, 1), dtype=np.float64)
+    err = np.zeros(4, dtype=np.int64)
+    d = None if dist is None else np.ascontiguousarray(dist, dtype=dtype)
+    rc = getattr(lib, "orc_knn_classify_" + _sfx(dtype))(
+        yc.ctypes.data, yc.size, n_classes, idx.ctypes.data, None if d is None else d.ctypes.data, nq, k,
+        int(bool(weighted)), proba.ctypes.data, labels.ctypes.data, acc.ctypes.data, w.ctypes.data,
+        err.ctypes.data)
+    if rc:
+        raise IndexError(("train_idx" if err[0] == 1 else "class_id", int(err[1]), int(err[2]), int(err[3])))
+    return proba, labels
