@@ -39,9 +39,13 @@ extern "C" {
 #define MLRS_ERR_HIP (-5)            /* a HIP runtime call failed (hip_error holds it) */
 #define MLRS_ERR_ALLOC (-6)          /* device workspace allocation failed */
 
-/* ---- metrics: the Metric enum of crates/mlrs-backend/src/prims/knn_graph.rs:61-75 ---- */
+/* ---- metrics: the variants of the Metric enum of crates/mlrs-backend/src/prims/knn_graph.rs:61-75
+ *      (numbered here, not in the enum's declaration order) ---- */
 #define MLRS_METRIC_EUCLIDEAN 0
 #define MLRS_METRIC_COSINE 1
+#define MLRS_METRIC_MANHATTAN 2
+#define MLRS_METRIC_CHEBYSHEV 3
+#define MLRS_METRIC_MINKOWSKI 4 /* exponent in the `p` argument, p >= 1 */
 
 typedef struct mlrs_error_info {
     int32_t code;        /* the MLRS_ERR_* value returned */
@@ -59,7 +63,7 @@ int32_t mlrs_last_error(mlrs_error_info *out);
 const char *mlrs_status_string(int32_t code);
 /* ABI version of this header (bumped on any signature change). */
 int32_t mlrs_abi_version(void);
-#define MLRS_ABI_VERSION 1
+#define MLRS_ABI_VERSION 2
 
 /*
  * Brute-force k nearest training rows of every query row.
@@ -73,8 +77,12 @@ int32_t mlrs_abi_version(void);
  * Layout: xq is n_query x n_features, x_train n_train x n_features, both
  *   row-major; out_dist / out_idx are n_query x k row-major, each row ascending
  *   by (distance, index).  Distances are TRUE distances (Euclidean: the root of
- *   the selected squared values; cosine: 1 - cos, clamped to [0, 2]).  A slot
- *   no admissible (non-NaN) candidate filled holds (+inf, 0).
+ *   the selected squared values; cosine: 1 - cos, clamped to [0, 2];
+ *   Manhattan: sum |x-y|; Chebyshev: max |x-y| by select, NaN never replacing;
+ *   Minkowski: (sum |x-y|^p)^(1/p), |x-y|^p by a multiply chain for an integer
+ *   p in 3..8 (minkowski_powi, prims/knn.rs:680-687), pow otherwise, and the
+ *   root pow(v, (F)(1/p)) on the selected values).  A slot no admissible
+ *   (non-NaN) candidate filled holds (+inf, 0).
  * Errors (checked in this order, before any launch, mirroring
  *   cpu_metric_rows_topk / knn_host_topk):
  *   ShapeMismatch "x"        n_query*n_features != xq_len
@@ -83,8 +91,9 @@ int32_t mlrs_abi_version(void);
  *   ShapeMismatch "features" n_features < 1
  *   ShapeMismatch "rows"     n_query or n_train > UINT32_MAX
  *   ShapeMismatch "out"      out_len != n_query*k
- *   MLRS_ERR_UNSUPPORTED     metric not served, or k above mlrs_knn_max_k()
- * `p` is the Minkowski exponent and is ignored by the two metrics served.
+ *   MLRS_ERR_UNSUPPORTED     metric not served, k above mlrs_knn_max_k(), or a
+ *                            Minkowski p below 1 (or NaN)
+ * `p` is the Minkowski exponent, ignored by the other metrics.
  */
 int32_t mlrs_knn_topk_f32(const float *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
                           const float *x_train, int64_t xt_len, int64_t n_train, int32_t k,
@@ -133,16 +142,20 @@ int32_t mlrs_kmeans_assign_f64(const double *x, int64_t x_len, int64_t n, int64_
  *   sqrt_elem (crates/mlrs-kernels/src/elementwise.rs:131-136) when
  *   do_sqrt != 0 -- and metric_distance's cosine_dist
  *   (crates/mlrs-kernels/src/distance.rs:257-310) for MLRS_METRIC_COSINE.
+ *   MLRS_METRIC_MANHATTAN / _CHEBYSHEV / _MINKOWSKI are manhattan_dist,
+ *   chebyshev_dist and minkowski_dist (distance.rs:67-227; Minkowski with pow
+ *   per feature and the root pow(acc, 1/p) with 1/p formed in F); do_sqrt is
+ *   ignored for them, p is read for Minkowski only.
  * Errors (validate_geometry, prims/distance.rs:260-302):
  *   ShapeMismatch "x" / "y", DimMismatch "cols", ShapeMismatch "out".
  */
 int32_t mlrs_pairwise_distance_f32(const float *x, int64_t x_len, int64_t rows_x, int64_t cols,
                                    const float *y, int64_t y_len, int64_t rows_y, int64_t cols_y,
-                                   int32_t metric, int32_t do_sqrt, float *out, int64_t out_len,
+                                   int32_t metric, int32_t do_sqrt, double p, float *out, int64_t out_len,
                                    void *stream);
 int32_t mlrs_pairwise_distance_f64(const double *x, int64_t x_len, int64_t rows_x, int64_t cols,
                                    const double *y, int64_t y_len, int64_t rows_y, int64_t cols_y,
-                                   int32_t metric, int32_t do_sqrt, double *out, int64_t out_len,
+                                   int32_t metric, int32_t do_sqrt, double p, double *out, int64_t out_len,
                                    void *stream);
 
 /*

@@ -19,6 +19,9 @@ MLRS_ERR_ALLOC = -6
 
 METRIC_EUCLIDEAN = 0
 METRIC_COSINE = 1
+METRIC_MANHATTAN = 2
+METRIC_CHEBYSHEV = 3
+METRIC_MINKOWSKI = 4
 
 
 class ErrorInfo(ctypes.Structure):
@@ -72,8 +75,10 @@ SIGNATURES = {
     "mlrs_knn_max_k": (_i32, [_i32, _i64, _i32]),
     "mlrs_kmeans_assign_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mlrs_kmeans_assign_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
-    "mlrs_pairwise_distance_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
-    "mlrs_pairwise_distance_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
+    "mlrs_pairwise_distance_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _f64, _vp, _i64,
+                                          _vp]),
+    "mlrs_pairwise_distance_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _f64, _vp, _i64,
+                                          _vp]),
     "mlrs_row_sqnorms_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "mlrs_row_sqnorms_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "mlrs_knn_regress_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),

@@ -177,10 +177,22 @@ void clear_timed() {
 // crates/mlrs-algos/src/neighbors/nearest.rs:910-947 with the caps of
 // cpu_rows_applicable (prims/knn.rs:400-412: d <= 32, k <= 16) and
 // cpu_metric_rows_applicable (prims/knn.rs:703-720: d <= 128, k <= 128).
-int knn_arm(int64_t d, int64_t k, int metric) {
+// minkowski_powi (crates/mlrs-backend/src/prims/knn.rs:680-687): an integer p
+// in 3..8 runs a multiply chain, anything else pow.
+static int minkowski_powi(double p) {
+    const double pf = std::floor(p);
+    return (p == pf && pf >= 3.0 && pf <= 8.0) ? (int)pf : 0;
+}
+
+int knn_arm(int64_t d, int64_t k, int metric, double p = 2.0) {
     const bool metric_family = d >= 1 && d <= 128 && k >= 1 && k <= 128;
-    if (metric == MLRS_METRIC_EUCLIDEAN) return metric_family ? ARM_EUCLID_FMA : ARM_EUCLID_MULADD;
-    return metric_family ? ARM_COS_FOLD : ARM_COS_HOST;
+    switch (metric) {
+    case MLRS_METRIC_EUCLIDEAN: return metric_family ? ARM_EUCLID_FMA : ARM_EUCLID_MULADD;
+    case MLRS_METRIC_COSINE: return metric_family ? ARM_COS_FOLD : ARM_COS_HOST;
+    case MLRS_METRIC_MANHATTAN: return ARM_MANHATTAN;    // one arithmetic on every arm
+    case MLRS_METRIC_CHEBYSHEV: return ARM_CHEBYSHEV;
+    default: return minkowski_powi(p) ? ARM_MINKOWSKI_INT : ARM_MINKOWSKI_POW;
+    }
 }
 
 // Split the index axis so the grid has enough workgroups to fill the chip,
@@ -226,7 +238,7 @@ int pick_strips_xcd(int64_t nblocks, int64_t nt, int64_t slots_per_xcd, int64_t 
 // ---------------------------------------------------------------------------
 template <typename T>
 int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, int k, int arm, int mode,
-                    T* out_v, uint32_t* out_i, hipStream_t s) {
+                    T* out_v, uint32_t* out_i, hipStream_t s, double p = 2.0) {
     if (k > select_rows_max_k())
         return set_err(MLRS_ERR_UNSUPPORTED, "k", 1, k, nt, 0, "k=%d above the largest k served (%d)", k,
                        select_rows_max_k());
@@ -266,11 +278,17 @@ int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d,
         {
             KernelTimer timer(s, "pairwise_tile_kernel");
             e = launch_pairwise_tile<T>(xq + q0 * d, rows, xt, nt, d, arm, cos ? qa + q0 : nullptr, xa, dist,
-                                        nt, 0, s);
+                                        nt, 0, s, (T)p, minkowski_powi(p));
         }
         if (e == hipSuccess)
             e = launch_select_rows<T>(dist, rows, nt, nt, k, mode, out_v + q0 * k, out_i + q0 * k, s);
         if (e != hipSuccess) return hip_err(e, "generic kNN");
+    }
+    // Minkowski's boundary root over the emitted values, exponent
+    // f64_to_host(1/p) (prims/knn.rs:882-888)
+    if (arm == ARM_MINKOWSKI_INT || arm == ARM_MINKOWSKI_POW) {
+        hipError_t e = launch_pow_inplace<T>(out_v, nq * k, (T)(1.0 / p), s);
+        if (e != hipSuccess) return hip_err(e, "minkowski root");
     }
     return ok();
 }
@@ -527,7 +545,7 @@ int32_t validate_knn(const T* xq, int64_t xq_len, int64_t nq, int64_t d, const T
     if (d < 1) return shape_err("features", d, 0, 0);
     if (nq > kU32Max || nt > kU32Max) return shape_err("rows", std::max(nq, nt), 0, kU32Max);
     if (!geom_ok(nq, k, out_len)) return shape_err("out", nq, k, out_len);
-    if (metric != MLRS_METRIC_EUCLIDEAN && metric != MLRS_METRIC_COSINE)
+    if (metric < MLRS_METRIC_EUCLIDEAN || metric > MLRS_METRIC_MINKOWSKI)
         return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0, "metric %d is not served", metric);
     if (nq > 0 && (!xq || !ov || !oi)) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
     if (!xt) return set_err(MLRS_ERR_NULL_POINTER, "y", 0, 0, 0, 0, "null pointer");
@@ -571,17 +589,19 @@ int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric) 
 int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
                           const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
                           double p, float* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
-    (void)p;
     std::lock_guard<std::mutex> lk(g_mu);
     int32_t rc = validate_knn<float>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
                                      out_dist, out_idx, out_len);
     if (rc) return rc;
+    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0))
+        return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
     if (n_query == 0) return MLRS_OK;
     hipStream_t s = (hipStream_t)stream;
-    const int arm = knn_arm(n_features, k, metric);
+    const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
     const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
-    const bool gram_ok = arm != ARM_COS_HOST && n_features <= gram_f32_max_d() && k <= gram_f32_max_k();
+    const bool gram_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD || arm == ARM_COS_FOLD) &&
+                         n_features <= gram_f32_max_d() && k <= gram_f32_max_k();
     int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)
         path = lowd_ok ? MLRS_PATH_LOWD
@@ -590,28 +610,29 @@ int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int6
         return knn_lowd32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     if (path == MLRS_PATH_FUSED)
         return knn_gram32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
-    return knn_generic<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+    return knn_generic<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s, p);
 }
 
 int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
                           const double* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
                           double p, double* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
-    (void)p;
     std::lock_guard<std::mutex> lk(g_mu);
     int32_t rc = validate_knn<double>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
                                       out_dist, out_idx, out_len);
     if (rc) return rc;
+    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0))
+        return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
     if (n_query == 0) return MLRS_OK;
     hipStream_t s = (hipStream_t)stream;
-    const int arm = knn_arm(n_features, k, metric);
+    const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
-    const bool gram_ok = n_features <= gram_f64_max_d() && k <= gram_f64_max_k();
+    const bool gram_ok = arm <= ARM_COS_HOST && n_features <= gram_f64_max_d() && k <= gram_f64_max_k();
     int path = pick_path(false, gram_ok);
     if (path == MLRS_PATH_AUTO)
         path = (gram_ok && !small_search(n_query, n_train, n_features)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
     if (path == MLRS_PATH_FUSED)
         return knn_gram64(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
-    return knn_generic<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+    return knn_generic<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s, p);
 }
 
 extern "C++" {
@@ -663,15 +684,17 @@ int32_t mlrs_kmeans_assign_f64(const double* x, int64_t x_len, int64_t n, int64_
 extern "C++" {
 template <typename T>
 static int32_t pairwise_impl(const T* x, int64_t x_len, int64_t rows_x, int64_t cols, const T* y, int64_t y_len,
-                             int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt, T* out,
+                             int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt, double p, T* out,
                              int64_t out_len, void* stream) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!geom_ok(rows_x, cols, x_len)) return shape_err("x", rows_x, cols, x_len);
     if (!geom_ok(rows_y, cols_y, y_len)) return shape_err("y", rows_y, cols_y, y_len);
     if (cols != cols_y) return dim_err("cols", cols, cols_y);
     if (!geom_ok(rows_x, rows_y, out_len)) return shape_err("out", rows_x, rows_y, out_len);
-    if (metric != MLRS_METRIC_EUCLIDEAN && metric != MLRS_METRIC_COSINE)
+    if (metric < MLRS_METRIC_EUCLIDEAN || metric > MLRS_METRIC_MINKOWSKI)
         return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0, "metric %d is not served", metric);
+    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0))
+        return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
     if (rows_x == 0 || rows_y == 0) return MLRS_OK;
     if (!x || !y || !out) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
     hipStream_t s = (hipStream_t)stream;
@@ -694,7 +717,24 @@ static int32_t pairwise_impl(const T* x, int64_t x_len, int64_t rows_x, int64_t 
         xa = xn;
         ya = yn;
     }
-    hipError_t e = launch_pairwise_tile<T>(x, rows_x, y, rows_y, cols, arm, xa, ya, out, rows_y, do_sqrt, s);
+    int root = do_sqrt ? 1 : 0;
+    T pe = T(0), root_exp = T(0);
+    if (metric == MLRS_METRIC_MANHATTAN) {
+        arm = ARM_MANHATTAN;
+        root = 0;
+    } else if (metric == MLRS_METRIC_CHEBYSHEV) {
+        arm = ARM_CHEBYSHEV;
+        root = 0;
+    } else if (metric == MLRS_METRIC_MINKOWSKI) {
+        // minkowski_dist: pow per feature, root exponent 1/p formed in F
+        // (crates/mlrs-kernels/src/distance.rs:201-227)
+        arm = ARM_MINKOWSKI_POW;
+        pe = (T)p;
+        root = 2;
+        root_exp = T(1) / pe;
+    }
+    hipError_t e = launch_pairwise_tile<T>(x, rows_x, y, rows_y, cols, arm, xa, ya, out, rows_y, root, s, pe, 0,
+                                           root_exp);
     if (e != hipSuccess) return hip_err(e, "pairwise_tile");
     return MLRS_OK;
 }
@@ -702,15 +742,15 @@ static int32_t pairwise_impl(const T* x, int64_t x_len, int64_t rows_x, int64_t 
 
 int32_t mlrs_pairwise_distance_f32(const float* x, int64_t x_len, int64_t rows_x, int64_t cols, const float* y,
                                    int64_t y_len, int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt,
-                                   float* out, int64_t out_len, void* stream) {
-    return pairwise_impl<float>(x, x_len, rows_x, cols, y, y_len, rows_y, cols_y, metric, do_sqrt, out, out_len,
+                                   double p, float* out, int64_t out_len, void* stream) {
+    return pairwise_impl<float>(x, x_len, rows_x, cols, y, y_len, rows_y, cols_y, metric, do_sqrt, p, out, out_len,
                                 stream);
 }
 
 int32_t mlrs_pairwise_distance_f64(const double* x, int64_t x_len, int64_t rows_x, int64_t cols, const double* y,
                                    int64_t y_len, int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt,
-                                   double* out, int64_t out_len, void* stream) {
-    return pairwise_impl<double>(x, x_len, rows_x, cols, y, y_len, rows_y, cols_y, metric, do_sqrt, out, out_len,
+                                   double p, double* out, int64_t out_len, void* stream) {
+    return pairwise_impl<double>(x, x_len, rows_x, cols, y, y_len, rows_y, cols_y, metric, do_sqrt, p, out, out_len,
                                  stream);
 }
 

@@ -31,6 +31,18 @@ enum Arm : int {
     // cosine_dist (crates/mlrs-kernels/src/distance.rs:257-310): acc + x*y,
     // sqrt(xn*yn) over row_sumsq norms, divide, clamp
     ARM_COS_PAIRWISE = 4,
+    // metric_step_manhattan / knn_host / manhattan_dist (knn.rs:3277-3286,
+    // knn_host.rs:715-718, distance.rs:67-91): acc + |x - y|
+    ARM_MANHATTAN = 5,
+    // metric_step_chebyshev / chebyshev_dist (knn.rs:3288-3312, distance.rs:
+    // 154-180): acc = (|x - y| > acc) ? |x - y| : acc, so NaN never replaces
+    ARM_CHEBYSHEV = 6,
+    // metric_step_minkowski_int (knn.rs:3330-3356): acc + |x - y|^pi by a
+    // multiply chain, integer pi in 3..8
+    ARM_MINKOWSKI_INT = 7,
+    // metric_step_minkowski / minkowski_dist (knn.rs:3314-3328, distance.rs:
+    // 201-227): acc + pow(|x - y|, p)
+    ARM_MINKOWSKI_POW = 8,
 };
 
 template <typename T> struct FloatTraits;
@@ -38,11 +50,15 @@ template <> struct FloatTraits<float> {
     static __device__ __forceinline__ float inf() { return __builtin_huge_valf(); }
     static __device__ __forceinline__ float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
     static __device__ __forceinline__ float sqrt_(float a) { return __builtin_sqrtf(a); }
+    static __device__ __forceinline__ float abs_(float a) { return __builtin_fabsf(a); }
+    static __device__ __forceinline__ float pow_(float a, float b) { return powf(a, b); }
 };
 template <> struct FloatTraits<double> {
     static __device__ __forceinline__ double inf() { return __builtin_huge_val(); }
     static __device__ __forceinline__ double fma_(double a, double b, double c) { return __builtin_fma(a, b, c); }
     static __device__ __forceinline__ double sqrt_(double a) { return __builtin_sqrt(a); }
+    static __device__ __forceinline__ double abs_(double a) { return __builtin_fabs(a); }
+    static __device__ __forceinline__ double pow_(double a, double b) { return pow(a, b); }
 };
 
 static constexpr uint32_t kSentinelIdx = 0xFFFFFFFFu;

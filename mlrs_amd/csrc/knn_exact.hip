@@ -142,12 +142,14 @@ __global__ void stats_finalize_kernel(NormStats* stats) {
 constexpr int PT = 64;   // output tile edge
 constexpr int PC = 16;   // staged columns per chunk
 
+// `root`: 0 none, 1 sqrt, 2 pow(v, root_exp) on the stored value; `pexp` /
+// `pint` are the Minkowski exponent of the pow and integer arms.
 template <typename T, int ARM>
 __global__ __launch_bounds__(256) void pairwise_tile_kernel(const T* __restrict__ x, int64_t nx,
                                                             const T* __restrict__ y, int64_t ny,
                                                             int64_t d, const T* __restrict__ xa,
                                                             const T* __restrict__ ya, T* __restrict__ out,
-                                                            int64_t ldo, int do_sqrt) {
+                                                            int64_t ldo, int root, T pexp, int pint, T root_exp) {
     using F = FloatTraits<T>;
     __shared__ T xs[PC][PT + 1];
     __shared__ T ys[PC][PT + 1];
@@ -187,6 +189,18 @@ __global__ __launch_bounds__(256) void pairwise_tile_kernel(const T* __restrict_
                         acc[a][b] = acc[a][b] + diff * diff;
                     } else if (ARM == ARM_COS_FOLD) {
                         acc[a][b] = F::fma_(xv[a], yv[b], acc[a][b]);
+                    } else if (ARM == ARM_MANHATTAN) {
+                        acc[a][b] = acc[a][b] + F::abs_(xv[a] - yv[b]);
+                    } else if (ARM == ARM_CHEBYSHEV) {
+                        const T v = F::abs_(xv[a] - yv[b]);
+                        acc[a][b] = (v > acc[a][b]) ? v : acc[a][b];
+                    } else if (ARM == ARM_MINKOWSKI_INT) {
+                        const T ad = F::abs_(xv[a] - yv[b]);
+                        T r = ad;
+                        for (int i = 1; i < pint; ++i) r = r * ad;
+                        acc[a][b] = acc[a][b] + r;
+                    } else if (ARM == ARM_MINKOWSKI_POW) {
+                        acc[a][b] = acc[a][b] + F::pow_(F::abs_(xv[a] - yv[b]), pexp);
                     } else {
                         acc[a][b] = acc[a][b] + xv[a] * yv[b];
                     }
@@ -210,8 +224,10 @@ __global__ __launch_bounds__(256) void pairwise_tile_kernel(const T* __restrict_
                 v = clamp02<T>(T(1) - sim);
             } else if (ARM == ARM_COS_HOST) {
                 v = clamp02<T>(T(1) - v * xa[gi] * ya[gj]);
-            } else if (do_sqrt) {
+            } else if (root == 1) {
                 v = F::sqrt_(v);
+            } else if (root == 2) {
+                v = F::pow_(v, root_exp);
             }
             out[gi * ldo + gj] = v;
         }
@@ -462,34 +478,44 @@ hipError_t launch_row_norms(const T* x, int64_t n, int64_t d, T* sq, T* inv, T* 
 
 template <typename T>
 hipError_t launch_pairwise_tile(const T* x, int64_t nx, const T* y, int64_t ny, int64_t d, int arm,
-                                const T* xa, const T* ya, T* out, int64_t ldo, int do_sqrt,
-                                hipStream_t s) {
+                                const T* xa, const T* ya, T* out, int64_t ldo, int root, hipStream_t s,
+                                T pexp, int pint, T root_exp) {
     if (nx == 0 || ny == 0) return hipSuccess;
     dim3 grid((unsigned)((ny + PT - 1) / PT), (unsigned)((nx + PT - 1) / PT));
+#define MLRS_PT_CASE(A)                                                                                   \
+    case A:                                                                                               \
+        hipLaunchKernelGGL((pairwise_tile_kernel<T, A>), grid, dim3(256), 0, s, x, nx, y, ny, d, xa, ya, out, \
+                           ldo, root, pexp, pint, root_exp);                                              \
+        break;
     switch (arm) {
-    case ARM_EUCLID_FMA:
-        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_EUCLID_FMA>), grid, dim3(256), 0, s, x, nx, y, ny,
-                           d, xa, ya, out, ldo, do_sqrt);
-        break;
-    case ARM_EUCLID_MULADD:
-        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_EUCLID_MULADD>), grid, dim3(256), 0, s, x, nx, y,
-                           ny, d, xa, ya, out, ldo, do_sqrt);
-        break;
-    case ARM_COS_FOLD:
-        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_COS_FOLD>), grid, dim3(256), 0, s, x, nx, y, ny, d,
-                           xa, ya, out, ldo, do_sqrt);
-        break;
-    case ARM_COS_HOST:
-        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_COS_HOST>), grid, dim3(256), 0, s, x, nx, y, ny, d,
-                           xa, ya, out, ldo, do_sqrt);
-        break;
-    case ARM_COS_PAIRWISE:
-        hipLaunchKernelGGL((pairwise_tile_kernel<T, ARM_COS_PAIRWISE>), grid, dim3(256), 0, s, x, nx, y,
-                           ny, d, xa, ya, out, ldo, do_sqrt);
-        break;
+        MLRS_PT_CASE(ARM_EUCLID_FMA)
+        MLRS_PT_CASE(ARM_EUCLID_MULADD)
+        MLRS_PT_CASE(ARM_COS_FOLD)
+        MLRS_PT_CASE(ARM_COS_HOST)
+        MLRS_PT_CASE(ARM_COS_PAIRWISE)
+        MLRS_PT_CASE(ARM_MANHATTAN)
+        MLRS_PT_CASE(ARM_CHEBYSHEV)
+        MLRS_PT_CASE(ARM_MINKOWSKI_INT)
+        MLRS_PT_CASE(ARM_MINKOWSKI_POW)
     default:
         return hipErrorInvalidValue;
     }
+#undef MLRS_PT_CASE
+    return hipGetLastError();
+}
+
+// out[i] = pow(out[i], e): the Minkowski boundary root over the n emitted
+// values (powf_elem, crates/mlrs-kernels/src/elementwise.rs:139-152).
+template <typename T>
+__global__ void pow_inplace_kernel(T* __restrict__ v, int64_t n, T e) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) v[i] = FloatTraits<T>::pow_(v[i], e);
+}
+
+template <typename T>
+hipError_t launch_pow_inplace(T* v, int64_t n, T e, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL((pow_inplace_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, v, n, e);
     return hipGetLastError();
 }
 
@@ -509,11 +535,14 @@ template hipError_t launch_row_norms<float>(const float*, int64_t, int64_t, floa
                                             NormStats*, hipStream_t);
 template hipError_t launch_row_norms<double>(const double*, int64_t, int64_t, double*, double*, double*,
                                              NormStats*, hipStream_t);
+template hipError_t launch_pow_inplace<float>(float*, int64_t, float, hipStream_t);
+template hipError_t launch_pow_inplace<double>(double*, int64_t, double, hipStream_t);
 template hipError_t launch_pairwise_tile<float>(const float*, int64_t, const float*, int64_t, int64_t, int,
-                                                const float*, const float*, float*, int64_t, int, hipStream_t);
+                                                const float*, const float*, float*, int64_t, int, hipStream_t,
+                                                float, int, float);
 template hipError_t launch_pairwise_tile<double>(const double*, int64_t, const double*, int64_t, int64_t,
                                                  int, const double*, const double*, double*, int64_t, int,
-                                                 hipStream_t);
+                                                 hipStream_t, double, int, double);
 template hipError_t launch_select_rows<float>(const float*, int64_t, int64_t, int64_t, int, int, float*,
                                               uint32_t*, hipStream_t);
 template hipError_t launch_select_rows<double>(const double*, int64_t, int64_t, int64_t, int, int, double*,

@@ -152,9 +152,13 @@ hipError_t launch_row_norms(const T* x, int64_t n, int64_t d, T* sq, T* inv, T* 
 
 // Generic exact path: tiled exact pairwise values under one arm.
 template <typename T>
+// `root`: 0 none, 1 sqrt, 2 pow(v, root_exp); pexp / pint: the Minkowski
+// exponent of the pow / integer arms.
 hipError_t launch_pairwise_tile(const T* x, int64_t nx, const T* y, int64_t ny, int64_t d, int arm,
-                                const T* xa, const T* ya, T* out, int64_t ldo, int do_sqrt,
-                                hipStream_t s);
+                                const T* xa, const T* ya, T* out, int64_t ldo, int root,
+                                hipStream_t s, T pexp = T(0), int pint = 0, T root_exp = T(0));
+template <typename T>
+hipError_t launch_pow_inplace(T* v, int64_t n, T e, hipStream_t s);
 
 // Generic exact path: per-row (value, index) top-k over a materialized
 // rows x cols matrix, NaN never admitted, sentinel-padded.

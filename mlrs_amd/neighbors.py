@@ -3,8 +3,8 @@ over the HIP engine -- the brute-force kNN estimator surface of
 ``mlrs.neighbors`` (crates/mlrs-py/python/mlrs/neighbors.py).
 
 Same parameter names, metric resolution, validation order and error messages
-as the reference shim for the metrics the engine serves (Euclidean and its
-aliases, cosine); ``kneighbors(X=None)`` queries the training set with k+1 and
+as the reference shim for the metrics the engine serves (Euclidean, Manhattan,
+Chebyshev, Minkowski-p and their aliases, cosine); ``kneighbors(X=None)`` queries the training set with k+1 and
 drops each row's own index by identity, not by position or distance
 (neighbors.py:217-238, 622-647).
 
@@ -39,7 +39,7 @@ _ALGORITHM_VALID_METRICS["auto"] = _SUPPORTED_METRICS
 # metric_from_str (crates/mlrs-py/src/estimators/neighbors.rs:900-923)
 _ENGINE_METRIC = {"euclidean": "euclidean", "l2": "euclidean", "cosine": "cosine",
                   "manhattan": "manhattan", "l1": "manhattan", "cityblock": "manhattan",
-                  "chebyshev": "chebyshev", "infinity": "chebyshev"}
+                  "chebyshev": "chebyshev", "infinity": "chebyshev", "minkowski": "minkowski"}
 
 
 def _resolve_metric(metric, p, metric_params):
@@ -149,6 +149,7 @@ class _NeighborsBase:
         _check_finite(t)
         self._fit_X_dev = t
         self._engine_metric = engine_metric
+        self._engine_p = float(eff_p) if engine_metric == "minkowski" else 2.0
         self.n_features_in_ = t.shape[1]
         self.n_samples_fit_ = t.shape[0]
         self.effective_metric_ = eff
@@ -177,7 +178,7 @@ class _NeighborsBase:
         return int(k), int(k_query)
 
     def _raw_kneighbors(self, Xq, k):
-        dist, idx = prims.knn_topk(Xq, self._fit_X_dev, k, self._engine_metric)
+        dist, idx = prims.knn_topk(Xq, self._fit_X_dev, k, self._engine_metric, p=self._engine_p)
         return dist, idx.to(torch.int32)
 
     def _check_query(self, q):

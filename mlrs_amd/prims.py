@@ -18,7 +18,8 @@ import torch
 
 from . import _lib
 
-METRICS = {"euclidean": _lib.METRIC_EUCLIDEAN, "cosine": _lib.METRIC_COSINE}
+METRICS = {"euclidean": _lib.METRIC_EUCLIDEAN, "cosine": _lib.METRIC_COSINE, "manhattan": _lib.METRIC_MANHATTAN,
+           "chebyshev": _lib.METRIC_CHEBYSHEV, "minkowski": _lib.METRIC_MINKOWSKI}
 _DT = {torch.float32: "f32", torch.float64: "f64"}
 
 
@@ -117,8 +118,9 @@ def kmeans_assign(x, centers, labels=None, sqdist=None):
     return lab, dist
 
 
-def pairwise_distance(x, y, metric="euclidean", sqrt=False, out=None):
-    """Full ``rows_x x rows_y`` distance matrix (squared Euclidean unless ``sqrt``)."""
+def pairwise_distance(x, y, metric="euclidean", sqrt=False, out=None, p=2.0):
+    """Full ``rows_x x rows_y`` distance matrix (squared Euclidean unless
+    ``sqrt``; ``p`` is the Minkowski exponent)."""
     _dev_check(x, y)
     s = _suffix(x)
     rx, cx = x.shape
@@ -126,7 +128,7 @@ def pairwise_distance(x, y, metric="euclidean", sqrt=False, out=None):
     o = torch.empty((rx, ry), dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     rc = getattr(lib, "mlrs_pairwise_distance_" + s)(
-        _ptr(x), x.numel(), rx, cx, _ptr(y), y.numel(), ry, cy, _metric_id(metric), int(bool(sqrt)),
+        _ptr(x), x.numel(), rx, cx, _ptr(y), y.numel(), ry, cy, _metric_id(metric), int(bool(sqrt)), float(p),
         _ptr(o), o.numel(), _stream(x.device))
     _lib.check(rc)
     return o

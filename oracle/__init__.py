@@ -21,7 +21,11 @@ _LIB_PATH = os.path.join(_HERE, "libmlrs_oracle.so")
 
 METRIC_EUCLIDEAN = 0
 METRIC_COSINE = 1
-METRICS = {"euclidean": METRIC_EUCLIDEAN, "cosine": METRIC_COSINE}
+METRIC_MANHATTAN = 2
+METRIC_CHEBYSHEV = 3
+METRIC_MINKOWSKI = 4
+METRICS = {"euclidean": METRIC_EUCLIDEAN, "cosine": METRIC_COSINE, "manhattan": METRIC_MANHATTAN,
+           "chebyshev": METRIC_CHEBYSHEV, "minkowski": METRIC_MINKOWSKI}
 
 ARM_DIRECT = 0
 ARM_METRIC = 1
@@ -45,13 +49,13 @@ def _load():
     lib.orc_max_threads.restype = i32
     for s in ("f32", "f64"):
         f = getattr(lib, "orc_knn_topk_" + s)
-        f.argtypes = [vp, i64, vp, i64, i64, i64, i32, vp, vp, i32]
+        f.argtypes = [vp, i64, vp, i64, i64, i64, i32, ctypes.c_double, vp, vp, i32]
         f.restype = i32
         f = getattr(lib, "orc_kmeans_assign_" + s)
         f.argtypes = [vp, i64, vp, i64, i64, vp, vp, i32]
         f.restype = i32
         f = getattr(lib, "orc_pairwise_" + s)
-        f.argtypes = [vp, i64, vp, i64, i64, i32, i32, vp, i32]
+        f.argtypes = [vp, i64, vp, i64, i64, i32, i32, ctypes.c_double, vp, i32]
         f.restype = i32
         f = getattr(lib, "orc_row_sqnorms_" + s)
         f.argtypes = [vp, i64, i64, vp]
@@ -92,8 +96,9 @@ def max_threads():
     return _load().orc_max_threads()
 
 
-def knn_topk(xq, xt, k, metric="euclidean", nthreads=0):
-    """(distances, uint32 indices), each (n_query, k), ascending (value, index)."""
+def knn_topk(xq, xt, k, metric="euclidean", nthreads=0, p=2.0):
+    """(distances, uint32 indices), each (n_query, k), ascending (value, index).
+    ``p`` is the Minkowski exponent (metric "minkowski" only)."""
     lib = _load()
     xq = np.ascontiguousarray(xq)
     xt = np.ascontiguousarray(xt, dtype=xq.dtype)
@@ -104,7 +109,7 @@ def knn_topk(xq, xt, k, metric="euclidean", nthreads=0):
     out_v = np.empty((nq, k), dtype=xq.dtype)
     out_i = np.empty((nq, k), dtype=np.uint32)
     rc = getattr(lib, "orc_knn_topk_" + s)(
-        xq.ctypes.data, nq, xt.ctypes.data, nt, d, int(k), _metric_id(metric),
+        xq.ctypes.data, nq, xt.ctypes.data, nt, d, int(k), _metric_id(metric), float(p),
         out_v.ctypes.data, out_i.ctypes.data, int(nthreads))
     if rc != 0:
         raise ValueError("oracle knn_topk rejected k=%d for n_train=%d" % (k, nt))
@@ -129,7 +134,7 @@ def kmeans_assign(x, centers, nthreads=0):
     return labels, dist
 
 
-def pairwise(x, y, metric="euclidean", sqrt=False, nthreads=0):
+def pairwise(x, y, metric="euclidean", sqrt=False, nthreads=0, p=2.0):
     lib = _load()
     x = np.ascontiguousarray(x)
     y = np.ascontiguousarray(y, dtype=x.dtype)
@@ -137,7 +142,7 @@ def pairwise(x, y, metric="euclidean", sqrt=False, nthreads=0):
     ny = y.shape[0]
     out = np.empty((nx, ny), dtype=x.dtype)
     rc = getattr(lib, "orc_pairwise_" + _suffix(x.dtype))(
-        x.ctypes.data, nx, y.ctypes.data, ny, d, _metric_id(metric), int(bool(sqrt)),
+        x.ctypes.data, nx, y.ctypes.data, ny, d, _metric_id(metric), int(bool(sqrt)), float(p),
         out.ctypes.data, int(nthreads))
     if rc != 0:
         raise ValueError("oracle pairwise rejected d=%d" % d)

@@ -44,6 +44,18 @@
 
 #define ORC_METRIC_EUCLIDEAN 0
 #define ORC_METRIC_COSINE 1
+#define ORC_METRIC_MANHATTAN 2
+#define ORC_METRIC_CHEBYSHEV 3
+#define ORC_METRIC_MINKOWSKI 4
+
+/* The integer-exponent Minkowski path: p an integer in 3..=8 runs a multiply
+ * chain instead of powf (minkowski_powi, crates/mlrs-backend/src/prims/
+ * knn.rs:680-687 and knn_host.rs:358-365). */
+static int minkowski_powi(double p)
+{
+    unsigned pi = (p >= 0.0 && p < 4294967296.0) ? (unsigned)p : 0u;
+    return (p == (double)pi && pi >= 3 && pi <= 8) ? (int)pi : 0;
+}
 
 #define ORC_ARM_DIRECT 0
 #define ORC_ARM_METRIC 1
@@ -87,7 +99,7 @@ int orc_max_threads(void)
  * The template below is instantiated for float and double.  T is the element
  * type, S the symbol suffix, FMA/SQRT the matching libm routines.
  */
-#define ORC_DEFINE(T, S, FMA, SQRT)                                                        \
+#define ORC_DEFINE(T, S, FMA, SQRT, POW, FABS)                                             \
                                                                                            \
 /* row_sumsq / row_sqnorm: acc += v*v over ascending c (kernels/knn.rs:2130-2149,         \
  * kernels/kmeans.rs:610). */                                                              \
@@ -142,7 +154,7 @@ static inline void insert_##S(T *lval, uint32_t *lidx, int64_t k, T v, uint32_t 
  * norms for the metric family, reciprocal norms for the host arm). */                     \
 static void scan_block_##S(const T *xt, int64_t active, const T *xtrain, int64_t nt,       \
                            int64_t d, int64_t k, int metric, int arm, const T *qn,         \
-                           const T *yn, T *lval, uint32_t *lidx)                           \
+                           const T *yn, T pe, int pi, T *lval, uint32_t *lidx)             \
 {                                                                                          \
     T acc[ORC_QB];                                                                         \
     T worst[ORC_QB];                                                                       \
@@ -170,6 +182,43 @@ static void scan_block_##S(const T *xt, int64_t active, const T *xtrain, int64_t
                         T diff = xc[a] - yc;                                               \
                         acc[a] = FMA(diff, diff, acc[a]);                                  \
                     }                                                                      \
+                }                                                                          \
+            }                                                                              \
+        } else if (metric == ORC_METRIC_MANHATTAN) {                                      \
+            /* acc + |x - y| (knn.rs:3277-3286, knn_host.rs:715-718) */                   \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++)                                           \
+                    acc[a] = acc[a] + FABS(xc[a] - yc);                                    \
+            }                                                                              \
+        } else if (metric == ORC_METRIC_CHEBYSHEV) {                                      \
+            /* running max as a select: NaN never replaces (knn.rs:3288-3312) */           \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++) {                                         \
+                    T v = FABS(xc[a] - yc);                                                \
+                    acc[a] = (v > acc[a]) ? v : acc[a];                                    \
+                }                                                                          \
+            }                                                                              \
+        } else if (metric == ORC_METRIC_MINKOWSKI) {                                      \
+            /* acc + |x - y|^p: multiply chain for integer p in 3..8, else powf           \
+             * (knn.rs:3314-3360, knn_host.rs:728-742) */                                 \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++) {                                         \
+                    T ad = FABS(xc[a] - yc);                                               \
+                    T r;                                                                   \
+                    if (pi > 0) {                                                          \
+                        r = ad;                                                            \
+                        for (int i = 1; i < pi; i++)                                       \
+                            r = r * ad;                                                    \
+                    } else {                                                               \
+                        r = POW(ad, pe);                                                   \
+                    }                                                                      \
+                    acc[a] = acc[a] + r;                                                   \
                 }                                                                          \
             }                                                                              \
         } else {                                                                           \
@@ -222,10 +271,15 @@ static void scan_block_##S(const T *xt, int64_t active, const T *xtrain, int64_t
  * knn_host.rs:826-851), indices as uint32 with the sentinel clamped to 0.               \
  * Returns 0, or -1 for a k outside [1, nt]. */                                            \
 int orc_knn_topk_##S(const T *xq, int64_t nq, const T *xtrain, int64_t nt, int64_t d,      \
-                     int64_t k, int metric, T *out_val, uint32_t *out_idx, int nthreads)   \
+                     int64_t k, int metric, double p, T *out_val, uint32_t *out_idx,       \
+                     int nthreads)                                                         \
 {                                                                                          \
     if (k < 1 || k > nt || nq < 0 || d < 1)                                                \
         return -1;                                                                         \
+    const int pi = (metric == ORC_METRIC_MINKOWSKI) ? minkowski_powi(p) : 0;               \
+    const T pe = (T)p;                                                                     \
+    /* powf_elem's exponent: f64_to_host(1.0 / p) (prims/knn.rs:882-888) */                \
+    const T inv_p = (T)(1.0 / p);                                                          \
     int arm = orc_knn_arm(d, k, metric);                                                   \
     T *qn = NULL, *yn = NULL;                                                              \
     if (metric == ORC_METRIC_COSINE) {                                                     \
@@ -260,14 +314,14 @@ int orc_knn_topk_##S(const T *xq, int64_t nq, const T *xtrain, int64_t nt, int64
                 lval[j] = (T)INFINITY;                                                     \
                 lidx[j] = UINT32_MAX;                                                      \
             }                                                                              \
-            scan_block_##S(xt, active, xtrain, nt, d, k, metric, arm, qblk, yn, lval,      \
-                           lidx);                                                          \
+            scan_block_##S(xt, active, xtrain, nt, d, k, metric, arm, qblk, yn, pe, pi,    \
+                           lval, lidx);                                                    \
             for (int64_t a = 0; a < active; a++)                                           \
                 for (int64_t j = 0; j < k; j++) {                                          \
                     T v = lval[a * k + j];                                                 \
                     uint32_t ix = lidx[a * k + j];                                         \
-                    out_val[(q0 + a) * k + j] =                                            \
-                        (metric == ORC_METRIC_EUCLIDEAN) ? SQRT(v) : v;                    \
+                    out_val[(q0 + a) * k + j] = (metric == ORC_METRIC_EUCLIDEAN) ? SQRT(v) \
+                        : (metric == ORC_METRIC_MINKOWSKI) ? POW(v, inv_p) : v;            \
                     out_idx[(q0 + a) * k + j] = (ix == UINT32_MAX) ? 0u : ix;              \
                 }                                                                          \
         }                                                                                  \
@@ -321,7 +375,7 @@ int orc_kmeans_assign_##S(const T *x, int64_t n, const T *centers, int64_t kc, i
  * dot += x*y, denom = sqrt(xn*yn) over row_sumsq norms, sim = dot/denom when             \
  * denom > 0 else 0, then the [0, 2] clamp. */                                             \
 int orc_pairwise_##S(const T *x, int64_t nx, const T *y, int64_t ny, int64_t d,            \
-                     int metric, int do_sqrt, T *out, int nthreads)                        \
+                     int metric, int do_sqrt, double p, T *out, int nthreads)              \
 {                                                                                          \
     if (d < 1)                                                                             \
         return -1;                                                                         \
@@ -339,7 +393,25 @@ int orc_pairwise_##S(const T *x, int64_t nx, const T *y, int64_t ny, int64_t d, 
         for (int64_t j = 0; j < ny; j++) {                                                 \
             const T *yr = y + j * d;                                                       \
             T acc = (T)0;                                                                  \
-            if (metric == ORC_METRIC_EUCLIDEAN) {                                          \
+            if (metric == ORC_METRIC_MANHATTAN || metric == ORC_METRIC_CHEBYSHEV ||        \
+                metric == ORC_METRIC_MINKOWSKI) {                                          \
+                /* manhattan_dist / chebyshev_dist / minkowski_dist                        \
+                 * (crates/mlrs-kernels/src/distance.rs:67-227): the Minkowski            \
+                 * pairwise form always uses powf, with the root 1/p formed in F */        \
+                const T pe = (T)p;                                                         \
+                for (int64_t c = 0; c < d; c++) {                                          \
+                    T diff = FABS(xr[c] - yr[c]);                                          \
+                    if (metric == ORC_METRIC_MANHATTAN)                                    \
+                        acc = acc + diff;                                                  \
+                    else if (metric == ORC_METRIC_CHEBYSHEV)                               \
+                        acc = (diff > acc) ? diff : acc;                                   \
+                    else                                                                   \
+                        acc = acc + POW(diff, pe);                                         \
+                }                                                                          \
+                if (metric == ORC_METRIC_MINKOWSKI)                                        \
+                    acc = POW(acc, (T)1 / pe);                                             \
+                out[i * ny + j] = acc;                                                     \
+            } else if (metric == ORC_METRIC_EUCLIDEAN) {                                   \
                 for (int64_t c = 0; c < d; c++) {                                          \
                     T diff = xr[c] - yr[c];                                                \
                     acc = acc + diff * diff;                                               \
@@ -366,5 +438,5 @@ int orc_pairwise_##S(const T *x, int64_t nx, const T *y, int64_t ny, int64_t d, 
     return 0;                                                                              \
 }
 
-ORC_DEFINE(float, f32, fmaf, sqrtf)
-ORC_DEFINE(double, f64, fma, sqrt)
+ORC_DEFINE(float, f32, fmaf, sqrtf, powf, fabsf)
+ORC_DEFINE(double, f64, fma, sqrt, pow, fabs)

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib.load()
-    assert lib.mlrs_abi_version() == 1
+    assert lib.mlrs_abi_version() == 2
     assert lib.mlrs_status_string(0) == b"ok"
     assert lib.mlrs_status_string(-1) == b"shape mismatch"
     assert lib.mlrs_status_string(-2) == b"dimension mismatch"
@@ -95,19 +95,19 @@ def test_kmeans_validation():
 def test_pairwise_validation():
     lib = _lib.load()
     f = lib.mlrs_pairwise_distance_f64
-    assert f(P, 14, 5, 3, P, 12, 4, 3, 0, 0, P, 20, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert f(P, 14, 5, 3, P, 12, 4, 3, 0, 0, 2.0, P, 20, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
     assert (_info().operand, _info().len) == (b"x", 14)
-    assert f(P, 15, 5, 3, P, 13, 4, 3, 0, 0, P, 20, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert f(P, 15, 5, 3, P, 13, 4, 3, 0, 0, 2.0, P, 20, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
     assert _info().operand == b"y"
 
 
 def test_pairwise_dim_mismatch_and_out():
     lib = _lib.load()
     f = lib.mlrs_pairwise_distance_f32
-    assert f(P, 15, 5, 3, P, 16, 4, 4, 0, 0, P, 20, None) == _lib.MLRS_ERR_DIM_MISMATCH
+    assert f(P, 15, 5, 3, P, 16, 4, 4, 0, 0, 2.0, P, 20, None) == _lib.MLRS_ERR_DIM_MISMATCH
     e = _info()
     assert (e.operand, e.rows, e.cols) == (b"cols", 3, 4)
-    assert f(P, 15, 5, 3, P, 12, 4, 3, 0, 0, P, 19, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert f(P, 15, 5, 3, P, 12, 4, 3, 0, 0, 2.0, P, 19, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
     assert _info().operand == b"out"
 
 
@@ -148,3 +148,16 @@ def test_force_path_validation():
     with pytest.raises(ValueError):
         prims.force_path("mfma")
     prims.force_path("auto")
+
+
+def test_metric_family_validation():
+    """Unknown metrics and Minkowski p < 1 are rejected before any launch."""
+    lib = _lib.load()
+    f = lib.mlrs_knn_topk_f32
+    assert f(P, 30, 10, 3, P, 30, 10, 2, 9, 2.0, P, P, 20, None) == _lib.MLRS_ERR_UNSUPPORTED
+    assert _info().operand == b"metric"
+    assert f(P, 30, 10, 3, P, 30, 10, 2, 4, 0.5, P, P, 20, None) == _lib.MLRS_ERR_UNSUPPORTED
+    assert _info().operand == b"p"
+    g = lib.mlrs_pairwise_distance_f64
+    assert g(P, 15, 5, 3, P, 12, 4, 3, 4, 0, float("nan"), P, 20, None) == _lib.MLRS_ERR_UNSUPPORTED
+    assert _info().operand == b"p"

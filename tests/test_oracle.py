@@ -228,11 +228,17 @@ def test_arm_dispatch_table():
 # ---------------------------------------------------------------------------
 # the reference's sklearn fixtures
 # ---------------------------------------------------------------------------
-def _brute(xq, xt, metric):
+def _brute(xq, xt, metric, p=2.0):
     q = xq.astype(np.float64)
     t = xt.astype(np.float64)
     if metric == "euclidean":
         return lambda r, j: float(np.sqrt(np.sum((q[r] - t[j]) ** 2)))
+    if metric == "manhattan":
+        return lambda r, j: float(np.sum(np.abs(q[r] - t[j])))
+    if metric == "chebyshev":
+        return lambda r, j: float(np.max(np.abs(q[r] - t[j])))
+    if metric == "minkowski":
+        return lambda r, j: float(np.sum(np.abs(q[r] - t[j]) ** p) ** (1.0 / p))
     return lambda r, j: float(1.0 - np.dot(q[r], t[j]) / (np.linalg.norm(q[r]) * np.linalg.norm(t[j])))
 
 
@@ -250,25 +256,30 @@ def test_fixture_knn_seed42(s):
     ("euclidean", ["euclidean", "alias_{}_euclidean", "alias_{}_l2", "alias_{}_minkowski", "alg_{}_auto",
                    "alg_{}_brute"]),
     ("cosine", ["cosine", "alias_{}_cosine"]),
+    ("manhattan", ["manhattan", "alias_{}_manhattan", "alias_{}_l1", "alias_{}_cityblock"]),
+    ("chebyshev", ["chebyshev", "alias_{}_chebyshev", "alias_{}_infinity"]),
+    ("minkowski", ["minkowski"]),
 ])
 def test_fixture_nn_params(s, metric, keys):
     z = load_golden("nn_params_%s_seed42" % s)
     k = int(z["k"][0])
-    d, i = oracle.knn_topk(z["Xq"], z["X"], k, metric)
+    p = float(z["p"][0])
+    d, i = oracle.knn_topk(z["Xq"], z["X"], k, metric, p=p)
     for key in keys:
         dk = ("distances_" + key) if "{}" not in key else key.format("distances")
         ik = ("indices_" + key) if "{}" not in key else key.format("indices")
-        assert_topk_matches(d, i, z[dk], z[ik].astype(np.int64), _brute(z["Xq"], z["X"], metric))
+        assert_topk_matches(d, i, z[dk], z[ik].astype(np.int64), _brute(z["Xq"], z["X"], metric, p))
 
 
 @pytest.mark.parametrize("s", ["f32", "f64"])
-@pytest.mark.parametrize("metric", ["euclidean", "cosine"])
+@pytest.mark.parametrize("metric", ["euclidean", "cosine", "manhattan", "chebyshev", "minkowski"])
 def test_fixture_knn_metric_graph(s, metric):
     """X-vs-X with k+1 (self included) and a planted duplicate pair."""
     z = load_golden("knn_%s_%s_seed42" % (metric, s))
     k = int(z["k"][0]) + 1
-    d, i = oracle.knn_topk(z["X"], z["X"], k, metric)
-    assert_topk_matches(d, i, z["distances"], z["indices"].astype(np.int64), _brute(z["X"], z["X"], metric))
+    p = float(z["p"][0]) if "p" in z.files else 2.0
+    d, i = oracle.knn_topk(z["X"], z["X"], k, metric, p=p)
+    assert_topk_matches(d, i, z["distances"], z["indices"].astype(np.int64), _brute(z["X"], z["X"], metric, p))
     a, b = int(z["dup_row_a"][0]), int(z["dup_row_b"][0])
     # identical rows score exactly 0 against each other; lowest index first
     assert d[a, 0] == 0 and d[a, 1] == 0 and list(i[a, :2]) == sorted([a, b])
@@ -399,3 +410,51 @@ def test_oracle_kmeans_vs_sklearn():
     km.cluster_centers_ = c.astype(np.float64)
     lab, _ = oracle.kmeans_assign(x, c)
     assert np.array_equal(lab, km.predict(x.astype(np.float64)).astype(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("metric,p", [("manhattan", 2.0), ("chebyshev", 2.0), ("minkowski", 3.0),
+                                      ("minkowski", 5.0), ("minkowski", 2.5)])
+def test_metric_family_matches_exact_model(dtype, metric, p):
+    """The oracle's manhattan / chebyshev / minkowski arithmetic against a
+    scalar restatement in the same dtype (numpy scalars round each operation):
+    running sum of |x-y|, running max by select, |x-y|^p by a multiply chain
+    for integer p in 3..8 and pow otherwise, then the 1/p root.  Bit for bit
+    except where a pow is involved: numpy's power and the C library's may
+    differ in the last place, so those values are held to 4 ulp."""
+    T = np.dtype(dtype).type
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((40, 5)).astype(dtype)
+    Q = rng.standard_normal((6, 5)).astype(dtype)
+    k = 7
+    d, i = oracle.knn_topk(Q, X, k, metric, p=p)
+    pi = int(p) if (p == int(p) and 3 <= int(p) <= 8) else 0
+    for r in range(Q.shape[0]):
+        vals = []
+        for t in range(X.shape[0]):
+            acc = T(0)
+            for c in range(X.shape[1]):
+                ad = T(abs(T(Q[r, c] - X[t, c])))
+                if metric == "manhattan":
+                    acc = T(acc + ad)
+                elif metric == "chebyshev":
+                    acc = ad if ad > acc else acc
+                else:
+                    if pi:
+                        rr = ad
+                        for _ in range(1, pi):
+                            rr = T(rr * ad)
+                    else:
+                        rr = T(np.power(ad, T(p)))
+                    acc = T(acc + rr)
+            vals.append((acc, t))
+        vals.sort()
+        want_i = [t for _, t in vals[:k]]
+        want_v = [v for v, _ in vals[:k]]
+        if metric == "minkowski":
+            want_v = [T(np.power(v, T(1.0 / p))) for v in want_v]
+        assert list(i[r]) == want_i
+        if metric == "minkowski":
+            np.testing.assert_allclose(d[r], np.array(want_v, dtype=dtype), rtol=4 * np.finfo(dtype).eps, atol=0)
+        else:
+            assert np.array_equal(d[r], np.array(want_v, dtype=dtype))

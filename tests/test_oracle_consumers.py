@@ -16,9 +16,12 @@ import oracle
 from conftest import load_golden
 
 
-def _neigh(X, Xq, k, metric="euclidean"):
-    d, i = oracle.knn_topk(Xq, X, k, metric)
+def _neigh(X, Xq, k, metric="euclidean", p=2.0):
+    d, i = oracle.knn_topk(Xq, X, k, metric, p=p)
     return d, i
+
+
+METRICS = ["euclidean", "cosine", "manhattan", "chebyshev", "minkowski"]
 
 
 @pytest.mark.parametrize("s", ["f32", "f64"])
@@ -36,12 +39,12 @@ def test_regress_and_classify_fixture(s):
 
 
 @pytest.mark.parametrize("s", ["f32", "f64"])
-@pytest.mark.parametrize("metric", ["euclidean", "cosine"])
+@pytest.mark.parametrize("metric", METRICS)
 @pytest.mark.parametrize("weights", ["uniform", "distance"])
 def test_regress_params_fixture(s, metric, weights):
     z = load_golden("knn_reg_params_%s_seed42" % s)
     X, Xq, k = z["X"], z["Xq"], int(z["k"][0])
-    d, i = _neigh(X, Xq, k, metric)
+    d, i = _neigh(X, Xq, k, metric, float(z["p"][0]))
     pred, _ = oracle.knn_regress(z["y"], i, d, weighted=weights == "distance")
     np.testing.assert_allclose(pred, z["predict_%s_%s" % (metric, weights)], rtol=1e-5, atol=1e-5)
     if metric == "euclidean":
@@ -50,12 +53,12 @@ def test_regress_params_fixture(s, metric, weights):
 
 
 @pytest.mark.parametrize("s", ["f32", "f64"])
-@pytest.mark.parametrize("metric", ["euclidean", "cosine"])
+@pytest.mark.parametrize("metric", METRICS)
 @pytest.mark.parametrize("weights", ["uniform", "distance"])
 def test_classify_params_fixture(s, metric, weights):
     z = load_golden("knn_clf_params_%s_seed42" % s)
     X, Xq, k = z["X"], z["Xq"], int(z["k"][0])
-    d, i = _neigh(X, Xq, k, metric)
+    d, i = _neigh(X, Xq, k, metric, float(z["p"][0]))
     classes, codes = np.unique(z["y"], return_inverse=True)
     np.testing.assert_array_equal(classes, z["classes"])
     proba, lab = oracle.knn_classify(codes, classes.size, i, d, weighted=weights == "distance", dtype=X.dtype)
