@@ -38,6 +38,7 @@ extern "C" {
 #define MLRS_ERR_NULL_POINTER (-4)   /* a required pointer was NULL */
 #define MLRS_ERR_HIP (-5)            /* a HIP runtime call failed (hip_error holds it) */
 #define MLRS_ERR_ALLOC (-6)          /* device workspace allocation failed */
+#define MLRS_ERR_INVALID_PARAM (-7)  /* AlgoError::InvalidEps-style rejection of a scalar (operand names it) */
 
 /* ---- metrics: the variants of the Metric enum of crates/mlrs-backend/src/prims/knn_graph.rs:61-75
  *      (numbered here, not in the enum's declaration order) ---- */
@@ -63,7 +64,7 @@ int32_t mlrs_last_error(mlrs_error_info *out);
 const char *mlrs_status_string(int32_t code);
 /* ABI version of this header (bumped on any signature change). */
 int32_t mlrs_abi_version(void);
-#define MLRS_ABI_VERSION 2
+#define MLRS_ABI_VERSION 3
 
 /*
  * Brute-force k nearest training rows of every query row.
@@ -227,6 +228,46 @@ int32_t mlrs_knn_classify_f64(const int32_t *y_class, int64_t n_train, int32_t n
                               int64_t idx_len, const double *dist, int64_t dist_len, int64_t n_query, int32_t k,
                               int32_t weighted, double *proba, int64_t proba_len, int32_t *labels,
                               int64_t labels_len, void *stream);
+
+/*
+ * Every training row within `radius` of each query row.
+ *
+ * Replaces: radius_neighbor_indices_metric (crates/mlrs-algos/src/neighbors/
+ *   nearest.rs:609-749) with its default arm, radius_host_scan
+ *   (crates/mlrs-backend/src/prims/radius_host.rs:140-234); the result is the
+ *   RadiusNeighbors layout (nearest.rs:564-582): counts[q] (n_query, device)
+ *   is row q's match count, and out_dist / out_idx (device) hold the matches
+ *   of row 0, then row 1, ..., each row's in ascending training index -- a CSR
+ *   matrix without its indptr.  Values are the host scan's: the knn_host lane
+ *   arithmetic compared as `v <= th` against th = (F)(radius^2 | radius^p |
+ *   radius) formed in f64 (NaN never matches), then sqrt (Euclidean),
+ *   pow(v, (F)(1/p)) (Minkowski) or identity on the matches; indices are the
+ *   training row numbers as int32.
+ * Sizes: *total (host) receives the number of matches.  With out_dist and
+ *   out_idx both NULL the call only counts (counts and *total filled).  With
+ *   buffers of `capacity` entries and *total > capacity nothing is written to
+ *   them and the call returns ShapeMismatch "out" {rows = total, cols = 1,
+ *   len = capacity}.  The usual sequence is a counting call, then a call with
+ *   buffers of the returned size and otherwise the same arguments, which
+ *   starts from the first call's counts (the second call re-checks them and
+ *   counts again if the data changed in between).
+ * Errors, before any launch: InvalidParam "radius" (radius not >= 0, NaN
+ *   included; the text of AlgoError::InvalidEps), ShapeMismatch "xq" (n_query
+ *   or n_features zero, or a length mismatch), DimMismatch "n_features",
+ *   ShapeMismatch "y" / "rows" (n_train above u32::MAX) / "counts",
+ *   Unsupported "metric" / "p" (Minkowski p < 1).
+ * Synchronous: returns after `stream` has finished the call's work.
+ */
+int32_t mlrs_radius_neighbors_f32(const float *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                                  const float *x_train, int64_t x_train_len, int64_t n_train,
+                                  int64_t train_features, int32_t metric, double p, double radius, uint32_t *counts,
+                                  int64_t counts_len, float *out_dist, int32_t *out_idx, int64_t capacity,
+                                  int64_t *total, void *stream);
+int32_t mlrs_radius_neighbors_f64(const double *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                                  const double *x_train, int64_t x_train_len, int64_t n_train,
+                                  int64_t train_features, int32_t metric, double p, double radius, uint32_t *counts,
+                                  int64_t counts_len, double *out_dist, int32_t *out_idx, int64_t capacity,
+                                  int64_t *total, void *stream);
 
 /* Release the cached device workspace of the current device. */
 int32_t mlrs_release_workspace(void);

@@ -16,6 +16,7 @@ MLRS_ERR_UNSUPPORTED = -3
 MLRS_ERR_NULL_POINTER = -4
 MLRS_ERR_HIP = -5
 MLRS_ERR_ALLOC = -6
+MLRS_ERR_INVALID_PARAM = -7
 
 METRIC_EUCLIDEAN = 0
 METRIC_COSINE = 1
@@ -56,6 +57,11 @@ class DimMismatch(PrimError):
     """PrimError::DimMismatch{dim, lhs, rhs}; `rows`/`cols` carry lhs/rhs."""
 
 
+class InvalidParam(PrimError):
+    """A scalar parameter outside its domain (AlgoError::InvalidEps and its like);
+    ``operand`` names it."""
+
+
 class UnsupportedError(NotImplementedError):
     pass
 
@@ -87,6 +93,10 @@ SIGNATURES = {
                                      _vp]),
     "mlrs_knn_classify_f64": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _i64,
                                      _vp]),
+    "mlrs_radius_neighbors_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _f64, _f64, _vp, _i64,
+                                         _vp, _vp, _i64, ctypes.POINTER(_i64), _vp]),
+    "mlrs_radius_neighbors_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _f64, _f64, _vp, _i64,
+                                         _vp, _vp, _i64, ctypes.POINTER(_i64), _vp]),
     "mlrs_release_workspace": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
     "mlrs_force_path": (_i32, [_i32]),
@@ -124,6 +134,8 @@ def check(rc):
         raise ShapeMismatch(info)
     if rc == MLRS_ERR_DIM_MISMATCH:
         raise DimMismatch(info)
+    if rc == MLRS_ERR_INVALID_PARAM:
+        raise InvalidParam(info)
     if rc == MLRS_ERR_UNSUPPORTED:
         raise UnsupportedError(info.message.decode())
     if rc == MLRS_ERR_NULL_POINTER:

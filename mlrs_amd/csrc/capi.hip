@@ -575,6 +575,7 @@ const char* mlrs_status_string(int32_t code) {
     case MLRS_ERR_NULL_POINTER: return "null pointer";
     case MLRS_ERR_HIP: return "HIP runtime error";
     case MLRS_ERR_ALLOC: return "device workspace allocation failed";
+    case MLRS_ERR_INVALID_PARAM: return "invalid parameter value";
     default: return "unknown status";
     }
 }
@@ -904,6 +905,297 @@ int32_t mlrs_knn_classify_f64(const int32_t* y_class, int64_t n_train, int32_t n
                                  proba, proba_len, labels, labels_len, stream);
 }
 
+// ---------------------------------------------------------------------------
+// radius_neighbors
+// ---------------------------------------------------------------------------
+// The count pass's products -- the in-row strip prefix, the row totals, the
+// row offsets and the match total -- are kept per device together with the
+// arguments of the call that made them.  A call with the same arguments (the
+// usual count-only call, then the call with buffers of the returned size)
+// starts from them instead of counting again.  The queries are staged afresh
+// in every call, and the fill pass checks each (strip, row) against its kept
+// count, so changed data is caught: on a mismatch the plan is dropped and the
+// call counts and fills again.
+extern "C++" {
+struct RadiusPlan {
+    bool valid = false;
+    const void* xq = nullptr;
+    const void* xt = nullptr;
+    int64_t nq = 0, nt = 0, d = 0;
+    int32_t metric = -1;
+    double p = 0.0, radius = 0.0;
+    int elem = 0;
+    void* stream = nullptr;
+    int nstrips = 0;
+    int64_t strip_len = 0;
+    unsigned long long total = 0;
+    char* base = nullptr;
+    size_t cap = 0;
+};
+RadiusPlan g_rplan[kMaxDevices];
+
+template <typename T>
+struct RadiusBufs {
+    uint32_t* cnt;
+    uint32_t* row_cnt;
+    unsigned long long* block_sum;
+    unsigned long long* qoff;
+    unsigned long long* total;
+    unsigned int* mismatch;
+    T* qT;
+    T* qsq;
+    T* qinv;
+    T* xsq;
+    T* xinv;
+};
+
+template <typename T>
+static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int nstrips, RadiusBufs<T>* b) {
+    const int RQ = radius_queries_per_wave<T>();
+    const int64_t G = (nq + RQ - 1) / RQ;
+    Carver cv(base);
+    b->cnt = cv.take<uint32_t>((size_t)std::max<int64_t>(1, (int64_t)nstrips * nq));
+    b->row_cnt = cv.take<uint32_t>((size_t)nq);
+    b->block_sum = cv.take<unsigned long long>((size_t)((nq + 255) / 256 + 1));
+    b->qoff = cv.take<unsigned long long>((size_t)nq);
+    b->total = cv.take<unsigned long long>(1);
+    b->mismatch = cv.take<unsigned int>(1);
+    b->qT = cv.take<T>((size_t)(G * RQ * d));
+    b->qsq = cv.take<T>((size_t)nq);
+    b->qinv = cv.take<T>((size_t)nq);
+    b->xsq = cv.take<T>((size_t)std::max<int64_t>(1, nt));
+    b->xinv = cv.take<T>((size_t)std::max<int64_t>(1, nt));
+    return cv.off + 256;
+}
+
+static int32_t radius_plan_memory(RadiusPlan& P, size_t bytes) {
+    if (P.cap >= bytes) return MLRS_OK;
+    P.valid = false;
+    if (P.base) {
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
+        (void)hipFree(P.base);
+        P.base = nullptr;
+        P.cap = 0;
+    }
+    size_t want = std::max(bytes + bytes / 4, (size_t)16 << 20);
+    hipError_t e = hipMalloc((void**)&P.base, want);
+    if (e != hipSuccess) {
+        P.base = nullptr;
+        return set_err(MLRS_ERR_ALLOC, "radius", (int64_t)want, 0, 0, (int)e,
+                       "device allocation of %zu bytes for the radius scan failed: %s", want, hipGetErrorString(e));
+    }
+    P.cap = want;
+    return MLRS_OK;
+}
+
+static int32_t read_u64(const unsigned long long* dev, hipStream_t s, unsigned long long* out) {
+    hipError_t e = hipMemcpyAsync(out, dev, sizeof(*out), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_err(e, "radius read-back");
+    return MLRS_OK;
+}
+
+template <typename T>
+static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, const T* xt, int64_t xt_len,
+                           int64_t nt, int64_t d_train, int32_t metric, double p, double radius, uint32_t* counts,
+                           int64_t counts_len, T* out_dist, int32_t* out_idx, int64_t capacity, int64_t* total,
+                           void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    // validate_radius_query (nearest.rs:755-797) and radius_host_scan's
+    // geometry checks (radius_host.rs:150-196)
+    if (!(radius >= 0.0))
+        return set_err(MLRS_ERR_INVALID_PARAM, "radius", 0, 0, 0, 0,
+                       "estimator 'nearest_neighbors': eps = %g is invalid (must be >= 0)", radius);
+    if (nq == 0 || d == 0 || !geom_ok(nq, d, xq_len)) return shape_err("xq", nq, d, xq_len);
+    if (d != d_train) return dim_err("n_features", d, d_train);
+    if (!geom_ok(nt, d_train, xt_len)) return shape_err("y", nt, d_train, xt_len);
+    if (nt > kU32Max) return shape_err("rows", nt, 0, kU32Max);
+    if (metric < MLRS_METRIC_EUCLIDEAN || metric > MLRS_METRIC_MINKOWSKI)
+        return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0, "metric %d is not served", metric);
+    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0))
+        return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
+    if (counts_len != nq) return shape_err("counts", nq, 1, counts_len);
+    if (!xq || (nt > 0 && !xt) || !counts || !total || ((out_dist == nullptr) != (out_idx == nullptr)))
+        return set_err(MLRS_ERR_NULL_POINTER, "ptr", 0, 0, 0, 0, "a required pointer is NULL");
+    if (out_dist && capacity < 0) return shape_err("out", 0, 1, capacity);
+    *total = 0;
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_err(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_err(MLRS_ERR_UNSUPPORTED, "device", dev, 0, 0, 0, "device ordinal %d out of range", dev);
+    char* ws;
+    int cus;
+    int32_t rc = workspace(256, s, &ws, &cus);  // the CU count
+    if (rc) return rc;
+
+    // arm: the host scan's lane arithmetic; threshold in the metric's internal
+    // units formed in f64 (scan_typed, radius_host.rs:239-271); boundary
+    // transform chosen by p as `transform` does (:559-569)
+    int arm = ARM_EUCLID_MULADD;
+    double thresh = radius, p_tr = 1.0;
+    int pint = 0;
+    switch (metric) {
+    case MLRS_METRIC_EUCLIDEAN: thresh = radius * radius; p_tr = 2.0; break;
+    case MLRS_METRIC_COSINE: arm = ARM_COS_HOST; break;
+    case MLRS_METRIC_MANHATTAN: arm = ARM_MANHATTAN; break;
+    case MLRS_METRIC_CHEBYSHEV: arm = ARM_CHEBYSHEV; break;
+    default:
+        pint = minkowski_powi(p);
+        arm = pint ? ARM_MINKOWSKI_INT : ARM_MINKOWSKI_POW;
+        thresh = std::pow(radius, p);
+        p_tr = p;
+    }
+
+    // strips: enough waves to fill the chip several times over
+    const int RQ = radius_queries_per_wave<T>();
+    const int64_t G = (nq + RQ - 1) / RQ;
+    const int64_t chunks = (nt + 63) / 64;
+    int64_t want_strips = ((int64_t)cus * 16 + G - 1) / G;
+    want_strips = std::max<int64_t>(1, std::min<int64_t>(want_strips, std::max<int64_t>(1, chunks)));
+    const int64_t strip_len = std::max<int64_t>(64, ((chunks + want_strips - 1) / want_strips) * 64);
+    const int nstrips = nt > 0 ? (int)((nt + strip_len - 1) / strip_len) : 0;
+
+    RadiusPlan& P = g_rplan[dev];
+    const int elem = (int)sizeof(T);
+    const bool same = P.valid && P.xq == xq && P.xt == xt && P.nq == nq && P.nt == nt && P.d == d &&
+                      P.metric == metric && P.p == p && P.radius == radius && P.elem == elem &&
+                      P.stream == stream && P.nstrips == nstrips && P.strip_len == strip_len;
+    RadiusBufs<T> B;
+    const size_t need = radius_carve<T>(nullptr, nq, nt, d, nstrips, &B);
+    if (!same) {
+        P.valid = false;
+        rc = radius_plan_memory(P, need);
+        if (rc) return rc;
+    }
+    (void)radius_carve<T>(P.base, nq, nt, d, nstrips, &B);
+
+    RadiusArgs<T> a{};
+    a.qT = B.qT;
+    a.x = xt;
+    a.qinv = B.qinv;
+    a.xinv = B.xinv;
+    a.nq = nq;
+    a.nt = nt;
+    a.d = d;
+    a.strip_len = strip_len;
+    a.nstrips = nstrips;
+    a.th = (T)thresh;
+    a.pexp = (T)p;
+    a.pint = pint;
+    const int transform = p_tr == 1.0 ? 0 : (p_tr == 2.0 ? 1 : 2);
+    a.cnt = B.cnt;
+    a.row_cnt = B.row_cnt;
+    a.qoff = B.qoff;
+    a.out_dist = out_dist;
+    a.out_idx = out_idx;
+    a.capacity = capacity;
+    a.mismatch = B.mismatch;
+
+    e = launch_radius_stage<T>(xq, nq, d, B.qT, s);
+    if (e == hipSuccess && arm == ARM_COS_HOST) {
+        // row_inv_norm_host (knn_host.rs:382-397)
+        e = launch_row_norms<T>(xq, nq, d, B.qsq, B.qinv, nullptr, nullptr, s);
+        if (e == hipSuccess && nt > 0) e = launch_row_norms<T>(xt, nt, d, B.xsq, B.xinv, nullptr, nullptr, s);
+    }
+    if (e != hipSuccess) return hip_err(e, "radius staging");
+
+    auto count = [&]() -> int32_t {
+        hipError_t e2 = launch_fill_u32(B.cnt, (int64_t)nstrips * nq, 0u, s);
+        if (e2 == hipSuccess) {
+            KernelTimer kt(s, "radius_scan_count");
+            e2 = launch_radius_scan<T>(a, arm, false, s);
+        }
+        if (e2 == hipSuccess) e2 = launch_radius_offsets(B.cnt, nq, nstrips, B.row_cnt, B.block_sum, B.qoff, B.total, s);
+        if (e2 != hipSuccess) return hip_err(e2, "radius count");
+        int32_t r2 = read_u64(B.total, s, &P.total);
+        if (r2) return r2;
+        P.valid = true;
+        P.xq = xq;
+        P.xt = xt;
+        P.nq = nq;
+        P.nt = nt;
+        P.d = d;
+        P.metric = metric;
+        P.p = p;
+        P.radius = radius;
+        P.elem = elem;
+        P.stream = stream;
+        P.nstrips = nstrips;
+        P.strip_len = strip_len;
+        return MLRS_OK;
+    };
+    auto fill = [&](unsigned int* bad) -> int32_t {
+        hipError_t e2 = launch_fill_u32(B.mismatch, 1, 0u, s);
+        if (e2 == hipSuccess) {
+            KernelTimer kt(s, "radius_scan_fill");
+            e2 = launch_radius_scan<T>(a, arm, true, s);
+        }
+        if (e2 != hipSuccess) return hip_err(e2, "radius fill");
+        e2 = hipMemcpyAsync(bad, B.mismatch, sizeof(*bad), hipMemcpyDeviceToHost, s);
+        if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
+        if (e2 != hipSuccess) return hip_err(e2, "radius read-back");
+        if (*bad) return MLRS_OK;
+        e2 = launch_radius_transform<T>(out_dist, (int64_t)P.total, transform, (T)(1.0 / p_tr), s);
+        if (e2 != hipSuccess) return hip_err(e2, "radius transform");
+        return MLRS_OK;
+    };
+    auto finish_counts = [&]() -> int32_t {
+        hipError_t e2 = hipMemcpyAsync(counts, B.row_cnt, sizeof(uint32_t) * (size_t)nq, hipMemcpyDeviceToDevice, s);
+        if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
+        if (e2 != hipSuccess) return hip_err(e2, "radius counts");
+        *total = (int64_t)P.total;
+        return MLRS_OK;
+    };
+
+    bool counted_now = false;
+    if (!same) {
+        rc = count();
+        if (rc) return rc;
+        counted_now = true;
+    }
+    for (;;) {
+        if (!out_dist || P.total > (unsigned long long)capacity) {
+            rc = finish_counts();
+            if (rc) return rc;
+            if (!out_dist) return ok();
+            return shape_err("out", (int64_t)P.total, 1, capacity);
+        }
+        unsigned int bad = 0;
+        rc = fill(&bad);
+        if (rc) return rc;
+        if (!bad) return finish_counts();
+        P.valid = false;
+        if (counted_now)
+            return set_err(MLRS_ERR_HIP, "radius", 0, 0, 0, 0,
+                           "radius fill pass disagrees with its own count pass (inputs modified during the call)");
+        rc = count();
+        if (rc) return rc;
+        counted_now = true;
+    }
+}
+}  // extern "C++"
+
+int32_t mlrs_radius_neighbors_f32(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                                  const float* x_train, int64_t x_train_len, int64_t n_train, int64_t train_features,
+                                  int32_t metric, double p, double radius, uint32_t* counts, int64_t counts_len,
+                                  float* out_dist, int32_t* out_idx, int64_t capacity, int64_t* total,
+                                  void* stream) {
+    return radius_impl<float>(xq, xq_len, n_query, n_features, x_train, x_train_len, n_train, train_features, metric,
+                              p, radius, counts, counts_len, out_dist, out_idx, capacity, total, stream);
+}
+
+int32_t mlrs_radius_neighbors_f64(const double* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                                  const double* x_train, int64_t x_train_len, int64_t n_train,
+                                  int64_t train_features, int32_t metric, double p, double radius, uint32_t* counts,
+                                  int64_t counts_len, double* out_dist, int32_t* out_idx, int64_t capacity,
+                                  int64_t* total, void* stream) {
+    return radius_impl<double>(xq, xq_len, n_query, n_features, x_train, x_train_len, n_train, train_features,
+                               metric, p, radius, counts, counts_len, out_dist, out_idx, capacity, total, stream);
+}
+
 int32_t mlrs_force_path(int32_t path) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (path < MLRS_PATH_AUTO || path > MLRS_PATH_GENERIC)
@@ -942,12 +1234,21 @@ int32_t mlrs_release_workspace(void) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MLRS_OK;
     Arena& A = g_arena[dev];
-    if (A.base) {
+    RadiusPlan& P = g_rplan[dev];
+    if (A.base || P.base) {
         hipError_t e = hipDeviceSynchronize();
         if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
+    }
+    if (A.base) {
         (void)hipFree(A.base);
         A.base = nullptr;
         A.cap = 0;
+    }
+    if (P.base) {
+        (void)hipFree(P.base);
+        P.base = nullptr;
+        P.cap = 0;
+        P.valid = false;
     }
     return MLRS_OK;
 }

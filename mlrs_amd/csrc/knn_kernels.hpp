@@ -216,4 +216,48 @@ hipError_t launch_knn_classify(const int32_t* y_class, int64_t n_train, int64_t 
                                T* proba, int32_t* labels, double* acc, int64_t* err, unsigned long long* first_bad,
                                hipStream_t s);
 
+// radius_neighbors (knn_radius.hip).  A query group of radius_queries_per_wave
+// rows is scanned against one strip of index rows per wave, 64 rows at a time
+// (lane = index row), in the arithmetic of the reference's host arm; the
+// matches of a group row within a 64-row chunk are placed by a wave ballot,
+// so each row's matches come out in ascending index order.  Two passes share
+// the kernel: COUNT writes each (strip, row) match count; FILL recomputes and
+// writes the matches' pre-boundary values at the offsets the count pass
+// fixed; launch_radius_transform then applies the boundary transform.
+template <typename T>
+struct RadiusArgs {
+    const T* qT;       // [G][d][RQ] query groups, transposed (zero rows past nq)
+    const T* x;        // [nt][d] index rows
+    const T* qinv;     // cosine: [G*RQ] query reciprocal norms
+    const T* xinv;     // cosine: [nt] index reciprocal norms
+    int64_t nq, nt, d;
+    int64_t strip_len; // index rows per strip (a multiple of 64)
+    int nstrips;
+    T th;              // threshold on the pre-boundary value
+    T pexp;            // Minkowski exponent of the pow arm
+    int pint;          // Minkowski integer exponent (3..8) of the multiply arm
+    uint32_t* cnt;     // [nstrips][nq]: COUNT writes counts; FILL reads the in-row exclusive prefix
+    const uint32_t* row_cnt;           // [nq] per-row totals (FILL: end check of the last strip)
+    const unsigned long long* qoff;    // [nq] first output position of each row
+    T* out_dist;
+    int32_t* out_idx;
+    int64_t capacity;                  // FILL: entries the outputs hold; no write at or past it
+    unsigned int* mismatch;            // FILL: set when a strip's matches differ from its count
+};
+template <typename T>
+int radius_queries_per_wave();
+template <typename T>
+hipError_t launch_radius_stage(const T* xq, int64_t nq, int64_t d, T* qT, hipStream_t s);
+template <typename T>
+hipError_t launch_radius_scan(const RadiusArgs<T>& a, int arm, bool fill, hipStream_t s);
+// Row totals, the in-row exclusive strip prefix, the row offsets and the
+// match total (one u64 on the device).
+hipError_t launch_radius_offsets(uint32_t* cnt, int64_t nq, int nstrips, uint32_t* row_cnt,
+                                 unsigned long long* block_sum, unsigned long long* qoff,
+                                 unsigned long long* total, hipStream_t s);
+// mode 1: v = sqrt(v); mode 2: v = pow(v, e); mode 0: nothing.
+template <typename T>
+hipError_t launch_radius_transform(T* v, int64_t n, int mode, T e, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
+
 }  // namespace mlrs

@@ -216,6 +216,117 @@ class _NeighborsBase:
             return idx
         return dist, idx
 
+    def kneighbors_graph(self, X=None, n_neighbors=None, mode="connectivity"):
+        """The ``(n_query, n_samples_fit_)`` sparse neighbour graph as a scipy
+        CSR matrix (neighbors.py:649-688): 1 per neighbour for
+        ``mode='connectivity'``, the distance for ``mode='distance'``."""
+        from scipy.sparse import csr_matrix
+
+        self._check_fitted()
+        if mode not in ("connectivity", "distance"):
+            raise ValueError('Unsupported mode, must be one of "connectivity" or "distance" but got "%s" instead'
+                             % (mode,))
+        dist, idx = self.kneighbors(X, n_neighbors, return_distance=True)
+        dist = dist.cpu().numpy() if isinstance(dist, torch.Tensor) else dist
+        idx = idx.cpu().numpy() if isinstance(idx, torch.Tensor) else idx
+        n_query, k = idx.shape
+        data = np.ones(n_query * k, dtype=np.float64) if mode == "connectivity" else \
+            np.asarray(dist, dtype=np.float64).ravel()
+        indptr = np.arange(0, n_query * k + 1, k)
+        return csr_matrix((data, idx.ravel(), indptr), shape=(n_query, self.n_samples_fit_))
+
+    # -- radius queries (neighbors.py:443-603) --
+    def _resolve_radius(self, radius):
+        r = self.radius if radius is None else radius
+        if not isinstance(r, (int, float, np.integer, np.floating)) or r < 0:
+            raise ValueError("radius must be non-negative, got %r" % (r,))
+        return float(r)
+
+    def _raw_radius_neighbors(self, X, radius):
+        """``(dist_list, idx_list, rows)``: each query row's matches, ascending
+        training index, from the device scan (mlrs_radius_neighbors_*)."""
+        if X is None:
+            q = self._fit_X_dev
+        else:
+            q, _ = _as_device_matrix(X, dtype=self._fit_X_dev.dtype, device=self._fit_X_dev.device)
+            self._check_query(q)
+        dist, idx, counts = prims.radius_neighbors(q, self._fit_X_dev, radius, self._engine_metric,
+                                                   p=self._engine_p)
+        dist = dist.cpu().numpy()
+        idx = idx.cpu().numpy()
+        counts = counts.cpu().numpy()
+        offsets = np.concatenate([[0], np.cumsum(counts)])
+        rows = counts.shape[0]
+        return ([dist[offsets[r]:offsets[r + 1]] for r in range(rows)],
+                [idx[offsets[r]:offsets[r + 1]] for r in range(rows)], rows)
+
+    @staticmethod
+    def _drop_self_ragged(dist_list, idx_list, rows):
+        """Drop each row's own index by identity (neighbors.py:493-510): a
+        duplicate training point at distance 0 stays."""
+        new_dist, new_idx = [], []
+        for i in range(rows):
+            keep = idx_list[i] != i
+            new_dist.append(dist_list[i][keep])
+            new_idx.append(idx_list[i][keep])
+        return new_dist, new_idx
+
+    @staticmethod
+    def _sort_ragged_by_distance(dist_list, idx_list, rows):
+        for i in range(rows):
+            order = np.argsort(dist_list[i], kind="stable")
+            dist_list[i] = dist_list[i][order]
+            idx_list[i] = idx_list[i][order]
+        return dist_list, idx_list
+
+    def _radius_lists(self, X, radius, sort_results):
+        self._check_fitted()
+        r = self._resolve_radius(radius)
+        dist_list, idx_list, rows = self._raw_radius_neighbors(X, r)
+        if X is None:
+            dist_list, idx_list = self._drop_self_ragged(dist_list, idx_list, rows)
+        if sort_results:
+            dist_list, idx_list = self._sort_ragged_by_distance(dist_list, idx_list, rows)
+        return dist_list, idx_list, rows
+
+    def radius_neighbors(self, X=None, radius=None, return_distance=True, sort_results=False):
+        """Every training point within ``radius`` of each row of ``X``
+        (neighbors.py:528-563): numpy object arrays with one sub-array per
+        query row, ascending training index unless ``sort_results``.
+        ``X=None`` queries the training set without each row's own index."""
+        self._check_fitted()
+        if sort_results and not return_distance:
+            raise ValueError("return_distance must be True if sort_results is True.")
+        dist_list, idx_list, rows = self._radius_lists(X, radius, sort_results)
+        indices = np.empty(rows, dtype=object)
+        for i in range(rows):
+            indices[i] = idx_list[i]
+        if not return_distance:
+            return indices
+        distances = np.empty(rows, dtype=object)
+        for i in range(rows):
+            distances[i] = dist_list[i]
+        return distances, indices
+
+    def radius_neighbors_graph(self, X=None, radius=None, mode="connectivity", sort_results=False):
+        """The ``(n_query, n_samples_fit_)`` sparse radius graph as a scipy CSR
+        matrix (neighbors.py:565-603)."""
+        from scipy.sparse import csr_matrix
+
+        self._check_fitted()
+        if mode not in ("connectivity", "distance"):
+            raise ValueError('Unsupported mode, must be one of "connectivity" or "distance" but got "%s" instead'
+                             % (mode,))
+        dist_list, idx_list, rows = self._radius_lists(X, radius, sort_results)
+        counts = np.array([len(a) for a in idx_list], dtype=np.int64)
+        indptr = np.concatenate([[0], np.cumsum(counts)])
+        all_idx = np.concatenate(idx_list) if rows else np.array([], dtype=np.int32)
+        if mode == "connectivity":
+            data = np.ones(all_idx.shape[0], dtype=np.float64)
+        else:
+            data = np.concatenate(dist_list).astype(np.float64) if rows else np.array([], dtype=np.float64)
+        return csr_matrix((data, all_idx, indptr), shape=(rows, self.n_samples_fit_))
+
 
 class NearestNeighbors(_NeighborsBase):
     """Brute-force neighbour search (mlrs.neighbors.NearestNeighbors)."""

@@ -13,7 +13,12 @@ Geometry is validated by the C ABI before any launch; a violation raises
 | ``kmeans_assign``   | assign_min, crates/mlrs-backend/src/prims/kmeans.rs:635-750      |
 | ``pairwise_distance`` | distance_direct / metric_distance, prims/distance.rs:428-727 |
 | ``row_sqnorms``     | row_sqnorms, crates/mlrs-backend/src/prims/kmeans.rs:805-832     |
+| ``radius_neighbors`` | radius_neighbor_indices_metric, crates/mlrs-algos/src/neighbors/nearest.rs:609-749 |
+| ``knn_regress``     | knn_regress_mean / knn_regress_gather, crates/mlrs-kernels/src/knn.rs:95-316 |
+| ``knn_classify``    | KNeighborsClassifier's host vote, crates/mlrs-algos/src/neighbors/classifier.rs:782-930 |
 """
+import ctypes
+
 import torch
 
 from . import _lib
@@ -144,6 +149,38 @@ def row_sqnorms(x, out=None):
                                                _stream(x.device))
     _lib.check(rc)
     return o
+
+
+def radius_neighbors(xq, x_train, radius, metric="euclidean", p=2.0):
+    """Every row of ``x_train`` within ``radius`` of each row of ``xq``
+    (mlrs_radius_neighbors_*).
+
+    Returns ``(distances, indices, counts)`` on the device: the matches of
+    query row 0, then row 1, ... concatenated, each row's in ascending
+    training index (the reference's RadiusNeighbors layout, a CSR matrix
+    without its indptr), ``indices`` int32, ``counts`` int64 per query row.
+    Synchronizes: the match total sizes the outputs."""
+    _dev_check(xq, x_train)
+    if x_train.dtype != xq.dtype:
+        raise TypeError("query and training dtypes differ")
+    s = _suffix(xq)
+    nq = xq.shape[0] if xq.dim() == 2 else 0
+    d = xq.shape[1] if xq.dim() == 2 else 0
+    nt = x_train.shape[0] if x_train.dim() == 2 else 0
+    dt = x_train.shape[1] if x_train.dim() == 2 else 0
+    counts = torch.empty(nq, dtype=torch.int32, device=xq.device)
+    total = ctypes.c_int64(0)
+    f = getattr(_lib.load(), "mlrs_radius_neighbors_" + s)
+    args = (_ptr(xq), xq.numel(), nq, d, _ptr(x_train), x_train.numel(), nt, dt, _metric_id(metric), float(p),
+            float(radius), _ptr(counts), counts.numel())
+    stream = _stream(xq.device)
+    _lib.check(f(*args, None, None, 0, ctypes.byref(total), stream))
+    n = int(total.value)
+    dist = torch.empty(n, dtype=xq.dtype, device=xq.device)
+    idx = torch.empty(n, dtype=torch.int32, device=xq.device)
+    if n:
+        _lib.check(f(*args, _ptr(dist), _ptr(idx), n, ctypes.byref(total), stream))
+    return dist, idx, counts.to(torch.int64)
 
 
 def _as_u32_idx(idx):

@@ -60,6 +60,9 @@ def _load():
         f = getattr(lib, "orc_row_sqnorms_" + s)
         f.argtypes = [vp, i64, i64, vp]
         f.restype = None
+        f = getattr(lib, "orc_radius_scan_" + s)
+        f.argtypes = [vp, i64, vp, i64, i64, i32, ctypes.c_double, ctypes.c_double, vp, vp, vp, vp, i32]
+        f.restype = i32
         f = getattr(lib, "orc_knn_regress_mean_" + s)
         f.argtypes = [vp, i64, vp, i64, i64, vp, vp]
         f.restype = None
@@ -147,6 +150,33 @@ def pairwise(x, y, metric="euclidean", sqrt=False, nthreads=0, p=2.0):
     if rc != 0:
         raise ValueError("oracle pairwise rejected d=%d" % d)
     return out
+
+
+def radius_neighbors(xq, xt, radius, metric="euclidean", nthreads=0, p=2.0):
+    """(distances, int32 indices, uint32 counts): every training row within
+    ``radius`` of each query row, concatenated row by row in ascending training
+    index (a CSR layout without indptr), distances through the metric's
+    boundary transform."""
+    lib = _load()
+    xq = np.ascontiguousarray(xq)
+    xt = np.ascontiguousarray(xt, dtype=xq.dtype)
+    nq, d = xq.shape
+    nt = xt.shape[0]
+    f = getattr(lib, "orc_radius_scan_" + _suffix(xq.dtype))
+    counts = np.zeros(nq, dtype=np.uint32)
+    rc = f(xq.ctypes.data, nq, xt.ctypes.data, nt, d, _metric_id(metric), float(p), float(radius),
+           counts.ctypes.data, None, None, None, int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle radius_neighbors rejected radius=%r, d=%d" % (radius, d))
+    offsets = np.zeros(nq, dtype=np.int64)
+    if nq > 1:
+        np.cumsum(counts[:-1], dtype=np.int64, out=offsets[1:])
+    total = int(counts.sum(dtype=np.int64))
+    dist = np.empty(total, dtype=xq.dtype)
+    idx = np.empty(total, dtype=np.int32)
+    f(xq.ctypes.data, nq, xt.ctypes.data, nt, d, _metric_id(metric), float(p), float(radius),
+      counts.ctypes.data, offsets.ctypes.data, dist.ctypes.data, idx.ctypes.data, int(nthreads))
+    return dist, idx, counts
 
 
 def row_sqnorms(x):

@@ -148,6 +148,107 @@ static inline void insert_##S(T *lval, uint32_t *lidx, int64_t k, T v, uint32_t 
     }                                                                                      \
 }                                                                                          \
                                                                                            \
+/* The lane loop: one training row y against the QB staged query lanes, in the             \
+ * arm's arithmetic; acc[a] receives lane a's pre-boundary value.  Shared by the           \
+ * k-nearest scan and the radius scan, as lane_distances is shared by knn_host             \
+ * and radius_host (knn_host.rs:693-760, radius_host.rs:51-60).  ynt is the                \
+ * training row's cosine norm operand. */                                                  \
+static inline void lane_dist_##S(const T *xt, const T *y, int64_t d, int metric, int arm,  \
+                                 const T *qn, T ynt, T pe, int pi, T *acc)                 \
+{                                                                                          \
+    for (int a = 0; a < ORC_QB; a++)                                                       \
+        acc[a] = (T)0;                                                                     \
+    if (metric == ORC_METRIC_EUCLIDEAN) {                                                  \
+        if (arm == ORC_ARM_HOST) {                                                         \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++) {                                         \
+                    T diff = xc[a] - yc;                                                   \
+                    acc[a] = acc[a] + diff * diff;                                         \
+                }                                                                          \
+            }                                                                              \
+        } else {                                                                           \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++) {                                         \
+                    T diff = xc[a] - yc;                                                   \
+                    acc[a] = FMA(diff, diff, acc[a]);                                      \
+                }                                                                          \
+            }                                                                              \
+        }                                                                                  \
+    } else if (metric == ORC_METRIC_MANHATTAN) {                                           \
+        /* acc + |x - y| (knn.rs:3277-3286, knn_host.rs:715-718) */                        \
+        for (int64_t c = 0; c < d; c++) {                                                  \
+            T yc = y[c];                                                                   \
+            const T *xc = xt + c * ORC_QB;                                                 \
+            for (int a = 0; a < ORC_QB; a++)                                               \
+                acc[a] = acc[a] + FABS(xc[a] - yc);                                        \
+        }                                                                                  \
+    } else if (metric == ORC_METRIC_CHEBYSHEV) {                                           \
+        /* running max as a select: NaN never replaces (knn.rs:3288-3312) */               \
+        for (int64_t c = 0; c < d; c++) {                                                  \
+            T yc = y[c];                                                                   \
+            const T *xc = xt + c * ORC_QB;                                                 \
+            for (int a = 0; a < ORC_QB; a++) {                                             \
+                T v = FABS(xc[a] - yc);                                                    \
+                acc[a] = (v > acc[a]) ? v : acc[a];                                        \
+            }                                                                              \
+        }                                                                                  \
+    } else if (metric == ORC_METRIC_MINKOWSKI) {                                           \
+        /* acc + |x - y|^p: multiply chain for integer p in 3..8, else powf                \
+         * (knn.rs:3314-3360, knn_host.rs:728-742) */                                      \
+        for (int64_t c = 0; c < d; c++) {                                                  \
+            T yc = y[c];                                                                   \
+            const T *xc = xt + c * ORC_QB;                                                 \
+            for (int a = 0; a < ORC_QB; a++) {                                             \
+                T ad = FABS(xc[a] - yc);                                                   \
+                T r;                                                                       \
+                if (pi > 0) {                                                              \
+                    r = ad;                                                                \
+                    for (int i = 1; i < pi; i++)                                           \
+                        r = r * ad;                                                        \
+                } else {                                                                   \
+                    r = POW(ad, pe);                                                       \
+                }                                                                          \
+                acc[a] = acc[a] + r;                                                       \
+            }                                                                              \
+        }                                                                                  \
+    } else {                                                                               \
+        if (arm == ORC_ARM_HOST) {                                                         \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++)                                           \
+                    acc[a] = acc[a] + xc[a] * yc;                                          \
+            }                                                                              \
+            T iy = ynt;                                                                    \
+            for (int a = 0; a < ORC_QB; a++) {                                             \
+                T dv = (T)1 - acc[a] * qn[a] * iy;                                         \
+                dv = (dv < (T)0) ? (T)0 : dv;                                              \
+                dv = (dv > (T)2) ? (T)2 : dv;                                              \
+                acc[a] = dv;                                                               \
+            }                                                                              \
+        } else {                                                                           \
+            for (int64_t c = 0; c < d; c++) {                                              \
+                T yc = y[c];                                                               \
+                const T *xc = xt + c * ORC_QB;                                             \
+                for (int a = 0; a < ORC_QB; a++)                                           \
+                    acc[a] = FMA(xc[a], yc, acc[a]);                                       \
+            }                                                                              \
+            for (int a = 0; a < ORC_QB; a++) {                                             \
+                T denom = SQRT(qn[a] * ynt);                                               \
+                T sim = (denom > (T)0) ? acc[a] / denom : (T)0;                            \
+                T dv = (T)1 - sim;                                                         \
+                dv = (dv < (T)0) ? (T)0 : dv;                                              \
+                dv = (dv > (T)2) ? (T)2 : dv;                                              \
+                acc[a] = dv;                                                               \
+            }                                                                              \
+        }                                                                                  \
+    }                                                                                      \
+}                                                                                          \
+                                                                                           \
 /* One 32-query block against every training row, under `arm`/`metric`.                 \
  * xt is the transposed tile xt[c*QB + a]; lanes >= active stage zeros and are            \
  * never emitted.  qn / yn are the cosine norm operands of the arm (squared              \
@@ -162,98 +263,7 @@ static void scan_block_##S(const T *xt, int64_t active, const T *xtrain, int64_t
         worst[a] = (a < active) ? (T)INFINITY : (T)-INFINITY;                              \
     for (int64_t t = 0; t < nt; t++) {                                                     \
         const T *y = xtrain + t * d;                                                       \
-        for (int a = 0; a < ORC_QB; a++)                                                   \
-            acc[a] = (T)0;                                                                 \
-        if (metric == ORC_METRIC_EUCLIDEAN) {                                              \
-            if (arm == ORC_ARM_HOST) {                                                     \
-                for (int64_t c = 0; c < d; c++) {                                          \
-                    T yc = y[c];                                                           \
-                    const T *xc = xt + c * ORC_QB;                                         \
-                    for (int a = 0; a < ORC_QB; a++) {                                     \
-                        T diff = xc[a] - yc;                                               \
-                        acc[a] = acc[a] + diff * diff;                                     \
-                    }                                                                      \
-                }                                                                          \
-            } else {                                                                       \
-                for (int64_t c = 0; c < d; c++) {                                          \
-                    T yc = y[c];                                                           \
-                    const T *xc = xt + c * ORC_QB;                                         \
-                    for (int a = 0; a < ORC_QB; a++) {                                     \
-                        T diff = xc[a] - yc;                                               \
-                        acc[a] = FMA(diff, diff, acc[a]);                                  \
-                    }                                                                      \
-                }                                                                          \
-            }                                                                              \
-        } else if (metric == ORC_METRIC_MANHATTAN) {                                      \
-            /* acc + |x - y| (knn.rs:3277-3286, knn_host.rs:715-718) */                   \
-            for (int64_t c = 0; c < d; c++) {                                              \
-                T yc = y[c];                                                               \
-                const T *xc = xt + c * ORC_QB;                                             \
-                for (int a = 0; a < ORC_QB; a++)                                           \
-                    acc[a] = acc[a] + FABS(xc[a] - yc);                                    \
-            }                                                                              \
-        } else if (metric == ORC_METRIC_CHEBYSHEV) {                                      \
-            /* running max as a select: NaN never replaces (knn.rs:3288-3312) */           \
-            for (int64_t c = 0; c < d; c++) {                                              \
-                T yc = y[c];                                                               \
-                const T *xc = xt + c * ORC_QB;                                             \
-                for (int a = 0; a < ORC_QB; a++) {                                         \
-                    T v = FABS(xc[a] - yc);                                                \
-                    acc[a] = (v > acc[a]) ? v : acc[a];                                    \
-                }                                                                          \
-            }                                                                              \
-        } else if (metric == ORC_METRIC_MINKOWSKI) {                                      \
-            /* acc + |x - y|^p: multiply chain for integer p in 3..8, else powf           \
-             * (knn.rs:3314-3360, knn_host.rs:728-742) */                                 \
-            for (int64_t c = 0; c < d; c++) {                                              \
-                T yc = y[c];                                                               \
-                const T *xc = xt + c * ORC_QB;                                             \
-                for (int a = 0; a < ORC_QB; a++) {                                         \
-                    T ad = FABS(xc[a] - yc);                                               \
-                    T r;                                                                   \
-                    if (pi > 0) {                                                          \
-                        r = ad;                                                            \
-                        for (int i = 1; i < pi; i++)                                       \
-                            r = r * ad;                                                    \
-                    } else {                                                               \
-                        r = POW(ad, pe);                                                   \
-                    }                                                                      \
-                    acc[a] = acc[a] + r;                                                   \
-                }                                                                          \
-            }                                                                              \
-        } else {                                                                           \
-            if (arm == ORC_ARM_HOST) {                                                     \
-                for (int64_t c = 0; c < d; c++) {                                          \
-                    T yc = y[c];                                                           \
-                    const T *xc = xt + c * ORC_QB;                                         \
-                    for (int a = 0; a < ORC_QB; a++)                                       \
-                        acc[a] = acc[a] + xc[a] * yc;                                      \
-                }                                                                          \
-                T iy = yn[t];                                                              \
-                for (int a = 0; a < ORC_QB; a++) {                                         \
-                    T dv = (T)1 - acc[a] * qn[a] * iy;                                     \
-                    dv = (dv < (T)0) ? (T)0 : dv;                                          \
-                    dv = (dv > (T)2) ? (T)2 : dv;                                          \
-                    acc[a] = dv;                                                           \
-                }                                                                          \
-            } else {                                                                       \
-                for (int64_t c = 0; c < d; c++) {                                          \
-                    T yc = y[c];                                                           \
-                    const T *xc = xt + c * ORC_QB;                                         \
-                    for (int a = 0; a < ORC_QB; a++)                                       \
-                        acc[a] = FMA(xc[a], yc, acc[a]);                                   \
-                }                                                                          \
-                T ynt = yn[t];                                                             \
-                for (int a = 0; a < ORC_QB; a++) {                                         \
-                    T denom = SQRT(qn[a] * ynt);                                           \
-                    T sim = (denom > (T)0) ? acc[a] / denom : (T)0;                        \
-                    T dv = (T)1 - sim;                                                     \
-                    dv = (dv < (T)0) ? (T)0 : dv;                                          \
-                    dv = (dv > (T)2) ? (T)2 : dv;                                          \
-                    acc[a] = dv;                                                           \
-                }                                                                          \
-            }                                                                              \
-        }                                                                                  \
+        lane_dist_##S(xt, y, d, metric, arm, qn, yn ? yn[t] : (T)0, pe, pi, acc);          \
         int hit = 0;                                                                       \
         for (int a = 0; a < ORC_QB; a++)                                                   \
             hit |= (acc[a] <= worst[a]);                                                   \
@@ -328,6 +338,85 @@ int orc_knn_topk_##S(const T *xq, int64_t nq, const T *xtrain, int64_t nt, int64
         free(xt);                                                                          \
         free(lval);                                                                        \
         free(lidx);                                                                        \
+    }                                                                                      \
+    free(qn);                                                                              \
+    free(yn);                                                                              \
+    return 0;                                                                              \
+}                                                                                          \
+                                                                                           \
+/* radius_neighbors under the reference's default arm, the fused host scan                 \
+ * (radius_host.rs:239-299 scan_typed, :302-420 scan, :488-528 threshold_block,            \
+ * :531-569 emit / transform), over the same lane loop as the k-nearest host arm.          \
+ * The threshold is formed in double -- radius*radius for Euclidean,                       \
+ * pow(radius, p) for Minkowski, radius otherwise -- then rounded to T once;               \
+ * a lane matches when its pre-boundary value is <= it (NaN never matches).                \
+ * counts[q] receives each query row's match count.  When out_val is given the             \
+ * matches are also written, row q's at offsets[q] on (the caller's exclusive              \
+ * prefix sum of counts), in ascending training index, each value through the              \
+ * boundary transform chosen by p_tr (2 Euclidean, p Minkowski, 1 otherwise):              \
+ * identity for 1, SQRT for 2, else POW(v, (T)(1/p_tr)).  Indices are written              \
+ * as int32, as the reference's `t as i32`.                                                \
+ * Returns 0, or -1 for d < 1 or a radius that is not >= 0. */                             \
+int orc_radius_scan_##S(const T *xq, int64_t nq, const T *xtrain, int64_t nt, int64_t d,   \
+                        int metric, double p, double radius, uint32_t *counts,             \
+                        const int64_t *offsets, T *out_val, int32_t *out_idx, int nthreads)\
+{                                                                                          \
+    if (d < 1 || nq < 0 || nt < 0 || !(radius >= 0.0))                                     \
+        return -1;                                                                         \
+    const int pi = (metric == ORC_METRIC_MINKOWSKI) ? minkowski_powi(p) : 0;               \
+    const T pe = (T)p;                                                                     \
+    const double thresh = (metric == ORC_METRIC_EUCLIDEAN) ? radius * radius               \
+                        : (metric == ORC_METRIC_MINKOWSKI) ? pow(radius, p) : radius;      \
+    const T th = (T)thresh;                                                                \
+    const double p_tr = (metric == ORC_METRIC_EUCLIDEAN) ? 2.0                             \
+                      : (metric == ORC_METRIC_MINKOWSKI) ? p : 1.0;                        \
+    const T inv_p = (T)(1.0 / p_tr);                                                       \
+    T *qn = NULL, *yn = NULL;                                                              \
+    if (metric == ORC_METRIC_COSINE) {                                                     \
+        qn = (T *)malloc(sizeof(T) * (size_t)(nq > 0 ? nq : 1));                           \
+        yn = (T *)malloc(sizeof(T) * (size_t)(nt > 0 ? nt : 1));                           \
+        inv_norms_##S(xq, nq, d, qn);                                                      \
+        inv_norms_##S(xtrain, nt, d, yn);                                                  \
+    }                                                                                      \
+    int64_t nblocks = (nq + ORC_QB - 1) / ORC_QB;                                          \
+    set_threads(nthreads);                                                                 \
+    _Pragma("omp parallel")                                                                \
+    {                                                                                      \
+        T *xt = (T *)malloc(sizeof(T) * (size_t)(d * ORC_QB));                             \
+        T acc[ORC_QB];                                                                     \
+        T qblk[ORC_QB];                                                                    \
+        int64_t cnt[ORC_QB];                                                               \
+        _Pragma("omp for schedule(dynamic, 1)")                                            \
+        for (int64_t b = 0; b < nblocks; b++) {                                            \
+            int64_t q0 = b * ORC_QB;                                                       \
+            int64_t active = nq - q0 < ORC_QB ? nq - q0 : ORC_QB;                          \
+            for (int64_t c = 0; c < d; c++)                                                \
+                for (int a = 0; a < ORC_QB; a++)                                           \
+                    xt[c * ORC_QB + a] = (a < active) ? xq[(q0 + a) * d + c] : (T)0;       \
+            for (int a = 0; a < ORC_QB; a++) {                                             \
+                qblk[a] = (qn && a < active) ? qn[q0 + a] : (T)0;                          \
+                cnt[a] = 0;                                                                \
+            }                                                                              \
+            for (int64_t t = 0; t < nt; t++) {                                             \
+                lane_dist_##S(xt, xtrain + t * d, d, metric, ORC_ARM_HOST, qblk,           \
+                              yn ? yn[t] : (T)0, pe, pi, acc);                             \
+                for (int64_t a = 0; a < active; a++) {                                     \
+                    if (!(acc[a] <= th))                                                   \
+                        continue;                                                          \
+                    if (out_val) {                                                         \
+                        T v = acc[a];                                                      \
+                        v = (p_tr == 1.0) ? v : (p_tr == 2.0) ? SQRT(v) : POW(v, inv_p);   \
+                        int64_t at = offsets[q0 + a] + cnt[a];                             \
+                        out_val[at] = v;                                                   \
+                        out_idx[at] = (int32_t)(uint32_t)t;                                \
+                    }                                                                      \
+                    cnt[a]++;                                                              \
+                }                                                                          \
+            }                                                                              \
+            for (int64_t a = 0; a < active; a++)                                           \
+                counts[q0 + a] = (uint32_t)cnt[a];                                         \
+        }                                                                                  \
+        free(xt);                                                                          \
     }                                                                                      \
     free(qn);                                                                              \
     free(yn);                                                                              \

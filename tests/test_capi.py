@@ -35,8 +35,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib.load()
-    assert lib.mlrs_abi_version() == 2
+    assert lib.mlrs_abi_version() == 3
     assert lib.mlrs_status_string(0) == b"ok"
+    assert lib.mlrs_status_string(-7) == b"invalid parameter value"
     assert lib.mlrs_status_string(-1) == b"shape mismatch"
     assert lib.mlrs_status_string(-2) == b"dimension mismatch"
 
@@ -161,3 +162,38 @@ def test_metric_family_validation():
     g = lib.mlrs_pairwise_distance_f64
     assert g(P, 15, 5, 3, P, 12, 4, 3, 4, 0, float("nan"), P, 20, None) == _lib.MLRS_ERR_UNSUPPORTED
     assert _info().operand == b"p"
+
+
+def _radius32(xq_len=40, nq=10, d=4, xt_len=80, nt=20, dt=4, metric=0, p=2.0, radius=1.0, counts_len=10,
+              out=None, cap=0):
+    total = ctypes.c_int64(-1)
+    rc = _lib.load().mlrs_radius_neighbors_f32(P, xq_len, nq, d, P, xt_len, nt, dt, metric, p, radius, P,
+                                              counts_len, out, out, cap, ctypes.byref(total), None)
+    return rc
+
+
+@pytest.mark.parametrize("kw,code,operand", [
+    (dict(radius=-1.0), _lib.MLRS_ERR_INVALID_PARAM, b"radius"),
+    (dict(radius=float("nan")), _lib.MLRS_ERR_INVALID_PARAM, b"radius"),
+    (dict(nq=0, xq_len=0), _lib.MLRS_ERR_SHAPE_MISMATCH, b"xq"),
+    (dict(d=0, xq_len=0, dt=0, xt_len=0), _lib.MLRS_ERR_SHAPE_MISMATCH, b"xq"),
+    (dict(xq_len=39), _lib.MLRS_ERR_SHAPE_MISMATCH, b"xq"),
+    (dict(dt=5, xt_len=100), _lib.MLRS_ERR_DIM_MISMATCH, b"n_features"),
+    (dict(xt_len=81), _lib.MLRS_ERR_SHAPE_MISMATCH, b"y"),
+    (dict(metric=5), _lib.MLRS_ERR_UNSUPPORTED, b"metric"),
+    (dict(metric=4, p=0.5), _lib.MLRS_ERR_UNSUPPORTED, b"p"),
+    (dict(counts_len=9), _lib.MLRS_ERR_SHAPE_MISMATCH, b"counts"),
+])
+def test_radius_validation(kw, code, operand):
+    """radius_neighbors rejects bad radii and geometry before any launch, in
+    validate_radius_query's order (nearest.rs:755-797)."""
+    assert _radius32(**kw) == code
+    assert _info().operand == operand
+
+
+def test_radius_error_text_and_python_mapping():
+    assert _radius32(radius=-0.5) == _lib.MLRS_ERR_INVALID_PARAM
+    assert b"eps = -0.5 is invalid (must be >= 0)" in _info().message
+    with pytest.raises(_lib.InvalidParam) as ei:
+        _lib.check(_radius32(radius=-0.5))
+    assert ei.value.operand == "radius"
