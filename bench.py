@@ -12,6 +12,11 @@ on; `cpu_baseline` is the CPU oracle (the C restatement of the mlrs cpu-backend
 arithmetic) timed on a bounded sample of the same workload on this host.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
+  python bench.py --radius R [--config c2]    # radius_neighbors on the same data
+
+With --radius a step is one radius_neighbors call (count pass, row offsets,
+fill pass, boundary transform) of all queries against the index; its parity
+is checked against the CPU oracle on a few query rows.
 """
 import argparse
 import ctypes
@@ -24,7 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAKS = {  # MI355X published dense peaks
-    "mfma_f32": 157.3, "mfma_f64": 78.6, "valu_f32": 78.6, "hbm": 8000.0,
+    "mfma_f32": 157.3, "mfma_f64": 78.6, "valu_f32": 78.6, "valu_f64": 78.6, "hbm": 8000.0,
 }
 METRIC = "kNN dist-evals/s, 1M×10k d=128 k=32 f32; % of MFMA/HBM roofline"
 
@@ -41,6 +46,8 @@ def main():
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--radius", type=float, default=None,
+                    help="measure radius_neighbors with this radius instead of the k-nearest search")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel "
                          "of known traffic, the scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -68,7 +75,14 @@ def main():
     k, metric = cfg["k"], cfg["metric"]
     n_query, n_index, d = a.shape[0], b.shape[0], a.shape[1]
 
+    radius = args.radius
+    if radius is not None and kmeans:
+        print("--radius needs a k-nearest configuration (c1-c4)", file=sys.stderr)
+        sys.exit(2)
+
     def step():
+        if radius is not None:
+            return prims.radius_neighbors(ta, tb, radius, metric)
         if kmeans:
             return prims.kmeans_assign(ta, tb)
         return prims.knn_topk(ta, tb, k, metric)
@@ -108,7 +122,20 @@ def main():
     # ---- parity of the measured run against the committed golden subset ----
     g = np.load(os.path.join(ROOT, "tests", "golden", "%s_golden.npz" % args.config))
     sub = g["subset"]
-    if kmeans:
+    if radius is not None:
+        import oracle
+        dist, idx, cnt = out
+        cnt = cnt.cpu().numpy()
+        off = np.concatenate([[0], np.cumsum(cnt)])
+        rows = np.unique(np.linspace(0, n_query - 1, 8).astype(np.int64))
+        wd, wi, wc = oracle.radius_neighbors(a[rows], b, radius, metric)
+        woff = np.concatenate([[0], np.cumsum(wc.astype(np.int64))])
+        gd, gi = dist.cpu().numpy(), idx.cpu().numpy()
+        ok = all(cnt[q] == wc[j] and np.array_equal(gi[off[q]:off[q + 1]], wi[woff[j]:woff[j + 1]])
+                 and np.array_equal(gd[off[q]:off[q + 1]], wd[woff[j]:woff[j + 1]]) for j, q in enumerate(rows))
+        sub = rows
+        matches = int(cnt.sum())
+    elif kmeans:
         lab, sq = out
         ok = (np.array_equal(lab.cpu().numpy()[sub], g["labels"].astype(np.int64))
               and np.array_equal(sq.cpu().numpy()[sub], g["sqdist"]))
@@ -116,13 +143,19 @@ def main():
         dist, idx = out
         ok = (np.array_equal(idx.cpu().numpy()[sub], g["idx"].astype(np.int64))
               and np.array_equal(dist.cpu().numpy()[sub], g["dist"]))
-    parity = "bitwise-equal to the CPU oracle on %d golden rows" % len(sub) if ok else "MISMATCH vs golden rows"
+    parity = ("bitwise-equal to the CPU oracle on %d %s rows" % (len(sub), "sampled" if radius is not None else "golden")
+              if ok else "MISMATCH vs the CPU oracle")
     log(parity)
 
     evals = float(n_query) * float(n_index)
     value = evals / (ms_per_step / 1000.0)
     flops = 2.0 * d * evals
-    if args.config == "c4":
+    if radius is not None:
+        # the exact scan: a subtract, a multiply and an add per pair and
+        # feature (no fused multiply-add: the reference's operation order)
+        flops = 3.0 * d * evals
+        bound, peak, unit = "valu", PEAKS["valu_f32" if cfg["dtype"] == "f32" else "valu_f64"], "TFLOP/s"
+    elif args.config == "c4":
         bound, peak, unit = "valu", PEAKS["valu_f32"], "TFLOP/s"
     elif args.config == "c3":
         bound, peak, unit = "mfma", PEAKS["mfma_f64"], "TFLOP/s"
@@ -130,7 +163,8 @@ def main():
         bound, peak, unit = "mfma", PEAKS["mfma_f32"], "TFLOP/s"
     achieved = flops / (kern_ms / 1000.0) / 1e12
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "traffic_%s.json" % args.config)
+    tfile = os.path.join(ROOT, "profiles", "traffic_%s%s.json" % ("radius_" if radius is not None else "",
+                                                                   args.config))
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
@@ -141,10 +175,14 @@ def main():
         # bounded sample: a prefix of the queries against the full index, run
         # repeatedly until about 10 s of CPU work has been timed
         sample = {"c1": n_query, "c2": 2000, "c3": 256, "c4": 20000, "c5": 400000}[args.config]
+        if radius is not None:
+            sample = {"c1": n_query, "c2": 512, "c3": 128, "c4": 20000}[args.config]
         log("CPU baseline: %d of %d queries, %d threads" % (sample, n_query, threads))
 
         def cpu_pass():
-            if kmeans:
+            if radius is not None:
+                oracle.radius_neighbors(a[:sample], b, radius, metric, nthreads=threads)
+            elif kmeans:
                 oracle.kmeans_assign(a[:sample], b, nthreads=threads)
             else:
                 oracle.knn_topk(a[:sample], b, k, metric, nthreads=threads)
@@ -165,8 +203,12 @@ def main():
           "c3": "c3: 200k x 5k, d=256, k=16, f64 cosine, U[0,1)",
           "c4": "c4: 500k self-kNN, d=3, k=8, f32, 5% exact duplicates",
           "c5": "c5: k-means assign, 5M points x 1024 centroids, d=64, f32"}[args.config]
+    if radius is not None:
+        wl = "radius_neighbors, radius %g, on %s (%d matches, %.1f per query)" % (radius, wl, matches,
+                                                                                 matches / n_query)
     line = {
-        "metric": METRIC if args.config == "c2" else "dist-evals/s (%s)" % args.config,
+        "metric": (METRIC if args.config == "c2" else "dist-evals/s (%s)" % args.config) if radius is None
+        else "radius_neighbors dist-evals/s (%s)" % args.config,
         "value": value,
         "unit": "dist-evals/s",
         "n_gpus": 1,
@@ -178,7 +220,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f64" if cfg["dtype"] == "f64" else "f32",
         "data": "synthetic (seeded generator, mlrs_amd/synthetic.py)",
-        "config": {"workload": wl, "n_index": n_index, "n_query": n_query, "d": d, "k": k, "metric": metric,
+        "config": {"workload": wl, "n_index": n_index, "n_query": n_query, "d": d,
+                   "k": k if radius is None else None, "radius": radius, "metric": metric,
                    "queries_per_s": n_query / (ms_per_step / 1000.0), "parity": parity},
         "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
                      "traffic": traffic, "kernel": name.value.decode(), "kernel_ms": kern_ms},

@@ -338,8 +338,6 @@ static int pick_path(bool lowd_ok, bool gram_ok) {
 int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
                    int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
     const bool cos = (arm == ARM_COS_FOLD);
-    const int64_t qpb = gram_f32_queries_per_block();
-    const int64_t nblocks = (nq + qpb - 1) / qpb;
     // sizes that do not depend on the strip count
     size_t fixed = aligned_bytes(sizeof(float) * nq) + 2 * aligned_bytes(sizeof(float) * nt) +
                    aligned_bytes(sizeof(NormStats)) + 1024;
@@ -910,9 +908,9 @@ int32_t mlrs_knn_classify_f64(const int32_t* y_class, int64_t n_train, int32_t n
 // ---------------------------------------------------------------------------
 // The count pass's products -- the in-row strip prefix, the row totals, the
 // row offsets and the match total -- are kept per device together with the
-// arguments of the call that made them.  A call with the same arguments (the
-// usual count-only call, then the call with buffers of the returned size)
-// starts from them instead of counting again.  The queries are staged afresh
+// arguments of the call that made them, until a call fills from them.  A call
+// with the same arguments (the usual count-only call, then the call with
+// buffers of the returned size) starts from them instead of counting again.  The queries are staged afresh
 // in every call, and the fill pass checks each (strip, row) against its kept
 // count, so changed data is caught: on a mismatch the plan is dropped and the
 // call counts and fills again.
@@ -1104,10 +1102,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
 
     auto count = [&]() -> int32_t {
         hipError_t e2 = launch_fill_u32(B.cnt, (int64_t)nstrips * nq, 0u, s);
-        if (e2 == hipSuccess) {
-            KernelTimer kt(s, "radius_scan_count");
-            e2 = launch_radius_scan<T>(a, arm, false, s);
-        }
+        if (e2 == hipSuccess) e2 = launch_radius_scan<T>(a, arm, false, s);
         if (e2 == hipSuccess) e2 = launch_radius_offsets(B.cnt, nq, nstrips, B.row_cnt, B.block_sum, B.qoff, B.total, s);
         if (e2 != hipSuccess) return hip_err(e2, "radius count");
         int32_t r2 = read_u64(B.total, s, &P.total);
@@ -1166,7 +1161,12 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         unsigned int bad = 0;
         rc = fill(&bad);
         if (rc) return rc;
-        if (!bad) return finish_counts();
+        if (!bad) {
+            // the kept counts serve the call right after the one that made
+            // them, not every later call with the same arguments
+            P.valid = false;
+            return finish_counts();
+        }
         P.valid = false;
         if (counted_now)
             return set_err(MLRS_ERR_HIP, "radius", 0, 0, 0, 0,

@@ -70,8 +70,12 @@ __device__ __forceinline__ T radius_step(T acc, T q, T x, T pexp, int pint) {
     }
 }
 
+// qT and the outputs come as their own restrict-qualified arguments: with
+// them the compiler knows the match stores cannot touch the query groups and
+// keeps the uniform query loads on the scalar unit.
 template <typename T, int RQ, int ARM, bool VEC, bool FILL>
-__global__ __launch_bounds__(256) void radius_scan_kernel(RadiusArgs<T> a) {
+__global__ __launch_bounds__(256) void radius_scan_kernel(RadiusArgs<T> a, const T* __restrict__ qT,
+                                                          T* __restrict__ out_dist, int32_t* __restrict__ out_idx) {
     constexpr int V = VEC ? 16 / (int)sizeof(T) : 1;
     const int lane = threadIdx.x & 63;
     const int s = (int)blockIdx.y * 4 + (threadIdx.x >> 6);
@@ -82,7 +86,7 @@ __global__ __launch_bounds__(256) void radius_scan_kernel(RadiusArgs<T> a) {
     const int64_t t_begin = (int64_t)s * a.strip_len;
     const int64_t t_end = (t_begin + a.strip_len) < a.nt ? t_begin + a.strip_len : a.nt;
     const int64_t d = a.d;
-    const T* __restrict__ qg = a.qT + g * d * RQ;
+    const T* __restrict__ qg = qT + g * d * RQ;
     const uint64_t below = (1ull << lane) - 1ull;
 
     // rel[r]: row r's matches so far in this strip (wave-uniform).  FILL:
@@ -141,8 +145,8 @@ __global__ __launch_bounds__(256) void radius_scan_kernel(RadiusArgs<T> a) {
                     if (hit) {
                         const unsigned long long pos = b + rel[r] + (unsigned long long)__popcll(m & below);
                         if (pos < (unsigned long long)a.capacity) {
-                            a.out_dist[pos] = v;
-                            a.out_idx[pos] = (int32_t)(uint32_t)t;
+                            out_dist[pos] = v;
+                            out_idx[pos] = (int32_t)(uint32_t)t;
                         }
                     }
                 }
@@ -255,9 +259,11 @@ template <typename T, int RQ, int ARM, bool VEC>
 hipError_t launch_scan_arm(const RadiusArgs<T>& a, bool fill, hipStream_t s) {
     const dim3 grid((unsigned)((a.nq + RQ - 1) / RQ), (unsigned)((a.nstrips + 3) / 4));
     if (fill)
-        hipLaunchKernelGGL((radius_scan_kernel<T, RQ, ARM, VEC, true>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((radius_scan_kernel<T, RQ, ARM, VEC, true>), grid, dim3(256), 0, s, a, a.qT, a.out_dist,
+                           a.out_idx);
     else
-        hipLaunchKernelGGL((radius_scan_kernel<T, RQ, ARM, VEC, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((radius_scan_kernel<T, RQ, ARM, VEC, false>), grid, dim3(256), 0, s, a, a.qT, a.out_dist,
+                           a.out_idx);
     return hipGetLastError();
 }
 
