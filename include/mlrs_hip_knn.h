@@ -269,6 +269,52 @@ int32_t mlrs_radius_neighbors_f64(const double *xq, int64_t xq_len, int64_t n_qu
                                   int64_t counts_len, double *out_dist, int32_t *out_idx, int64_t capacity,
                                   int64_t *total, void *stream);
 
+/*
+ * Directed k-nearest-neighbour graph of a row set against itself.
+ *
+ * Replaces: knn_graph (crates/mlrs-backend/src/prims/knn_graph.rs:180-311) as
+ *   the cpu backend serves its callers, through host_knn (crates/mlrs-algos/src/
+ *   manifold/umap_host_knn.rs:212-515, UMAP, include_self = 0) and the
+ *   self-inclusive graph HDBSCAN reads (include_self = 1).  The arithmetic is
+ *   that host scan's, in f64 (f32 rows are widened first): Euclidean
+ *   sqrt(sum diff*diff), cosine 0.5*|x^ - y^|^2 over L2-normalised rows,
+ *   Manhattan, Chebyshev (NaN never replaces the running max), Minkowski
+ *   pow(sum pow(|diff|, p), 1/p).  out_idx / out_dist (n x k, device): per row
+ *   ascending (distance, index); include_self = 0 leaves out the row's own
+ *   index (by identity, not by distance: a duplicate point stays); an entry
+ *   the scan cannot fill is (0, 0.0).  One difference of order: candidates are
+ *   ranked by the aggregate before the root, where the host scan ranks the
+ *   rooted value -- two aggregates one rounding apart that root to the same
+ *   double may come out in the other order.
+ * Errors (knn_graph.rs:475-539): ShapeMismatch "x" {n, d, len} (or a
+ *   dimension above u32::MAX), "k" {1, k, max_k} with max_k = n - 1 (n with
+ *   include_self), "p" {1, 0, 1} (Minkowski p < 1), "out"; Unsupported
+ *   "metric", or k (+1) above mlrs_knn_max_k().
+ */
+int32_t mlrs_knn_graph_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features, int64_t k, int32_t metric,
+                           double p, int32_t include_self, uint32_t *out_idx, double *out_dist, int64_t out_len,
+                           void *stream);
+int32_t mlrs_knn_graph_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features, int64_t k,
+                           int32_t metric, double p, int32_t include_self, uint32_t *out_idx, double *out_dist,
+                           int64_t out_len, void *stream);
+
+/*
+ * HDBSCAN core distances: out[i] (n, device, f64) = the (k-1)-th smallest
+ *   distance from row i to every row, itself included, k = clamp(min_samples,
+ *   1, n); +inf when fewer than k distances are finite.
+ * Replaces: the core-distance step of feature_metric_single_linkage
+ *   (crates/mlrs-algos/src/cluster/hdbscan.rs:1495-1566), served on the cpu
+ *   backend by core_distances_host (cluster/hdbscan/host_core.rs:253-540); same
+ *   f64 arithmetic as mlrs_knn_graph_*.  Cosine is not served (the reference
+ *   takes cosine core distances from a dense matrix): Unsupported "metric".
+ */
+int32_t mlrs_hdbscan_core_distances_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features,
+                                        int32_t metric, double p, int64_t min_samples, double *out, int64_t out_len,
+                                        void *stream);
+int32_t mlrs_hdbscan_core_distances_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features,
+                                        int32_t metric, double p, int64_t min_samples, double *out, int64_t out_len,
+                                        void *stream);
+
 /* Release the cached device workspace of the current device. */
 int32_t mlrs_release_workspace(void);
 

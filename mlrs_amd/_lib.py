@@ -97,6 +97,10 @@ SIGNATURES = {
                                          _vp, _vp, _i64, ctypes.POINTER(_i64), _vp]),
     "mlrs_radius_neighbors_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _f64, _f64, _vp, _i64,
                                          _vp, _vp, _i64, ctypes.POINTER(_i64), _vp]),
+    "mlrs_knn_graph_f32": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _f64, _i32, _vp, _vp, _i64, _vp]),
+    "mlrs_knn_graph_f64": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _f64, _i32, _vp, _vp, _i64, _vp]),
+    "mlrs_hdbscan_core_distances_f32": (_i32, [_vp, _i64, _i64, _i64, _i32, _f64, _i64, _vp, _i64, _vp]),
+    "mlrs_hdbscan_core_distances_f64": (_i32, [_vp, _i64, _i64, _i64, _i32, _f64, _i64, _vp, _i64, _vp]),
     "mlrs_release_workspace": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
     "mlrs_force_path": (_i32, [_i32]),

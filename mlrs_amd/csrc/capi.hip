@@ -1196,6 +1196,193 @@ int32_t mlrs_radius_neighbors_f64(const double* xq, int64_t xq_len, int64_t n_qu
                                metric, p, radius, counts, counts_len, out_dist, out_idx, capacity, total, stream);
 }
 
+// ---------------------------------------------------------------------------
+// X-vs-X graphs: the UMAP kNN graph and the HDBSCAN core distances
+// ---------------------------------------------------------------------------
+extern "C++" {
+// A second cached device buffer for operands and lists that must survive the
+// search, whose own workspace() calls may move the main arena.
+Arena g_aux[kMaxDevices];
+
+static int32_t aux_workspace(size_t bytes, char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_err(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_err(MLRS_ERR_UNSUPPORTED, "device", dev, 0, 0, 0, "device ordinal %d out of range", dev);
+    Arena& A = g_aux[dev];
+    if (A.cap < bytes) {
+        if (A.base) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
+            (void)hipFree(A.base);
+            A.base = nullptr;
+            A.cap = 0;
+        }
+        size_t want = std::max(bytes + bytes / 4, (size_t)16 << 20);
+        e = hipMalloc((void**)&A.base, want);
+        if (e != hipSuccess) {
+            A.base = nullptr;
+            return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)want, 0, 0, (int)e,
+                           "device allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+        }
+        A.cap = want;
+    }
+    *out = A.base;
+    return MLRS_OK;
+}
+
+// The f64 search under an explicit arm: the Gram-MFMA kernel where it serves
+// the arm and shape, else exact tiles + selection.
+static int32_t search_f64(const double* xq, int64_t nq, const double* xt, int64_t nt, int64_t d, int k, int arm,
+                          int mode, double p, double* ov, uint32_t* oi, hipStream_t s) {
+    const bool gram_ok = arm <= ARM_COS_HOST && d <= gram_f64_max_d() && k <= gram_f64_max_k();
+    int path = pick_path(false, gram_ok);
+    if (path == MLRS_PATH_AUTO) path = (gram_ok && !small_search(nq, nt, d)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+    if (path == MLRS_PATH_FUSED) return knn_gram64(xq, nq, xt, nt, d, k, arm, mode, ov, oi, s);
+    return knn_generic<double>(xq, nq, xt, nt, d, k, arm, mode, ov, oi, s, p);
+}
+
+// knn_graph's validate_geometry (crates/mlrs-backend/src/prims/knn_graph.rs:475-539).
+static int32_t validate_graph(const void* x, int64_t x_len, int64_t n, int64_t d, int64_t k, int32_t metric,
+                              double p, bool include_self) {
+    if (!geom_ok(n, d, x_len) || d < 1) return shape_err("x", n, d, x_len);
+    const int64_t max_k = include_self ? n : std::max<int64_t>(0, n - 1);
+    if (k < 1 || k > max_k) return shape_err("k", 1, k, max_k);
+    if (metric < MLRS_METRIC_EUCLIDEAN || metric > MLRS_METRIC_MINKOWSKI)
+        return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0, "metric %d is not served", metric);
+    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0)) return shape_err("p", 1, 0, 1);
+    if (n > kU32Max) return shape_err("x", n, 0, kU32Max);
+    if (d > kU32Max) return shape_err("x", d, 0, kU32Max);
+    if (k + 1 > kU32Max) return shape_err("k", k + 1, 0, kU32Max);
+    if (!x) return set_err(MLRS_ERR_NULL_POINTER, "x", 0, 0, 0, 0, "null pointer");
+    return MLRS_OK;
+}
+
+// The host scans' per-metric arithmetic as engine arms (umap_host_knn.rs:318-411):
+// Euclidean and cosine accumulate diff*diff with separate rounding (cosine over
+// normalised rows), Minkowski always through pow.
+static void graph_arm(int32_t metric, int* arm, int* mode) {
+    switch (metric) {
+    case MLRS_METRIC_EUCLIDEAN: *arm = ARM_EUCLID_MULADD; *mode = EMIT_SQRT; break;
+    case MLRS_METRIC_COSINE: *arm = ARM_EUCLID_MULADD; *mode = EMIT_IDENTITY; break;
+    case MLRS_METRIC_MANHATTAN: *arm = ARM_MANHATTAN; *mode = EMIT_IDENTITY; break;
+    case MLRS_METRIC_CHEBYSHEV: *arm = ARM_CHEBYSHEV; *mode = EMIT_IDENTITY; break;
+    default: *arm = ARM_MINKOWSKI_POW; *mode = EMIT_IDENTITY; break;
+    }
+}
+
+// Operand in f64 (widened / normalised as the host scan sees it) plus the
+// (n x kk) lists, carved from the auxiliary buffer.
+template <typename TIn>
+static int32_t graph_search(const TIn* x, int64_t n, int64_t d, int kk, int32_t metric, double p, hipStream_t s,
+                            double** val, uint32_t** idx) {
+    const bool widen = sizeof(TIn) == 4;
+    const bool cos = metric == MLRS_METRIC_COSINE;
+    size_t bytes = aligned_bytes(sizeof(double) * (size_t)n * kk) + aligned_bytes(sizeof(uint32_t) * (size_t)n * kk) +
+                   2 * aligned_bytes(sizeof(double) * (size_t)n * d) + 2 * aligned_bytes(sizeof(double) * (size_t)n) +
+                   1024;
+    char* aux;
+    int32_t rc = aux_workspace(bytes, &aux);
+    if (rc) return rc;
+    Carver cv(aux);
+    *val = cv.take<double>((size_t)n * kk);
+    *idx = cv.take<uint32_t>((size_t)n * kk);
+    const double* xd = reinterpret_cast<const double*>(x);
+    hipError_t e = hipSuccess;
+    if (widen) {
+        double* w = cv.take<double>((size_t)n * d);
+        e = launch_widen(reinterpret_cast<const float*>(x), n * d, w, s);
+        xd = w;
+    }
+    if (e == hipSuccess && cos) {
+        double* sq = cv.take<double>((size_t)n);
+        double* inv = cv.take<double>((size_t)n);
+        double* xn = cv.take<double>((size_t)n * d);
+        e = launch_row_norms<double>(xd, n, d, sq, inv, nullptr, nullptr, s);
+        if (e == hipSuccess) e = launch_normalize_rows(xd, n, d, inv, xn, s);
+        xd = xn;
+    }
+    if (e != hipSuccess) return hip_err(e, "graph operand");
+    int arm, mode;
+    graph_arm(metric, &arm, &mode);
+    return search_f64(xd, n, xd, n, d, kk, arm, mode, p, *val, *idx, s);
+}
+
+template <typename TIn>
+static int32_t knn_graph_impl(const TIn* x, int64_t x_len, int64_t n, int64_t d, int64_t k, int32_t metric,
+                              double p, int32_t include_self, uint32_t* out_idx, double* out_dist, int64_t out_len,
+                              void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int32_t rc = validate_graph(x, x_len, n, d, k, metric, p, include_self != 0);
+    if (rc) return rc;
+    if (!geom_ok(n, k, out_len)) return shape_err("out", n, k, out_len);
+    if (!out_idx || !out_dist) return set_err(MLRS_ERR_NULL_POINTER, "out", 0, 0, 0, 0, "null pointer");
+    const int kk = (int)(include_self ? k : k + 1);
+    if (kk > select_rows_max_k())
+        return set_err(MLRS_ERR_UNSUPPORTED, "k", 1, k, n, 0, "k=%lld above the largest k served (%d)",
+                       (long long)k, select_rows_max_k() - (include_self ? 0 : 1));
+    hipStream_t s = (hipStream_t)stream;
+    double* val;
+    uint32_t* idx;
+    rc = graph_search<TIn>(x, n, d, kk, metric, p, s, &val, &idx);
+    if (rc) return rc;
+    hipError_t e = launch_graph_finish(val, idx, n, kk, (int)k, include_self ? 0 : 1,
+                                       metric == MLRS_METRIC_COSINE ? 1 : 0, out_dist, out_idx, s);
+    if (e != hipSuccess) return hip_err(e, "graph finish");
+    return ok();
+}
+
+template <typename TIn>
+static int32_t core_impl(const TIn* x, int64_t x_len, int64_t n, int64_t d, int32_t metric, double p,
+                         int64_t min_samples, double* out, int64_t out_len, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    // k = min_samples clamped to [1, n] (hdbscan.rs:1508-1510)
+    const int64_t k = std::max<int64_t>(1, std::min<int64_t>(min_samples, n));
+    int32_t rc = validate_graph(x, x_len, n, d, n >= 1 ? k : 1, metric, p, true);
+    if (rc) return rc;
+    if (metric == MLRS_METRIC_COSINE)
+        return set_err(MLRS_ERR_UNSUPPORTED, "metric", metric, 0, 0, 0,
+                       "cosine core distances come from the dense cosine matrix, not a kNN scan");
+    if (out_len != n) return shape_err("out", n, 1, out_len);
+    if (!out) return set_err(MLRS_ERR_NULL_POINTER, "out", 0, 0, 0, 0, "null pointer");
+    if (k > select_rows_max_k())
+        return set_err(MLRS_ERR_UNSUPPORTED, "min_samples", 1, k, n, 0, "min_samples=%lld above the largest served (%d)",
+                       (long long)k, select_rows_max_k());
+    hipStream_t s = (hipStream_t)stream;
+    double* val;
+    uint32_t* idx;
+    rc = graph_search<TIn>(x, n, d, (int)k, metric, p, s, &val, &idx);
+    if (rc) return rc;
+    hipError_t e = launch_core_column(val, n, (int)k, out, s);
+    if (e != hipSuccess) return hip_err(e, "core column");
+    return ok();
+}
+}  // extern "C++"
+
+int32_t mlrs_knn_graph_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features, int64_t k, int32_t metric,
+                           double p, int32_t include_self, uint32_t* out_idx, double* out_dist, int64_t out_len,
+                           void* stream) {
+    return knn_graph_impl<float>(x, x_len, n, n_features, k, metric, p, include_self, out_idx, out_dist, out_len,
+                                 stream);
+}
+int32_t mlrs_knn_graph_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features, int64_t k,
+                           int32_t metric, double p, int32_t include_self, uint32_t* out_idx, double* out_dist,
+                           int64_t out_len, void* stream) {
+    return knn_graph_impl<double>(x, x_len, n, n_features, k, metric, p, include_self, out_idx, out_dist, out_len,
+                                  stream);
+}
+int32_t mlrs_hdbscan_core_distances_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features,
+                                        int32_t metric, double p, int64_t min_samples, double* out, int64_t out_len,
+                                        void* stream) {
+    return core_impl<float>(x, x_len, n, n_features, metric, p, min_samples, out, out_len, stream);
+}
+int32_t mlrs_hdbscan_core_distances_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features,
+                                        int32_t metric, double p, int64_t min_samples, double* out, int64_t out_len,
+                                        void* stream) {
+    return core_impl<double>(x, x_len, n, n_features, metric, p, min_samples, out, out_len, stream);
+}
+
 int32_t mlrs_force_path(int32_t path) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (path < MLRS_PATH_AUTO || path > MLRS_PATH_GENERIC)
@@ -1234,8 +1421,9 @@ int32_t mlrs_release_workspace(void) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MLRS_OK;
     Arena& A = g_arena[dev];
+    Arena& X = g_aux[dev];
     RadiusPlan& P = g_rplan[dev];
-    if (A.base || P.base) {
+    if (A.base || P.base || X.base) {
         hipError_t e = hipDeviceSynchronize();
         if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
     }
@@ -1243,6 +1431,11 @@ int32_t mlrs_release_workspace(void) {
         (void)hipFree(A.base);
         A.base = nullptr;
         A.cap = 0;
+    }
+    if (X.base) {
+        (void)hipFree(X.base);
+        X.base = nullptr;
+        X.cap = 0;
     }
     if (P.base) {
         (void)hipFree(P.base);

@@ -260,4 +260,13 @@ template <typename T>
 hipError_t launch_radius_transform(T* v, int64_t n, int mode, T e, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 
+// X-vs-X graphs (knn_graph.hip): operand preparation and list finishing
+// around the f64 kNN search.
+hipError_t launch_widen(const float* x, int64_t n, double* y, hipStream_t s);
+hipError_t launch_normalize_rows(const double* x, int64_t n, int64_t d, const double* inv, double* y,
+                                 hipStream_t s);
+hipError_t launch_graph_finish(const double* val, const uint32_t* idx, int64_t n, int kk, int k, int drop_self,
+                               int halve, double* out_dist, uint32_t* out_idx, hipStream_t s);
+hipError_t launch_core_column(const double* val, int64_t n, int k, double* out, hipStream_t s);
+
 }  // namespace mlrs

@@ -538,6 +538,22 @@ class KNeighborsClassifier(_NeighborsBase):
         return _out(proba, was_numpy)
 
 
+def knn_graph(X, k, metric="euclidean", p=2.0, include_self=False):
+    """Directed k-nearest graph of the rows of ``X`` against themselves, as the
+    reference builds it for UMAP (include_self=False) and HDBSCAN
+    (include_self=True): ``(indices int64 (n, k), distances float64 (n, k))``
+    as device tensors, in the reference host scan's f64 arithmetic."""
+    t, _ = _as_device_matrix(X)
+    return prims.knn_graph(t, k, metric, p=p, include_self=include_self)
+
+
+def hdbscan_core_distances(X, min_samples, metric="euclidean", p=2.0):
+    """HDBSCAN core distances (float64 device tensor of n): the distance from
+    each row to its ``min_samples``-th nearest row, itself included."""
+    t, _ = _as_device_matrix(X)
+    return prims.core_distances(t, min_samples, metric, p=p)
+
+
 def kneighbors(X_train, X_query, k, metric="euclidean"):
     """Functional form: ``(distances, int64 indices)`` as device tensors."""
     t, _ = _as_device_matrix(X_train)

@@ -14,6 +14,8 @@ Geometry is validated by the C ABI before any launch; a violation raises
 | ``pairwise_distance`` | distance_direct / metric_distance, prims/distance.rs:428-727 |
 | ``row_sqnorms``     | row_sqnorms, crates/mlrs-backend/src/prims/kmeans.rs:805-832     |
 | ``radius_neighbors`` | radius_neighbor_indices_metric, crates/mlrs-algos/src/neighbors/nearest.rs:609-749 |
+| ``knn_graph``       | knn_graph via host_knn, crates/mlrs-algos/src/manifold/umap_host_knn.rs:212-515 |
+| ``core_distances``  | HDBSCAN core distances, crates/mlrs-algos/src/cluster/hdbscan/host_core.rs:253-540 |
 | ``knn_regress``     | knn_regress_mean / knn_regress_gather, crates/mlrs-kernels/src/knn.rs:95-316 |
 | ``knn_classify``    | KNeighborsClassifier's host vote, crates/mlrs-algos/src/neighbors/classifier.rs:782-930 |
 """
@@ -181,6 +183,38 @@ def radius_neighbors(xq, x_train, radius, metric="euclidean", p=2.0):
     if n:
         _lib.check(f(*args, _ptr(dist), _ptr(idx), n, ctypes.byref(total), stream))
     return dist, idx, counts.to(torch.int64)
+
+
+def knn_graph(x, k, metric="euclidean", p=2.0, include_self=False):
+    """Directed k-nearest graph of the rows of ``x`` against themselves in the
+    reference host scan's f64 arithmetic (mlrs_knn_graph_*): ``(indices int64
+    (n, k), distances float64 (n, k))``; ``include_self=False`` leaves out each
+    row's own index by identity."""
+    _dev_check(x)
+    s = _suffix(x)
+    n, d = x.shape
+    idx = torch.empty((n, int(k)), dtype=torch.int32, device=x.device)
+    dist = torch.empty((n, int(k)), dtype=torch.float64, device=x.device)
+    rc = getattr(_lib.load(), "mlrs_knn_graph_" + s)(
+        _ptr(x), x.numel(), n, d, int(k), _metric_id(metric), float(p), int(bool(include_self)), _ptr(idx),
+        _ptr(dist), dist.numel(), _stream(x.device))
+    _lib.check(rc)
+    return idx.to(torch.int64) & 0xFFFFFFFF, dist
+
+
+def core_distances(x, min_samples, metric="euclidean", p=2.0):
+    """HDBSCAN core distances (mlrs_hdbscan_core_distances_*): float64 (n,),
+    the (k-1)-th smallest distance of each row to the set, itself included,
+    k = clamp(min_samples, 1, n)."""
+    _dev_check(x)
+    s = _suffix(x)
+    n, d = x.shape
+    out = torch.empty(n, dtype=torch.float64, device=x.device)
+    rc = getattr(_lib.load(), "mlrs_hdbscan_core_distances_" + s)(
+        _ptr(x), x.numel(), n, d, _metric_id(metric), float(p), int(min_samples), _ptr(out), out.numel(),
+        _stream(x.device))
+    _lib.check(rc)
+    return out
 
 
 def _as_u32_idx(idx):

@@ -47,6 +47,10 @@ def _load():
     lib.orc_knn_arm.restype = i32
     lib.orc_max_threads.argtypes = []
     lib.orc_max_threads.restype = i32
+    lib.orc_knn_graph_f64.argtypes = [vp, i64, i64, i64, i32, ctypes.c_double, i32, vp, vp]
+    lib.orc_knn_graph_f64.restype = i32
+    lib.orc_core_distances_f64.argtypes = [vp, i64, i64, i32, ctypes.c_double, i64, vp]
+    lib.orc_core_distances_f64.restype = i32
     for s in ("f32", "f64"):
         f = getattr(lib, "orc_knn_topk_" + s)
         f.argtypes = [vp, i64, vp, i64, i64, i64, i32, ctypes.c_double, vp, vp, i32]
@@ -177,6 +181,36 @@ def radius_neighbors(xq, xt, radius, metric="euclidean", nthreads=0, p=2.0):
     f(xq.ctypes.data, nq, xt.ctypes.data, nt, d, _metric_id(metric), float(p), float(radius),
       counts.ctypes.data, offsets.ctypes.data, dist.ctypes.data, idx.ctypes.data, int(nthreads))
     return dist, idx, counts
+
+
+def knn_graph(x, k, metric="euclidean", p=2.0, include_self=False):
+    """(uint32 indices, f64 distances), each (n, k): the directed k-nearest
+    graph of the rows of ``x`` against themselves in the reference's host f64
+    arithmetic (``x`` is widened to f64 first, as the reference does)."""
+    lib = _load()
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    n, d = x.shape
+    idx = np.empty((n, k), dtype=np.uint32)
+    dist = np.empty((n, k), dtype=np.float64)
+    rc = lib.orc_knn_graph_f64(x.ctypes.data, n, d, int(k), _metric_id(metric), float(p), int(bool(include_self)),
+                               idx.ctypes.data, dist.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle knn_graph rejected k=%d for n=%d" % (k, n))
+    return idx, dist
+
+
+def core_distances(x, min_samples, metric="euclidean", p=2.0):
+    """HDBSCAN core distances (f64): the (k-1)-th smallest distance of each row
+    to the whole set, self included, k = clamp(min_samples, 1, n)."""
+    lib = _load()
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    n, d = x.shape
+    out = np.empty(n, dtype=np.float64)
+    rc = lib.orc_core_distances_f64(x.ctypes.data, n, d, _metric_id(metric), float(p), int(min_samples),
+                                    out.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle core_distances rejected the input")
+    return out
 
 
 def row_sqnorms(x):

@@ -197,3 +197,24 @@ def test_radius_error_text_and_python_mapping():
     with pytest.raises(_lib.InvalidParam) as ei:
         _lib.check(_radius32(radius=-0.5))
     assert ei.value.operand == "radius"
+
+
+def test_graph_validation():
+    """knn_graph's validate_geometry order (knn_graph.rs:475-539) before any launch."""
+    lib = _lib.load()
+    f = lib.mlrs_knn_graph_f32
+    assert f(P, 29, 10, 3, 3, 0, 2.0, 0, P, P, 30, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"x"
+    assert f(P, 30, 10, 3, 10, 0, 2.0, 0, P, P, 100, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    e = _info()
+    assert (e.operand, e.rows, e.cols, e.len) == (b"k", 1, 10, 9)
+    assert f(P, 30, 10, 3, 0, 0, 2.0, 1, P, P, 0, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert f(P, 30, 10, 3, 3, 4, 0.5, 0, P, P, 30, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert (_info().operand, _info().len) == (b"p", 1)
+    assert f(P, 30, 10, 3, 3, 6, 2.0, 0, P, P, 30, None) == _lib.MLRS_ERR_UNSUPPORTED
+    assert f(P, 30, 10, 3, 3, 0, 2.0, 0, P, P, 29, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"out"
+    g = lib.mlrs_hdbscan_core_distances_f64
+    assert g(P, 30, 10, 3, 1, 2.0, 5, P, 10, None) == _lib.MLRS_ERR_UNSUPPORTED
+    assert g(P, 30, 10, 3, 0, 2.0, 5, P, 9, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+    assert _info().operand == b"out"
