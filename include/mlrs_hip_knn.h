@@ -315,6 +315,41 @@ int32_t mlrs_hdbscan_core_distances_f64(const double *x, int64_t x_len, int64_t 
                                         int32_t metric, double p, int64_t min_samples, double *out, int64_t out_len,
                                         void *stream);
 
+/*
+ * k-means fit: restarts, initialisation and the Lloyd loop around the fused
+ * nearest-centre assignment.
+ *
+ * Replaces: KMeans::fit (crates/mlrs-algos/src/cluster/kmeans.rs:1353-1580)
+ *   with single_run (:929-1155) and the prims it drives (crates/mlrs-backend/
+ *   src/prims/kmeans.rs): feature_mean_var (tol scaled by the mean feature
+ *   variance), kmeanspp_sample / random_sample on SplitMix64 seeded
+ *   seed + restart, assign_min, centroid_sums_dev (F sums over the reference's
+ *   row blocks, block partials summed in order, widened to f64),
+ *   relocate_empty_clusters, the f64 mean update, the strict label-equality
+ *   break then the tol break, inertia_rows + sum_device, and the restart rule
+ *   (strictly lower inertia on a partition that is not a relabelling).
+ *   algorithm = 'elkan' returns the same fit in the reference, so this loop
+ *   serves both.
+ * init_kind: 0 explicit centres (init, device, k x n_features; one run), 1
+ *   k-means++, 2 random.  out_centers (k x n_features, device, F),
+ *   out_labels (n, device), *out_inertia and *out_n_iter (host) of the
+ *   winning restart.  Synchronous.
+ * Errors: InvalidParam "k" (AlgoError::InvalidK text), "n_init", "max_iter",
+ *   "tol"; ShapeMismatch "x", "init", "centers", "labels", and "labels"
+ *   {n, k, empty clusters} when an empty cluster finds no donor row;
+ *   Unsupported "init".
+ */
+int32_t mlrs_kmeans_fit_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
+                            int32_t init_kind, const float *init, int64_t init_len, uint64_t seed, int64_t n_init,
+                            int64_t max_iter, double tol, float *out_centers, int64_t centers_len,
+                            uint32_t *out_labels, int64_t labels_len, double *out_inertia, int64_t *out_n_iter,
+                            void *stream);
+int32_t mlrs_kmeans_fit_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
+                            int32_t init_kind, const double *init, int64_t init_len, uint64_t seed, int64_t n_init,
+                            int64_t max_iter, double tol, double *out_centers, int64_t centers_len,
+                            uint32_t *out_labels, int64_t labels_len, double *out_inertia, int64_t *out_n_iter,
+                            void *stream);
+
 /* Release the cached device workspace of the current device. */
 int32_t mlrs_release_workspace(void);
 

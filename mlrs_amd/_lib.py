@@ -101,6 +101,10 @@ SIGNATURES = {
     "mlrs_knn_graph_f64": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _f64, _i32, _vp, _vp, _i64, _vp]),
     "mlrs_hdbscan_core_distances_f32": (_i32, [_vp, _i64, _i64, _i64, _i32, _f64, _i64, _vp, _i64, _vp]),
     "mlrs_hdbscan_core_distances_f64": (_i32, [_vp, _i64, _i64, _i64, _i32, _f64, _i64, _vp, _i64, _vp]),
+    "mlrs_kmeans_fit_f32": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, ctypes.c_uint64, _i64, _i64, _f64,
+                                   _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
+    "mlrs_kmeans_fit_f64": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, ctypes.c_uint64, _i64, _i64, _f64,
+                                   _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
     "mlrs_release_workspace": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
     "mlrs_force_path": (_i32, [_i32]),

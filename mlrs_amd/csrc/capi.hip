@@ -1383,6 +1383,396 @@ int32_t mlrs_hdbscan_core_distances_f64(const double* x, int64_t x_len, int64_t 
     return core_impl<double>(x, x_len, n, n_features, metric, p, min_samples, out, out_len, stream);
 }
 
+// ---------------------------------------------------------------------------
+// k-means fit: restarts, initialisation and the Lloyd loop around the fused
+// assignment (KMeans::fit, crates/mlrs-algos/src/cluster/kmeans.rs:1353-1580;
+// single_run :929-1155)
+// ---------------------------------------------------------------------------
+extern "C++" {
+static int32_t km_assign(const float* x, int64_t n, const float* c, int64_t k, int64_t d, uint32_t* labels,
+                         float* dist, hipStream_t s) {
+    if (d <= gram_f32_max_d() && pick_path(false, true) != MLRS_PATH_GENERIC)
+        return knn_gram32(x, n, c, k, d, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, dist, labels, s);
+    return kmeans_generic<float>(x, n, c, k, d, labels, dist, s);
+}
+static int32_t km_assign(const double* x, int64_t n, const double* c, int64_t k, int64_t d, uint32_t* labels,
+                         double* dist, hipStream_t s) {
+    if (d <= gram_f64_max_d() && pick_path(false, true) != MLRS_PATH_GENERIC)
+        return knn_gram64(x, n, c, k, d, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, dist, labels, s);
+    return kmeans_generic<double>(x, n, c, k, d, labels, dist, s);
+}
+
+// The reference's row-block layout: nb = clamp(ceil(n/256), 1, cap), rpb =
+// ceil(n/nb), nb = ceil(n/rpb).
+static void km_layout(int64_t n, int64_t cap, int64_t* nb, int64_t* rpb) {
+    int64_t b = std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, cap));
+    *rpb = (n + b - 1) / b;
+    *nb = (n + *rpb - 1) / *rpb;
+}
+
+// SplitMix64 (crates/mlrs-backend/src/prims/rng.rs:58-110).
+struct KmRng {
+    uint64_t state;
+    uint64_t next_u64() {
+        state += 0x9E3779B97F4A7C15ull;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double next_f64() { return (double)(next_u64() >> 11) / 9007199254740992.0; }
+    uint64_t next_below(uint64_t bound) {
+        if (bound <= 1) return 0;
+        const uint64_t zone = UINT64_MAX - (UINT64_MAX % bound);
+        for (;;) {
+            const uint64_t v = next_u64();
+            if (v < zone) return v % bound;
+        }
+    }
+};
+
+template <typename T>
+static int32_t km_d2h(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? MLRS_OK : hip_err(e, "kmeans read-back");
+}
+
+template <typename T>
+static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, int64_t k, int32_t init_kind,
+                               const T* init, int64_t init_len, uint64_t seed, int64_t n_init, int64_t max_iter,
+                               double tol, T* out_centers, int64_t centers_len, uint32_t* out_labels,
+                               int64_t labels_len, double* out_inertia, int64_t* out_n_iter, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (k < 1 || k > n)
+        return set_err(MLRS_ERR_INVALID_PARAM, "k", 1, k, n, 0,
+                       "estimator 'kmeans': k = %lld is out of range (must be 1..=%lld = n_samples)", (long long)k,
+                       (long long)n);
+    if (!geom_ok(n, d, x_len) || d < 1) return shape_err("x", n, d, x_len);
+    if (n > kU32Max) return shape_err("n", n, 0, kU32Max);
+    if (d > kU32Max) return shape_err("d", d, 0, kU32Max);
+    if (init_kind < 0 || init_kind > 2)
+        return set_err(MLRS_ERR_UNSUPPORTED, "init", init_kind, 0, 0, 0, "init kind %d is not served", init_kind);
+    if (init_kind == 0 && init_len != k * d) return shape_err("init", k, d, init_len);
+    if (n_init < 1) return set_err(MLRS_ERR_INVALID_PARAM, "n_init", n_init, 0, 0, 0, "n_init must be >= 1");
+    if (max_iter < 0) return set_err(MLRS_ERR_INVALID_PARAM, "max_iter", max_iter, 0, 0, 0, "max_iter must be >= 0");
+    if (!(tol >= 0.0)) return set_err(MLRS_ERR_INVALID_PARAM, "tol", 0, 0, 0, 0, "tol must be >= 0");
+    if (centers_len != k * d) return shape_err("centers", k, d, centers_len);
+    if (labels_len != n) return shape_err("labels", n, 1, labels_len);
+    if (!x || !out_centers || !out_labels || !out_inertia || !out_n_iter || (init_kind == 0 && !init))
+        return set_err(MLRS_ERR_NULL_POINTER, "ptr", 0, 0, 0, 0, "a required pointer is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t kd = k * d;
+    const int64_t runs = init_kind == 0 ? 1 : n_init;  // NInit::resolve: an explicit init runs once
+
+    int64_t nb, rpb, nbv, rpbv, nbi, rpbi;
+    km_layout(n, std::max<int64_t>(((int64_t)8 << 20) / kd, 64), &nb, &rpb);   // centroid_sums_dev
+    km_layout(n, std::max<int64_t>(((int64_t)4 << 20) / d, 64), &nbv, &rpbv);  // feature_mean_var
+    km_layout(n, 256, &nbi, &rpbi);                                            // sum_device
+
+    size_t bytes = 4 * aligned_bytes(sizeof(uint32_t) * (size_t)n) + 2 * aligned_bytes(sizeof(T) * (size_t)n) +
+                   3 * aligned_bytes(sizeof(uint32_t) * (size_t)(nb * k)) + 2 * aligned_bytes(sizeof(uint32_t) * k) +
+                   aligned_bytes(sizeof(T) * (size_t)(nb * kd)) + 2 * aligned_bytes(sizeof(T) * (size_t)kd) +
+                   aligned_bytes(sizeof(T) * (size_t)std::max(nbi, nbv * d)) + aligned_bytes(sizeof(T) * d) +
+                   aligned_bytes(sizeof(int64_t) * k) + 1024;
+    char* aux;
+    int32_t rc = aux_workspace(bytes, &aux);
+    if (rc) return rc;
+    Carver cv(aux);
+    uint32_t* lab[2] = {cv.take<uint32_t>(n), cv.take<uint32_t>(n)};
+    uint32_t* perm = cv.take<uint32_t>(n);
+    uint32_t* best_lab = cv.take<uint32_t>(n);
+    T* dist = cv.take<T>(n);
+    T* mind2 = cv.take<T>(n);
+    KmScratch<T> w;
+    w.pcount = cv.take<uint32_t>(nb * k);
+    w.seg = cv.take<uint32_t>(nb * k);
+    w.cursor = cv.take<uint32_t>(nb * k);
+    w.counts = cv.take<uint32_t>(k);
+    w.starts = cv.take<uint32_t>(k);
+    w.perm = perm;
+    w.psum = cv.take<T>(nb * kd);
+    w.sums = cv.take<T>(kd);
+    T* cdev = cv.take<T>(kd);
+    T* parts = cv.take<T>(std::max(nbi, nbv * d));
+    T* means_dev = cv.take<T>(d);
+    int64_t* idx_dev = cv.take<int64_t>(k);
+    unsigned int* changed_dev = reinterpret_cast<unsigned int*>(cv.take<uint32_t>(1));
+
+    // ---- tol_scaled = tol * mean(var(X, axis=0)) (feature_mean_var) ----
+    std::vector<T> hp((size_t)std::max(nbi, nbv * d));
+    hipError_t e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, nullptr, parts, s);
+    if (e != hipSuccess) return hip_err(e, "kmeans col sums");
+    rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)(nbv * d), s);
+    if (rc) return rc;
+    const double inv_n = 1.0 / (double)n;
+    std::vector<double> means((size_t)d, 0.0);
+    for (int64_t b = 0; b < nbv; ++b)
+        for (int64_t j = 0; j < d; ++j) means[j] += (double)hp[b * d + j];
+    std::vector<T> means_t((size_t)d);
+    for (int64_t j = 0; j < d; ++j) {
+        means[j] *= inv_n;
+        means_t[j] = (T)means[j];
+    }
+    e = hipMemcpyAsync(means_dev, means_t.data(), sizeof(T) * (size_t)d, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, means_dev, parts, s);
+    if (e != hipSuccess) return hip_err(e, "kmeans col sqdiff");
+    rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)(nbv * d), s);
+    if (rc) return rc;
+    double var_sum = 0.0;
+    for (int64_t q = 0; q < nbv * d; ++q) var_sum += (double)hp[q];
+    const double tol_scaled = tol * ((var_sum * inv_n) / (double)d);
+
+    std::vector<double> cen((size_t)kd), best_cen((size_t)kd), nc((size_t)kd);
+    std::vector<T> ct((size_t)kd), sums_h((size_t)kd);
+    std::vector<uint32_t> counts_h((size_t)k), lab_h, best_lab_h, lab_rel;
+    std::vector<T> dist_h;
+    bool have = false;
+    double best_inertia = 0.0;
+    int64_t best_iter = 0;
+    std::vector<int64_t> chosen;  // outlives the asynchronous upload of the picks
+    for (int64_t restart = 0; restart < runs; ++restart) {
+        // ---- initial centres (init_centers, cluster/kmeans.rs:893-920) ----
+        if (init_kind == 0) {
+            e = hipMemcpyAsync(cdev, init, sizeof(T) * (size_t)kd, hipMemcpyDeviceToDevice, s);
+            if (e != hipSuccess) return hip_err(e, "kmeans init");
+        } else {
+            KmRng rng{seed + (uint64_t)restart};
+            chosen.clear();
+            chosen.reserve((size_t)k);
+            if (init_kind == 2) {  // random_sample (prims/kmeans.rs:1769-1786)
+                std::vector<int64_t> ids((size_t)n);
+                for (int64_t i = 0; i < n; ++i) ids[i] = i;
+                for (int64_t i = 0; i < k; ++i) {
+                    const int64_t j = i + (int64_t)rng.next_below((uint64_t)(n - i));
+                    std::swap(ids[i], ids[j]);
+                }
+                chosen.assign(ids.begin(), ids.begin() + k);
+            } else {  // kmeanspp_sample (prims/kmeans.rs:381-491)
+                std::vector<char> is_chosen((size_t)n, 0);
+                std::vector<T> m2((size_t)n);
+                std::vector<double> wgt((size_t)n);
+                int64_t cur = (int64_t)rng.next_below((uint64_t)n);
+                chosen.push_back(cur);
+                is_chosen[cur] = 1;
+                for (int64_t m = 0; m + 1 < k; ++m) {
+                    e = launch_km_mind2<T>(x, n, d, cur, m == 0 ? 1 : 0, mind2, s);
+                    if (e != hipSuccess) return hip_err(e, "kmeans++ distances");
+                    rc = km_d2h<T>(m2.data(), mind2, sizeof(T) * (size_t)n, s);
+                    if (rc) return rc;
+                    double total = 0.0;
+                    for (int64_t i = 0; i < n; ++i) {
+                        wgt[i] = (double)m2[i];
+                        total += wgt[i];
+                    }
+                    int64_t next = -1;
+                    if (total <= 0.0) {
+                        for (int64_t i = 0; i < n; ++i)
+                            if (!is_chosen[i]) {
+                                next = i;
+                                break;
+                            }
+                        if (next < 0) return shape_err("k", 1, k, n);
+                    } else {
+                        const double target = rng.next_f64() * total;
+                        double acc = 0.0;
+                        int64_t pick = n - 1;
+                        for (int64_t i = 0; i < n; ++i) {
+                            acc += wgt[i];
+                            if (acc >= target) {
+                                pick = i;
+                                break;
+                            }
+                        }
+                        if (wgt[pick] <= 0.0)
+                            for (int64_t i = n - 1; i >= 0; --i)
+                                if (wgt[i] > 0.0) {
+                                    pick = i;
+                                    break;
+                                }
+                        if (is_chosen[pick])
+                            for (int64_t i = 0; i < n; ++i)
+                                if (!is_chosen[i]) {
+                                    pick = i;
+                                    break;
+                                }
+                        next = pick;
+                    }
+                    chosen.push_back(next);
+                    is_chosen[next] = 1;
+                    cur = next;
+                }
+            }
+            e = hipMemcpyAsync(idx_dev, chosen.data(), sizeof(int64_t) * (size_t)k, hipMemcpyHostToDevice, s);
+            if (e == hipSuccess) e = launch_km_gather<T>(x, idx_dev, k, d, cdev, s);
+            if (e != hipSuccess) return hip_err(e, "kmeans init gather");
+        }
+        rc = km_d2h<T>(ct.data(), cdev, sizeof(T) * (size_t)kd, s);
+        if (rc) return rc;
+        for (int64_t q = 0; q < kd; ++q) cen[q] = (double)ct[q];
+
+        // ---- single_run ----
+        int cur = 0;
+        rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s);
+        if (rc) return rc;
+        int64_t iters = 0;
+        for (int64_t it = 0; it < max_iter; ++it) {
+            ++iters;
+            {
+                KernelTimer kt(s, "km_centroid_sums");
+                e = launch_km_centroid_sums<T>(x, lab[cur], n, d, k, nb, rpb, w, s);
+            }
+            if (e == hipSuccess) e = hipMemcpyAsync(sums_h.data(), w.sums, sizeof(T) * (size_t)kd,
+                                                    hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess) e = hipMemcpyAsync(counts_h.data(), w.counts, sizeof(uint32_t) * (size_t)k,
+                                                    hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) return hip_err(e, "kmeans centroid sums");
+            std::vector<int64_t> cnt((size_t)k);
+            for (int64_t c = 0; c < k; ++c) cnt[c] = counts_h[c];
+            for (int64_t q = 0; q < kd; ++q) nc[q] = (double)sums_h[q];
+            int64_t empties = 0;
+            for (int64_t c = 0; c < k; ++c) empties += cnt[c] == 0;
+            if (empties) {
+                // relocate_empty_clusters (prims/kmeans.rs:1323-1410): the
+                // farthest rows by (distance desc, index asc) into the empty
+                // clusters, never emptying their donor
+                lab_h.resize((size_t)n);
+                dist_h.resize((size_t)n);
+                rc = km_d2h<T>(lab_h.data(), lab[cur], sizeof(uint32_t) * (size_t)n, s);
+                if (!rc) rc = km_d2h<T>(dist_h.data(), dist, sizeof(T) * (size_t)n, s);
+                if (rc) return rc;
+                std::vector<int64_t> order((size_t)n);
+                for (int64_t i = 0; i < n; ++i) order[i] = i;
+                std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
+                    const double da = (double)dist_h[a], db = (double)dist_h[b];
+                    if (db < da) return true;
+                    if (da < db) return false;
+                    return a < b;
+                });
+                std::vector<char> moved((size_t)n, 0);
+                std::vector<T> row((size_t)d);
+                int64_t cursor = 0;
+                for (int64_t c = 0; c < k; ++c) {
+                    if (cnt[c] != 0) continue;
+                    bool ok_move = false;
+                    while (cursor < n) {
+                        const int64_t i = order[cursor++];
+                        if (moved[i]) continue;
+                        const int64_t donor = lab_h[i];
+                        if (cnt[donor] <= 1) continue;
+                        rc = km_d2h<T>(row.data(), x + i * d, sizeof(T) * (size_t)d, s);
+                        if (rc) return rc;
+                        for (int64_t j = 0; j < d; ++j) {
+                            const double xij = (double)row[j];
+                            nc[c * d + j] += xij;
+                            nc[donor * d + j] -= xij;
+                        }
+                        ++cnt[c];
+                        --cnt[donor];
+                        moved[i] = 1;
+                        ok_move = true;
+                        break;
+                    }
+                    if (!ok_move) return shape_err("labels", n, k, empties);
+                }
+            }
+            // mean divide in f64 and the centre shift (single_run :1010-1030)
+            for (int64_t c = 0; c < k; ++c) {
+                const double inv = 1.0 / (double)cnt[c];
+                for (int64_t j = 0; j < d; ++j) nc[c * d + j] = nc[c * d + j] * inv;
+            }
+            double shift = 0.0;
+            for (int64_t q = 0; q < kd; ++q) {
+                const double diff = nc[q] - cen[q];
+                shift += diff * diff;
+            }
+            cen.swap(nc);
+            for (int64_t q = 0; q < kd; ++q) ct[q] = (T)cen[q];
+            e = hipMemcpyAsync(cdev, ct.data(), sizeof(T) * (size_t)kd, hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return hip_err(e, "kmeans centres upload");
+            cur ^= 1;
+            rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s);
+            if (rc) return rc;
+            e = launch_km_changed(lab[cur], lab[cur ^ 1], n, changed_dev, s);
+            if (e != hipSuccess) return hip_err(e, "kmeans labels_changed");
+            unsigned int changed = 0;
+            rc = km_d2h<T>(&changed, changed_dev, sizeof(changed), s);
+            if (rc) return rc;
+            if (changed == 0) break;       // strict convergence first
+            if (shift <= tol_scaled) break;
+        }
+        // ---- inertia_ = sum of the per-row squared distances (inertia_rows +
+        //      sum_device) ----
+        e = launch_km_inertia<T>(x, cdev, lab[cur], n, d, dist, nbi, rpbi, parts, s);
+        if (e != hipSuccess) return hip_err(e, "kmeans inertia");
+        rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)nbi, s);
+        if (rc) return rc;
+        double inertia = 0.0;
+        for (int64_t b = 0; b < nbi; ++b) inertia += (double)hp[b];
+        // ---- keep the restart? strictly lower inertia on a different partition ----
+        bool keep = !have;
+        if (have && inertia < best_inertia) {
+            lab_h.resize((size_t)n);
+            rc = km_d2h<T>(lab_h.data(), lab[cur], sizeof(uint32_t) * (size_t)n, s);
+            if (rc) return rc;
+            std::vector<int64_t> map((size_t)k, -1);
+            bool same = true;
+            for (int64_t i = 0; i < n && same; ++i) {
+                const uint32_t a = lab_h[i], b = best_lab_h[i];
+                if (map[a] < 0)
+                    map[a] = b;
+                else if (map[a] != (int64_t)b)
+                    same = false;
+            }
+            keep = !same;
+        }
+        if (keep) {
+            have = true;
+            best_inertia = inertia;
+            best_iter = iters;
+            best_cen = cen;
+            e = hipMemcpyAsync(best_lab, lab[cur], sizeof(uint32_t) * (size_t)n, hipMemcpyDeviceToDevice, s);
+            if (e != hipSuccess) return hip_err(e, "kmeans keep");
+            if (runs > 1) {
+                best_lab_h.resize((size_t)n);
+                rc = km_d2h<T>(best_lab_h.data(), lab[cur], sizeof(uint32_t) * (size_t)n, s);
+                if (rc) return rc;
+            }
+        }
+    }
+    for (int64_t q = 0; q < kd; ++q) ct[q] = (T)best_cen[q];
+    e = hipMemcpyAsync(out_centers, ct.data(), sizeof(T) * (size_t)kd, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(out_labels, best_lab, sizeof(uint32_t) * (size_t)n, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_err(e, "kmeans results");
+    *out_inertia = best_inertia;
+    *out_n_iter = best_iter;
+    (void)perm;
+    return ok();
+}
+}  // extern "C++"
+
+int32_t mlrs_kmeans_fit_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
+                            int32_t init_kind, const float* init, int64_t init_len, uint64_t seed, int64_t n_init,
+                            int64_t max_iter, double tol, float* out_centers, int64_t centers_len,
+                            uint32_t* out_labels, int64_t labels_len, double* out_inertia, int64_t* out_n_iter,
+                            void* stream) {
+    return kmeans_fit_impl<float>(x, x_len, n, n_features, n_clusters, init_kind, init, init_len, seed, n_init,
+                                  max_iter, tol, out_centers, centers_len, out_labels, labels_len, out_inertia,
+                                  out_n_iter, stream);
+}
+int32_t mlrs_kmeans_fit_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
+                            int32_t init_kind, const double* init, int64_t init_len, uint64_t seed, int64_t n_init,
+                            int64_t max_iter, double tol, double* out_centers, int64_t centers_len,
+                            uint32_t* out_labels, int64_t labels_len, double* out_inertia, int64_t* out_n_iter,
+                            void* stream) {
+    return kmeans_fit_impl<double>(x, x_len, n, n_features, n_clusters, init_kind, init, init_len, seed, n_init,
+                                   max_iter, tol, out_centers, centers_len, out_labels, labels_len, out_inertia,
+                                   out_n_iter, stream);
+}
+
 int32_t mlrs_force_path(int32_t path) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (path < MLRS_PATH_AUTO || path > MLRS_PATH_GENERIC)

@@ -1,0 +1,337 @@
+// Device pieces of the k-means fit loop around the fused assignment
+// (crates/mlrs-algos/src/cluster/kmeans.rs:929-1155, prims/kmeans.rs).
+//
+// Centroid sums.  The reference forms, for every row block b of its layout
+// (nb = clamp(ceil(n/256), 1, max(8M/(k*d), 64)), rpb = ceil(n/nb)), the F sum
+// of x[i][j] over the block's rows i with label c in ascending i, then the F
+// sum of the nb partials in block order (centroid_sumcount_blocked +
+// centroid_reduce_partials, crates/mlrs-kernels/src/kmeans.rs:329-479).  It
+// evaluates that with one thread per (b, c, j) scanning the whole block, n*k*d
+// label tests.  Here the rows are first bucketed by (block, label) -- a
+// per-block label histogram, offsets, and a stable scatter of the row
+// numbers -- so the thread of (b, c, j) walks exactly the rows of its bucket,
+// in ascending order: the same sums in the same order for O(n*d) work.
+//
+//   km_hist_kernel      pcount[b][c]: one workgroup per block (LDS histogram)
+//   km_offsets_kernel   per label: its total and the start of each (b, c)
+//                       bucket in the label-major permutation
+//   km_scatter_kernel   stable scatter of the block's rows into their buckets
+//   km_psum_kernel      psum[b][c][j] over the bucket, ascending rows
+//   km_reduce_kernel    sums[c][j] = sum over b in order
+//
+// Also: km_changed_kernel (labels that differ), km_inertia_rows_kernel and
+// km_block_sum_kernel (inertia_rows + block_sum_f, kernels/kmeans.rs:123-145,
+// 523-545), km_col_sum_kernel / km_col_sqdiff_kernel (col_sum_blocked /
+// col_sqdiff_blocked, :704-762), km_mind2_kernel (kmeanspp_mind2, :576-603) and
+// km_gather_kernel (gather_rows_idx, :552-570).  Every sum is the reference's
+// element type and order.
+#include "knn_common.hpp"
+#include "knn_kernels.hpp"
+
+namespace mlrs {
+
+namespace {
+
+constexpr int kLdsLabels = 8192;  // labels an LDS histogram / cursor array holds
+
+__global__ __launch_bounds__(256) void km_hist_kernel(const uint32_t* __restrict__ labels, int64_t n, int64_t rpb,
+                                                      int64_t k, uint32_t* __restrict__ pcount) {
+    __shared__ uint32_t h[kLdsLabels];
+    const int64_t b = blockIdx.x;
+    const int64_t start = b * rpb;
+    const int64_t end = (start + rpb) < n ? start + rpb : n;
+    uint32_t* out = pcount + b * k;
+    if (k <= kLdsLabels) {
+        for (int64_t c = threadIdx.x; c < k; c += 256) h[c] = 0u;
+        __syncthreads();
+        for (int64_t i = start + threadIdx.x; i < end; i += 256) atomicAdd(&h[labels[i]], 1u);
+        __syncthreads();
+        for (int64_t c = threadIdx.x; c < k; c += 256) out[c] = h[c];
+    } else {
+        // out[] was zeroed by the caller
+        for (int64_t i = start + threadIdx.x; i < end; i += 256) atomicAdd(&out[labels[i]], 1u);
+    }
+}
+
+// One thread per label: counts[c], and seg[b][c] = the bucket's first slot
+// relative to the label's own start (the label offsets come next).
+__global__ __launch_bounds__(256) void km_label_totals_kernel(const uint32_t* __restrict__ pcount, int64_t nb,
+                                                              int64_t k, uint32_t* __restrict__ seg,
+                                                              uint32_t* __restrict__ counts) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= k) return;
+    uint32_t run = 0;
+    for (int64_t b = 0; b < nb; ++b) {
+        seg[b * k + c] = run;
+        run += pcount[b * k + c];
+    }
+    counts[c] = run;
+}
+
+// One block: exclusive scan of the label totals (label starts in the permutation).
+__global__ __launch_bounds__(256) void km_label_starts_kernel(const uint32_t* __restrict__ counts, int64_t k,
+                                                              uint32_t* __restrict__ starts) {
+    __shared__ uint32_t wsum[4];
+    __shared__ uint32_t carry_s;
+    if (threadIdx.x == 0) carry_s = 0;
+    __syncthreads();
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int64_t c0 = 0; c0 < k; c0 += 256) {
+        const int64_t c = c0 + threadIdx.x;
+        const uint32_t v = c < k ? counts[c] : 0u;
+        uint32_t inc = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t u = (uint32_t)__shfl_up((int)inc, o, 64);
+            if (lane >= o) inc += u;
+        }
+        if (lane == 63) wsum[w] = inc;
+        __syncthreads();
+        uint32_t before = carry_s;
+        for (int i = 0; i < w; ++i) before += wsum[i];
+        if (c < k) starts[c] = before + inc - v;
+        __syncthreads();
+        if (threadIdx.x == 0) carry_s += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void km_add_starts_kernel(uint32_t* __restrict__ seg, int64_t nb, int64_t k,
+                                                            const uint32_t* __restrict__ starts) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < nb * k; t += stride) seg[t] += starts[t % k];
+}
+
+// One workgroup per block: rows in chunks of 256, each row placed after the
+// rows of its label earlier in the block.  cursor[b][c] starts as the bucket
+// start and advances chunk by chunk.
+__global__ __launch_bounds__(256) void km_scatter_kernel(const uint32_t* __restrict__ labels, int64_t n, int64_t rpb,
+                                                         int64_t k, uint32_t* __restrict__ cursor,
+                                                         uint32_t* __restrict__ perm) {
+    __shared__ uint32_t lab[256];
+    __shared__ uint32_t cur[kLdsLabels];
+    const int64_t b = blockIdx.x;
+    const int64_t start = b * rpb;
+    const int64_t end = (start + rpb) < n ? start + rpb : n;
+    uint32_t* gcur = cursor + b * k;
+    const bool lds = k <= kLdsLabels;
+    uint32_t* cp = lds ? cur : gcur;
+    if (lds) {
+        for (int64_t c = threadIdx.x; c < k; c += 256) cur[c] = gcur[c];
+    }
+    __syncthreads();
+    for (int64_t i0 = start; i0 < end; i0 += 256) {
+        const int t = threadIdx.x;
+        const int64_t i = i0 + t;
+        const int cnt = (end - i0) < 256 ? (int)(end - i0) : 256;
+        if (t < cnt) lab[t] = labels[i];
+        __syncthreads();
+        uint32_t rank = 0, after = 0, c = 0, base = 0;
+        if (t < cnt) {
+            c = lab[t];
+            for (int u = 0; u < t; ++u) rank += (lab[u] == c) ? 1u : 0u;
+            for (int u = t + 1; u < cnt; ++u) after += (lab[u] == c) ? 1u : 0u;
+            base = cp[c];
+            perm[base + rank] = (uint32_t)i;
+        }
+        __syncthreads();
+        if (t < cnt && after == 0) cp[c] = base + rank + 1u;  // the label's last row in this chunk
+        __threadfence_block();
+        __syncthreads();
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_psum_kernel(const T* __restrict__ x, int64_t d, int64_t nb, int64_t k,
+                                                      const uint32_t* __restrict__ pcount,
+                                                      const uint32_t* __restrict__ seg,
+                                                      const uint32_t* __restrict__ perm, T* __restrict__ psum) {
+    const int64_t total = nb * k * d;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+        const int64_t bc = t / d, j = t - bc * d;
+        const uint32_t s0 = seg[bc], m = pcount[bc];
+        T acc = T(0);
+        for (uint32_t p = 0; p < m; ++p) acc = acc + x[(int64_t)perm[s0 + p] * d + j];
+        psum[t] = acc;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_reduce_kernel(const T* __restrict__ psum, int64_t nb, int64_t kd,
+                                                        T* __restrict__ sums) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= kd) return;
+    T acc = T(0);
+    for (int64_t b = 0; b < nb; ++b) acc = acc + psum[b * kd + t];
+    sums[t] = acc;
+}
+
+__global__ __launch_bounds__(256) void km_changed_kernel(const uint32_t* __restrict__ a,
+                                                         const uint32_t* __restrict__ b, int64_t n,
+                                                         unsigned int* __restrict__ count) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    unsigned int local = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) local += (a[i] != b[i]) ? 1u : 0u;
+    for (int o = 32; o > 0; o >>= 1) local += (unsigned int)__shfl_xor((int)local, o, 64);
+    if ((threadIdx.x & 63) == 0 && local) atomicAdd(count, local);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restrict__ x, const T* __restrict__ c,
+                                                              const uint32_t* __restrict__ labels, int64_t n,
+                                                              int64_t d, T* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const T* xr = x + i * d;
+    const T* cr = c + (int64_t)labels[i] * d;
+    T acc = T(0);
+    for (int64_t j = 0; j < d; ++j) {
+        const T diff = xr[j] - cr[j];
+        acc = acc + diff * diff;
+    }
+    out[i] = acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_block_sum_kernel(const T* __restrict__ v, int64_t n, int64_t nb,
+                                                           int64_t rpb, T* __restrict__ out) {
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nb) return;
+    const int64_t start = b * rpb;
+    const int64_t end = (start + rpb) < n ? start + rpb : n;
+    T acc = T(0);
+    for (int64_t i = start; i < end; ++i) acc = acc + v[i];
+    out[b] = acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_col_sum_kernel(const T* __restrict__ x, int64_t n, int64_t d, int64_t nb,
+                                                         int64_t rpb, const T* __restrict__ means,
+                                                         T* __restrict__ out) {
+    const int64_t total = nb * d;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+        const int64_t b = t / d, j = t - b * d;
+        const int64_t start = b * rpb;
+        const int64_t end = (start + rpb) < n ? start + rpb : n;
+        T acc = T(0);
+        if (means) {
+            const T m = means[j];
+            for (int64_t i = start; i < end; ++i) {
+                const T diff = x[i * d + j] - m;
+                acc = acc + diff * diff;
+            }
+        } else {
+            for (int64_t i = start; i < end; ++i) acc = acc + x[i * d + j];
+        }
+        out[t] = acc;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_mind2_kernel(const T* __restrict__ x, int64_t n, int64_t d, int64_t cidx,
+                                                       int first, T* __restrict__ mind2) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const T* xr = x + i * d;
+    const T* cr = x + cidx * d;
+    T acc = T(0);
+    for (int64_t j = 0; j < d; ++j) {
+        const T diff = xr[j] - cr[j];
+        acc = acc + diff * diff;
+    }
+    if (first || acc < mind2[i]) mind2[i] = acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_gather_kernel(const T* __restrict__ x, const int64_t* __restrict__ idx,
+                                                        int64_t k, int64_t d, T* __restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= k * d) return;
+    const int64_t c = t / d, j = t - c * d;
+    out[t] = x[idx[c] * d + j];
+}
+
+unsigned blocks_for(int64_t n, int64_t cap) {
+    int64_t b = (n + 255) / 256;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return (unsigned)b;
+}
+
+}  // namespace
+
+template <typename T>
+hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n, int64_t d, int64_t k, int64_t nb,
+                                   int64_t rpb, const KmScratch<T>& w, hipStream_t s) {
+    if (k > kLdsLabels) {
+        hipError_t e = launch_fill_u32(w.pcount, nb * k, 0u, s);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(km_hist_kernel, dim3((unsigned)nb), dim3(256), 0, s, labels, n, rpb, k, w.pcount);
+    hipLaunchKernelGGL(km_label_totals_kernel, dim3(blocks_for(k, 1 << 20)), dim3(256), 0, s, w.pcount, nb, k, w.seg,
+                       w.counts);
+    hipLaunchKernelGGL(km_label_starts_kernel, dim3(1), dim3(256), 0, s, w.counts, k, w.starts);
+    hipLaunchKernelGGL(km_add_starts_kernel, dim3(blocks_for(nb * k, 4096)), dim3(256), 0, s, w.seg, nb, k, w.starts);
+    hipError_t e = hipMemcpyAsync(w.cursor, w.seg, sizeof(uint32_t) * (size_t)(nb * k), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(km_scatter_kernel, dim3((unsigned)nb), dim3(256), 0, s, labels, n, rpb, k, w.cursor, w.perm);
+    hipLaunchKernelGGL((km_psum_kernel<T>), dim3(blocks_for(nb * k * d, 65536)), dim3(256), 0, s, x, d, nb, k,
+                       w.pcount, w.seg, w.perm, w.psum);
+    hipLaunchKernelGGL((km_reduce_kernel<T>), dim3(blocks_for(k * d, 1 << 20)), dim3(256), 0, s, w.psum, nb, k * d,
+                       w.sums);
+    return hipGetLastError();
+}
+
+hipError_t launch_km_changed(const uint32_t* a, const uint32_t* b, int64_t n, unsigned int* count, hipStream_t s) {
+    hipError_t e = launch_fill_u32(count, 1, 0u, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(km_changed_kernel, dim3(blocks_for(n, 4096)), dim3(256), 0, s, a, b, n, count);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int64_t n, int64_t d, T* rows,
+                             int64_t nb, int64_t rpb, T* parts, hipStream_t s) {
+    hipLaunchKernelGGL((km_inertia_rows_kernel<T>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, c, labels, n, d,
+                       rows);
+    hipLaunchKernelGGL((km_block_sum_kernel<T>), dim3(blocks_for(nb, 1 << 20)), dim3(256), 0, s, rows, n, nb, rpb,
+                       parts);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_col_sums(const T* x, int64_t n, int64_t d, int64_t nb, int64_t rpb, const T* means, T* out,
+                              hipStream_t s) {
+    hipLaunchKernelGGL((km_col_sum_kernel<T>), dim3(blocks_for(nb * d, 65536)), dim3(256), 0, s, x, n, d, nb, rpb,
+                       means, out);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_mind2(const T* x, int64_t n, int64_t d, int64_t cidx, int first, T* mind2, hipStream_t s) {
+    hipLaunchKernelGGL((km_mind2_kernel<T>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, n, d, cidx, first,
+                       mind2);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_gather(const T* x, const int64_t* idx, int64_t k, int64_t d, T* out, hipStream_t s) {
+    hipLaunchKernelGGL((km_gather_kernel<T>), dim3(blocks_for(k * d, 1 << 30)), dim3(256), 0, s, x, idx, k, d, out);
+    return hipGetLastError();
+}
+
+#define MLRS_KM_INST(T)                                                                                            \
+    template hipError_t launch_km_centroid_sums<T>(const T*, const uint32_t*, int64_t, int64_t, int64_t, int64_t,   \
+                                                   int64_t, const KmScratch<T>&, hipStream_t);                     \
+    template hipError_t launch_km_inertia<T>(const T*, const T*, const uint32_t*, int64_t, int64_t, T*, int64_t,    \
+                                             int64_t, T*, hipStream_t);                                            \
+    template hipError_t launch_km_col_sums<T>(const T*, int64_t, int64_t, int64_t, int64_t, const T*, T*,           \
+                                              hipStream_t);                                                        \
+    template hipError_t launch_km_mind2<T>(const T*, int64_t, int64_t, int64_t, int, T*, hipStream_t);              \
+    template hipError_t launch_km_gather<T>(const T*, const int64_t*, int64_t, int64_t, T*, hipStream_t);
+MLRS_KM_INST(float)
+MLRS_KM_INST(double)
+#undef MLRS_KM_INST
+
+}  // namespace mlrs

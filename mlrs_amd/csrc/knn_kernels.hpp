@@ -269,4 +269,35 @@ hipError_t launch_graph_finish(const double* val, const uint32_t* idx, int64_t n
                                int halve, double* out_dist, uint32_t* out_idx, hipStream_t s);
 hipError_t launch_core_column(const double* val, int64_t n, int k, double* out, hipStream_t s);
 
+// k-means fit loop (kmeans_loop.hip).  Centroid sums over the reference's row
+// blocks: buckets of rows by (block, label), then per-(block, label, feature)
+// sums over each bucket in ascending row order, then the block partials summed
+// in block order.
+template <typename T>
+struct KmScratch {
+    uint32_t* pcount;  // [nb][k] rows of label c in block b
+    uint32_t* seg;     // [nb][k] first slot of bucket (b, c) in perm
+    uint32_t* cursor;  // [nb][k] scatter cursors
+    uint32_t* counts;  // [k]
+    uint32_t* starts;  // [k]
+    uint32_t* perm;    // [n] row numbers, bucket by bucket
+    T* psum;           // [nb][k][d]
+    T* sums;           // [k][d]
+};
+template <typename T>
+hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n, int64_t d, int64_t k, int64_t nb,
+                                   int64_t rpb, const KmScratch<T>& w, hipStream_t s);
+hipError_t launch_km_changed(const uint32_t* a, const uint32_t* b, int64_t n, unsigned int* count, hipStream_t s);
+template <typename T>
+hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int64_t n, int64_t d, T* rows,
+                             int64_t nb, int64_t rpb, T* parts, hipStream_t s);
+// means == nullptr: column sums; else column sums of (x - means)^2.
+template <typename T>
+hipError_t launch_km_col_sums(const T* x, int64_t n, int64_t d, int64_t nb, int64_t rpb, const T* means, T* out,
+                              hipStream_t s);
+template <typename T>
+hipError_t launch_km_mind2(const T* x, int64_t n, int64_t d, int64_t cidx, int first, T* mind2, hipStream_t s);
+template <typename T>
+hipError_t launch_km_gather(const T* x, const int64_t* idx, int64_t k, int64_t d, T* out, hipStream_t s);
+
 }  // namespace mlrs

@@ -16,6 +16,7 @@ Geometry is validated by the C ABI before any launch; a violation raises
 | ``radius_neighbors`` | radius_neighbor_indices_metric, crates/mlrs-algos/src/neighbors/nearest.rs:609-749 |
 | ``knn_graph``       | knn_graph via host_knn, crates/mlrs-algos/src/manifold/umap_host_knn.rs:212-515 |
 | ``core_distances``  | HDBSCAN core distances, crates/mlrs-algos/src/cluster/hdbscan/host_core.rs:253-540 |
+| ``kmeans_fit``      | KMeans::fit, crates/mlrs-algos/src/cluster/kmeans.rs:1353-1580 |
 | ``knn_regress``     | knn_regress_mean / knn_regress_gather, crates/mlrs-kernels/src/knn.rs:95-316 |
 | ``knn_classify``    | KNeighborsClassifier's host vote, crates/mlrs-algos/src/neighbors/classifier.rs:782-930 |
 """
@@ -215,6 +216,33 @@ def core_distances(x, min_samples, metric="euclidean", p=2.0):
         _stream(x.device))
     _lib.check(rc)
     return out
+
+
+_KMEANS_INIT = {"array": 0, "k-means++": 1, "random": 2}
+
+
+def kmeans_fit(x, n_clusters, init="k-means++", init_centers=None, seed=0, n_init=1, max_iter=300, tol=1e-4):
+    """k-means fit on the device (mlrs_kmeans_fit_*): ``(centers (k, d) in
+    x's dtype, labels int64 (n,), inertia float, n_iter int)`` of the winning
+    restart.  ``init`` is "k-means++", "random" or "array" (then
+    ``init_centers`` is a (k, d) device tensor of x's dtype)."""
+    _dev_check(x)
+    s = _suffix(x)
+    n, d = x.shape
+    k = int(n_clusters)
+    ini = None
+    if init == "array":
+        ini = init_centers.to(device=x.device, dtype=x.dtype).contiguous()
+    centers = torch.empty((k, d), dtype=x.dtype, device=x.device)
+    labels = torch.empty(n, dtype=torch.int32, device=x.device)
+    inertia = ctypes.c_double()
+    n_iter = ctypes.c_int64()
+    rc = getattr(_lib.load(), "mlrs_kmeans_fit_" + s)(
+        _ptr(x), x.numel(), n, d, k, _KMEANS_INIT[init], _ptr(ini), ini.numel() if ini is not None else 0,
+        int(seed) & 0xFFFFFFFFFFFFFFFF, int(n_init), int(max_iter), float(tol), _ptr(centers), centers.numel(),
+        _ptr(labels), labels.numel(), ctypes.byref(inertia), ctypes.byref(n_iter), _stream(x.device))
+    _lib.check(rc)
+    return centers, labels.to(torch.int64), inertia.value, int(n_iter.value)
 
 
 def _as_u32_idx(idx):

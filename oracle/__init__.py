@@ -47,6 +47,18 @@ def _load():
     lib.orc_knn_arm.restype = i32
     lib.orc_max_threads.argtypes = []
     lib.orc_max_threads.restype = i32
+    for s_ in ("f32", "f64"):
+        f = getattr(lib, "orc_kmeans_fit_" + s_)
+        f.argtypes = [vp, i64, i64, i64, i32, vp, ctypes.c_uint64, i64, i64, ctypes.c_double, vp, vp, vp, vp]
+        f.restype = i32
+        f = getattr(lib, "orc_kmeans_init_" + s_)
+        f.argtypes = [vp, i64, i64, i64, i32, ctypes.c_uint64, vp]
+        f.restype = i32
+        f = getattr(lib, "orc_feature_mean_var_" + s_)
+        f.argtypes = [vp, i64, i64]
+        f.restype = ctypes.c_double
+    lib.orc_splitmix64_stream.argtypes = [ctypes.c_uint64, i64, vp]
+    lib.orc_splitmix64_stream.restype = None
     lib.orc_knn_graph_f64.argtypes = [vp, i64, i64, i64, i32, ctypes.c_double, i32, vp, vp]
     lib.orc_knn_graph_f64.restype = i32
     lib.orc_core_distances_f64.argtypes = [vp, i64, i64, i32, ctypes.c_double, i64, vp]
@@ -211,6 +223,57 @@ def core_distances(x, min_samples, metric="euclidean", p=2.0):
     if rc != 0:
         raise ValueError("oracle core_distances rejected the input")
     return out
+
+
+KMEANS_INIT = {"array": 0, "k-means++": 1, "random": 2}
+
+
+def kmeans_fit(x, k, init="k-means++", init_centers=None, seed=0, n_init=1, max_iter=300, tol=1e-4):
+    """KMeans.fit as the reference's cpu backend runs it: ``(centers (k, d) in
+    x's dtype, uint32 labels, inertia (f64), n_iter)``."""
+    lib = _load()
+    x = np.ascontiguousarray(x)
+    n, d = x.shape
+    s = _suffix(x.dtype)
+    ini = None
+    if init == "array":
+        ini = np.ascontiguousarray(init_centers, dtype=x.dtype)
+    centers = np.empty((k, d), dtype=x.dtype)
+    labels = np.empty(n, dtype=np.uint32)
+    inertia = ctypes.c_double()
+    n_iter = ctypes.c_int64()
+    rc = getattr(lib, "orc_kmeans_fit_" + s)(
+        x.ctypes.data, n, d, int(k), KMEANS_INIT[init], ini.ctypes.data if ini is not None else None,
+        int(seed), int(n_init), int(max_iter), float(tol), centers.ctypes.data, labels.ctypes.data,
+        ctypes.byref(inertia), ctypes.byref(n_iter))
+    if rc != 0:
+        raise ValueError("oracle kmeans_fit failed (%d)" % rc)
+    return centers, labels, inertia.value, n_iter.value
+
+
+def kmeans_init(x, k, init="k-means++", seed=0):
+    """The row indices k-means++ / random initialisation picks (SplitMix64)."""
+    lib = _load()
+    x = np.ascontiguousarray(x)
+    n, d = x.shape
+    out = np.empty(k, dtype=np.int64)
+    rc = getattr(lib, "orc_kmeans_init_" + _suffix(x.dtype))(x.ctypes.data, n, d, int(k), KMEANS_INIT[init],
+                                                              int(seed), out.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle kmeans_init failed")
+    return out
+
+
+def splitmix64(seed, n):
+    out = np.empty(n, dtype=np.uint64)
+    _load().orc_splitmix64_stream(int(seed), int(n), out.ctypes.data)
+    return out
+
+
+def feature_mean_var(x):
+    x = np.ascontiguousarray(x)
+    n, d = x.shape
+    return getattr(_load(), "orc_feature_mean_var_" + _suffix(x.dtype))(x.ctypes.data, n, d)
 
 
 def row_sqnorms(x):

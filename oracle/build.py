@@ -13,7 +13,8 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SRCS = [os.path.join(HERE, "ref_cpu.c"), os.path.join(HERE, "consumers_cpu.c"), os.path.join(HERE, "graph_cpu.c")]
+SRCS = [os.path.join(HERE, "ref_cpu.c"), os.path.join(HERE, "consumers_cpu.c"), os.path.join(HERE, "graph_cpu.c"),
+        os.path.join(HERE, "kmeans_cpu.c")]
 OUT = os.path.join(HERE, "libmlrs_oracle.so")
 FLAGS = ["-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fno-math-errno",
          "-fopenmp", "-fPIC", "-shared", "-std=c11", "-Wall", "-Wextra"]

@@ -218,3 +218,25 @@ def test_graph_validation():
     assert g(P, 30, 10, 3, 1, 2.0, 5, P, 10, None) == _lib.MLRS_ERR_UNSUPPORTED
     assert g(P, 30, 10, 3, 0, 2.0, 5, P, 9, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
     assert _info().operand == b"out"
+
+
+def test_kmeans_fit_validation():
+    lib = _lib.load()
+    f = lib.mlrs_kmeans_fit_f32
+    inertia, n_iter = ctypes.c_double(), ctypes.c_int64()
+
+    def call(n=10, d=3, k=3, kind=1, init_len=0, n_init=1, max_iter=10, tol=1e-4, x_len=None, c_len=None,
+             l_len=None):
+        return f(P, n * d if x_len is None else x_len, n, d, k, kind, P, init_len, 0, n_init, max_iter, tol, P,
+                 k * d if c_len is None else c_len, P, n if l_len is None else l_len, ctypes.byref(inertia),
+                 ctypes.byref(n_iter), None)
+    assert call(k=11) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"k"
+    assert b"out of range" in _info().message
+    assert call(k=0) == _lib.MLRS_ERR_INVALID_PARAM
+    assert call(x_len=29) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"x"
+    assert call(kind=0, init_len=8) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"init"
+    assert call(kind=5) == _lib.MLRS_ERR_UNSUPPORTED
+    assert call(n_init=0) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"n_init"
+    assert call(tol=-1.0) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"tol"
+    assert call(c_len=8) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"centers"
+    assert call(l_len=9) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"labels"

@@ -1,0 +1,99 @@
+"""GPU parity of the device k-means fit (mlrs_kmeans_fit_*) against the CPU
+oracle's restatement of the reference's KMeans::fit, bit for bit: centres,
+labels, inertia and iteration count, for explicit, k-means++ and random
+initialisation, restarts, empty-cluster relocation, both assignment kernel
+families and both centroid-sum bucket paths (labels below and above the LDS
+histogram); and the estimator against the reference's fixtures.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import load_golden
+from mlrs_amd import _lib, prims
+from mlrs_amd.cluster import KMeans
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _blobs(seed, n, d, k, spread=1.0, dtype=np.float64):
+    rng = np.random.default_rng(seed)
+    centres = rng.uniform(-6, 6, size=(k, d))
+    lab = rng.integers(0, k, n)
+    return (centres[lab] + spread * rng.standard_normal((n, d))).astype(dtype)
+
+
+def _same(got, want):
+    gc, gl, gi, gn = got
+    wc, wl, wi, wn = want
+    np.testing.assert_array_equal(gl.cpu().numpy(), wl.astype(np.int64))
+    np.testing.assert_array_equal(gc.cpu().numpy(), wc)
+    assert gi == wi
+    assert gn == wn
+
+
+@pytest.fixture(params=["auto", "generic"])
+def family(request):
+    prims.force_path(request.param)
+    yield request.param
+    prims.force_path("auto")
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("init", ["array", "k-means++", "random"])
+@pytest.mark.parametrize("case", [(1, 3000, 5, 7, 1), (2, 20000, 16, 40, 2), (3, 5000, 3, 300, 1)])
+def test_fit_matches_oracle(family, dtype, init, case):
+    seed, n, d, k, n_init = case
+    X = _blobs(seed, n, d, max(2, k // 3), spread=2.0, dtype=dtype)
+    ini = X[np.random.default_rng(seed).choice(n, k, replace=False)] if init == "array" else None
+    want = oracle.kmeans_fit(X, k, init, ini, seed=seed, n_init=n_init, max_iter=60, tol=1e-4)
+    got = prims.kmeans_fit(_t(X), k, init, _t(ini) if ini is not None else None, seed=seed, n_init=n_init,
+                           max_iter=60, tol=1e-4)
+    _same(got, want)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_fit_many_labels_global_buckets(dtype):
+    """k above the LDS label histogram: the global-memory bucket path."""
+    X = _blobs(4, 40000, 2, 50, spread=3.0, dtype=dtype)
+    ini = X[np.random.default_rng(4).choice(40000, 9000, replace=False)]
+    want = oracle.kmeans_fit(X, 9000, "array", ini, max_iter=4, tol=0.0)
+    got = prims.kmeans_fit(_t(X), 9000, "array", _t(ini), max_iter=4, tol=0.0)
+    _same(got, want)
+
+
+def test_fit_relocates_empty_clusters():
+    X = _blobs(5, 2000, 3, 3, spread=0.8)
+    ini = np.array([X[0], X[1], [500.0, 500.0, 500.0], [-400.0, 0.0, 0.0]])
+    want = oracle.kmeans_fit(X, 4, "array", ini)
+    got = prims.kmeans_fit(_t(X), 4, "array", _t(ini))
+    _same(got, want)
+    assert len(set(got[1].cpu().tolist())) == 4
+
+
+@pytest.mark.parametrize("s", ["f32", "f64"])
+def test_estimator_fixture(s):
+    z = load_golden("kmeans_%s_seed42" % s)
+    km = KMeans(n_clusters=z["init"].shape[0], init=z["init"], n_init=1).fit(z["X"])
+    np.testing.assert_array_equal(km.labels_, z["labels"].astype(np.int32))
+    np.testing.assert_allclose(km.cluster_centers_, z["centers"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(km.inertia_, z["inertia"][0], rtol=1e-5)
+    np.testing.assert_array_equal(km.predict(z["X"]), km.labels_)
+
+
+def test_estimator_defaults_and_errors():
+    X = _blobs(6, 4000, 4, 5, spread=1.0, dtype=np.float32)
+    km = KMeans(n_clusters=5, random_state=3).fit(X)
+    c, l, inertia, it = oracle.kmeans_fit(X, 5, "k-means++", seed=3, n_init=1)
+    np.testing.assert_array_equal(km.labels_, l.astype(np.int32))
+    np.testing.assert_array_equal(km.cluster_centers_, c)
+    assert km.n_iter_ == it and km._n_init == 1
+    assert KMeans(n_clusters=5, init="random").fit(X)._n_init == 10
+    with pytest.raises(_lib.InvalidParam):
+        KMeans(n_clusters=5000).fit(X[:100])
