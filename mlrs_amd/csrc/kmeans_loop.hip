@@ -12,16 +12,17 @@
 // numbers -- so the thread of (b, c, j) walks exactly the rows of its bucket,
 // in ascending order: the same sums in the same order for O(n*d) work.
 //
-//   km_hist_kernel      pcount[b][c]: one workgroup per block (LDS histogram)
-//   km_offsets_kernel   per label: its total and the start of each (b, c)
-//                       bucket in the label-major permutation
-//   km_scatter_kernel   stable scatter of the block's rows into their buckets
-//   km_psum_kernel      psum[b][c][j] over the bucket, ascending rows
-//   km_reduce_kernel    sums[c][j] = sum over b in order
+//   km_hist_kernel          pcount[b][c]: one workgroup per block (LDS histogram)
+//   km_label_totals_kernel  per label: its total and each (b, c) bucket's
+//   km_label_starts_kernel  start in the label-major permutation (a prefix
+//   km_add_starts_kernel    over blocks, then over labels)
+//   km_scatter_kernel       stable scatter of the block's rows into their buckets
+//   km_psum_kernel          psum[b][c][j] over the bucket, ascending rows
+//   km_reduce_kernel        sums[c][j] = sum over b in order
 //
 // Also: km_changed_kernel (labels that differ), km_inertia_rows_kernel and
 // km_block_sum_kernel (inertia_rows + block_sum_f, kernels/kmeans.rs:123-145,
-// 523-545), km_col_sum_kernel / km_col_sqdiff_kernel (col_sum_blocked /
+// 523-545), km_col_sum_kernel (col_sum_blocked and, given the means,
 // col_sqdiff_blocked, :704-762), km_mind2_kernel (kmeanspp_mind2, :576-603) and
 // km_gather_kernel (gather_rows_idx, :552-570).  Every sum is the reference's
 // element type and order.
@@ -33,6 +34,23 @@ namespace mlrs {
 namespace {
 
 constexpr int kLdsLabels = 8192;  // labels an LDS histogram / cursor array holds
+
+// acc + p[0] + p[stride] + ... in order; the loads are issued 16 at a time
+// ahead of the dependent adds, so a long strided sum is not latency-bound.
+template <typename T>
+__device__ __forceinline__ T ordered_sum(const T* __restrict__ p, int64_t count, int64_t stride) {
+    T acc = T(0);
+    int64_t b = 0;
+    for (; b + 16 <= count; b += 16) {
+        T v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = p[(b + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc = acc + v[u];
+    }
+    for (; b < count; ++b) acc = acc + p[b * stride];
+    return acc;
+}
 
 __global__ __launch_bounds__(256) void km_hist_kernel(const uint32_t* __restrict__ labels, int64_t n, int64_t rpb,
                                                       int64_t k, uint32_t* __restrict__ pcount) {
@@ -61,7 +79,18 @@ __global__ __launch_bounds__(256) void km_label_totals_kernel(const uint32_t* __
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (c >= k) return;
     uint32_t run = 0;
-    for (int64_t b = 0; b < nb; ++b) {
+    int64_t b = 0;
+    for (; b + 16 <= nb; b += 16) {
+        uint32_t v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = pcount[(b + u) * k + c];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            seg[(b + u) * k + c] = run;
+            run += v[u];
+        }
+    }
+    for (; b < nb; ++b) {
         seg[b * k + c] = run;
         run += pcount[b * k + c];
     }
@@ -161,9 +190,7 @@ __global__ __launch_bounds__(256) void km_reduce_kernel(const T* __restrict__ ps
                                                         T* __restrict__ sums) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= kd) return;
-    T acc = T(0);
-    for (int64_t b = 0; b < nb; ++b) acc = acc + psum[b * kd + t];
-    sums[t] = acc;
+    sums[t] = ordered_sum<T>(psum + t, nb, kd);
 }
 
 __global__ __launch_bounds__(256) void km_changed_kernel(const uint32_t* __restrict__ a,
@@ -199,9 +226,7 @@ __global__ __launch_bounds__(256) void km_block_sum_kernel(const T* __restrict__
     if (b >= nb) return;
     const int64_t start = b * rpb;
     const int64_t end = (start + rpb) < n ? start + rpb : n;
-    T acc = T(0);
-    for (int64_t i = start; i < end; ++i) acc = acc + v[i];
-    out[b] = acc;
+    out[b] = ordered_sum<T>(v + start, end - start, 1);
 }
 
 template <typename T>
@@ -222,7 +247,7 @@ __global__ __launch_bounds__(256) void km_col_sum_kernel(const T* __restrict__ x
                 acc = acc + diff * diff;
             }
         } else {
-            for (int64_t i = start; i < end; ++i) acc = acc + x[i * d + j];
+            acc = ordered_sum<T>(x + start * d + j, end - start, d);
         }
         out[t] = acc;
     }
