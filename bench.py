@@ -150,17 +150,21 @@ def main():
     evals = float(n_query) * float(n_index)
     value = evals / (ms_per_step / 1000.0)
     flops = 2.0 * d * evals
+    kname = name.value.decode()
+    f64 = cfg["dtype"] == "f64"
     if radius is not None:
         # the exact scan: a subtract, a multiply and an add per pair and
         # feature (no fused multiply-add: the reference's operation order)
         flops = 3.0 * d * evals
-        bound, peak, unit = "valu", PEAKS["valu_f32" if cfg["dtype"] == "f32" else "valu_f64"], "TFLOP/s"
-    elif args.config == "c4":
-        bound, peak, unit = "valu", PEAKS["valu_f32"], "TFLOP/s"
-    elif args.config == "c3":
+        bound, peak, unit = "valu", PEAKS["valu_f64" if f64 else "valu_f32"], "TFLOP/s"
+    elif kname.startswith("knn_gram_f64"):
         bound, peak, unit = "mfma", PEAKS["mfma_f64"], "TFLOP/s"
-    else:
+    elif kname.startswith("knn_gram_f32"):
         bound, peak, unit = "mfma", PEAKS["mfma_f32"], "TFLOP/s"
+    else:
+        # the low-d ALU kernel and the exact tiles of small searches: vector
+        # units without packed math (an FMA counts two flops)
+        bound, peak, unit = "valu", PEAKS["valu_f64" if f64 else "valu_f32"], "TFLOP/s"
     achieved = flops / (kern_ms / 1000.0) / 1e12
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "traffic_%s%s.json" % ("radius_" if radius is not None else "",

@@ -2,7 +2,7 @@
 //
 // The MI355X counterpart of euclidean_topk_rows_cpu_direct
 // (crates/mlrs-kernels/src/knn.rs:2968-3227).  Each lane owns QL query rows
-// (QL = 4 for k <= 8, 2 for k <= 16, 1 above), keeps their sorted k-lists in
+// (QL = 2 for k <= 16, 1 above), keeps their sorted k-lists in
 // VGPRs and walks every index row of its strip.  Per (query, row) pair the
 // screen costs d FMAs: the expansion ||x||^2 - 2 x.q accumulated from the
 // row's precomputed squared norm, against the threshold derived from the
