@@ -348,10 +348,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     int64_t grid_wgs = 1;
     int nslots = 1;
     gram_f32_split(nq, nt, cus, &grid_wgs, &nslots);
-    // per-(segment slot, query) exact lists: the kernel's top-k state, merged at the end
-    size_t parts = (size_t)nslots * nq * k;
+    // per-(segment slot, query) lists: the kernel's top-k state, merged at the end
+    size_t parts = (size_t)nslots * nq * gram_list_cap(k);
+    size_t qvals = (k > 1) ? gram_f32_qval_elems(grid_wgs) : 0;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
-                   aligned_bytes(sizeof(unsigned int) * nq);
+                   aligned_bytes(qvals * sizeof(float)) + aligned_bytes(sizeof(unsigned int) * nq);
     rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
@@ -393,6 +394,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     a.nslots = nslots;
     a.part_val = cv.take<float>(parts);
     a.part_idx = cv.take<uint32_t>(parts);
+    if (qvals) a.qval = cv.take<float>(qvals);
     if (nslots > 1 || k > 1) a.shared_r = cv.take<unsigned int>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
@@ -401,7 +403,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
         KernelTimer timer(s, "knn_gram_f32_kernel");
         e = launch_gram_f32(a, arm, s);
     }
-    if (e == hipSuccess) e = launch_gram_f32_merge(a, s);
+    if (e == hipSuccess) e = launch_gram_f32_merge(a, arm, s);
     if (e != hipSuccess) return hip_err(e, "knn_gram_f32");
     return ok();
 }
@@ -418,9 +420,10 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     int64_t grid_wgs = 1;
     int nslots = 1;
     gram_f64_split(nq, nt, cus, &grid_wgs, &nslots);
-    size_t parts = (size_t)nslots * nq * k;
+    size_t parts = (size_t)nslots * nq * gram_list_cap(k);
+    size_t qvals = gram_f64_qval_elems(grid_wgs);
     size_t bytes = fixed + aligned_bytes(parts * sizeof(double)) + aligned_bytes(parts * sizeof(uint32_t)) +
-                   aligned_bytes(sizeof(unsigned long long) * nq);
+                   aligned_bytes(qvals * sizeof(double)) + aligned_bytes(sizeof(unsigned long long) * nq);
     rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
@@ -463,6 +466,7 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     a.nslots = nslots;
     a.part_val = cv.take<double>(parts);
     a.part_idx = cv.take<uint32_t>(parts);
+    a.qval = cv.take<double>(qvals);
     a.shared_r = cv.take<unsigned long long>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
@@ -471,7 +475,7 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
         KernelTimer timer(s, "knn_gram_f64_kernel");
         e = launch_gram_f64(a, arm, s);
     }
-    if (e == hipSuccess) e = launch_gram_f64_merge(a, s);
+    if (e == hipSuccess) e = launch_gram_f64_merge(a, arm, s);
     if (e != hipSuccess) return hip_err(e, "knn_gram_f64");
     return ok();
 }

@@ -67,7 +67,8 @@ static constexpr uint32_t kSentinelIdx = 0xFFFFFFFFu;
 // 2655-2706): smaller value first, lower index on an equal value.
 template <typename T>
 __device__ __forceinline__ bool pair_less(T va, uint32_t ia, T vb, uint32_t ib) {
-    return va < vb || (va == vb && ia < ib);
+    // bitwise, not short-circuit: evaluated as lane masks with no branches
+    return (va < vb) | ((va == vb) & (ia < ib));
 }
 
 // The reference clamp written in statement form: NaN passes through.
@@ -150,14 +151,78 @@ __device__ __forceinline__ float round_up_f(double t) {
 // Wave64 bitonic machinery over (value, index) pairs, one pair per lane.
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
-__device__ __forceinline__ double shfl_xor_f(double v, int m) { return __shfl_xor(v, m, 64); }
-__device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int m) {
-    return (uint32_t)__shfl_xor((int)v, m, 64);
+// Lane exchanges.  The partner lane ^ m of a constant m comes from DPP (quad
+// permutations for m = 1, 2; row shifts left and right for m = 4, 8) or from
+// v_permlane{16,32}_swap (m = 16, 32): VALU operations, no round trip
+// through the LDS crossbar as ds_bpermute (the generic __shfl_xor) takes.
+// Every lane of the wave must be active.  The bitonic loops below are fully
+// unrolled, so m is a constant by the time these are inlined.
+__device__ __forceinline__ uint32_t lane_id_u() {
+    return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
 }
+__device__ __forceinline__ uint32_t xor_lane_u(uint32_t v, int m) {
+    const uint32_t lane = lane_id_u();
+    switch (m) {
+    case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    case 4: {
+        const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, false);  // row_shl:4
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+        return (lane & 4u) ? dn : up;
+    }
+    case 8: {
+        const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x108, 0xF, 0xF, false);  // row_shl:8
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+        return (lane & 8u) ? dn : up;
+    }
+    case 16: {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16u) ? r[0] : r[1];
+    }
+    case 32: {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32u) ? r[0] : r[1];
+    }
+    default: return (uint32_t)__shfl_xor((int)v, m, 64);
+    }
+}
+// Value of lane 63 - lane: the mirror inside each 16-lane row, then the rows
+// reversed (rows 0..3 -> 3..0 is lane ^ 48).
+__device__ __forceinline__ uint32_t reverse_lane_u(uint32_t v) {
+    const uint32_t r = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);  // row_mirror
+    return xor_lane_u(xor_lane_u(r, 16), 32);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __uint_as_float(xor_lane_u(__float_as_uint(v), m)); }
+__device__ __forceinline__ double shfl_xor_f(double v, int m) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = xor_lane_u((uint32_t)b, m), hi = xor_lane_u((uint32_t)(b >> 32), m);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int m) { return xor_lane_u(v, m); }
+__device__ __forceinline__ float reverse_f(float v) { return __uint_as_float(reverse_lane_u(__float_as_uint(v))); }
+__device__ __forceinline__ double reverse_f(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = reverse_lane_u((uint32_t)b), hi = reverse_lane_u((uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ uint32_t reverse_u(uint32_t v) { return reverse_lane_u(v); }
 __device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, 64); }
 __device__ __forceinline__ double shfl_f(double v, int src) { return __shfl(v, src, 64); }
 __device__ __forceinline__ uint32_t shfl_u(uint32_t v, int src) { return (uint32_t)__shfl((int)v, src, 64); }
+// Value of lane `src`, the same lane for the whole wave (v_readlane).
+__device__ __forceinline__ float bcast_f(float v, int src) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), src));
+}
+__device__ __forceinline__ double bcast_f(double v, int src) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, src);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), src);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ uint32_t bcast_u(uint32_t v, int src) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
+}
 
 // One compare-exchange step with the partner lane^m.  `up` says whether this
 // lane's sub-sequence sorts ascending.
@@ -165,14 +230,13 @@ template <typename T>
 __device__ __forceinline__ void bitonic_step(T& v, uint32_t& ix, int lane, int m, bool up) {
     T ov = shfl_xor_f(v, m);
     uint32_t oi = shfl_xor_u(ix, m);
-    bool lower = (lane & m) == 0;
+    const bool lower = (lane & m) == 0;
     // The lower lane of an ascending pair keeps the smaller element, the upper
-    // lane the larger; a descending pair the reverse.
-    bool take = (lower == up) ? pair_less<T>(ov, oi, v, ix) : pair_less<T>(v, ix, ov, oi);
-    if (take) {
-        v = ov;
-        ix = oi;
-    }
+    // lane the larger; a descending pair the reverse.  Selects, no branches.
+    const bool first = (lower == up);
+    const bool take = (first & pair_less<T>(ov, oi, v, ix)) | (!first & pair_less<T>(v, ix, ov, oi));
+    v = take ? ov : v;
+    ix = take ? oi : ix;
 }
 
 // Full ascending bitonic sort of 64 lanes.
@@ -191,14 +255,103 @@ __device__ __forceinline__ void wave_sort64(T& v, uint32_t& ix, int lane) {
 // ascending.  Both inputs must be sorted.
 template <typename T>
 __device__ __forceinline__ void wave_merge64(T& lv, uint32_t& li, T v, uint32_t ix, int lane) {
-    T rv = shfl_f(v, 63 - lane);
-    uint32_t ri = shfl_u(ix, 63 - lane);
-    if (pair_less<T>(rv, ri, lv, li)) {
-        lv = rv;
-        li = ri;
-    }
+    T rv = reverse_f(v);
+    uint32_t ri = reverse_u(ix);
+    const bool take = pair_less<T>(rv, ri, lv, li);
+    lv = take ? rv : lv;
+    li = take ? ri : li;
 #pragma unroll
     for (int m = 32; m > 0; m >>= 1) bitonic_step<T>(lv, li, lane, m, true);
+}
+
+// wave_merge64 that also returns the smallest value it discards (the upper
+// half of the union), +inf when only sentinels are discarded.  Values must
+// not be NaN.
+template <typename T>
+__device__ __forceinline__ T wave_merge64_drop(T& lv, uint32_t& li, T v, uint32_t ix, int lane) {
+    T rv = reverse_f(v);
+    uint32_t ri = reverse_u(ix);
+    const bool take = pair_less<T>(rv, ri, lv, li);
+    const T dv0 = take ? lv : rv;
+    lv = take ? rv : lv;
+    li = take ? ri : li;
+    T dv = dv0;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) bitonic_step<T>(lv, li, lane, m, true);
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        const T o = shfl_xor_f(dv, m);
+        dv = (o < dv) ? o : dv;
+    }
+    return dv;
+}
+
+// ---------------------------------------------------------------------------
+// The same machinery on 64-bit keys: for f32 values the (value, index) order
+// is the unsigned order of (orderable value bits << 32 | index), so one
+// 64-bit compare replaces the two-part comparison.
+// ---------------------------------------------------------------------------
+
+// Order-preserving map of float bits to unsigned (negative values flipped).
+__device__ __forceinline__ uint32_t f32_order_bits(float v) {
+    const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0: equal values order by index
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float f32_from_order_bits(uint32_t o) {
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+__device__ __forceinline__ unsigned long long pair_key(float v, uint32_t ix) {
+    return ((unsigned long long)f32_order_bits(v) << 32) | ix;
+}
+__device__ __forceinline__ float key_value(unsigned long long key) { return f32_from_order_bits((uint32_t)(key >> 32)); }
+__device__ __forceinline__ uint32_t key_index(unsigned long long key) { return (uint32_t)key; }
+constexpr unsigned long long kKeyEmpty = 0xFF800000FFFFFFFFull;  // (+inf, sentinel index)
+
+__device__ __forceinline__ unsigned long long xor_lane_key(unsigned long long v, int m) {
+    return ((unsigned long long)xor_lane_u((uint32_t)(v >> 32), m) << 32) | xor_lane_u((uint32_t)v, m);
+}
+
+// Compare-exchange with lane ^ m.  Equal keys may be exchanged: they are
+// the same pair (or both empty), so the sequence is unchanged.
+__device__ __forceinline__ void bitonic_step_key(unsigned long long& v, int lane, int m, bool up) {
+    const unsigned long long o = xor_lane_key(v, m);
+    const bool first = (((lane & m) == 0) == up);
+    const bool take = (o < v) == first;
+    v = take ? o : v;
+}
+
+__device__ __forceinline__ void wave_sort64_key(unsigned long long& v, int lane) {
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+        const bool up = (lane & size) == 0 || size == 64;
+#pragma unroll
+        for (int m = size >> 1; m > 0; m >>= 1) bitonic_step_key(v, lane, m, up);
+    }
+}
+
+// Merge the ascending sequence v into the ascending list lv (the 64 smallest
+// keys of the union stay in lv) and return the smallest key discarded.
+__device__ __forceinline__ unsigned long long wave_merge64_key_drop(unsigned long long& lv, unsigned long long v,
+                                                                    int lane) {
+    const unsigned long long r =
+        ((unsigned long long)reverse_lane_u((uint32_t)(v >> 32)) << 32) | reverse_lane_u((uint32_t)v);
+    unsigned long long dv = (r < lv) ? lv : r;
+    lv = (r < lv) ? r : lv;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) bitonic_step_key(lv, lane, m, true);
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        const unsigned long long o = xor_lane_key(dv, m);
+        dv = (o < dv) ? o : dv;
+    }
+    return dv;
+}
+__device__ __forceinline__ void wave_merge64_key(unsigned long long& lv, unsigned long long v, int lane) {
+    const unsigned long long r =
+        ((unsigned long long)reverse_lane_u((uint32_t)(v >> 32)) << 32) | reverse_lane_u((uint32_t)v);
+    lv = (r < lv) ? r : lv;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) bitonic_step_key(lv, lane, m, true);
 }
 
 }  // namespace mlrs

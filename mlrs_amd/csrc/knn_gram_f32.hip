@@ -65,6 +65,7 @@ struct WaveLds {
     float qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
     float eps[kQpw];  // screen error bound
     uint32_t off[kQpw];                 // k = 1: queue offsets of the batched flush
+    uint32_t mode[kQpw];                // k > 1: 0 = screen-value list, 1 = exact list
     unsigned long long best[kQpw];      // k = 1: (value bits << 32 | index) of the kept pair
 };
 
@@ -206,6 +207,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     unsigned int* __restrict__ SHARED_R = a.shared_r;
     const int64_t nq = a.nq, nt = a.nt, d = a.d;
     const int k = a.k;
+    const int K2 = gram_list_cap(k);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -213,6 +215,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     const int jl = lane & 31;
     WaveLds& L = wl[w];
     const float inf = __builtin_huge_valf();
+    // screen values of this wave's queued pairs, [queue position][query]
+    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * (kQpw * kQcap);
 
     // ---- work split (StreamSplit): this workgroup's range of (query block,
     //      tile) units, panel-major; each piece of a job in the range is a
@@ -226,8 +230,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     sp.decode(u, panel, qblock, tile0, left);
     const int64_t tile1 = tile0 + ((left < u_hi - u) ? left : (u_hi - u));
     const int64_t slot = sp.slot(wg, panel, qblock);
-    float* __restrict__ LV = a.part_val + slot * nq * k;
-    uint32_t* __restrict__ LI = a.part_idx + slot * nq * k;
+    float* __restrict__ LV = a.part_val + slot * nq * K2;
+    uint32_t* __restrict__ LI = a.part_idx + slot * nq * K2;
 
     const int64_t qwave = qblock * kQpb + w * kQpw;  // first query of this wave
     const int64_t qmine = qwave + jl;
@@ -250,15 +254,22 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             L.qa[lane] = qsq;
             L.eps[lane] = (float)a.eps_abs;
         }
+        // Screen-value lists need |screen distance - exact| <= eps for every
+        // pair, which the error bound gives while no sum can overflow: norms
+        // well inside the float range (and a nonzero query for cosine).
+        // Other queries keep exact lists.
+        bool sv = qvalid && ((double)qsq + (double)a.stats->xsq_max <= 0x1p124) && (L.eps[lane] < inf);
+        if (COS) sv = sv && (L.qs[lane] > 0.0f);
+        L.mode[lane] = sv ? 0u : 1u;
     }
     if (K1) {
         if (lane < kQpw) L.best[lane] = kBestEmpty;
     } else {
         for (int j = 0; j < kQpw; ++j) {
             const int64_t qg = qwave + j;
-            if (qg < nq && lane < k) {
-                LV[qg * k + lane] = inf;
-                LI[qg * k + lane] = kSentinelIdx;
+            if (qg < nq && lane < K2) {
+                LV[qg * K2 + lane] = inf;
+                LI[qg * K2 + lane] = kSentinelIdx;
             }
         }
     }
@@ -334,32 +345,72 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         }                                                                                    \
     } while (0)
 
-    // ---- flush: exact evaluation of one query's queue, sort, merge ----
+    // ---- flush (k > 1): one query's queue sorted and merged into its list.
+    //      Screen-value mode: a queued pair enters with its screen value
+    //      mapped back to a distance, within eps of its exact value; the list
+    //      keeps the K2 smallest, and the segment's bound is its k-th + eps.
+    //      A pair whose screen value is NaN, and every pair of an exact-mode
+    //      query, is evaluated exactly in the arm's operation order.  When a
+    //      discarded pair lies within 2 eps of the k-th (it could still be
+    //      among the k best), the old list and the queue are re-evaluated
+    //      exactly and the query's list stays exact from then on. ----
+#define MLRS_EXACT_AT(T_)                                                                    \
+    exact_f32<ARM, VEC4>(Q + qg_ * d, X + (int64_t)(T_) * d, d, L.qa[j_],                    \
+                         (ARM == ARM_COS_FOLD) ? XSQ[(T_)] : 0.0f)
 #define MLRS_FLUSH(J)                                                                        \
     do {                                                                                     \
         const int j_ = (J);                                                                  \
         const int64_t qg_ = qwave + j_;                                                      \
-        const uint32_t n_ = shfl_u(cntr, j_);                                                \
-        float lv_ = (lane < k) ? LV[qg_ * k + lane] : inf;                                   \
-        uint32_t li_ = (lane < k) ? LI[qg_ * k + lane] : kSentinelIdx;                       \
+        const uint32_t n_ = bcast_u(cntr, j_);                                               \
+        const bool exact_ = L.mode[j_] != 0u;                                                \
+        unsigned long long lk_ = kKeyEmpty;                                                  \
+        if (lane < K2) lk_ = pair_key(LV[qg_ * K2 + lane], LI[qg_ * K2 + lane]);             \
         float e_ = inf;                                                                      \
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
             t_ = L.qidx[j_][lane];                                                           \
-            const float ya_ = (ARM == ARM_COS_FOLD) ? XSQ[t_] : 0.0f;                        \
-            e_ = exact_f32<ARM, VEC4>(Q + qg_ * d, X + (int64_t)t_ * d, d, L.qa[j_], ya_);   \
+            const float s_ = exact_ ? 0.0f : QVw[lane * kQpw + j_];                          \
+            if (exact_ || s_ != s_)                                                          \
+                e_ = MLRS_EXACT_AT(t_);                                                      \
+            else                                                                             \
+                e_ = COS ? 1.0f + s_ / L.qs[j_] : s_ + L.qs[j_];                             \
             if (e_ != e_) { /* NaN is never admitted */                                      \
                 e_ = inf;                                                                    \
                 t_ = kSentinelIdx;                                                           \
             }                                                                                \
         }                                                                                    \
-        wave_sort64<float>(e_, t_, lane);                                                    \
-        wave_merge64<float>(lv_, li_, e_, t_, lane);                                         \
-        if (lane < k) {                                                                      \
-            LV[qg_ * k + lane] = lv_;                                                        \
-            LI[qg_ * k + lane] = li_;                                                        \
+        unsigned long long ek_ = pair_key(e_, t_);                                           \
+        wave_sort64_key(ek_, lane);                                                          \
+        const unsigned long long ok_ = lk_;                                                  \
+        const unsigned long long dk_ = wave_merge64_key_drop(lk_, ek_, lane);                \
+        float R_ = f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), k - 1));               \
+        if (!exact_) {                                                                       \
+            const float dr_ = (K2 < 64) ? f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), K2)) \
+                                        : key_value(dk_);                                    \
+            double w_ = (double)R_ + 2.0 * (double)L.eps[j_];                                \
+            w_ += __builtin_fabs(w_) * 0x1p-40;                                              \
+            if (dr_ < inf && (double)dr_ <= w_) {                                            \
+                float x1_ = inf, x2_ = inf;                                                  \
+                uint32_t i1_ = key_index(ok_), i2_ = key_index(ek_);                         \
+                if (i1_ != kSentinelIdx) x1_ = MLRS_EXACT_AT(i1_);                           \
+                if (i2_ != kSentinelIdx) x2_ = MLRS_EXACT_AT(i2_);                           \
+                if (x1_ != x1_) { x1_ = inf; i1_ = kSentinelIdx; }                           \
+                if (x2_ != x2_) { x2_ = inf; i2_ = kSentinelIdx; }                           \
+                unsigned long long k1_ = pair_key(x1_, i1_), k2_ = pair_key(x2_, i2_);       \
+                wave_sort64_key(k1_, lane);                                                  \
+                wave_sort64_key(k2_, lane);                                                  \
+                wave_merge64_key(k1_, k2_, lane);                                            \
+                lk_ = k1_;                                                                   \
+                R_ = f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), k - 1));             \
+                if (lane == 0) L.mode[j_] = 1u;                                              \
+            } else if (R_ < inf) {                                                           \
+                R_ = round_up_f((double)R_ + (double)L.eps[j_]);                             \
+            }                                                                                \
         }                                                                                    \
-        float R_ = shfl_f(lv_, k - 1);                                                       \
+        if (lane < K2) {                                                                     \
+            LV[qg_ * K2 + lane] = key_value(lk_);                                            \
+            LI[qg_ * K2 + lane] = key_index(lk_);                                            \
+        }                                                                                    \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf) {                                                      \
                 unsigned int old_ = atomicMin(&SHARED_R[qg_], __float_as_uint(R_));          \
@@ -489,10 +540,21 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             const uint32_t co = shfl_xor_u(c, 32);
             uint32_t pos = cntr + (h ? co : 0u);
             const uint32_t tb = (uint32_t)t0 + 4u * (uint32_t)h;
-            while (m) {
-                const int r = __builtin_ctz(m);
-                m &= m - 1;
-                L.qidx[jl][pos++] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
+            if (K1) {
+                while (m) {
+                    const int r = __builtin_ctz(m);
+                    m &= m - 1;
+                    L.qidx[jl][pos++] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    if (m & (1u << r)) {
+                        L.qidx[jl][pos] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
+                        QVw[pos * kQpw + jl] = acc[r];
+                        ++pos;
+                    }
+                }
             }
             cntr += c + co;
         }
@@ -503,6 +565,9 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             if (K1) {
                 MLRS_FLUSH_K1();
             } else {
+                // the queued screen values were stored by other lanes of this wave
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
                 while (mask) {
                     const int j = __builtin_ctzll(mask);
                     mask &= mask - 1;
@@ -527,6 +592,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         if (K1) {
             if (mask) MLRS_FLUSH_K1();
         } else {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             while (mask) {
                 const int j = __builtin_ctzll(mask);
                 mask &= mask - 1;
@@ -536,6 +603,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     }
 #undef MLRS_FLUSH_K1
 #undef MLRS_FLUSH
+#undef MLRS_EXACT_AT
 #undef MLRS_PREFETCH
 
     // ---- k = 1: the kept pair becomes this segment's one-entry list ----
@@ -581,34 +649,87 @@ __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t
     if (lane == a.k - 1) a.shared_r[qg] = __float_as_uint(lv);
 }
 
-// Merge the per-strip exact lists of one query per wave (the strip merge of
-// select_k_onepass_indexed, crates/mlrs-kernels/src/topk.rs:612-758, here a
-// wave-wide bitonic merge of sorted lists) and emit the output transform.
+// Merge the per-segment lists of one query per wave and emit the output
+// transform (the strip merge of select_k_onepass_indexed,
+// crates/mlrs-kernels/src/topk.rs:612-758, here over sorted lists).  Every
+// list entry's value lies within eps of its pair's exact value (exact-mode
+// entries equal it), and the segments hold disjoint index rows.  So with V
+// the k-th smallest value over all lists, k distinct pairs are exactly <=
+// V + eps, and a pair can be among the k best only if its value is
+// <= V + 2 eps: exactly those pairs are evaluated in the reference arm's
+// operation order and ranked by (exact value, index), NaN never admitted.
+template <int ARM, bool VEC4>
 __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
+    __shared__ uint32_t cand[4][128];
     const int lane = threadIdx.x & 63;
-    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wv = threadIdx.x >> 6;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + wv;
     if (qg >= a.nq) return;
     const int k = a.k;
+    const int K2 = gram_list_cap(k);
+    const int64_t d = a.d;
     const float inf = __builtin_huge_valf();
-    float lv = inf;
-    uint32_t li = kSentinelIdx;
-    if (lane < k) {
-        lv = a.part_val[qg * k + lane];
-        li = a.part_idx[qg * k + lane];
-    }
-    // the list slots of this query's block
     const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
     const int64_t nsl = sp.slots_of(qg / kQpb);
-    for (int64_t s = 1; s < nsl; ++s) {
+    // the k-th smallest value over the union of the lists
+    float uv = inf;
+    uint32_t ui = kSentinelIdx;
+    for (int64_t s = 0; s < nsl; ++s) {
         float v = inf;
         uint32_t ix = kSentinelIdx;
-        if (lane < k) {
-            const int64_t o = (s * a.nq + qg) * k + lane;
+        if (lane < K2) {
+            const int64_t o = (s * a.nq + qg) * K2 + lane;
             v = a.part_val[o];
             ix = a.part_idx[o];
         }
-        wave_merge64<float>(lv, li, v, ix, lane);
+        wave_merge64<float>(uv, ui, v, ix, lane);
     }
+    const float qsq = a.qsq[qg];
+    const float eps = (ARM == ARM_COS_FOLD)
+                          ? (float)a.eps_abs
+                          : (float)(a.eps_rel * ((double)qsq + (double)a.stats->xsq_max) + a.eps_abs);
+    double W = (double)bcast_f(uv, k - 1) + 2.0 * (double)eps;
+    W += __builtin_fabs(W) * 0x1p-40;
+    // exact evaluation of the window's pairs, compacted 64 at a time
+    float lv = inf;
+    uint32_t li = kSentinelIdx;
+    uint32_t nc = 0;
+    auto evaluate = [&](uint32_t count) {
+        float e = inf;
+        uint32_t t = kSentinelIdx;
+        if ((uint32_t)lane < count) {
+            t = cand[wv][lane];
+            e = exact_f32<ARM, VEC4>(a.q + qg * d, a.x + (int64_t)t * d, d, qsq,
+                                     (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f);
+            if (e != e) {
+                e = inf;
+                t = kSentinelIdx;
+            }
+        }
+        wave_sort64<float>(e, t, lane);
+        wave_merge64<float>(lv, li, e, t, lane);
+    };
+    for (int64_t s = 0; s < nsl; ++s) {
+        bool in = false;
+        uint32_t ix = kSentinelIdx;
+        if (lane < K2) {
+            const int64_t o = (s * a.nq + qg) * K2 + lane;
+            ix = a.part_idx[o];
+            in = (ix != kSentinelIdx) && !((double)a.part_val[o] > W);
+        }
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+        const uint32_t pre = (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull));
+        if (in) cand[wv][nc + pre] = ix;
+        nc += (uint32_t)__builtin_popcountll(bal);
+        if (nc >= 64) {
+            evaluate(64);
+            const uint32_t rest = nc - 64;
+            const uint32_t mv = ((uint32_t)lane < rest) ? cand[wv][64 + lane] : 0u;
+            if ((uint32_t)lane < rest) cand[wv][lane] = mv;
+            nc = rest;
+        }
+    }
+    if (nc > 0) evaluate(nc);
     if (lane < k) emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, k, qg, lane, lv, li, a.out_val, a.out_idx);
 }
 
@@ -702,12 +823,26 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_gram_f32_merge(const GramArgs32& a, hipStream_t s) {
-    if (a.k == 1)
-        hipLaunchKernelGGL(knn_merge1_f32_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(knn_merge_f32_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+template <int ARM, bool VEC4>
+hipError_t launch_merge(const GramArgs32& a, hipStream_t s) {
+    hipLaunchKernelGGL((knn_merge_f32_kernel<ARM, VEC4>), dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s) {
+    if (a.k == 1) {
+        hipLaunchKernelGGL(knn_merge1_f32_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    if (arm == ARM_EUCLID_FMA)
+        return vec4 ? launch_merge<ARM_EUCLID_FMA, true>(a, s) : launch_merge<ARM_EUCLID_FMA, false>(a, s);
+    if (arm == ARM_EUCLID_MULADD)
+        return vec4 ? launch_merge<ARM_EUCLID_MULADD, true>(a, s) : launch_merge<ARM_EUCLID_MULADD, false>(a, s);
+    if (arm == ARM_COS_FOLD)
+        return vec4 ? launch_merge<ARM_COS_FOLD, true>(a, s) : launch_merge<ARM_COS_FOLD, false>(a, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {

@@ -48,6 +48,7 @@ struct WaveLds64 {
     double qa[kQpw];   // exact arm's query operand (squared or reciprocal norm)
     double qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
     double eps[kQpw];  // screen error bound
+    uint32_t mode[kQpw];  // 0 = screen-value list, 1 = exact list
 };
 
 constexpr unsigned long long kInfBits64 = 0x7FF0000000000000ull;
@@ -140,6 +141,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     unsigned long long* __restrict__ SHARED_R = a.shared_r;
     const int64_t nq = a.nq, nt = a.nt, d = a.d;
     const int k = a.k;
+    const int K2 = gram_list_cap(k);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -147,6 +149,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     const int jl = lane & 15;  // query of the lane within the wave
     WaveLds64& L = wl[w];
     const double inf = __builtin_huge_val();
+    // screen values of this wave's queued pairs, [query][queue position]
+    double* __restrict__ QVw = a.qval + ((int64_t)blockIdx.x * kWaves + w) * (kQpw * kQcap);
 
     // ---- work split (StreamSplit), as in the f32 kernel ----
     const StreamSplit sp(nq, nt, kQpb, kBn, a.grid_wgs);
@@ -157,8 +161,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     sp.decode(u, panel, qblock, tile0, left);
     const int64_t tile1 = tile0 + ((left < u_hi - u) ? left : (u_hi - u));
     const int64_t slot = sp.slot(wg, panel, qblock);
-    double* __restrict__ LV = a.part_val + slot * nq * k;
-    uint32_t* __restrict__ LI = a.part_idx + slot * nq * k;
+    double* __restrict__ LV = a.part_val + slot * nq * K2;
+    uint32_t* __restrict__ LI = a.part_idx + slot * nq * K2;
 
     const int64_t qwave = qblock * kQpb + w * kQpw;
     const int64_t qmine = qwave + jl;
@@ -181,12 +185,18 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
             L.qa[lane] = (ARM == ARM_COS_HOST) ? (qvalid ? QINV[qmine] : 0.0) : qsq;
             L.eps[lane] = a.eps_abs;
         }
+        // Screen-value lists need |screen distance - exact| <= eps for every
+        // pair: norms well inside the double range (a nonzero query for
+        // cosine), and k > 1 (a one-entry list has no room for near ties).
+        bool sv = qvalid && k > 1 && (qsq + a.stats->xsq_max64 <= 0x1p1020) && (L.eps[lane] < inf);
+        if (COS) sv = sv && (L.qs[lane] > 0.0);
+        L.mode[lane] = sv ? 0u : 1u;
     }
     for (int j = 0; j < kQpw; ++j) {
         const int64_t qg = qwave + j;
-        if (qg < nq && lane < k) {
-            LV[qg * k + lane] = inf;
-            LI[qg * k + lane] = kSentinelIdx;
+        if (qg < nq && lane < K2) {
+            LV[qg * K2 + lane] = inf;
+            LI[qg * K2 + lane] = kSentinelIdx;
         }
     }
     if (SHARED_R && lane < kQpw && qvalid) {
@@ -245,31 +255,69 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
         }                                                                                    \
     } while (0)
 
+// Flush: one query's queue sorted and merged into its list.  Screen-value
+// mode: a queued pair enters with its screen value mapped back to a
+// distance, within eps of its exact value; the list keeps the K2 smallest and
+// the segment's bound is its k-th + eps.  A pair whose screen value is NaN,
+// and every pair of an exact-mode query, is evaluated exactly in the arm's
+// operation order.  When a discarded pair lies within 2 eps of the k-th, the
+// old list and the queue are re-evaluated exactly and the query's list stays
+// exact from then on.
+#define MLRS_EXACT64_AT(T_)                                                                  \
+    exact_f64<ARM, VEC2>(Q + qg_ * d, X + (int64_t)(T_) * d, d, L.qa[j_],                    \
+                         (ARM == ARM_COS_FOLD) ? XSQ[(T_)] : (ARM == ARM_COS_HOST) ? XINV[(T_)] : 0.0)
 #define MLRS_FLUSH64(J)                                                                      \
     do {                                                                                     \
         const int j_ = (J);                                                                  \
         const int64_t qg_ = qwave + j_;                                                      \
-        const uint32_t n_ = shfl_u(cntr, j_);                                                \
-        double lv_ = (lane < k) ? LV[qg_ * k + lane] : inf;                                  \
-        uint32_t li_ = (lane < k) ? LI[qg_ * k + lane] : kSentinelIdx;                       \
+        const uint32_t n_ = bcast_u(cntr, j_);                                                \
+        const bool exact_ = L.mode[j_] != 0u;                                                \
+        double lv_ = (lane < K2) ? LV[qg_ * K2 + lane] : inf;                                \
+        uint32_t li_ = (lane < K2) ? LI[qg_ * K2 + lane] : kSentinelIdx;                     \
         double e_ = inf;                                                                     \
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
             t_ = L.qidx[j_][lane];                                                           \
-            const double ya_ = (ARM == ARM_COS_FOLD) ? XSQ[t_] : (ARM == ARM_COS_HOST) ? XINV[t_] : 0.0; \
-            e_ = exact_f64<ARM, VEC2>(Q + qg_ * d, X + (int64_t)t_ * d, d, L.qa[j_], ya_);  \
+            const double s_ = exact_ ? 0.0 : QVw[j_ * kQcap + lane];                         \
+            if (exact_ || s_ != s_)                                                          \
+                e_ = MLRS_EXACT64_AT(t_);                                                    \
+            else                                                                             \
+                e_ = COS ? 1.0 + s_ / L.qs[j_] : s_ + L.qs[j_];                              \
             if (e_ != e_) {                                                                  \
                 e_ = inf;                                                                    \
                 t_ = kSentinelIdx;                                                           \
             }                                                                                \
         }                                                                                    \
         wave_sort64<double>(e_, t_, lane);                                                   \
-        wave_merge64<double>(lv_, li_, e_, t_, lane);                                        \
-        if (lane < k) {                                                                      \
-            LV[qg_ * k + lane] = lv_;                                                        \
-            LI[qg_ * k + lane] = li_;                                                        \
+        const uint32_t oi_ = li_;                                                            \
+        const double dm_ = wave_merge64_drop<double>(lv_, li_, e_, t_, lane);                \
+        double R_ = bcast_f(lv_, k - 1);                                                      \
+        if (!exact_) {                                                                       \
+            const double dr_ = (K2 < 64) ? bcast_f(lv_, K2) : dm_;                            \
+            double w_ = R_ + 2.0 * L.eps[j_];                                                \
+            w_ += __builtin_fabs(w_) * 0x1p-40;                                              \
+            if (dr_ < inf && dr_ <= w_) {                                                    \
+                double x1_ = inf, x2_ = inf;                                                 \
+                uint32_t i1_ = oi_, i2_ = t_;                                                \
+                if (i1_ != kSentinelIdx) x1_ = MLRS_EXACT64_AT(i1_);                         \
+                if (i2_ != kSentinelIdx) x2_ = MLRS_EXACT64_AT(i2_);                         \
+                if (x1_ != x1_) { x1_ = inf; i1_ = kSentinelIdx; }                           \
+                if (x2_ != x2_) { x2_ = inf; i2_ = kSentinelIdx; }                           \
+                wave_sort64<double>(x1_, i1_, lane);                                         \
+                wave_sort64<double>(x2_, i2_, lane);                                         \
+                wave_merge64<double>(x1_, i1_, x2_, i2_, lane);                              \
+                lv_ = x1_;                                                                   \
+                li_ = i1_;                                                                   \
+                R_ = bcast_f(lv_, k - 1);                                                     \
+                if (lane == 0) L.mode[j_] = 1u;                                              \
+            } else if (R_ < inf) {                                                           \
+                R_ = R_ + L.eps[j_];                                                         \
+            }                                                                                \
         }                                                                                    \
-        double R_ = shfl_f(lv_, k - 1);                                                      \
+        if (lane < K2) {                                                                     \
+            LV[qg_ * K2 + lane] = lv_;                                                       \
+            LI[qg_ * K2 + lane] = li_;                                                       \
+        }                                                                                    \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf && R_ >= 0.0) {                                         \
                 const unsigned long long old_ =                                              \
@@ -339,19 +387,29 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
         if (__builtin_amdgcn_ballot_w64(m != 0)) {
             // the query's four lanes (groups 0..3) append in group order
             const uint32_t c = (uint32_t)__builtin_popcount(m);
-            const uint32_t c0 = shfl_u(c, jl), c1 = shfl_u(c, jl + 16), c2 = shfl_u(c, jl + 32),
-                           c3 = shfl_u(c, jl + 48);
+            // the counts of the query's other three lanes: groups g^1, g^2, g^3
+            const uint32_t x1 = shfl_xor_u(c, 16), x2 = shfl_xor_u(c, 32), x3 = shfl_xor_u(x1, 32);
+            const uint32_t c0 = (g == 0) ? c : (g == 1) ? x1 : (g == 2) ? x2 : x3;
+            const uint32_t c1 = (g == 1) ? c : (g == 0) ? x1 : (g == 3) ? x2 : x3;
+            const uint32_t c2 = (g == 2) ? c : (g == 3) ? x1 : (g == 0) ? x2 : x3;
+            const uint32_t c3 = (g == 3) ? c : (g == 2) ? x1 : (g == 1) ? x2 : x3;
             uint32_t pos = cntr + (g > 0 ? c0 : 0u) + (g > 1 ? c1 : 0u) + (g > 2 ? c2 : 0u);
-            while (m) {
-                const int r = __builtin_ctz(m);
-                m &= m - 1;
-                L.qidx[jl][pos++] = (uint32_t)t0 + (uint32_t)(g + 4 * r);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (m & (1u << r)) {
+                    L.qidx[jl][pos] = (uint32_t)t0 + (uint32_t)(g + 4 * r);
+                    QVw[jl * kQcap + pos] = acc[r];
+                    ++pos;
+                }
             }
             cntr += c0 + c1 + c2 + c3;
         }
         uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > (uint32_t)kFlushAt);
         if (mask) {
             if (lane < kQpw) L.thr[lane] = fmin(L.thr[lane], thr);
+            // the queued screen values were stored by other lanes of this wave
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             while (mask) {
                 const int j = __builtin_ctzll(mask);
                 mask &= mask - 1;
@@ -369,6 +427,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     }
     {
         uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > 0u);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         while (mask) {
             const int j = __builtin_ctzll(mask);
             mask &= mask - 1;
@@ -376,6 +436,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
         }
     }
 #undef MLRS_FLUSH64
+#undef MLRS_EXACT64_AT
 #undef MLRS_STORE64
 #undef MLRS_PREFETCH64
     u += tile1 - tile0;
@@ -383,33 +444,84 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     }
 }
 
-// Merge the per-segment exact lists of one query per wave and emit the output
+// Merge the per-segment lists of one query per wave and emit the output
 // transform (boundary sqrt, identity, or the k-means pair with the centre-0
 // NaN rule of argmin_dist_rows, crates/mlrs-kernels/src/kmeans.rs:284-310).
+// Every list entry's value lies within eps of its pair's exact value (exact
+// entries equal it) and the segments hold disjoint index rows, so with V the
+// k-th smallest value over all lists a pair can be among the k best only if
+// its value is <= V + 2 eps: exactly those pairs are evaluated in the arm's
+// operation order and ranked by (exact value, index), NaN never admitted.
+template <int ARM, bool VEC2>
 __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
+    __shared__ uint32_t cand[4][128];
     const int lane = threadIdx.x & 63;
-    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wv = threadIdx.x >> 6;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + wv;
     if (qg >= a.nq) return;
     const int k = a.k;
+    const int K2 = gram_list_cap(k);
+    const int64_t d = a.d;
     const double inf = __builtin_huge_val();
-    double lv = inf;
-    uint32_t li = kSentinelIdx;
-    if (lane < k) {
-        lv = a.part_val[qg * k + lane];
-        li = a.part_idx[qg * k + lane];
-    }
     const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
     const int64_t nsl = sp.slots_of(qg / kQpb);
-    for (int64_t s = 1; s < nsl; ++s) {
+    double uv = inf;
+    uint32_t ui = kSentinelIdx;
+    for (int64_t s = 0; s < nsl; ++s) {
         double v = inf;
         uint32_t ix = kSentinelIdx;
-        if (lane < k) {
-            const int64_t o = (s * a.nq + qg) * k + lane;
+        if (lane < K2) {
+            const int64_t o = (s * a.nq + qg) * K2 + lane;
             v = a.part_val[o];
             ix = a.part_idx[o];
         }
-        wave_merge64<double>(lv, li, v, ix, lane);
+        wave_merge64<double>(uv, ui, v, ix, lane);
     }
+    const double qsq = a.qsq[qg];
+    const bool cos = (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST);
+    const double eps = cos ? a.eps_abs : a.eps_rel * (qsq + a.stats->xsq_max64) + a.eps_abs;
+    double W = bcast_f(uv, k - 1) + 2.0 * eps;
+    W += __builtin_fabs(W) * 0x1p-40;
+    const double qa = (ARM == ARM_COS_HOST) ? a.qinv[qg] : qsq;
+    double lv = inf;
+    uint32_t li = kSentinelIdx;
+    uint32_t nc = 0;
+    auto evaluate = [&](uint32_t count) {
+        double e = inf;
+        uint32_t t = kSentinelIdx;
+        if ((uint32_t)lane < count) {
+            t = cand[wv][lane];
+            const double ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : (ARM == ARM_COS_HOST) ? a.xinv[t] : 0.0;
+            e = exact_f64<ARM, VEC2>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
+            if (e != e) {
+                e = inf;
+                t = kSentinelIdx;
+            }
+        }
+        wave_sort64<double>(e, t, lane);
+        wave_merge64<double>(lv, li, e, t, lane);
+    };
+    for (int64_t s = 0; s < nsl; ++s) {
+        bool in = false;
+        uint32_t ix = kSentinelIdx;
+        if (lane < K2) {
+            const int64_t o = (s * a.nq + qg) * K2 + lane;
+            ix = a.part_idx[o];
+            in = (ix != kSentinelIdx) && !(a.part_val[o] > W);
+        }
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+        const uint32_t pre = (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull));
+        if (in) cand[wv][nc + pre] = ix;
+        nc += (uint32_t)__builtin_popcountll(bal);
+        if (nc >= 64) {
+            evaluate(64);
+            const uint32_t rest = nc - 64;
+            const uint32_t mv = ((uint32_t)lane < rest) ? cand[wv][64 + lane] : 0u;
+            if ((uint32_t)lane < rest) cand[wv][lane] = mv;
+            nc = rest;
+        }
+    }
+    if (nc > 0) evaluate(nc);
     if (lane < k) {
         const int64_t o = qg * k + lane;
         if (a.mode == EMIT_KMEANS) {
@@ -486,9 +598,24 @@ hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gram_f64_merge(const GramArgs64& a, hipStream_t s) {
-    hipLaunchKernelGGL(knn_merge_f64_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+template <int ARM>
+hipError_t launch_merge64(const GramArgs64& a, bool vec2, hipStream_t s) {
+    const dim3 grid((unsigned)((a.nq + 3) / 4));
+    if (vec2)
+        hipLaunchKernelGGL((knn_merge_f64_kernel<ARM, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((knn_merge_f64_kernel<ARM, false>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_gram_f64_merge(const GramArgs64& a, int arm, hipStream_t s) {
+    const bool vec2 = (a.d % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    if (arm == ARM_EUCLID_FMA) return launch_merge64<ARM_EUCLID_FMA>(a, vec2, s);
+    if (arm == ARM_EUCLID_MULADD) return launch_merge64<ARM_EUCLID_MULADD>(a, vec2, s);
+    if (arm == ARM_COS_FOLD) return launch_merge64<ARM_COS_FOLD>(a, vec2, s);
+    if (arm == ARM_COS_HOST) return launch_merge64<ARM_COS_HOST>(a, vec2, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace mlrs

@@ -91,12 +91,22 @@ struct GramArgs32 {
     double eps_abs;    // cosine screen bound (absolute)
     int64_t grid_wgs;  // the G0 the StreamSplit is built from (<= one resident round)
     int nslots;        // list slots per query (StreamSplit::nslots)
-    float* part_val;   // [nslots][nq][k] exact lists, one per (segment, query)
+    float* part_val;   // [nslots][nq][gram_list_cap(k)] lists, one per (segment, query)
     uint32_t* part_idx;
+    float* qval;       // [grid_wgs][4 waves][32 queries][64]: screen values of the queued pairs (k > 1)
     float* out_val;    // [nq][k]
     uint32_t* out_idx;
     unsigned int* shared_r;  // [nq] best known exact k-th value per query (float bits), or null
 };
+
+// Entries of one (segment, query) list of the Gram kernels: the k best plus
+// room for the pairs whose screen values lie within the error window of the
+// k-th (k = 1 keeps the single best pair, exactly).
+__host__ __device__ inline int gram_list_cap(int k) { return k == 1 ? 1 : (k + 32 < 64 ? k + 32 : 64); }
+
+// Screen values kept per workgroup while pairs wait in the queues (k > 1).
+inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64; }
+inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 32; }
 
 // G0, launched workgroups and per-query list slots of the Gram kernel's split.
 void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
@@ -106,7 +116,7 @@ void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nsl
 // output transform.
 hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s);
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
-hipError_t launch_gram_f32_merge(const GramArgs32& a, hipStream_t s);
+hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s);
 int gram_f32_max_k();
 int gram_f32_max_d();
 int gram_f32_queries_per_block();
@@ -130,8 +140,9 @@ struct GramArgs64 {
     double eps_abs;       // cosine screen bound (absolute)
     int64_t grid_wgs;
     int nslots;
-    double* part_val;     // [nslots][nq][k]
+    double* part_val;     // [nslots][nq][gram_list_cap(k)]
     uint32_t* part_idx;
+    double* qval;         // [grid_wgs][4 waves][16 queries][32]: screen values of the queued pairs (k > 1)
     double* out_val;      // [nq][k]
     uint32_t* out_idx;
     unsigned long long* shared_r;  // [nq] best known exact k-th value per query (double bits)
@@ -140,7 +151,7 @@ struct GramArgs64 {
 void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
 hipError_t launch_gram_f64_prep(const GramArgs64& a, hipStream_t s);
 hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s);
-hipError_t launch_gram_f64_merge(const GramArgs64& a, hipStream_t s);
+hipError_t launch_gram_f64_merge(const GramArgs64& a, int arm, hipStream_t s);
 int gram_f64_max_k();
 int gram_f64_max_d();
 

@@ -136,6 +136,36 @@ def test_nan_rows(d):
     check_knn(xq[:20], small, 8, "euclidean", "nan sentinel")
 
 
+@pytest.mark.parametrize("perturb", [0.0, 1e-4])
+def test_near_ties_across_segments(perturb):
+    """Copies of each query (exact, or perturbed far inside the screen's error
+    window) spread through a large index, so they fall in different segments
+    of the fused split: each segment's list and the final merge must resolve
+    them by exact value, then index."""
+    rng = np.random.default_rng(31)
+    d = 64
+    xt = rng.standard_normal((80000, d)).astype(np.float32)
+    xq = rng.standard_normal((12, d)).astype(np.float32)
+    for j in range(12):
+        rows = np.arange(40) * 1999 + 17 * j + 5
+        xt[rows] = xq[j] + perturb * rng.standard_normal((40, d)).astype(np.float32)
+    check_knn(xq, xt, 32, "euclidean", "near ties %g" % perturb)
+    check_knn(xq, xt, 32, "cosine", "near ties cosine %g" % perturb)
+
+
+def test_cosine_nan_rows():
+    """A NaN index row scores exactly 1 under the fold arm (its squared norm is
+    NaN, so the similarity falls back to 0): it competes as a real row."""
+    rng = np.random.default_rng(32)
+    xt = rng.standard_normal((3000, 40)).astype(np.float32)
+    xq = rng.standard_normal((64, 40)).astype(np.float32)
+    xt = np.abs(xt)
+    xt[[2, 1500, 2999]] = np.nan
+    xq[:32] = -np.abs(xq[:32])             # every real row is farther than 1 from these
+    gd, gi = check_knn(xq, xt, 16, "cosine", "cosine nan")
+    assert gi[0, :3].tolist() == [2, 1500, 2999] and np.all(gd[0, :3] == 1.0)
+
+
 def test_cosine_zero_rows():
     xq, xt = _data(9, 100, 1000, 40)
     xt[[0, 5, 999]] = 0.0
