@@ -14,7 +14,8 @@
 //    double-buffered and prefetched into registers one tile ahead.
 //  * Euclidean: the accumulator starts at ||x_t||^2, so after the contraction
 //    acc = ||x_t||^2 - 2 x_t.q_j, the expansion minus the per-query constant.
-//    Cosine: tile rows are pre-scaled by -1/||x_t||, acc = -x_t.q_j/||x_t||.
+//    Cosine: the contraction is scaled by -1/||x_t|| per row afterwards,
+//    acc = -x_t.q_j/||x_t||.
 //  * Screen: acc is compared against a per-query threshold derived from the
 //    best exact k-th value known for the query (its own list, or any strip's,
 //    shared through a per-query word in global memory) plus a rigorous bound
@@ -328,20 +329,16 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
                         (c0_ + e < d) ? src[e] : 0.0f;                                       \
                     v = make_float4(e4[0], e4[1], e4[2], e4[3]);                             \
                 }                                                                            \
-                if (COS) {                                                                   \
-                    const float s_ = XSCALE[t];                                              \
-                    v.x *= s_;                                                               \
-                    v.y *= s_;                                                               \
-                    v.z *= s_;                                                               \
-                    v.w *= s_;                                                               \
-                }                                                                            \
             }                                                                                \
             pf[p] = v;                                                                       \
             pf_src[p] += kBn * d;                                                            \
         }                                                                                    \
-        if (!COS && tid < kBn) {                                                             \
+        if (tid < kBn) {                                                                     \
             const uint32_t t = t0_ + (uint32_t)tid;                                          \
-            pfn = (t < t_end32) ? XSQ[t] : inf;                                              \
+            if (COS)                                                                         \
+                pfn = (t < t_end32) ? XSCALE[t] : 0.0f;                                      \
+            else                                                                             \
+                pfn = (t < t_end32) ? XSQ[t] : inf;                                          \
         }                                                                                    \
     } while (0)
 
@@ -477,7 +474,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
                 *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = pf[p];
             }
         }
-        if (!COS && tid < kBn) tnorm[buf][tid] = pfn;
+        if (tid < kBn) tnorm[buf][tid] = pfn;
         __syncthreads();
         if (t0 + kBn < t_end) MLRS_PREFETCH(t0 + kBn);
 
@@ -511,6 +508,19 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             av = an;
+        }
+        if (COS) {
+            // rows scaled by -1/||x_t|| after the contraction (the scales ride
+            // in tnorm), so the prefetched loads need no arithmetic before the
+            // next tile's LDS store
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float4 s4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                acc[4 * g4 + 0] *= s4.x;
+                acc[4 * g4 + 1] *= s4.y;
+                acc[4 * g4 + 2] *= s4.z;
+                acc[4 * g4 + 3] *= s4.w;
+            }
         }
 
         // ---- k = 1: tighten with this tile's smallest expansion value ----
@@ -637,7 +647,7 @@ __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t
         if (s < nsamp) {
             t = (uint32_t)((s * a.nt) / nsamp);
             const float ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f;
-            e = exact_f32<ARM, VEC4>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
+            e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
             if (e != e) {
                 e = inf;
                 t = kSentinelIdx;
@@ -699,7 +709,7 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
         uint32_t t = kSentinelIdx;
         if ((uint32_t)lane < count) {
             t = cand[wv][lane];
-            e = exact_f32<ARM, VEC4>(a.q + qg * d, a.x + (int64_t)t * d, d, qsq,
+            e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qsq,
                                      (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f);
             if (e != e) {
                 e = inf;

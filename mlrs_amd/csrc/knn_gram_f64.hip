@@ -63,10 +63,10 @@ __device__ __forceinline__ double screen_threshold64(double R, double qs, double
 }
 
 // Exact value of one (query, row) pair in the arm's operation order; loads
-// issued two 16-byte pairs at a time when rows are 16-byte aligned (the
-// d = 256 kernel holds 128 VGPRs of query operand, which leaves room for no
-// more in flight).
-template <int ARM, bool VEC2>
+// issued U 16-byte pairs at a time when rows are 16-byte aligned (inside the
+// Gram kernel U = 2: the d = 256 kernel holds 128 VGPRs of query operand;
+// the merge kernel has registers for more in flight).
+template <int ARM, bool VEC2, int U = 2>
 __device__ __forceinline__ double exact_f64(const double* __restrict__ q, const double* __restrict__ y,
                                             int64_t d, double qa, double ya) {
     if (!VEC2) return exact_pair<double, ARM>(q, y, d, qa, ya);
@@ -74,7 +74,6 @@ __device__ __forceinline__ double exact_f64(const double* __restrict__ q, const 
     const double2* y2 = reinterpret_cast<const double2*>(y);
     const int n2 = (int)(d >> 1);
     double acc = 0.0;
-    constexpr int U = 2;
     int c = 0;
     for (; c < n2; c += U) {
         double2 a[U], b[U];
@@ -240,18 +239,16 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
                     v.x = src[0];                                                            \
                     v.y = (2 * pc2 + 1 < d) ? src[1] : 0.0;                                  \
                 }                                                                            \
-                if (COS) {                                                                   \
-                    const double s_ = XSCALE[t];                                             \
-                    v.x *= s_;                                                               \
-                    v.y *= s_;                                                               \
-                }                                                                            \
             }                                                                                \
             pf[p] = v;                                                                       \
         }                                                                                    \
         pfp += kBn * d;                                                                      \
-        if (!COS && tid < kBn) {                                                             \
+        if (tid < kBn) {                                                                     \
             const uint32_t t = t0_ + (uint32_t)tid;                                          \
-            pfn = (t < t_end32) ? XSQ[t] : inf;                                              \
+            if (COS)                                                                         \
+                pfn = (t < t_end32) ? XSCALE[t] : 0.0;                                       \
+            else                                                                             \
+                pfn = (t < t_end32) ? XSQ[t] : inf;                                          \
         }                                                                                    \
     } while (0)
 
@@ -336,7 +333,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
             _Pragma("unroll") for (int p = 0; p < PF; ++p)                                   \
                 *reinterpret_cast<double2*>(dst_ + p * RPG * STRIDE) = pf[p];                \
         }                                                                                    \
-        if (!COS && tid < kBn) tnorm[(B)][tid] = pfn;                                        \
+        if (tid < kBn) tnorm[(B)][tid] = pfn;                                                \
     } while (0)
 
     // The next tile is loaded into registers before this tile's MFMAs and
@@ -371,6 +368,13 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
             acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av.y, qreg[2 * p + 1], acc, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             av = an;
+        }
+        if (COS) {
+            // rows scaled by -1/||x_t|| after the contraction (the scales ride
+            // in tnorm), so the prefetched loads need no arithmetic until the
+            // LDS store after the MFMAs
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] *= tnorm[buf][g + 4 * r];
         }
         if (more) MLRS_STORE64(buf ^ 1);
 
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
         if ((uint32_t)lane < count) {
             t = cand[wv][lane];
             const double ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : (ARM == ARM_COS_HOST) ? a.xinv[t] : 0.0;
-            e = exact_f64<ARM, VEC2>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
+            e = exact_f64<ARM, VEC2, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
             if (e != e) {
                 e = inf;
                 t = kSentinelIdx;
