@@ -351,8 +351,10 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     // per-(segment slot, query) lists: the kernel's top-k state, merged at the end
     size_t parts = (size_t)nslots * nq * gram_list_cap(k);
     size_t qvals = (k > 1) ? gram_f32_qval_elems(grid_wgs) : 0;
+    size_t summs = (k > 1) ? (size_t)nslots * nq : 0;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
-                   aligned_bytes(qvals * sizeof(float)) + aligned_bytes(sizeof(unsigned int) * nq);
+                   aligned_bytes(qvals * sizeof(float)) + aligned_bytes(summs * sizeof(float4)) +
+                   aligned_bytes(sizeof(unsigned int) * nq);
     rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
@@ -395,6 +397,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     a.part_val = cv.take<float>(parts);
     a.part_idx = cv.take<uint32_t>(parts);
     if (qvals) a.qval = cv.take<float>(qvals);
+    if (summs) a.summ = cv.take<float4>(summs);
     if (nslots > 1 || k > 1) a.shared_r = cv.take<unsigned int>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;

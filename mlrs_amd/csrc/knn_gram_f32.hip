@@ -51,7 +51,8 @@ constexpr int kBn = 32;                  // index rows per tile (MFMA M dimensio
 constexpr int kKcap = 64;                // largest k this kernel keeps
 constexpr int kQcap = 64;                // queued candidates per query
 constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
-constexpr int kShareEvery = 32;          // tiles between reads of the shared thresholds
+constexpr int kShareEvery = 64;          // tiles between reads of the shared thresholds
+constexpr int kSumSlots = 16;            // segment summaries read per refresh (k > 1)
 #ifndef MLRS_SEED_ROWS
 #define MLRS_SEED_ROWS 512
 #endif
@@ -233,6 +234,12 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     const int64_t slot = sp.slot(wg, panel, qblock);
     float* __restrict__ LV = a.part_val + slot * nq * K2;
     uint32_t* __restrict__ LI = a.part_idx + slot * nq * K2;
+    // Summaries of the query block's segment lists: segment s holds at least
+    // rank_i pairs whose exact value is <= summ[s][q].i (rank_i = ceil(i k/4));
+    // the union over segments (disjoint rows) bounds the query's k-th value.
+    float4* __restrict__ SUMM = a.summ;
+    const int64_t nsum = SUMM ? (sp.slots_of(qblock) < kSumSlots ? sp.slots_of(qblock) : kSumSlots) : 0;
+    const int rk1 = (k + 3) / 4, rk2 = (k + 1) / 2, rk3 = (3 * k + 3) / 4;
 
     const int64_t qwave = qblock * kQpb + w * kQpw;  // first query of this wave
     const int64_t qmine = qwave + jl;
@@ -407,6 +414,18 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         if (lane < K2) {                                                                     \
             LV[qg_ * K2 + lane] = key_value(lk_);                                            \
             LI[qg_ * K2 + lane] = key_index(lk_);                                            \
+        }                                                                                    \
+        if (SUMM) {                                                                          \
+            const bool sv_ = !exact_ && L.mode[j_] == 0u;                                    \
+            float p_[4] = {f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), rk1 - 1)),    \
+                           f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), rk2 - 1)),    \
+                           f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), rk3 - 1)),    \
+                           f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), k - 1))};     \
+            if (lane == 0) {                                                                 \
+                _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                             \
+                    if (sv_ && p_[i_] < inf) p_[i_] = round_up_f((double)p_[i_] + (double)L.eps[j_]); \
+                SUMM[slot * nq + qg_] = make_float4(p_[0], p_[1], p_[2], p_[3]);             \
+            }                                                                                \
         }                                                                                    \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf) {                                                      \
@@ -590,6 +609,55 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         if (SHARED_R && (++tiles % kShareEvery) == 0) {
             if (lane < kQpw && qvalid) {
                 float R = __uint_as_float(SHARED_R[qmine]);
+                if (nsum > 0) {
+                    // the smallest T with at least k pairs <= T over the
+                    // segment summaries: the four smallest (value, rank
+                    // increment) pairs, accumulated in order
+                    float b0 = inf, b1 = inf, b2 = inf, b3 = inf;
+                    int i0 = 0, i1 = 0, i2 = 0, i3 = 0;
+                    const int inc[4] = {rk1, rk2 - rk1, rk3 - rk2, k - rk3};
+                    for (int64_t s0 = 0; s0 < nsum; s0 += 4) {
+                        // four summaries in flight, then folded in
+                        float4 v4s[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            v4s[u] = (s0 + u < nsum) ? SUMM[(s0 + u) * nq + qmine] : make_float4(inf, inf, inf, inf);
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const float4 v4 = v4s[i >> 2];
+                            const float v = ((i & 3) == 0) ? v4.x : ((i & 3) == 1) ? v4.y : ((i & 3) == 2) ? v4.z : v4.w;
+                            const int n = inc[i & 3];
+                            const bool c0 = v < b0, c1 = v < b1, c2 = v < b2, c3 = v < b3;
+                            b3 = c2 ? b2 : (c3 ? v : b3);
+                            i3 = c2 ? i2 : (c3 ? n : i3);
+                            b2 = c1 ? b1 : (c2 ? v : b2);
+                            i2 = c1 ? i1 : (c2 ? n : i2);
+                            b1 = c0 ? b0 : (c1 ? v : b1);
+                            i1 = c0 ? i0 : (c1 ? n : i1);
+                            b0 = c0 ? v : b0;
+                            i0 = c0 ? n : i0;
+                        }
+                    }
+                    float T = inf;
+                    int got = i0;
+                    if (got >= k) {
+                        T = b0;
+                    } else {
+                        got += i1;
+                        if (got >= k) {
+                            T = b1;
+                        } else {
+                            got += i2;
+                            if (got >= k) {
+                                T = b2;
+                            } else {
+                                got += i3;
+                                if (got >= k) T = b3;
+                            }
+                        }
+                    }
+                    R = fminf(R, T);
+                }
                 L.thr[lane] = fminf(fminf(L.thr[lane], thr), screen_threshold<COS>(R, L.qs[lane], L.eps[lane]));
             }
             thr = L.thr[jl];
@@ -816,6 +884,13 @@ int gram_f32_rows_per_tile() { return kBn; }
 
 hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
     if (!a.shared_r) return hipSuccess;
+    if (a.summ) {
+        const int64_t n = (int64_t)a.nslots * a.nq * 4;
+        hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           reinterpret_cast<unsigned int*>(a.summ), n);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     if (a.k > 1 && kSeedRows > 0) {
         const int64_t nsamp = a.nt < kSeedRows ? a.nt : kSeedRows;
         const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&

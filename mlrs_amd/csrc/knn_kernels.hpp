@@ -94,6 +94,7 @@ struct GramArgs32 {
     float* part_val;   // [nslots][nq][gram_list_cap(k)] lists, one per (segment, query)
     uint32_t* part_idx;
     float* qval;       // [grid_wgs][4 waves][32 queries][64]: screen values of the queued pairs (k > 1)
+    float4* summ;      // [nslots][nq]: per-(segment, query) list summaries (k > 1), or null
     float* out_val;    // [nq][k]
     uint32_t* out_idx;
     unsigned int* shared_r;  // [nq] best known exact k-th value per query (float bits), or null
