@@ -152,8 +152,11 @@ def main():
     flops = 2.0 * d * evals
     kname = name.value.decode()
     f64 = cfg["dtype"] == "f64"
-    if radius is not None:
-        # the exact scan: a subtract, a multiply and an add per pair and
+    if radius is not None and kname.startswith("radius_gram"):
+        # the matrix-core screen: the Gram contraction, 2 d flops per pair
+        bound, peak, unit = "mfma", PEAKS["mfma_f32"], "TFLOP/s"
+    elif radius is not None:
+        # the exact host scan: a subtract, a multiply and an add per pair and
         # feature (no fused multiply-add: the reference's operation order)
         flops = 3.0 * d * evals
         bound, peak, unit = "valu", PEAKS["valu_f64" if f64 else "valu_f32"], "TFLOP/s"

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libmlrs_hip_knn.so")
 SOURCES = ["capi.hip", "knn_exact.hip", "knn_gram_f32.hip", "knn_gram_f64.hip", "knn_lowd.hip",
-           "knn_consumers.hip", "knn_radius.hip", "knn_graph.hip",
+           "knn_consumers.hip", "knn_radius.hip", "knn_radius_gram.hip", "knn_graph.hip",
            "kmeans_loop.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

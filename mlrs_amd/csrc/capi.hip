@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/mlrs_hip_knn.h"
@@ -933,6 +934,7 @@ struct RadiusPlan {
     void* stream = nullptr;
     int nstrips = 0;
     int64_t strip_len = 0;
+    bool gram = false;
     unsigned long long total = 0;
     char* base = nullptr;
     size_t cap = 0;
@@ -952,6 +954,7 @@ struct RadiusBufs {
     T* qinv;
     T* xsq;
     T* xinv;
+    NormStats* stats;
 };
 
 template <typename T>
@@ -970,6 +973,7 @@ static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int ns
     b->qinv = cv.take<T>((size_t)nq);
     b->xsq = cv.take<T>((size_t)std::max<int64_t>(1, nt));
     b->xinv = cv.take<T>((size_t)std::max<int64_t>(1, nt));
+    b->stats = cv.take<NormStats>(1);
     return cv.off + 256;
 }
 
@@ -1054,20 +1058,36 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         p_tr = p;
     }
 
-    // strips: enough waves to fill the chip several times over
+    // The matrix-core screen serves f32 Euclidean and cosine for 16 < d <=
+    // 128 when the search is large enough to fill the matrix cores (or when
+    // the fused family is forced); the host-scan kernel serves the rest.
+    const bool gram_ok = sizeof(T) == 4 && radius_gram_serves(arm, d);
+    const bool gram = gram_ok && (g_force_path == MLRS_PATH_FUSED ||
+                                  (g_force_path == MLRS_PATH_AUTO && d > 16 &&
+                                   (double)nq * (double)nt * (double)d >= 1073741824.0));
+
+    // strips: enough waves (host scan) or workgroups (matrix cores) to fill
+    // the chip several times over; strip lengths are multiples of 64 rows
     const int RQ = radius_queries_per_wave<T>();
     const int64_t G = (nq + RQ - 1) / RQ;
     const int64_t chunks = (nt + 63) / 64;
-    int64_t want_strips = ((int64_t)cus * 16 + G - 1) / G;
+    int64_t want_strips;
+    if (gram) {
+        const int64_t nqb = (nq + radius_gram_queries_per_block() - 1) / radius_gram_queries_per_block();
+        want_strips = ((int64_t)cus * 8 + nqb - 1) / std::max<int64_t>(1, nqb);
+    } else {
+        want_strips = ((int64_t)cus * 16 + G - 1) / G;
+    }
     want_strips = std::max<int64_t>(1, std::min<int64_t>(want_strips, std::max<int64_t>(1, chunks)));
-    const int64_t strip_len = std::max<int64_t>(64, ((chunks + want_strips - 1) / want_strips) * 64);
+    int64_t strip_len = std::max<int64_t>(64, ((chunks + want_strips - 1) / want_strips) * 64);
+    if (gram) strip_len = std::max<int64_t>(strip_len, ((nt + 65534) / 65535 + 63) / 64 * 64);  // grid.y limit
     const int nstrips = nt > 0 ? (int)((nt + strip_len - 1) / strip_len) : 0;
 
     RadiusPlan& P = g_rplan[dev];
     const int elem = (int)sizeof(T);
     const bool same = P.valid && P.xq == xq && P.xt == xt && P.nq == nq && P.nt == nt && P.d == d &&
                       P.metric == metric && P.p == p && P.radius == radius && P.elem == elem &&
-                      P.stream == stream && P.nstrips == nstrips && P.strip_len == strip_len;
+                      P.stream == stream && P.nstrips == nstrips && P.strip_len == strip_len && P.gram == gram;
     RadiusBufs<T> B;
     const size_t need = radius_carve<T>(nullptr, nq, nt, d, nstrips, &B);
     if (!same) {
@@ -1098,18 +1118,45 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     a.out_idx = out_idx;
     a.capacity = capacity;
     a.mismatch = B.mismatch;
+    a.q = xq;
+    a.qsq = B.qsq;
+    a.xsq = B.xsq;
+    a.stats = B.stats;
+    // the fused kNN screen's bounds (u = 2^-23): 8(d+4)u (||q||^2 + max ||x||^2)
+    // plus a subnormal floor (Euclidean), (8d+32)u (cosine)
+    const double u23 = std::ldexp(1.0, -23);
+    a.eps_rel = (arm == ARM_COS_HOST) ? 0.0 : 8.0 * (double)(d + 4) * u23;
+    a.eps_abs = (arm == ARM_COS_HOST) ? (8.0 * (double)d + 32.0) * u23 : (double)(d + 4) * std::ldexp(1.0, -120);
 
-    e = launch_radius_stage<T>(xq, nq, d, B.qT, s);
-    if (e == hipSuccess && arm == ARM_COS_HOST) {
-        // row_inv_norm_host (knn_host.rs:382-397)
+    e = gram ? hipSuccess : launch_radius_stage<T>(xq, nq, d, B.qT, s);
+    if (e == hipSuccess && (arm == ARM_COS_HOST || gram)) {
+        // row_inv_norm_host (knn_host.rs:382-397); the squared norms and the
+        // largest index norm feed the matrix-core screen
         e = launch_row_norms<T>(xq, nq, d, B.qsq, B.qinv, nullptr, nullptr, s);
-        if (e == hipSuccess && nt > 0) e = launch_row_norms<T>(xt, nt, d, B.xsq, B.xinv, nullptr, nullptr, s);
+        if (e == hipSuccess && nt > 0)
+            e = launch_row_norms<T>(xt, nt, d, B.xsq, B.xinv, nullptr, gram ? B.stats : nullptr, s);
     }
     if (e != hipSuccess) return hip_err(e, "radius staging");
+    auto scan = [&](bool fill_pass) -> hipError_t {
+        if constexpr (std::is_same<T, float>::value) {
+            if (gram) {
+                if (fill_pass) {
+                    KernelTimer kt(s, "radius_gram_fill");
+                    return launch_radius_gram(a, arm, true, s);
+                }
+                return launch_radius_gram(a, arm, false, s);
+            }
+        }
+        if (fill_pass) {
+            KernelTimer kt(s, "radius_scan_fill");
+            return launch_radius_scan<T>(a, arm, true, s);
+        }
+        return launch_radius_scan<T>(a, arm, false, s);
+    };
 
     auto count = [&]() -> int32_t {
         hipError_t e2 = launch_fill_u32(B.cnt, (int64_t)nstrips * nq, 0u, s);
-        if (e2 == hipSuccess) e2 = launch_radius_scan<T>(a, arm, false, s);
+        if (e2 == hipSuccess) e2 = scan(false);
         if (e2 == hipSuccess) e2 = launch_radius_offsets(B.cnt, nq, nstrips, B.row_cnt, B.block_sum, B.qoff, B.total, s);
         if (e2 != hipSuccess) return hip_err(e2, "radius count");
         int32_t r2 = read_u64(B.total, s, &P.total);
@@ -1127,14 +1174,12 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         P.stream = stream;
         P.nstrips = nstrips;
         P.strip_len = strip_len;
+        P.gram = gram;
         return MLRS_OK;
     };
     auto fill = [&](unsigned int* bad) -> int32_t {
         hipError_t e2 = launch_fill_u32(B.mismatch, 1, 0u, s);
-        if (e2 == hipSuccess) {
-            KernelTimer kt(s, "radius_scan_fill");
-            e2 = launch_radius_scan<T>(a, arm, true, s);
-        }
+        if (e2 == hipSuccess) e2 = scan(true);
         if (e2 != hipSuccess) return hip_err(e2, "radius fill");
         e2 = hipMemcpyAsync(bad, B.mismatch, sizeof(*bad), hipMemcpyDeviceToHost, s);
         if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);

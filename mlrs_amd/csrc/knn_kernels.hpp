@@ -255,7 +255,18 @@ struct RadiusArgs {
     int32_t* out_idx;
     int64_t capacity;                  // FILL: entries the outputs hold; no write at or past it
     unsigned int* mismatch;            // FILL: set when a strip's matches differ from its count
+    // the matrix-core screen (knn_radius_gram.hip)
+    const T* q;                        // [nq][d] query rows
+    const T* qsq;                      // [nq] query row_sumsq
+    const T* xsq;                      // [nt] index row_sumsq
+    const NormStats* stats;            // largest index squared norm
+    double eps_rel, eps_abs;           // screen error bound (as the fused kNN screen's)
 };
+// The matrix-core radius scan: f32, Euclidean and cosine, d <= 128.
+bool radius_gram_serves(int arm, int64_t d);
+int64_t radius_gram_rows_per_tile();
+int64_t radius_gram_queries_per_block();
+hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, bool fill, hipStream_t s);
 template <typename T>
 int radius_queries_per_wave();
 template <typename T>

@@ -110,6 +110,54 @@ def test_radius_nan_rows_and_coincident_points():
         _compare(xq, xt, float(np.inf), metric)
 
 
+@pytest.fixture
+def matrix_core_path():
+    """Route f32 Euclidean / cosine radius scans to the matrix-core screen
+    (knn_radius_gram.hip) whatever their size."""
+    prims.force_path("fused")
+    yield
+    prims.force_path("auto")
+
+
+@pytest.mark.parametrize("metric", ["euclidean", "cosine"])
+@pytest.mark.parametrize("shape", [(70, 3000, 8), (130, 2500, 65), (300, 5000, 128), (129, 4000, 33),
+                                   (5, 900, 6), (257, 20000, 100), (1, 40, 17)])
+def test_radius_matrix_core_screen(matrix_core_path, metric, shape):
+    nq, nt, d = shape
+    rng = np.random.default_rng(nq * 5 + d)
+    xt = rng.standard_normal((nt, d)).astype(np.float32)
+    xq = rng.standard_normal((nq, d)).astype(np.float32)
+    xt[17 % nt] = xt[3 % nt]
+    xq[0] = xt[3 % nt]
+    dist_all = oracle.pairwise(xq, xt, metric, sqrt=True)
+    for frac in (0.001, 0.02, 0.5):
+        _compare(xq, xt, _radius(dist_all, frac), metric)
+    _compare(xq, xt, 0.0, metric)
+    _compare(xq, xt, float(np.inf), metric)
+
+
+def test_radius_matrix_core_dense_matches_and_specials(matrix_core_path):
+    """Clustered rows (hundreds of matches per query, so queues flush many
+    times per strip), NaN and zero rows, duplicates of the queries, and a
+    query set whose norms overflow the screen (every pair evaluated)."""
+    rng = np.random.default_rng(21)
+    centres = rng.uniform(-4, 4, size=(6, 48)).astype(np.float32)
+    xt = (centres[rng.integers(0, 6, 30000)] + 0.5 * rng.standard_normal((30000, 48))).astype(np.float32)
+    xq = (centres[rng.integers(0, 6, 200)] + 0.5 * rng.standard_normal((200, 48))).astype(np.float32)
+    xt[[5, 70, 29999]] = np.nan
+    xt[[6, 71]] = 0.0
+    xt[1000:1040] = xq[3]
+    xq[9] = np.nan
+    xq[10] = 0.0
+    for metric in ("euclidean", "cosine"):
+        dist_all = oracle.pairwise(xq[:20], xt, metric, sqrt=True)
+        for frac in (0.05, 0.2):
+            wc = _compare(xq, xt, _radius(dist_all, frac), metric)
+            assert wc.max() > 500
+    big = xq * np.float32(1e19)
+    _compare(big, xt * np.float32(1e19), 1e20, "euclidean")
+
+
 def test_radius_empty_index_and_no_matches():
     xq = np.ones((10, 3), np.float32)
     d, i, c = prims.radius_neighbors(_t(xq), _t(np.zeros((0, 3), np.float32)), 1.0)
@@ -128,9 +176,18 @@ def _raw_call(xq, xt, radius, counts, out_d, out_i, cap):
     return rc, total.value
 
 
-def test_radius_capacity_and_changed_data_between_calls():
+@pytest.mark.parametrize("path", ["auto", "fused"])
+def test_radius_capacity_and_changed_data_between_calls(path):
     """A short buffer is refused with the needed size; a fill call after the
     data changed under the same pointers counts again and stays exact."""
+    prims.force_path(path)
+    try:
+        _capacity_and_changed_data()
+    finally:
+        prims.force_path("auto")
+
+
+def _capacity_and_changed_data():
     rng = np.random.default_rng(5)
     xt_np = rng.standard_normal((4000, 6)).astype(np.float32)
     xq_np = rng.standard_normal((50, 6)).astype(np.float32)
