@@ -372,7 +372,9 @@ int32_t mlrs_timing_read(double *total_ms, int64_t *launches, char *kernel_name,
  * cosine arm; f64: d <= 256, k <= 64; k-means: d <= 128 / 256); 2 = the
  * low-d ALU kernel wherever it serves the shape (f32 Euclidean, d <= 16,
  * k <= 32); 3 = the generic exact-tile path.  A family that does not serve
- * a shape falls back to the automatic choice.  Process-wide.
+ * a shape falls back to the automatic choice.  radius_neighbors: 1 = the
+ * matrix-core screen wherever it serves (f32 Euclidean / cosine, d <= 128),
+ * 3 = the host-scan kernel.  Process-wide.
  */
 #define MLRS_PATH_AUTO 0
 #define MLRS_PATH_FUSED 1
