@@ -287,20 +287,36 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         L.thr[lane] = fminf(L.thr[lane], screen_threshold<COS>(R0, L.qs[lane], L.eps[lane]));
     }
 
-    // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3] ----
+    // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3]; with
+    //      aligned rows one 16-byte load per group, all issued before use ----
     float4 qreg[NG];
     {
         const float scale = COS ? 1.0f : -2.0f;
         const float* qp = Q + qmine * d;
+        if (VEC4) {
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                int64_t c = 8 * g + 4 * h + e;
-                v[e] = (qvalid && c < d) ? qp[c] * scale : 0.0f;
+            for (int g = 0; g < NG; ++g) {
+                const int64_t c = 8 * g + 4 * h;
+                qreg[g] = (qvalid && c < d) ? *reinterpret_cast<const float4*>(qp + c) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            qreg[g] = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                qreg[g].x *= scale;
+                qreg[g].y *= scale;
+                qreg[g].z *= scale;
+                qreg[g].w *= scale;
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int64_t c = 8 * g + 4 * h + e;
+                    v[e] = (qvalid && c < d) ? qp[c] * scale : 0.0f;
+                }
+                qreg[g] = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
     }
 

@@ -208,10 +208,22 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     {
         const double scale = COS ? 1.0 : -2.0;
         const double* qp = Q + qmine * d;
+        if (VEC2) {  // 16-byte loads, all issued before use (NS and d even)
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int64_t c = (int64_t)g * NS + s;
-            qreg[s] = (qvalid && c < d) ? qp[c] * scale : 0.0;
+            for (int s = 0; s < NS; s += 2) {
+                const int64_t c = (int64_t)g * NS + s;
+                const double2 v = (qvalid && c < d) ? *reinterpret_cast<const double2*>(qp + c) : make_double2(0.0, 0.0);
+                qreg[s] = v.x;
+                qreg[s + 1] = v.y;
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s) qreg[s] *= scale;
+        } else {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int64_t c = (int64_t)g * NS + s;
+                qreg[s] = (qvalid && c < d) ? qp[c] * scale : 0.0;
+            }
         }
     }
 

@@ -153,15 +153,30 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
     {
         const float scale = COS ? 1.0f : -2.0f;
         const float* qp = Q + qmine * d;
+        if (VEC4) {  // one 16-byte load per group, all issued before use
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int64_t c = 8 * g + 4 * h + e;
-                v[e] = (qvalid && c < d) ? qp[c] * scale : 0.0f;
+            for (int g = 0; g < NG; ++g) {
+                const int64_t c = 8 * g + 4 * h;
+                qreg[g] = (qvalid && c < d) ? *reinterpret_cast<const float4*>(qp + c) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            qreg[g] = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                qreg[g].x *= scale;
+                qreg[g].y *= scale;
+                qreg[g].z *= scale;
+                qreg[g].w *= scale;
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t c = 8 * g + 4 * h + e;
+                    v[e] = (qvalid && c < d) ? qp[c] * scale : 0.0f;
+                }
+                qreg[g] = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
     }
 
