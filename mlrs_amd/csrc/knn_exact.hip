@@ -443,6 +443,107 @@ __global__ void argmin_rows_kernel(const T* __restrict__ dist, int64_t rows, int
     best_out[r] = best;
 }
 
+// k <= 64: one wave per row, two streaming passes.  Pass 1: each lane keeps
+// the smallest (value, column) pair of its strided share of the row; the
+// k-th smallest of those 64 pairs is a bound B on the row's k-th pair (k
+// distinct pairs are <= B).  Pass 2 re-reads the row (L2-resident) and
+// compacts the pairs <= B into LDS (ballot + popcount, columns ascending),
+// sorting and merging them into the row's list 64 at a time -- typically
+// once.  NaN is never admitted; +inf is a value like any other; -0 is
+// emitted as +0 (as the radix kernel's key map does).  The same
+// (value, index) top-k as select_rows_kernel.
+template <typename T>
+__global__ __launch_bounds__(256) void select_small_kernel(const T* __restrict__ dist, int64_t rows, int64_t cols,
+                                                           int64_t ld, int k, int mode, T* __restrict__ out_val,
+                                                           uint32_t* __restrict__ out_idx) {
+    constexpr int U = 8;
+    __shared__ T cv[4][128];
+    __shared__ uint32_t ci[4][128];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+    if (row >= rows) return;
+    const T* __restrict__ dr = dist + row * ld;
+    const T inf = FloatTraits<T>::inf();
+    const uint64_t below = (1ull << lane) - 1ull;
+
+    // pass 1: per-lane smallest pair
+    T mv = inf;
+    uint32_t mi = kSentinelIdx;
+    for (int64_t base = 0; base < cols; base += 64 * U) {
+        T vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = base + 64 * u + lane;
+            vv[u] = (c < cols) ? dr[c] : inf;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = base + 64 * u + lane;
+            const bool take = (c < cols) && pair_less<T>(vv[u], (uint32_t)c, mv, mi);
+            mv = take ? vv[u] : mv;
+            mi = take ? (uint32_t)c : mi;
+        }
+    }
+    wave_sort64<T>(mv, mi, lane);
+    const T bv = bcast_f(mv, k - 1);
+    const uint32_t bi = bcast_u(mi, k - 1);
+
+    // pass 2: the pairs <= (bv, bi), compacted and merged 64 at a time
+    T lv = inf;
+    uint32_t li = kSentinelIdx;
+    uint32_t nc = 0;
+    auto merge_batch = [&](uint32_t count) {
+        T e = ((uint32_t)lane < count) ? cv[wv][lane] : inf;
+        uint32_t t = ((uint32_t)lane < count) ? ci[wv][lane] : kSentinelIdx;
+        wave_sort64<T>(e, t, lane);
+        wave_merge64<T>(lv, li, e, t, lane);
+    };
+    for (int64_t base = 0; base < cols; base += 64 * U) {
+        T vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = base + 64 * u + lane;
+            vv[u] = (c < cols) ? dr[c] : inf;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = base + 64 * u + lane;
+            const T v = vv[u];
+            const bool in = (c < cols) && !pair_less<T>(bv, bi, v, (uint32_t)c) && (v == v);
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+            if (bal) {
+                const uint32_t pos = nc + (uint32_t)__builtin_popcountll(bal & below);
+                if (in) {
+                    cv[wv][pos] = v;
+                    ci[wv][pos] = (uint32_t)c;
+                }
+                nc += (uint32_t)__builtin_popcountll(bal);
+                if (nc >= 64) {
+                    merge_batch(64);
+                    const uint32_t rest = nc - 64;
+                    const T mvv = ((uint32_t)lane < rest) ? cv[wv][64 + lane] : inf;
+                    const uint32_t mii = ((uint32_t)lane < rest) ? ci[wv][64 + lane] : 0u;
+                    if ((uint32_t)lane < rest) {
+                        cv[wv][lane] = mvv;
+                        ci[wv][lane] = mii;
+                    }
+                    nc = rest;
+                }
+            }
+        }
+    }
+    if (nc > 0) merge_batch(nc);
+    if (lane < k) {
+        T v = lv + T(0);  // -0 -> +0
+        const uint32_t ix = (li == kSentinelIdx) ? 0u : li;
+        if (li == kSentinelIdx) v = inf;
+        if (mode == EMIT_SQRT) v = FloatTraits<T>::sqrt_(v);
+        out_val[row * k + lane] = v;
+        out_idx[row * k + lane] = ix;
+    }
+}
+
 }  // namespace
 
 template <typename T>
@@ -526,6 +627,11 @@ hipError_t launch_select_rows(const T* dist, int64_t rows, int64_t cols, int64_t
                               T* out_val, uint32_t* out_idx, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     if (k < 1 || k > SEL_MAXK) return hipErrorInvalidValue;
+    if (k <= 64) {
+        hipLaunchKernelGGL((select_small_kernel<T>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, dist, rows,
+                           cols, ld, k, mode, out_val, out_idx);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL((select_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, s, dist, rows, cols,
                        ld, k, mode, out_val, out_idx);
     return hipGetLastError();
