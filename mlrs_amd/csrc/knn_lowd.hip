@@ -113,17 +113,26 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
                     row[rr][4 * c4 + 2] = v.z;
                     row[rr][4 * c4 + 3] = v.w;
                 }
-            // screen: acc = ||x||^2 - 2 x.q; NaN passes (!(acc > thr)).
+            // screen: acc = ||x||^2 - 2 x.q, the group's smallest against the
+            // threshold (one min per pair instead of a compare).  fminf drops
+            // a NaN value unless the whole group is NaN (which then passes);
+            // a NaN screen value means a NaN or infinite input, whose exact
+            // value is NaN (never admitted) or +inf (admitted only while the
+            // list is not full, when thr is +inf and every finite value
+            // passes too), so dropping it here never loses a pair.
             bool any = false;
 #pragma unroll
-            for (int i = 0; i < QL; ++i)
+            for (int i = 0; i < QL; ++i) {
+                float mn = __builtin_huge_valf();
 #pragma unroll
                 for (int rr = 0; rr < RU; ++rr) {
                     float s_ = row[rr][D];
 #pragma unroll
                     for (int c = 0; c < D; ++c) s_ = __builtin_fmaf(qm2[i][c], row[rr][c], s_);
-                    any |= !(s_ > thr[i]);
+                    mn = (rr == 0) ? s_ : __builtin_fminf(mn, s_);
                 }
+                any |= !(mn > thr[i]);
+            }
             if (!any) continue;
             // exact rescoring of the passing pairs (rare after the lists fill):
             // the screen is redone from the row registers into a bit mask,
