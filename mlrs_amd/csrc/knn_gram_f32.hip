@@ -248,10 +248,29 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     int64_t t_end = tile1 * kBn;
     if (t_end > nt) t_end = nt;
 
+    // ---- segment start: the loads first, from clamped rows so that they are
+    //      unconditional and all in flight together (a segment of k-means
+    //      assignment lasts only 32 tiles), then the per-query state.  Wide
+    //      rows (NG > 8) load the operand later: early it would spill. ----
+    constexpr bool kEarlyQ = NG <= 8;
+    const int64_t qrow = qvalid ? qmine : nq - 1;
+    const float qsq_l = QSQ[qrow];
+    const float r0_l = SHARED_R ? __uint_as_float(SHARED_R[qrow]) : inf;
+    float4 qreg[NG];
+    if (VEC4 && kEarlyQ) {
+        const float* qp = Q + qrow * d;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int64_t c = 8 * g + 4 * h;
+            const float4 v = *reinterpret_cast<const float4*>(qp + (c < d ? c : d - 4));
+            qreg[g] = (qvalid && c < d) ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+
     // ---- per-query constants, lists, queues ----
     uint32_t cntr = 0u;  // queued candidates of query jl
     if (lane < kQpw) {
-        float qsq = qvalid ? QSQ[qmine] : 0.0f;
+        const float qsq = qvalid ? qsq_l : 0.0f;
         L.thr[lane] = qvalid ? inf : -inf;
         if (!COS) {
             L.qs[lane] = qsq;
@@ -282,22 +301,22 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         }
     }
     // Strips that start late begin from the bound earlier strips have reached.
-    if (SHARED_R && lane < kQpw && qvalid) {
-        const float R0 = __uint_as_float(SHARED_R[qmine]);
-        L.thr[lane] = fminf(L.thr[lane], screen_threshold<COS>(R0, L.qs[lane], L.eps[lane]));
-    }
+    if (SHARED_R && lane < kQpw && qvalid)
+        L.thr[lane] = fminf(L.thr[lane], screen_threshold<COS>(r0_l, L.qs[lane], L.eps[lane]));
 
-    // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3]; with
-    //      aligned rows one 16-byte load per group, all issued before use ----
-    float4 qreg[NG];
+    // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3] (aligned rows:
+    //      loaded above, one 16-byte load per group) ----
     {
         const float scale = COS ? 1.0f : -2.0f;
         const float* qp = Q + qmine * d;
         if (VEC4) {
+            if (!kEarlyQ) {
 #pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                const int64_t c = 8 * g + 4 * h;
-                qreg[g] = (qvalid && c < d) ? *reinterpret_cast<const float4*>(qp + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int g = 0; g < NG; ++g) {
+                    const int64_t c = 8 * g + 4 * h;
+                    qreg[g] = (qvalid && c < d) ? *reinterpret_cast<const float4*>(qp + c)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
             }
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
