@@ -127,20 +127,29 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
     if (t_end > nt) t_end = nt;
     const uint32_t t_end32 = (uint32_t)t_end;
 
-    // ---- per-query screen threshold, counters, output bases ----
-    float thr = -inf;
+    // ---- per-query screen thresholds, counters, output bases.  thr: a pair
+    //      whose exact value can be <= th passes it.  thr_lo (count pass): a
+    //      pair at or below it is a match for certain (exact <= screen + eps
+    //      <= th) and is counted without evaluation; only the pairs between
+    //      the two are evaluated. ----
+    float thr = -inf, thr_lo = -inf;
     if (qvalid) {
         const float qsq = a.qsq[qmine];
         const bool bounded = (double)qsq + (double)a.stats->xsq_max <= 0x1p124;  // false for NaN / inf too
+        double lo = -__builtin_huge_val();
         if (!bounded) {
             thr = inf;
         } else if (!COS) {
             const double eps = a.eps_rel * ((double)qsq + (double)a.stats->xsq_max) + a.eps_abs;
             thr = round_up_f((double)a.th - (double)qsq + eps);
+            lo = (double)a.th - (double)qsq - eps;
         } else {
             thr = round_up_f((double)a.th + a.eps_abs);
+            lo = (double)a.th - a.eps_abs;
         }
+        if (!FILL && lo > -__builtin_huge_val()) thr_lo = -round_up_f(-(lo - __builtin_fabs(lo) * 0x1p-40));
     }
+    uint32_t sure = 0u;  // count pass: this lane's certain matches
     if (lane < kQpw) {
         L.rel[lane] = 0u;
         L.qa[lane] = (COS && qvalid) ? a.qinv[qmine] : 0.0f;
@@ -320,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
         }
 
         // ---- screen: lane (jl, h) holds rows 8*(r/4) + 4h + (r%4) of the tile ----
-        uint32_t m = 0;
+        uint32_t m = 0, dm = 0;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
             float sc[4] = {1.f, 1.f, 1.f, 1.f};
@@ -336,6 +345,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
                 const int r = 4 * g4 + e;
                 const float wv = COS ? 1.0f - (acc[r] * sc[e]) * qa_mine : acc[r];
                 m |= (uint32_t)!(wv > thr) << r;
+                if (!FILL) dm |= (uint32_t)(wv <= thr_lo) << r;
             }
         }
         if (!qvalid) m = 0;
@@ -343,6 +353,11 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if ((uint32_t)t0 + (uint32_t)(8 * (r >> 2) + 4 * h + (r & 3)) >= t_end32) m &= ~(1u << r);
+        }
+        if (!FILL) {
+            dm &= m;
+            sure += (uint32_t)__builtin_popcount(dm);
+            m &= ~dm;
         }
         if (__builtin_amdgcn_ballot_w64(m != 0)) {
             // row-ordered 32-bit mask of the query's passing tile rows
@@ -365,8 +380,9 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
 #undef MLRS_RG_PREFETCH
 
     // ---- per (strip, query): the count, or the end check of the fill ----
+    if (!FILL) sure += shfl_xor_u(sure, 32);  // the query's two lanes
     if (lane < kQpw && qvalid) {
-        const uint32_t mine = L.rel[lane];
+        const uint32_t mine = L.rel[lane] + sure;
         if (!FILL) {
             a.cnt[s * nq + qmine] = mine;
         } else {
