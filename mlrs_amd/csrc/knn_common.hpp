@@ -354,4 +354,27 @@ __device__ __forceinline__ void wave_merge64_key(unsigned long long& lv, unsigne
     for (int m = 32; m > 0; m >>= 1) bitonic_step_key(lv, lane, m, true);
 }
 
+// Element r of a 16-float accumulator for a lane-varying r: a v_bfi_b32
+// select tree on the bits of r (15 bitfield selects).  Written in asm: as
+// C++ selects the compiler rebuilds a dynamic extract and expands it into a
+// compare chain per element.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ float pick16(const f32x16_t& a, int r) {
+    const uint32_t s0 = 0u - ((uint32_t)r & 1u), s1 = 0u - (((uint32_t)r >> 1) & 1u),
+                   s2 = 0u - (((uint32_t)r >> 2) & 1u), s3 = 0u - (((uint32_t)r >> 3) & 1u);
+    uint32_t l1[8], l2[4], l3[2], v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l1[i]) : "v"(s0), "v"(__float_as_uint(a[2 * i + 1])),
+            "v"(__float_as_uint(a[2 * i])));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l2[i]) : "v"(s1), "v"(l1[2 * i + 1]), "v"(l1[2 * i]));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l3[i]) : "v"(s2), "v"(l2[2 * i + 1]), "v"(l2[2 * i]));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(v) : "v"(s3), "v"(l3[1]), "v"(l3[0]));
+    return __uint_as_float(v);
+}
+
 }  // namespace mlrs

@@ -611,13 +611,13 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
                     L.qidx[jl][pos++] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
                 }
             } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (m & (1u << r)) {
-                        L.qidx[jl][pos] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
-                        QVw[pos * kQpw + jl] = acc[r];
-                        ++pos;
-                    }
+                // one iteration per admitted row of the lane (usually one)
+                while (m) {
+                    const int r = __builtin_ctz(m);
+                    m &= m - 1;
+                    L.qidx[jl][pos] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
+                    QVw[pos * kQpw + jl] = pick16(acc, r);
+                    ++pos;
                 }
             }
             cntr += c + co;
