@@ -354,6 +354,16 @@ __device__ __forceinline__ void wave_merge64_key(unsigned long long& lv, unsigne
     for (int m = 32; m > 0; m >>= 1) bitonic_step_key(lv, lane, m, true);
 }
 
+// A 16-byte load through the global address space.  A pointer the compiler
+// cannot prove global (one walked in a register array) is otherwise loaded
+// with a flat instruction, which also counts against the LDS wait counter:
+// every later wait for an LDS read would then wait for this load as well.
+__device__ __forceinline__ float4 gload4(const float* p) {
+    typedef float f4v_t __attribute__((ext_vector_type(4)));
+    const f4v_t v = *(const __attribute__((address_space(1))) f4v_t*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // Element r of a 16-float accumulator for a lane-varying r: a v_bfi_b32
 // select tree on the bits of r (15 bitfield selects).  Written in asm: as
 // C++ selects the compiler rebuilds a dynamic extract and expands it into a

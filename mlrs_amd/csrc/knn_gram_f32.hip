@@ -354,16 +354,24 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
         pf_on[p] = (f < TILE_F4) && (VEC4 ? (4 * c4 < d) : (4 * c4 < d));
         pf_src[p] = X + (t_begin + pf_r[p]) * d + 4 * c4;
     }
+    // Whole tiles of rows without padded columns load unconditionally.
+    const bool pf_fast = VEC4 && (PF * 256 == TILE_F4) && (d == DP);
 #define MLRS_PREFETCH(T0)                                                                    \
     do {                                                                                     \
         const uint32_t t0_ = (uint32_t)(T0);                                                 \
+        if (pf_fast && t0_ + (uint32_t)kBn <= t_end32) {                                     \
+            _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                 \
+                pf[p] = gload4(pf_src[p]);                                                   \
+                pf_src[p] += kBn * d;                                                        \
+            }                                                                                \
+        } else {                                                                             \
         _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);                                      \
             const uint32_t t = t0_ + (uint32_t)pf_r[p];                                      \
             if (pf_on[p] && t < t_end32) {                                                   \
                 const float* src = pf_src[p];                                                \
                 if (VEC4) {                                                                  \
-                    v = *reinterpret_cast<const float4*>(src);                               \
+                    v = gload4(src);                                                         \
                 } else {                                                                     \
                     const int c0_ = (int)((tid + 256 * p) % (DP / 4)) * 4;                   \
                     float e4[4];                                                             \
@@ -374,6 +382,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
             }                                                                                \
             pf[p] = v;                                                                       \
             pf_src[p] += kBn * d;                                                            \
+        }                                                                                    \
         }                                                                                    \
         if (tid < kBn) {                                                                     \
             const uint32_t t = t0_ + (uint32_t)tid;                                          \

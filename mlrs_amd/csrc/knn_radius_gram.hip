@@ -203,16 +203,24 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
     }
     float4 pf[PF];
     float pfn = 0.0f;
+    // Whole tiles of rows without padded columns load unconditionally.
+    const bool pf_fast = VEC4 && (PF * 256 == TILE_F4) && (d == DP);
 #define MLRS_RG_PREFETCH(T0)                                                                 \
     do {                                                                                     \
         const uint32_t t0_ = (uint32_t)(T0);                                                 \
+        if (pf_fast && t0_ + (uint32_t)kBn <= t_end32) {                                     \
+            _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                 \
+                pf[p] = gload4(pf_src[p]);                                                   \
+                pf_src[p] += kBn * d;                                                        \
+            }                                                                                \
+        } else {                                                                             \
         _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);                                      \
             const uint32_t t = t0_ + (uint32_t)pf_r[p];                                      \
             if (pf_on[p] && t < t_end32) {                                                   \
                 const float* src = pf_src[p];                                                \
                 if (VEC4) {                                                                  \
-                    v = *reinterpret_cast<const float4*>(src);                               \
+                    v = gload4(src);                                                         \
                 } else {                                                                     \
                     const int c0_ = (int)((tid + 256 * p) % (DP / 4)) * 4;                   \
                     float e4[4];                                                             \
@@ -223,6 +231,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
             }                                                                                \
             pf[p] = v;                                                                       \
             pf_src[p] += kBn * d;                                                            \
+        }                                                                                    \
         }                                                                                    \
         if (tid < kBn) {                                                                     \
             const uint32_t t = t0_ + (uint32_t)tid;                                          \
