@@ -50,7 +50,7 @@ constexpr int kQpb = kWaves * kQpw;      // queries per workgroup
 constexpr int kBn = 32;                  // index rows per tile (MFMA M dimension)
 constexpr int kKcap = 64;                // largest k this kernel keeps
 constexpr int kQcap = 64;                // queued candidates per query
-constexpr int kFlushAt = kQcap - kBn;    // flush when a queue may overflow next tile
+constexpr int kQcapK1 = 48;              // k = 1: the screen tightens every tile, queues stay short
 constexpr int kShareEvery = 64;          // tiles between reads of the shared thresholds
 constexpr int kSumSlots = 16;            // segment summaries read per refresh (k > 1)
 #ifndef MLRS_SEED_ROWS
@@ -60,8 +60,9 @@ constexpr int64_t kSeedRows = MLRS_SEED_ROWS;  // index rows sampled for the ini
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+template <int QCAP>
 struct WaveLds {
-    uint32_t qidx[kQpw][kQcap];
+    uint32_t qidx[kQpw][QCAP];
     float thr[kQpw];
     float qa[kQpw];   // exact arm's query operand (row_sumsq for the fold arm)
     float qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
@@ -189,8 +190,15 @@ __device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q,
     out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
 }
 
+// k = 1 with d <= 64 fits three workgroups per CU (168 VGPRs, ~46 KB LDS):
+// the short segments of an assignment (one per query block) overlap better.
+template <int NG, bool K1>
+struct GramOcc {
+    static constexpr int wgs = (K1 && NG <= 8) ? 3 : 2;
+};
+
 template <int NG, int ARM, bool COS, bool VEC4, bool K1>
-__global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
+__global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kernel(GramArgs32 a) {
     constexpr int DP = NG * 8;        // padded feature count
     constexpr int STRIDE = DP + 4;    // LDS row stride (floats)
     constexpr int TILE_F4 = kBn * DP / 4;
@@ -198,7 +206,9 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
 
     __shared__ __attribute__((aligned(16))) float tile[2][kBn][STRIDE];
     __shared__ __attribute__((aligned(16))) float tnorm[2][kBn];
-    __shared__ WaveLds wl[kWaves];
+    constexpr int QCAP = K1 ? kQcapK1 : kQcap;
+    constexpr int kFlushAt = QCAP - kBn;  // flush when a queue may overflow next tile
+    __shared__ WaveLds<QCAP> wl[kWaves];
 
     // Kernel arguments as locals: they stay in SGPRs.
     const float* __restrict__ Q = a.q;
@@ -215,7 +225,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f32_kernel(GramArgs32 a) {
     const int w = tid >> 6;
     const int h = lane >> 5;
     const int jl = lane & 31;
-    WaveLds& L = wl[w];
+    WaveLds<QCAP>& L = wl[w];
     const float inf = __builtin_huge_valf();
     // screen values of this wave's queued pairs, [queue position][query]
     float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * (kQpw * kQcap);
@@ -911,10 +921,12 @@ hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
 
 }  // namespace
 
-void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots) {
+void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots) {
     const StreamSplit full(nq, nt, kQpb, kBn, 1);
-    // one resident round (two workgroups per CU), but at least 16 tiles each
-    int64_t g0 = 2 * (int64_t)(cus > 0 ? cus : 1);
+    // one resident round (two workgroups per CU, three for k = 1 at d <= 64:
+    // GramOcc), but at least 16 tiles each
+    const int per_cu = (k == 1 && d <= 64) ? 3 : 2;
+    int64_t g0 = per_cu * (int64_t)(cus > 0 ? cus : 1);
     if (g0 > full.T / 16) g0 = full.T / 16;
     if (g0 < 1) g0 = 1;
     *grid_wgs = g0;

@@ -110,7 +110,7 @@ inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 32; }
 
 // G0, launched workgroups and per-query list slots of the Gram kernel's split.
-void gram_f32_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
+void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots);
 
 // Three launches per search: prep (the shared per-query bound: seeded from a
 // row sample for k > 1, else reset), the Gram kernel, the strip merge +
