@@ -269,6 +269,38 @@ def test_kmeans_ties_and_nan(d):
     assert lab[30].item() == 0 and np.isnan(sq[30].item())
 
 
+@pytest.mark.parametrize("d", [8, 33, 64, 100])
+def test_kmeans_queue_overflow_ties(d):
+    """500 identical centres: every row of a tile passes the k = 1 screen, so
+    the candidate queues overflow and flush inside the tile loop many times;
+    the lowest index still wins and the squared distances are the oracle's."""
+    rng = np.random.default_rng(21 + d)
+    c = rng.standard_normal((700, d)).astype(np.float32)
+    c[100:600] = c[3]
+    x = rng.standard_normal((3000, d)).astype(np.float32)
+    x[::3] = c[3]
+    x[1::3] = c[3] + np.float32(1e-3) * rng.standard_normal((1000, d)).astype(np.float32)
+    lab, sq = prims.kmeans_assign(_t(x), _t(c))
+    torch.cuda.synchronize()
+    wl, ws = oracle.kmeans_assign(x, c)
+    assert np.array_equal(lab.cpu().numpy(), wl.astype(np.int64))
+    assert np.array_equal(sq.cpu().numpy(), ws)
+    assert lab[0].item() == 3 and sq[0].item() == 0.0
+
+
+@pytest.mark.parametrize("d", [24, 64])
+def test_k1_search_all_duplicates(d):
+    """k = 1 search over an index of mostly identical rows (every query's queue
+    overflows on every tile): the lowest index of the tied rows wins."""
+    rng = np.random.default_rng(40 + d)
+    xt = rng.standard_normal((5000, d)).astype(np.float32)
+    xt[1000:4500] = xt[999]
+    xq = np.concatenate([xt[999:1000], xt[2000:2001] + np.float32(1e-4),
+                         rng.standard_normal((200, d)).astype(np.float32)])
+    gd, gi = check_knn(xq, xt, 1, "euclidean", "k1 dups d=%d" % d)
+    assert gi[0, 0] == 999 and gd[0, 0] == 0
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("metric,sqrt", [("euclidean", False), ("euclidean", True), ("cosine", False)])
 def test_pairwise_bitwise(dtype, metric, sqrt):
