@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     //      segment with its own exact lists [slot][nq][k], merged at the end
     //      by knn_merge_f32_kernel. ----
     const StreamSplit sp(nq, nt, kQpb, kBn, a.grid_wgs);
-    const int64_t wg = blockIdx.x;
+    const int64_t wg = xcd_grouped_wg(blockIdx.x, gridDim.x);
     const int64_t u_hi = ((wg + 1) * sp.P < sp.T) ? (wg + 1) * sp.P : sp.T;
     for (int64_t u = wg * sp.P; u < u_hi;) {
     int64_t panel, qblock, tile0, left;

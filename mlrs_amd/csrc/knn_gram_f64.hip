@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
 
     // ---- work split (StreamSplit), as in the f32 kernel ----
     const StreamSplit sp(nq, nt, kQpb, kBn, a.grid_wgs);
-    const int64_t wg = blockIdx.x;
+    const int64_t wg = xcd_grouped_wg(blockIdx.x, gridDim.x);
     const int64_t u_hi = ((wg + 1) * sp.P < sp.T) ? (wg + 1) * sp.P : sp.T;
     for (int64_t u = wg * sp.P; u < u_hi;) {
     int64_t panel, qblock, tile0, left;

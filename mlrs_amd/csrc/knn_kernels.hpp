@@ -75,6 +75,17 @@ struct StreamSplit {
     __host__ __device__ int64_t nslots() const { return S + 1; }
 };
 
+// XCD-aware workgroup numbering.  Consecutive workgroup ids are handed to
+// the eight XCDs in turn, and each XCD has its own L2.  Renumbering so that
+// the workgroups resident on one XCD take one contiguous range of the
+// StreamSplit order puts the workgroups that stream one index panel on the
+// same XCD, where one L2 fill serves all of them.  A bijection of [0, G).
+__device__ __forceinline__ int64_t xcd_grouped_wg(int64_t b, int64_t G) {
+    constexpr int64_t kXcds = 8;
+    const int64_t x = b % kXcds, i = b / kXcds, per = G / kXcds, rem = G % kXcds;
+    return x * per + (x < rem ? x : rem) + i;
+}
+
 struct GramArgs32 {
     const float* q;
     int64_t nq;
