@@ -118,8 +118,12 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
     const float inf = __builtin_huge_valf();
     const uint64_t below = (1ull << lane) - 1ull;
 
-    const int64_t s = blockIdx.y;
-    const int64_t qwave = (int64_t)blockIdx.x * kQpb + w * kQpw;
+    // (query block, strip) from the XCD-grouped number of this workgroup:
+    // the query blocks of one strip (the same index rows) run on one XCD.
+    const int64_t gx = gridDim.x;
+    const int64_t gid = xcd_grouped_wg((int64_t)blockIdx.y * gx + blockIdx.x, gx * (int64_t)gridDim.y);
+    const int64_t s = gid / gx;
+    const int64_t qwave = (gid % gx) * kQpb + w * kQpw;
     const int64_t qmine = qwave + jl;
     const bool qvalid = qmine < nq;
     const int64_t t_begin = s * a.strip_len;
