@@ -215,32 +215,62 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
     }
 }
 
-// Strip merge, one wave per query (lists are sorted; k <= 32 <= 64 lanes).
+// Strip merge, one lane per query: the query's list and each strip's list
+// (sorted, k <= K entries, padded with sentinels) are merged in registers.
+// The K smallest of two sorted lists by the (value, index) order are
+// min(A[j], B[K-1-j]), a bitonic sequence; K log2(K) / 2 compare-exchanges
+// sort it.  The order is total (indices are distinct across strips), so the
+// result is the first k of the union, whatever the network.
+template <int K>
 __global__ __launch_bounds__(256) void lowd_merge_kernel(LowdArgs32 a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (q >= a.nq) return;
     const int k = a.k;
     const float inf = __builtin_huge_valf();
-    float lv = inf;
-    uint32_t li = kSentinelIdx;
-    if (lane < k) {
-        lv = a.part_val[q * k + lane];
-        li = a.part_idx[q * k + lane];
+    float lv[K];
+    uint32_t li[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        lv[j] = (j < k) ? a.part_val[q * k + j] : inf;
+        li[j] = (j < k) ? a.part_idx[q * k + j] : kSentinelIdx;
     }
     for (int s = 1; s < a.nstrips; ++s) {
-        float v = inf;
-        uint32_t ix = kSentinelIdx;
-        if (lane < k) {
-            int64_t o = ((int64_t)s * a.nq + q) * k + lane;
-            v = a.part_val[o];
-            ix = a.part_idx[o];
+        const int64_t o = ((int64_t)s * a.nq + q) * k;
+        float bv[K];
+        uint32_t bi[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            bv[j] = (j < k) ? a.part_val[o + j] : inf;
+            bi[j] = (j < k) ? a.part_idx[o + j] : kSentinelIdx;
         }
-        wave_merge64<float>(lv, li, v, ix, lane);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const bool t = pair_less<float>(bv[K - 1 - j], bi[K - 1 - j], lv[j], li[j]);
+            lv[j] = t ? bv[K - 1 - j] : lv[j];
+            li[j] = t ? bi[K - 1 - j] : li[j];
+        }
+#pragma unroll
+        for (int m = K / 2; m > 0; m >>= 1) {
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                if ((j & m) == 0) {
+                    const bool t = pair_less<float>(lv[j + m], li[j + m], lv[j], li[j]);
+                    const float v0 = lv[j], v1 = lv[j + m];
+                    const uint32_t i0 = li[j], i1 = li[j + m];
+                    lv[j] = t ? v1 : v0;
+                    li[j] = t ? i1 : i0;
+                    lv[j + m] = t ? v0 : v1;
+                    li[j + m] = t ? i0 : i1;
+                }
+            }
+        }
     }
-    if (lane < k) {
-        a.out_val[q * k + lane] = (a.mode == EMIT_SQRT) ? __builtin_sqrtf(lv) : lv;
-        a.out_idx[q * k + lane] = (li == kSentinelIdx) ? 0u : li;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        if (j < k) {
+            a.out_val[q * k + j] = (a.mode == EMIT_SQRT) ? __builtin_sqrtf(lv[j]) : lv[j];
+            a.out_idx[q * k + j] = (li[j] == kSentinelIdx) ? 0u : li[j];
+        }
     }
 }
 
@@ -310,7 +340,17 @@ hipError_t launch_lowd_f32(const LowdArgs32& a, int arm, hipStream_t s) {
     else
         return hipErrorInvalidValue;
     if (e != hipSuccess || a.nstrips <= 1) return e;
-    hipLaunchKernelGGL(lowd_merge_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+    const dim3 mg((unsigned)((a.nq + 255) / 256));
+    if (a.k <= 1)
+        hipLaunchKernelGGL(lowd_merge_kernel<1>, mg, dim3(256), 0, s, a);
+    else if (a.k <= 4)
+        hipLaunchKernelGGL(lowd_merge_kernel<4>, mg, dim3(256), 0, s, a);
+    else if (a.k <= 8)
+        hipLaunchKernelGGL(lowd_merge_kernel<8>, mg, dim3(256), 0, s, a);
+    else if (a.k <= 16)
+        hipLaunchKernelGGL(lowd_merge_kernel<16>, mg, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(lowd_merge_kernel<32>, mg, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
