@@ -250,7 +250,13 @@ int32_t mlrs_knn_classify_f64(const int32_t *y_class, int64_t n_train, int32_t n
  *   len = capacity}.  The usual sequence is a counting call, then a call with
  *   buffers of the returned size and otherwise the same arguments, which
  *   starts from the first call's counts (the second call re-checks them and
- *   counts again if the data changed in between).
+ *   counts again if the data changed in between).  A call that brings
+ *   buffers without a counting call before it (a caller that knows a bound
+ *   on the total, e.g. from an earlier search) is served by one pass when
+ *   the f32 matrix-core path keeps every strip's matches (at most 1,024 per
+ *   strip and row): they are counted, kept and copied into place in the
+ *   same call.  Buffers too small: as above, and the counts are kept for
+ *   the next call.
  * Errors, before any launch: InvalidParam "radius" (radius not >= 0, NaN
  *   included; the text of AlgoError::InvalidEps), ShapeMismatch "xq" (n_query
  *   or n_features zero, or a length mismatch), DimMismatch "n_features",

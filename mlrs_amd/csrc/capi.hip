@@ -955,10 +955,16 @@ struct RadiusBufs {
     T* xsq;
     T* xinv;
     NormStats* stats;
+    unsigned int* stage_over;
+    T* stage_val;
+    int32_t* stage_idx;
 };
 
+// The staging area (last, so the other buffers keep their places whatever
+// its size) holds stage_cap matches per (strip, row).
 template <typename T>
-static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int nstrips, RadiusBufs<T>* b) {
+static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int nstrips, int64_t stage_cap,
+                           RadiusBufs<T>* b) {
     const int RQ = radius_queries_per_wave<T>();
     const int64_t G = (nq + RQ - 1) / RQ;
     Carver cv(base);
@@ -974,6 +980,13 @@ static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int ns
     b->xsq = cv.take<T>((size_t)std::max<int64_t>(1, nt));
     b->xinv = cv.take<T>((size_t)std::max<int64_t>(1, nt));
     b->stats = cv.take<NormStats>(1);
+    b->stage_over = cv.take<unsigned int>(1);
+    b->stage_val = nullptr;
+    b->stage_idx = nullptr;
+    if (stage_cap > 0) {
+        b->stage_val = cv.take<T>((size_t)nstrips * (size_t)nq * (size_t)stage_cap);
+        b->stage_idx = cv.take<int32_t>((size_t)nstrips * (size_t)nq * (size_t)stage_cap);
+    }
     return cv.off + 256;
 }
 
@@ -1088,14 +1101,26 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     const bool same = P.valid && P.xq == xq && P.xt == xt && P.nq == nq && P.nt == nt && P.d == d &&
                       P.metric == metric && P.p == p && P.radius == radius && P.elem == elem &&
                       P.stream == stream && P.nstrips == nstrips && P.strip_len == strip_len && P.gram == gram;
+    // A call that brings its output buffers and finds no kept plan counts
+    // with the staged pass on the matrix-core path: each (strip, row)'s first
+    // stage_cap matches are kept, so when every strip fits and the buffers
+    // are large enough the matches are copied into place and no fill pass
+    // runs.  Staging holds at most 1,024 matches per (strip, row) and 2 GiB
+    // in all; below 64 per (strip, row) it is not used.
+    int64_t stage_cap = 0;
+    if (gram && out_dist && !same && nstrips > 0) {
+        const double per = (double)(2ull << 30) / ((double)nstrips * (double)nq * (double)(sizeof(T) + 4));
+        stage_cap = per >= 1024.0 ? 1024 : ((int64_t)per / 16) * 16;
+        if (stage_cap < 64) stage_cap = 0;
+    }
     RadiusBufs<T> B;
-    const size_t need = radius_carve<T>(nullptr, nq, nt, d, nstrips, &B);
+    const size_t need = radius_carve<T>(nullptr, nq, nt, d, nstrips, stage_cap, &B);
     if (!same) {
         P.valid = false;
         rc = radius_plan_memory(P, need);
         if (rc) return rc;
     }
-    (void)radius_carve<T>(P.base, nq, nt, d, nstrips, &B);
+    (void)radius_carve<T>(P.base, nq, nt, d, nstrips, stage_cap, &B);
 
     RadiusArgs<T> a{};
     a.qT = B.qT;
@@ -1127,6 +1152,10 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     const double u23 = std::ldexp(1.0, -23);
     a.eps_rel = (arm == ARM_COS_HOST) ? 0.0 : 8.0 * (double)(d + 4) * u23;
     a.eps_abs = (arm == ARM_COS_HOST) ? (8.0 * (double)d + 32.0) * u23 : (double)(d + 4) * std::ldexp(1.0, -120);
+    a.stage_val = B.stage_val;
+    a.stage_idx = B.stage_idx;
+    a.stage_cap = stage_cap;
+    a.stage_over = B.stage_over;
 
     e = gram ? hipSuccess : launch_radius_stage<T>(xq, nq, d, B.qT, s);
     if (e == hipSuccess && (arm == ARM_COS_HOST || gram)) {
@@ -1137,14 +1166,19 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
             e = launch_row_norms<T>(xt, nt, d, B.xsq, B.xinv, nullptr, gram ? B.stats : nullptr, s);
     }
     if (e != hipSuccess) return hip_err(e, "radius staging");
-    auto scan = [&](bool fill_pass) -> hipError_t {
+    auto scan = [&](int mode) -> hipError_t {
+        const bool fill_pass = mode == RADIUS_FILL;
         if constexpr (std::is_same<T, float>::value) {
             if (gram) {
                 if (fill_pass) {
                     KernelTimer kt(s, "radius_gram_fill");
-                    return launch_radius_gram(a, arm, true, s);
+                    return launch_radius_gram(a, arm, RADIUS_FILL, s);
                 }
-                return launch_radius_gram(a, arm, false, s);
+                if (mode == RADIUS_STAGE) {
+                    KernelTimer kt(s, "radius_gram_stage");
+                    return launch_radius_gram(a, arm, RADIUS_STAGE, s);
+                }
+                return launch_radius_gram(a, arm, RADIUS_COUNT, s);
             }
         }
         if (fill_pass) {
@@ -1154,9 +1188,10 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         return launch_radius_scan<T>(a, arm, false, s);
     };
 
-    auto count = [&]() -> int32_t {
+    auto count = [&](bool staged) -> int32_t {
         hipError_t e2 = launch_fill_u32(B.cnt, (int64_t)nstrips * nq, 0u, s);
-        if (e2 == hipSuccess) e2 = scan(false);
+        if (e2 == hipSuccess && staged) e2 = launch_fill_u32(B.stage_over, 1, 0u, s);
+        if (e2 == hipSuccess) e2 = scan(staged ? RADIUS_STAGE : RADIUS_COUNT);
         if (e2 == hipSuccess) e2 = launch_radius_offsets(B.cnt, nq, nstrips, B.row_cnt, B.block_sum, B.qoff, B.total, s);
         if (e2 != hipSuccess) return hip_err(e2, "radius count");
         int32_t r2 = read_u64(B.total, s, &P.total);
@@ -1179,7 +1214,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     };
     auto fill = [&](unsigned int* bad) -> int32_t {
         hipError_t e2 = launch_fill_u32(B.mismatch, 1, 0u, s);
-        if (e2 == hipSuccess) e2 = scan(true);
+        if (e2 == hipSuccess) e2 = scan(RADIUS_FILL);
         if (e2 != hipSuccess) return hip_err(e2, "radius fill");
         e2 = hipMemcpyAsync(bad, B.mismatch, sizeof(*bad), hipMemcpyDeviceToHost, s);
         if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
@@ -1199,9 +1234,25 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
 
     bool counted_now = false;
     if (!same) {
-        rc = count();
+        rc = count(stage_cap > 0);
         if (rc) return rc;
         counted_now = true;
+        if (stage_cap > 0 && P.total <= (unsigned long long)capacity) {
+            unsigned int over = 1;
+            hipError_t e2 = hipMemcpyAsync(&over, B.stage_over, sizeof(over), hipMemcpyDeviceToHost, s);
+            if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
+            if (e2 != hipSuccess) return hip_err(e2, "radius read-back");
+            if (!over) {
+                if constexpr (std::is_same<T, float>::value) {
+                    e2 = launch_radius_unstage(a, s);
+                    if (e2 == hipSuccess)
+                        e2 = launch_radius_transform<T>(out_dist, (int64_t)P.total, transform, (T)(1.0 / p_tr), s);
+                    if (e2 != hipSuccess) return hip_err(e2, "radius unstage");
+                }
+                P.valid = false;
+                return finish_counts();
+            }
+        }
     }
     for (;;) {
         if (!out_dist || P.total > (unsigned long long)capacity) {
@@ -1223,7 +1274,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         if (counted_now)
             return set_err(MLRS_ERR_HIP, "radius", 0, 0, 0, 0,
                            "radius fill pass disagrees with its own count pass (inputs modified during the call)");
-        rc = count();
+        rc = count(false);
         if (rc) return rc;
         counted_now = true;
     }

@@ -272,12 +272,21 @@ struct RadiusArgs {
     const T* xsq;                      // [nt] index row_sumsq
     const NormStats* stats;            // largest index squared norm
     double eps_rel, eps_abs;           // screen error bound (as the fused kNN screen's)
+    // STAGE (matrix-core screen): [nstrips][nq][stage_cap] first matches of
+    // each (strip, row), and a flag set when a (strip, row) has more
+    T* stage_val;
+    int32_t* stage_idx;
+    int64_t stage_cap;
+    unsigned int* stage_over;
 };
+enum RadiusMode : int { RADIUS_COUNT = 0, RADIUS_FILL = 1, RADIUS_STAGE = 2 };
 // The matrix-core radius scan: f32, Euclidean and cosine, d <= 128.
 bool radius_gram_serves(int arm, int64_t d);
 int64_t radius_gram_rows_per_tile();
 int64_t radius_gram_queries_per_block();
-hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, bool fill, hipStream_t s);
+hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, int mode, hipStream_t s);
+// The staged matches of a STAGE pass copied into the outputs (after the offsets).
+hipError_t launch_radius_unstage(const RadiusArgs<float>& a, hipStream_t s);
 template <typename T>
 int radius_queries_per_wave();
 template <typename T>

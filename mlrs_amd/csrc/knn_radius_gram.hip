@@ -27,7 +27,10 @@
 //  * COUNT writes each (strip, query) match count; FILL writes the
 //    pre-boundary values and indices at the offsets the count pass produced,
 //    never at or past the caller's capacity, and flags a strip whose matches
-//    differ from its count.
+//    differ from its count.  STAGE counts as COUNT does and also keeps each
+//    (strip, query)'s first stage_cap matches, in order, in a staging area
+//    (flagging a strip with more), so that a call which already holds its
+//    output buffers copies them into place instead of running FILL.
 #include "knn_common.hpp"
 #include "knn_kernels.hpp"
 
@@ -93,7 +96,7 @@ __device__ __forceinline__ float host_value(const float* __restrict__ q, const f
     return acc;
 }
 
-template <int NG, bool COS, bool VEC4, bool FILL>
+template <int NG, bool COS, bool VEC4, bool FILL, bool STAGE>
 __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a, float* __restrict__ out_dist,
                                                              int32_t* __restrict__ out_idx) {
     constexpr int DP = NG * 8;        // padded feature count
@@ -289,6 +292,14 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
                     out_idx[pos_] = (int32_t)t_;                                             \
                 }                                                                            \
             }                                                                                \
+            if (STAGE && hit_) {                                                             \
+                const uint32_t rk_ = r0_ + (uint32_t)__popcll(H_ & below & from_);           \
+                if (rk_ < (uint32_t)a.stage_cap) {                                           \
+                    const int64_t so_ = (s * nq + qwave + j_) * a.stage_cap + rk_;           \
+                    a.stage_val[so_] = v_;                                                   \
+                    a.stage_idx[so_] = (int32_t)t_;                                          \
+                }                                                                            \
+            }                                                                                \
             if (act_ && (uint32_t)lane == hi_ - 1u) {                                        \
                 const uint64_t upto_ = (hi_ >= 64u) ? ~0ull : ((1ull << hi_) - 1ull);        \
                 L.rel[j_] = r0_ + (uint32_t)__popcll(H_ & from_ & upto_);                    \
@@ -358,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
                 const int r = 4 * g4 + e;
                 const float wv = COS ? 1.0f - (acc[r] * sc[e]) * qa_mine : acc[r];
                 m |= (uint32_t)!(wv > thr) << r;
-                if (!FILL) dm |= (uint32_t)(wv <= thr_lo) << r;
+                if (!FILL && !STAGE) dm |= (uint32_t)(wv <= thr_lo) << r;
             }
         }
         if (!qvalid) m = 0;
@@ -367,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
             for (int r = 0; r < 16; ++r)
                 if ((uint32_t)t0 + (uint32_t)(8 * (r >> 2) + 4 * h + (r & 3)) >= t_end32) m &= ~(1u << r);
         }
-        if (!FILL) {
+        if (!FILL && !STAGE) {  // staging needs every match's value: no certain-match shortcut
             dm &= m;
             sure += (uint32_t)__builtin_popcount(dm);
             m &= ~dm;
@@ -398,6 +409,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
         const uint32_t mine = L.rel[lane] + sure;
         if (!FILL) {
             a.cnt[s * nq + qmine] = mine;
+            if (STAGE && mine > (uint32_t)a.stage_cap) atomicOr(a.stage_over, 1u);
         } else {
             const unsigned long long want =
                 a.qoff[qmine] + (s + 1 < a.nstrips ? (unsigned long long)a.cnt[(s + 1) * nq + qmine]
@@ -408,24 +420,48 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
 }
 
 template <int NG, bool COS, bool VEC4>
-hipError_t launch_rg(const RadiusArgs<float>& a, bool fill, hipStream_t s) {
+hipError_t launch_rg(const RadiusArgs<float>& a, int mode, hipStream_t s) {
     const dim3 grid((unsigned)((a.nq + kQpb - 1) / kQpb), (unsigned)a.nstrips);
-    if (fill)
-        hipLaunchKernelGGL((radius_gram_kernel<NG, COS, VEC4, true>), grid, dim3(256), 0, s, a, a.out_dist,
+    if (mode == RADIUS_FILL)
+        hipLaunchKernelGGL((radius_gram_kernel<NG, COS, VEC4, true, false>), grid, dim3(256), 0, s, a, a.out_dist,
+                           a.out_idx);
+    else if (mode == RADIUS_STAGE)
+        hipLaunchKernelGGL((radius_gram_kernel<NG, COS, VEC4, false, true>), grid, dim3(256), 0, s, a, a.out_dist,
                            a.out_idx);
     else
-        hipLaunchKernelGGL((radius_gram_kernel<NG, COS, VEC4, false>), grid, dim3(256), 0, s, a, a.out_dist,
+        hipLaunchKernelGGL((radius_gram_kernel<NG, COS, VEC4, false, false>), grid, dim3(256), 0, s, a, a.out_dist,
                            a.out_idx);
     return hipGetLastError();
 }
 
 template <bool COS, bool VEC4>
-hipError_t launch_rg_ng(const RadiusArgs<float>& a, bool fill, hipStream_t s) {
+hipError_t launch_rg_ng(const RadiusArgs<float>& a, int mode, hipStream_t s) {
     const int ng = (int)((a.d + 7) / 8);
-    if (ng <= 4) return launch_rg<4, COS, VEC4>(a, fill, s);
-    if (ng <= 8) return launch_rg<8, COS, VEC4>(a, fill, s);
-    if (ng <= 12) return launch_rg<12, COS, VEC4>(a, fill, s);
-    return launch_rg<16, COS, VEC4>(a, fill, s);
+    if (ng <= 4) return launch_rg<4, COS, VEC4>(a, mode, s);
+    if (ng <= 8) return launch_rg<8, COS, VEC4>(a, mode, s);
+    if (ng <= 12) return launch_rg<12, COS, VEC4>(a, mode, s);
+    return launch_rg<16, COS, VEC4>(a, mode, s);
+}
+
+// The staged matches of every (strip, row) copied to the row's output
+// offset plus the strip's in-row prefix: one wave per (strip, row).
+__global__ __launch_bounds__(256) void radius_unstage_kernel(RadiusArgs<float> a) {
+    const int64_t sq = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // strip * nq + row
+    const int lane = threadIdx.x & 63;
+    if (sq >= (int64_t)a.nstrips * a.nq) return;
+    const int64_t q = sq % a.nq, st = sq / a.nq;
+    const uint32_t beg = a.cnt[sq];
+    const uint32_t end = (st + 1 < a.nstrips) ? a.cnt[sq + a.nq] : a.row_cnt[q];
+    const int64_t n = (int64_t)(end - beg) < a.stage_cap ? (int64_t)(end - beg) : a.stage_cap;
+    const unsigned long long base = a.qoff[q] + beg;
+    const int64_t src = sq * a.stage_cap;
+    for (int64_t r = lane; r < n; r += 64) {
+        const unsigned long long pos = base + (unsigned long long)r;
+        if (pos < (unsigned long long)a.capacity) {
+            a.out_dist[pos] = a.stage_val[src + r];
+            a.out_idx[pos] = a.stage_idx[src + r];
+        }
+    }
 }
 
 }  // namespace
@@ -436,15 +472,24 @@ bool radius_gram_serves(int arm, int64_t d) {
 int64_t radius_gram_rows_per_tile() { return kBn; }
 int64_t radius_gram_queries_per_block() { return kQpb; }
 
-hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, bool fill, hipStream_t s) {
+hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, int mode, hipStream_t s) {
     if (a.nq == 0 || a.nstrips == 0) return hipSuccess;
+    if (mode == RADIUS_STAGE && (a.stage_cap <= 0 || !a.stage_val || !a.stage_idx || !a.stage_over))
+        return hipErrorInvalidValue;
     const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
     if (arm == ARM_EUCLID_MULADD)
-        return vec4 ? launch_rg_ng<false, true>(a, fill, s) : launch_rg_ng<false, false>(a, fill, s);
+        return vec4 ? launch_rg_ng<false, true>(a, mode, s) : launch_rg_ng<false, false>(a, mode, s);
     if (arm == ARM_COS_HOST)
-        return vec4 ? launch_rg_ng<true, true>(a, fill, s) : launch_rg_ng<true, false>(a, fill, s);
+        return vec4 ? launch_rg_ng<true, true>(a, mode, s) : launch_rg_ng<true, false>(a, mode, s);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_radius_unstage(const RadiusArgs<float>& a, hipStream_t s) {
+    const int64_t n = (int64_t)a.nstrips * a.nq;
+    if (n == 0 || a.stage_cap <= 0) return hipSuccess;
+    hipLaunchKernelGGL(radius_unstage_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace mlrs

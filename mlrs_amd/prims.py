@@ -154,6 +154,17 @@ def row_sqnorms(x, out=None):
     return o
 
 
+# Last match total per search shape (device, dtype, sizes, metric, p, radius):
+# sizes the buffers of the next search of that shape.
+_RADIUS_TOTAL_HINT = {}
+
+
+def _remember_radius_total(key, n):
+    if key not in _RADIUS_TOTAL_HINT and len(_RADIUS_TOTAL_HINT) >= 64:
+        _RADIUS_TOTAL_HINT.clear()
+    _RADIUS_TOTAL_HINT[key] = n
+
+
 def radius_neighbors(xq, x_train, radius, metric="euclidean", p=2.0):
     """Every row of ``x_train`` within ``radius`` of each row of ``xq``
     (mlrs_radius_neighbors_*).
@@ -162,7 +173,10 @@ def radius_neighbors(xq, x_train, radius, metric="euclidean", p=2.0):
     query row 0, then row 1, ... concatenated, each row's in ascending
     training index (the reference's RadiusNeighbors layout, a CSR matrix
     without its indptr), ``indices`` int32, ``counts`` int64 per query row.
-    Synchronizes: the match total sizes the outputs."""
+    Synchronizes: the match total sizes the outputs.  A search of a shape
+    searched before passes buffers sized from that search's total, so one
+    call (one matrix-core pass when every strip's matches fit the library's
+    staging) returns the matches."""
     _dev_check(xq, x_train)
     if x_train.dtype != xq.dtype:
         raise TypeError("query and training dtypes differ")
@@ -177,8 +191,26 @@ def radius_neighbors(xq, x_train, radius, metric="euclidean", p=2.0):
     args = (_ptr(xq), xq.numel(), nq, d, _ptr(x_train), x_train.numel(), nt, dt, _metric_id(metric), float(p),
             float(radius), _ptr(counts), counts.numel())
     stream = _stream(xq.device)
+    key = (xq.device.index, xq.dtype, nq, nt, d, metric, float(p), float(radius))
+    hint = _RADIUS_TOTAL_HINT.get(key)
+    if hint is not None:
+        # One call with buffers sized from the last search of this shape: the
+        # library then counts and keeps the matches in the same pass and
+        # copies them into place.  Too small, and the call returns the total
+        # with its counts kept for the exact-size call below.
+        cap = hint + hint // 8 + 1024
+        dist = torch.empty(cap, dtype=xq.dtype, device=xq.device)
+        idx = torch.empty(cap, dtype=torch.int32, device=xq.device)
+        rc = f(*args, _ptr(dist), _ptr(idx), cap, ctypes.byref(total), stream)
+        if rc == 0:
+            n = int(total.value)
+            _remember_radius_total(key, n)
+            return dist[:n], idx[:n], counts.to(torch.int64)
+        if rc != _lib.MLRS_ERR_SHAPE_MISMATCH or int(total.value) <= cap:
+            _lib.check(rc)
     _lib.check(f(*args, None, None, 0, ctypes.byref(total), stream))
     n = int(total.value)
+    _remember_radius_total(key, n)
     dist = torch.empty(n, dtype=xq.dtype, device=xq.device)
     idx = torch.empty(n, dtype=torch.int32, device=xq.device)
     if n:

@@ -278,3 +278,72 @@ def test_estimator_radius_graph_self_drop_and_sorting():
         nn.radius_neighbors(X[:2], return_distance=False, sort_results=True)
     with pytest.raises(ValueError, match="radius must be non-negative"):
         nn.radius_neighbors(X[:2], radius=-1)
+
+
+def _one_call(xq_np, xt_np, radius, cap, metric_id=0):
+    """One call with output buffers of `cap` entries (no counting call before
+    it): the matrix-core path counts and stages the matches in one pass."""
+    xq, xt = _t(xq_np), _t(xt_np)
+    counts = torch.empty(xq_np.shape[0], dtype=torch.int32, device=DEV)
+    out_d = torch.empty(max(cap, 1), dtype=torch.float32, device=DEV)
+    out_i = torch.empty(max(cap, 1), dtype=torch.int32, device=DEV)
+    total = ctypes.c_int64(-1)
+    f = _lib.load().mlrs_radius_neighbors_f32
+    rc = f(xq.data_ptr(), xq.numel(), xq.shape[0], xq.shape[1], xt.data_ptr(), xt.numel(), xt.shape[0],
+           xt.shape[1], metric_id, 2.0, float(radius), counts.data_ptr(), counts.numel(), out_d.data_ptr(),
+           out_i.data_ptr(), cap, ctypes.byref(total), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    n = max(total.value, 0)
+    return rc, total.value, counts.cpu().numpy(), out_d[:n].cpu().numpy(), out_i[:n].cpu().numpy()
+
+
+@pytest.mark.parametrize("metric,mid", [("euclidean", 0), ("cosine", 1)])
+def test_radius_staged_single_call(matrix_core_path, metric, mid):
+    """A call that brings large enough buffers is served by the staged count
+    pass alone (matches kept per strip, then copied into place), and a strip
+    holding more matches than the staging keeps (1,024 per strip and row;
+    here 3,000 rows near query 0 over strips of 1,600 rows) falls back to the
+    fill pass: both exact."""
+    rng = np.random.default_rng(77)
+    xt = rng.standard_normal((50000, 20)).astype(np.float32)
+    xq = rng.standard_normal((8192, 20)).astype(np.float32)
+    dist_all = oracle.pairwise(xq[:40], xt, metric, sqrt=True)
+    r = _radius(dist_all, 0.002, rel=1e-4)
+    wd, wi, wc = oracle.radius_neighbors(xq, xt, r, metric)
+    rc, n, c, d, i = _one_call(xq, xt, r, wi.size + 100, mid)
+    assert rc == 0 and n == wi.size
+    np.testing.assert_array_equal(c, wc.astype(np.int32))
+    np.testing.assert_array_equal(i, wi)
+    np.testing.assert_array_equal(d, wd)
+    # overflowing staging: a dense cluster around query 0
+    xt2 = xt.copy()
+    xt2[:3000] = xq[0] + np.float32(1e-3) * rng.standard_normal((3000, 20)).astype(np.float32)
+    r2 = 0.2 if metric == "euclidean" else 1e-4
+    wd, wi, wc = oracle.radius_neighbors(xq, xt2, r2, metric)
+    assert wc[0] >= 2900
+    rc, n, c, d, i = _one_call(xq, xt2, r2, wi.size, mid)
+    assert rc == 0 and n == wi.size
+    np.testing.assert_array_equal(c, wc.astype(np.int32))
+    np.testing.assert_array_equal(i, wi)
+    np.testing.assert_array_equal(d, wd)
+    # buffers too small: the total comes back, nothing is written
+    rc, n, c, d, i = _one_call(xq, xt2, r2, wi.size - 1, mid)
+    assert rc == _lib.MLRS_ERR_SHAPE_MISMATCH and n == wi.size
+
+
+def test_radius_repeated_search_uses_size_hint(matrix_core_path):
+    """The Python wrapper sizes a repeated search's buffers from the previous
+    total: the second search of a shape takes the one-call path, and a later
+    search of the same shape with more matches than the hint allows still
+    comes back exact (the call reports the total, then counts are reused)."""
+    rng = np.random.default_rng(78)
+    xt = rng.standard_normal((20000, 40)).astype(np.float32)
+    xq = rng.standard_normal((300, 40)).astype(np.float32)
+    r = _radius(oracle.pairwise(xq[:20], xt, "euclidean", sqrt=True), 0.01, rel=1e-4)
+    for _ in range(2):
+        _compare(xq, xt, r, "euclidean")
+    xt_dense = xt.copy()
+    xt_dense[:15000] = xq[rng.integers(0, 300, 15000)] + np.float32(0.01)
+    wc = _compare(xq, xt_dense, r, "euclidean")
+    assert wc.sum() > 15000
+    _compare(xq, xt, r, "euclidean")
