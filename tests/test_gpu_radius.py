@@ -329,6 +329,20 @@ def test_radius_staged_single_call(matrix_core_path, metric, mid):
     # buffers too small: the total comes back, nothing is written
     rc, n, c, d, i = _one_call(xq, xt2, r2, wi.size - 1, mid)
     assert rc == _lib.MLRS_ERR_SHAPE_MISMATCH and n == wi.size
+    # NaN and zero rows on both sides, duplicates of a query, through staging
+    xt3 = xt.copy()
+    xq3 = xq.copy()
+    xt3[[11, 4000, 49999]] = np.nan
+    xt3[[12, 4001]] = 0.0
+    xt3[100:140] = xq3[5]
+    xq3[7] = np.nan
+    xq3[8] = 0.0
+    wd, wi, wc = oracle.radius_neighbors(xq3, xt3, r, metric)
+    rc, n, c, d, i = _one_call(xq3, xt3, r, wi.size + 7, mid)
+    assert rc == 0 and n == wi.size
+    np.testing.assert_array_equal(c, wc.astype(np.int32))
+    np.testing.assert_array_equal(i, wi)
+    np.testing.assert_array_equal(d, wd)
 
 
 def test_radius_repeated_search_uses_size_hint(matrix_core_path):
