@@ -1745,14 +1745,22 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                 rc = km_d2h<T>(lab_h.data(), lab[cur], sizeof(uint32_t) * (size_t)n, s);
                 if (!rc) rc = km_d2h<T>(dist_h.data(), dist, sizeof(T) * (size_t)n, s);
                 if (rc) return rc;
+                // the ranking is only needed over a prefix: the top
+                // m = 8 * empties + 64 rows are selected in O(n) and sorted,
+                // the rest sorted only if the walk runs past them (the
+                // reference's select_nth_unstable_by + sort_by, :1347-1359)
                 std::vector<int64_t> order((size_t)n);
                 for (int64_t i = 0; i < n; ++i) order[i] = i;
-                std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
+                auto by_rank = [&](int64_t a, int64_t b) {
                     const double da = (double)dist_h[a], db = (double)dist_h[b];
                     if (db < da) return true;
                     if (da < db) return false;
                     return a < b;
-                });
+                };
+                const int64_t m_top = std::min<int64_t>(8 * empties + 64, n);
+                if (m_top < n) std::nth_element(order.begin(), order.begin() + m_top, order.end(), by_rank);
+                std::sort(order.begin(), order.begin() + m_top, by_rank);
+                int64_t ranked = m_top;
                 std::vector<char> moved((size_t)n, 0);
                 std::vector<T> row((size_t)d);
                 int64_t cursor = 0;
@@ -1760,6 +1768,10 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                     if (cnt[c] != 0) continue;
                     bool ok_move = false;
                     while (cursor < n) {
+                        if (cursor == ranked) {  // past the selected prefix: rank the rest
+                            std::sort(order.begin() + ranked, order.end(), by_rank);
+                            ranked = n;
+                        }
                         const int64_t i = order[cursor++];
                         if (moved[i]) continue;
                         const int64_t donor = lab_h[i];
