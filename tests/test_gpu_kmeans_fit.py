@@ -77,6 +77,23 @@ def test_fit_relocates_empty_clusters():
     assert len(set(got[1].cpu().tolist())) == 4
 
 
+def test_fit_relocation_walks_past_the_selected_prefix():
+    """The farthest rows all sit alone in their clusters (100 outliers, each
+    50 from its own centre), so the relocation walk skips every row of the
+    selected top 8 * empties + 64 and ranks the rest before it finds donors."""
+    X = _blobs(6, 2000, 3, 3, spread=0.8)
+    outliers = np.zeros((100, 3))
+    outliers[:, 0] = 1000.0 * np.arange(1, 101)
+    X = np.concatenate([X, outliers])
+    far = outliers.copy()
+    far[:, 0] += 50.0
+    ini = np.concatenate([X[[0, 1, 2]], far, [[-5000.0, 0.0, 0.0], [0.0, -5000.0, 0.0]]])
+    want = oracle.kmeans_fit(X, ini.shape[0], "array", ini, max_iter=3, tol=0.0)
+    got = prims.kmeans_fit(_t(X), ini.shape[0], "array", _t(ini), max_iter=3, tol=0.0)
+    _same(got, want)
+    assert len(set(got[1].cpu().tolist())) == ini.shape[0]
+
+
 @pytest.mark.parametrize("s", ["f32", "f64"])
 def test_estimator_fixture(s):
     z = load_golden("kmeans_%s_seed42" % s)
