@@ -1653,20 +1653,41 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                 chosen.assign(ids.begin(), ids.begin() + k);
             } else {  // kmeanspp_sample (prims/kmeans.rs:381-491)
                 std::vector<char> is_chosen((size_t)n, 0);
-                std::vector<T> m2((size_t)n);
-                std::vector<double> wgt((size_t)n);
+                // the D^2 weights come back every draw: pinned host memory
+                // (allocated here, freed on every exit) lets that copy run
+                // as one DMA
+                struct PinnedT {
+                    T* p = nullptr;
+                    ~PinnedT() {
+                        if (p) (void)hipHostFree(p);
+                    }
+                } m2buf;
+                e = hipHostMalloc((void**)&m2buf.p, sizeof(T) * (size_t)n, hipHostMallocDefault);
+                if (e != hipSuccess) {
+                    m2buf.p = nullptr;
+                    return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)(sizeof(T) * (size_t)n), 0, 0, (int)e,
+                                   "pinned host allocation of %zu bytes failed: %s", sizeof(T) * (size_t)n,
+                                   hipGetErrorString(e));
+                }
+                T* const m2 = m2buf.p;
+                // the weights' sequential f64 prefix, kept before every block
+                // of kCk rows: the draw rescans one block, from the same
+                // running sum, instead of every row before the pick
+                constexpr int64_t kCk = 4096;
+                std::vector<double> ck((size_t)((n + kCk - 1) / kCk + 1));
                 int64_t cur = (int64_t)rng.next_below((uint64_t)n);
                 chosen.push_back(cur);
                 is_chosen[cur] = 1;
                 for (int64_t m = 0; m + 1 < k; ++m) {
                     e = launch_km_mind2<T>(x, n, d, cur, m == 0 ? 1 : 0, mind2, s);
                     if (e != hipSuccess) return hip_err(e, "kmeans++ distances");
-                    rc = km_d2h<T>(m2.data(), mind2, sizeof(T) * (size_t)n, s);
+                    rc = km_d2h<T>(m2, mind2, sizeof(T) * (size_t)n, s);
                     if (rc) return rc;
                     double total = 0.0;
-                    for (int64_t i = 0; i < n; ++i) {
-                        wgt[i] = (double)m2[i];
-                        total += wgt[i];
+                    for (int64_t b0 = 0; b0 < n; b0 += kCk) {
+                        ck[(size_t)(b0 / kCk)] = total;
+                        const int64_t b1 = std::min<int64_t>(b0 + kCk, n);
+                        for (int64_t i = b0; i < b1; ++i) total += (double)m2[i];
                     }
                     int64_t next = -1;
                     if (total <= 0.0) {
@@ -1678,18 +1699,36 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                         if (next < 0) return shape_err("k", 1, k, n);
                     } else {
                         const double target = rng.next_f64() * total;
-                        double acc = 0.0;
+                        // first row whose running sum reaches the target:
+                        // the rows before the block whose starting sum is the
+                        // last one below the target never reach it (the sums
+                        // only grow), so the scan starts there with that sum.
+                        // A non-finite total scans from the first row.
+                        int64_t b = 0;
+                        if (std::isfinite(total)) {
+                            const int64_t nbk = (n + kCk - 1) / kCk;
+                            int64_t lo = 0, hi = nbk;  // first block with start sum >= target
+                            while (lo < hi) {
+                                const int64_t mid = (lo + hi) / 2;
+                                if (ck[(size_t)mid] < target)
+                                    lo = mid + 1;
+                                else
+                                    hi = mid;
+                            }
+                            b = lo > 0 ? lo - 1 : 0;
+                        }
+                        double acc = ck[(size_t)b];
                         int64_t pick = n - 1;
-                        for (int64_t i = 0; i < n; ++i) {
-                            acc += wgt[i];
+                        for (int64_t i = b * kCk; i < n; ++i) {
+                            acc += (double)m2[i];
                             if (acc >= target) {
                                 pick = i;
                                 break;
                             }
                         }
-                        if (wgt[pick] <= 0.0)
+                        if ((double)m2[pick] <= 0.0)
                             for (int64_t i = n - 1; i >= 0; --i)
-                                if (wgt[i] > 0.0) {
+                                if ((double)m2[i] > 0.0) {
                                     pick = i;
                                     break;
                                 }
