@@ -10,11 +10,19 @@
  *     MLRS_ERR_* code; mlrs_last_error() then describes the failure with the
  *     same fields as mlrs_core::PrimError (crates/mlrs-core/src/error.rs:62);
  *   - enqueues its work on `stream` (a hipStream_t; NULL = the null stream)
- *     and returns without synchronizing, except when it must grow its cached
- *     device workspace;
+ *     and returns without synchronizing, except when it must grow one of its
+ *     cached device buffers: growth synchronizes the WHOLE device (every
+ *     stream, other libraries' work included) before freeing the old buffer;
  *   - is callable from any thread, one call at a time per process (the
  *     Rust side serializes through its global pool mutex,
- *     crates/mlrs-py/src/lib.rs:104-186); calls are serialized internally.
+ *     crates/mlrs-py/src/lib.rs:104-186); calls are serialized internally;
+ *   - runs after the previous call on the same device even when the two
+ *     calls name different streams: the cached buffers are shared, so a call
+ *     on another stream than the last call's first makes its stream wait for
+ *     the last call's work (an event recorded at the end of every call), as
+ *     the reference's single stream orders them
+ *     (crates/mlrs-backend/src/stream_cap.rs:69).  The caller still orders
+ *     its own reads of the outputs after the call's stream.
  * Results equal mlrs's cpu-backend arithmetic bit for bit: the same arm
  * (direct / metric / host) the cpu dispatch would pick for the shape
  * (crates/mlrs-algos/src/neighbors/nearest.rs:891-953) is evaluated in the same
@@ -64,7 +72,7 @@ int32_t mlrs_last_error(mlrs_error_info *out);
 const char *mlrs_status_string(int32_t code);
 /* ABI version of this header (bumped on any signature change). */
 int32_t mlrs_abi_version(void);
-#define MLRS_ABI_VERSION 3
+#define MLRS_ABI_VERSION 4
 
 /*
  * Brute-force k nearest training rows of every query row.
@@ -92,8 +100,10 @@ int32_t mlrs_abi_version(void);
  *   ShapeMismatch "features" n_features < 1
  *   ShapeMismatch "rows"     n_query or n_train > UINT32_MAX
  *   ShapeMismatch "out"      out_len != n_query*k
- *   MLRS_ERR_UNSUPPORTED     metric not served, k above mlrs_knn_max_k(), or a
- *                            Minkowski p below 1 (or NaN)
+ *   MLRS_ERR_UNSUPPORTED     metric not served, or a Minkowski p below 1 (or NaN)
+ * Every 1 <= k <= n_train is served (knn_host_possible,
+ *   crates/mlrs-backend/src/prims/knn_host.rs:182-184; top_k,
+ *   crates/mlrs-backend/src/prims/topk.rs:208-212).
  * `p` is the Minkowski exponent, ignored by the other metrics.
  */
 int32_t mlrs_knn_topk_f32(const float *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
@@ -104,8 +114,10 @@ int32_t mlrs_knn_topk_f64(const double *xq, int64_t xq_len, int64_t n_query, int
                           const double *x_train, int64_t xt_len, int64_t n_train, int32_t k,
                           int32_t metric, double p, double *out_dist, uint32_t *out_idx,
                           int64_t out_len, void *stream);
-/* Largest k served for (dtype_bytes, n_features, metric). */
+/* Largest k served for (dtype_bytes, n_features, metric): INT32_MAX, i.e.
+ * every k up to n_train (the arguments are kept for ABI stability). */
 int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric);
+
 
 /*
  * Nearest-centre assignment (the k-means assignment step, k = 1 search).
@@ -295,7 +307,7 @@ int32_t mlrs_radius_neighbors_f64(const double *xq, int64_t xq_len, int64_t n_qu
  * Errors (knn_graph.rs:475-539): ShapeMismatch "x" {n, d, len} (or a
  *   dimension above u32::MAX), "k" {1, k, max_k} with max_k = n - 1 (n with
  *   include_self), "p" {1, 0, 1} (Minkowski p < 1), "out"; Unsupported
- *   "metric", or k (+1) above mlrs_knn_max_k().
+ *   "metric".  Every k up to max_k is served.
  */
 int32_t mlrs_knn_graph_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features, int64_t k, int32_t metric,
                            double p, int32_t include_self, uint32_t *out_idx, double *out_dist, int64_t out_len,

@@ -98,11 +98,87 @@ struct Carver {
 
 static size_t aligned_bytes(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// ---------------------------------------------------------------------------
+// call ordering across streams
+// ---------------------------------------------------------------------------
+// Every call enqueues on its caller's stream and returns without waiting, and
+// all calls on a device carve the same cached buffers.  So a call that runs
+// on another stream than the previous call first makes its stream wait for
+// the previous call's work (an event recorded at the end of every call that
+// touched a cached buffer): calls on one device run in call order, as on the
+// reference's single stream (crates/mlrs-backend/src/stream_cap.rs:69).
+struct DevOrder {
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+    bool have = false;
+};
+DevOrder g_order[kMaxDevices];
+
+struct CallState {
+    hipStream_t s = nullptr;
+    int dev = -1;
+    bool armed = false;
+};
+CallState* g_call = nullptr;  // the running entry-point call (under g_mu)
+
+// Holds the process-wide lock for one entry-point call; records the call's
+// end on its stream when the call touched a cached buffer.
+struct CallGuard {
+    std::lock_guard<std::mutex> lk;
+    CallState st;
+    CallGuard() : lk(g_mu) { g_call = &st; }
+    ~CallGuard() {
+        if (st.armed) {
+            DevOrder& O = g_order[st.dev];
+            if (hipEventRecord(O.ev, st.s) == hipSuccess) {
+                O.last = st.s;
+                O.have = true;
+            }
+        }
+        g_call = nullptr;
+    }
+    CallGuard(const CallGuard&) = delete;
+    CallGuard& operator=(const CallGuard&) = delete;
+};
+
+// Before the running call first touches a cached buffer of `dev`.
+int32_t order_after_last_call(int dev, hipStream_t s) {
+    if (!g_call || g_call->armed) return MLRS_OK;
+    DevOrder& O = g_order[dev];
+    hipError_t e;
+    if (!O.ev) {
+        e = hipEventCreateWithFlags(&O.ev, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            O.ev = nullptr;
+            return hip_err(e, "hipEventCreateWithFlags");
+        }
+    }
+    if (O.have && O.last != s) {
+        e = hipStreamWaitEvent(s, O.ev, 0);
+        if (e != hipSuccess) return hip_err(e, "hipStreamWaitEvent");
+    }
+    g_call->armed = true;
+    g_call->dev = dev;
+    g_call->s = s;
+    return MLRS_OK;
+}
+
+int32_t current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return hip_err(e, "hipGetDevice");
+    if (*dev < 0 || *dev >= kMaxDevices)
+        return set_err(MLRS_ERR_UNSUPPORTED, "device", *dev, 0, 0, 0, "device ordinal %d out of range", *dev);
+    return MLRS_OK;
+}
+
+// Growing a cached buffer synchronizes the whole device (the old buffer may
+// still be read by earlier work on any stream, and hipFree synchronizes the
+// device anyway).
 int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_err(e, "hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices) return set_err(MLRS_ERR_UNSUPPORTED, "device", dev, 0, 0, 0, "device ordinal %d out of range", dev);
+    int32_t rc = current_device(&dev);
+    if (rc) return rc;
+    hipError_t e;
     Arena& A = g_arena[dev];
     if (A.cus == 0) {
         int n = 0;
@@ -112,8 +188,9 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
     }
     *cus = A.cus;
     if (bytes == 0) bytes = 256;
+    rc = order_after_last_call(dev, s);
+    if (rc) return rc;
     if (A.cap < bytes) {
-        // Earlier work may still read the old buffer: drain the device first.
         if (A.base) {
             e = hipDeviceSynchronize();
             if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
@@ -131,7 +208,6 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
         A.cap = want;
     }
     *out = A.base;
-    (void)s;
     return MLRS_OK;
 }
 
@@ -240,20 +316,22 @@ int pick_strips_xcd(int64_t nblocks, int64_t nt, int64_t slots_per_xcd, int64_t 
 template <typename T>
 int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, int k, int arm, int mode,
                     T* out_v, uint32_t* out_i, hipStream_t s, double p = 2.0) {
-    if (k > select_rows_max_k())
-        return set_err(MLRS_ERR_UNSUPPORTED, "k", 1, k, nt, 0, "k=%d above the largest k served (%d)", k,
-                       select_rows_max_k());
     const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
+    // per query row of a tile: its exact values plus the selection's scratch
+    const size_t fixed = 4 * aligned_bytes(sizeof(T) * (nq + nt)) + 4096;
+    const size_t per_row = sizeof(T) * (size_t)std::max<int64_t>(nt, 1) + select_rows_scratch_bytes(1, k, sizeof(T));
     const size_t tile_budget = (size_t)256 << 20;
-    int64_t qt = (int64_t)(tile_budget / (sizeof(T) * (size_t)std::max<int64_t>(nt, 1)));
+    int64_t qt = (int64_t)(tile_budget / per_row);
     qt = std::max<int64_t>(1, std::min<int64_t>(qt, nq));
-    size_t bytes = aligned_bytes(sizeof(T) * (size_t)qt * nt) + 4 * aligned_bytes(sizeof(T) * (nq + nt)) + 4096;
+    const size_t sel_bytes = select_rows_scratch_bytes(qt, k, sizeof(T));
+    size_t bytes = aligned_bytes(sizeof(T) * (size_t)qt * nt) + sel_bytes + fixed;
     char* ws;
     int cus;
     int32_t rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
     T* dist = cv.take<T>((size_t)qt * nt);
+    void* sel = sel_bytes ? (void*)cv.take<char>(sel_bytes) : nullptr;
     T* qa = nullptr;
     T* xa = nullptr;
     if (cos) {
@@ -282,7 +360,7 @@ int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d,
                                         nt, 0, s, (T)p, minkowski_powi(p));
         }
         if (e == hipSuccess)
-            e = launch_select_rows<T>(dist, rows, nt, nt, k, mode, out_v + q0 * k, out_i + q0 * k, s);
+            e = launch_select_rows<T>(dist, rows, nt, nt, k, mode, out_v + q0 * k, out_i + q0 * k, sel, s);
         if (e != hipSuccess) return hip_err(e, "generic kNN");
     }
     // Minkowski's boundary root over the emitted values, exponent
@@ -590,20 +668,15 @@ int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric) 
     (void)dtype_bytes;
     (void)n_features;
     (void)metric;
-    return select_rows_max_k();
+    return INT32_MAX;  // every 1 <= k <= n_train
 }
 
-int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
-                          const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
-                          double p, float* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    int32_t rc = validate_knn<float>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
-                                     out_dist, out_idx, out_len);
-    if (rc) return rc;
-    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0))
-        return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
-    if (n_query == 0) return MLRS_OK;
-    hipStream_t s = (hipStream_t)stream;
+}  // extern "C"
+
+namespace {
+int32_t knn_topk_f32_dispatch(const float* xq, int64_t n_query, int64_t n_features, const float* x_train,
+                              int64_t n_train, int32_t k, int32_t metric, double p, float* out_dist,
+                              uint32_t* out_idx, hipStream_t s) {
     const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
     const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
@@ -620,10 +693,36 @@ int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int6
     return knn_generic<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s, p);
 }
 
+int32_t knn_topk_f32_validate(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                              const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
+                              double p, float* out_dist, uint32_t* out_idx, int64_t out_len) {
+    int32_t rc = validate_knn<float>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
+                                     out_dist, out_idx, out_len);
+    if (rc) return rc;
+    if (metric == MLRS_METRIC_MINKOWSKI && !(p >= 1.0))
+        return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
+    return MLRS_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                          const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
+                          double p, float* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
+    CallGuard cg;
+    int32_t rc = knn_topk_f32_validate(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric, p,
+                                       out_dist, out_idx, out_len);
+    if (rc) return rc;
+    if (n_query == 0) return MLRS_OK;
+    return knn_topk_f32_dispatch(xq, n_query, n_features, x_train, n_train, k, metric, p, out_dist, out_idx,
+                                 (hipStream_t)stream);
+}
+
 int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
                           const double* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
                           double p, double* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     int32_t rc = validate_knn<double>(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric,
                                       out_dist, out_idx, out_len);
     if (rc) return rc;
@@ -664,7 +763,7 @@ static int32_t validate_kmeans(const T* x, int64_t x_len, int64_t n, int64_t d, 
 int32_t mlrs_kmeans_assign_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features, const float* centers,
                                int64_t centers_len, int64_t n_centers, uint32_t* labels, int64_t labels_len,
                                float* sqdist, int64_t dist_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     int32_t rc = validate_kmeans<float>(x, x_len, n, n_features, centers, centers_len, n_centers, labels,
                                         labels_len, sqdist, dist_len);
     if (rc) return rc;
@@ -678,7 +777,7 @@ int32_t mlrs_kmeans_assign_f32(const float* x, int64_t x_len, int64_t n, int64_t
 int32_t mlrs_kmeans_assign_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features,
                                const double* centers, int64_t centers_len, int64_t n_centers, uint32_t* labels,
                                int64_t labels_len, double* sqdist, int64_t dist_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     int32_t rc = validate_kmeans<double>(x, x_len, n, n_features, centers, centers_len, n_centers, labels,
                                          labels_len, sqdist, dist_len);
     if (rc) return rc;
@@ -693,7 +792,7 @@ template <typename T>
 static int32_t pairwise_impl(const T* x, int64_t x_len, int64_t rows_x, int64_t cols, const T* y, int64_t y_len,
                              int64_t rows_y, int64_t cols_y, int32_t metric, int32_t do_sqrt, double p, T* out,
                              int64_t out_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     if (!geom_ok(rows_x, cols, x_len)) return shape_err("x", rows_x, cols, x_len);
     if (!geom_ok(rows_y, cols_y, y_len)) return shape_err("y", rows_y, cols_y, y_len);
     if (cols != cols_y) return dim_err("cols", cols, cols_y);
@@ -765,7 +864,7 @@ extern "C++" {
 template <typename T>
 static int32_t sqnorms_impl(const T* x, int64_t x_len, int64_t n, int64_t d, T* out, int64_t out_len,
                             void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     if (!geom_ok(n, d, x_len)) return shape_err("x", n, d, x_len);
     if (out_len != n) return shape_err("out", n, 1, out_len);
     if (n == 0) return MLRS_OK;
@@ -805,7 +904,7 @@ template <typename T>
 static int32_t regress_impl(const T* y, int64_t y_len, int64_t n_train, int64_t n_out, const uint32_t* idx,
                             int64_t idx_len, const T* dist, int64_t dist_len, int64_t nq, int32_t k,
                             int32_t weighted, T* out, int64_t out_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     // knn_regress_gather_weighted / knn_regress_mean_gather's checks
     // (crates/mlrs-backend/src/prims/knn.rs:59-323)
     if (k < 1 || nq < 1 || n_out < 1 || n_train < 1) return shape_err("k", nq, k, idx_len);
@@ -840,7 +939,7 @@ static int32_t classify_impl(const int32_t* y_class, int64_t n_train, int32_t n_
                              int64_t idx_len, const T* dist, int64_t dist_len, int64_t nq, int32_t k,
                              int32_t weighted, T* proba, int64_t proba_len, int32_t* labels, int64_t labels_len,
                              void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     if (k < 1 || nq < 1 || n_train < 1) return shape_err("k", nq, k, idx_len);
     if (!geom_ok(nq, k, idx_len)) return shape_err("idx", nq, k, idx_len);
     if (weighted && dist_len != idx_len) return shape_err("dist", nq, k, dist_len);
@@ -1023,7 +1122,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
                            int64_t nt, int64_t d_train, int32_t metric, double p, double radius, uint32_t* counts,
                            int64_t counts_len, T* out_dist, int32_t* out_idx, int64_t capacity, int64_t* total,
                            void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     // validate_radius_query (nearest.rs:755-797) and radius_host_scan's
     // geometry checks (radius_host.rs:150-196)
     if (!(radius >= 0.0))
@@ -1307,12 +1406,13 @@ extern "C++" {
 // search, whose own workspace() calls may move the main arena.
 Arena g_aux[kMaxDevices];
 
-static int32_t aux_workspace(size_t bytes, char** out) {
+static int32_t aux_workspace(size_t bytes, hipStream_t s, char** out) {
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_err(e, "hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices)
-        return set_err(MLRS_ERR_UNSUPPORTED, "device", dev, 0, 0, 0, "device ordinal %d out of range", dev);
+    int32_t rc = current_device(&dev);
+    if (rc) return rc;
+    rc = order_after_last_call(dev, s);
+    if (rc) return rc;
+    hipError_t e;
     Arena& A = g_aux[dev];
     if (A.cap < bytes) {
         if (A.base) {
@@ -1386,7 +1486,7 @@ static int32_t graph_search(const TIn* x, int64_t n, int64_t d, int kk, int32_t 
                    2 * aligned_bytes(sizeof(double) * (size_t)n * d) + 2 * aligned_bytes(sizeof(double) * (size_t)n) +
                    1024;
     char* aux;
-    int32_t rc = aux_workspace(bytes, &aux);
+    int32_t rc = aux_workspace(bytes, s, &aux);
     if (rc) return rc;
     Carver cv(aux);
     *val = cv.take<double>((size_t)n * kk);
@@ -1416,21 +1516,19 @@ template <typename TIn>
 static int32_t knn_graph_impl(const TIn* x, int64_t x_len, int64_t n, int64_t d, int64_t k, int32_t metric,
                               double p, int32_t include_self, uint32_t* out_idx, double* out_dist, int64_t out_len,
                               void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     int32_t rc = validate_graph(x, x_len, n, d, k, metric, p, include_self != 0);
     if (rc) return rc;
     if (!geom_ok(n, k, out_len)) return shape_err("out", n, k, out_len);
     if (!out_idx || !out_dist) return set_err(MLRS_ERR_NULL_POINTER, "out", 0, 0, 0, 0, "null pointer");
-    const int kk = (int)(include_self ? k : k + 1);
-    if (kk > select_rows_max_k())
-        return set_err(MLRS_ERR_UNSUPPORTED, "k", 1, k, n, 0, "k=%lld above the largest k served (%d)",
-                       (long long)k, select_rows_max_k() - (include_self ? 0 : 1));
+    const int64_t kk = include_self ? k : k + 1;
+    if (kk > INT32_MAX) return shape_err("k", 1, k, INT32_MAX);
     hipStream_t s = (hipStream_t)stream;
     double* val;
     uint32_t* idx;
-    rc = graph_search<TIn>(x, n, d, kk, metric, p, s, &val, &idx);
+    rc = graph_search<TIn>(x, n, d, (int)kk, metric, p, s, &val, &idx);
     if (rc) return rc;
-    hipError_t e = launch_graph_finish(val, idx, n, kk, (int)k, include_self ? 0 : 1,
+    hipError_t e = launch_graph_finish(val, idx, n, (int)kk, (int)k, include_self ? 0 : 1,
                                        metric == MLRS_METRIC_COSINE ? 1 : 0, out_dist, out_idx, s);
     if (e != hipSuccess) return hip_err(e, "graph finish");
     return ok();
@@ -1439,7 +1537,7 @@ static int32_t knn_graph_impl(const TIn* x, int64_t x_len, int64_t n, int64_t d,
 template <typename TIn>
 static int32_t core_impl(const TIn* x, int64_t x_len, int64_t n, int64_t d, int32_t metric, double p,
                          int64_t min_samples, double* out, int64_t out_len, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     // k = min_samples clamped to [1, n] (hdbscan.rs:1508-1510)
     const int64_t k = std::max<int64_t>(1, std::min<int64_t>(min_samples, n));
     int32_t rc = validate_graph(x, x_len, n, d, n >= 1 ? k : 1, metric, p, true);
@@ -1449,9 +1547,7 @@ static int32_t core_impl(const TIn* x, int64_t x_len, int64_t n, int64_t d, int3
                        "cosine core distances come from the dense cosine matrix, not a kNN scan");
     if (out_len != n) return shape_err("out", n, 1, out_len);
     if (!out) return set_err(MLRS_ERR_NULL_POINTER, "out", 0, 0, 0, 0, "null pointer");
-    if (k > select_rows_max_k())
-        return set_err(MLRS_ERR_UNSUPPORTED, "min_samples", 1, k, n, 0, "min_samples=%lld above the largest served (%d)",
-                       (long long)k, select_rows_max_k());
+    if (k > INT32_MAX) return shape_err("min_samples", 1, k, INT32_MAX);
     hipStream_t s = (hipStream_t)stream;
     double* val;
     uint32_t* idx;
@@ -1546,7 +1642,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                                const T* init, int64_t init_len, uint64_t seed, int64_t n_init, int64_t max_iter,
                                double tol, T* out_centers, int64_t centers_len, uint32_t* out_labels,
                                int64_t labels_len, double* out_inertia, int64_t* out_n_iter, void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    CallGuard cg;
     if (k < 1 || k > n)
         return set_err(MLRS_ERR_INVALID_PARAM, "k", 1, k, n, 0,
                        "estimator 'kmeans': k = %lld is out of range (must be 1..=%lld = n_samples)", (long long)k,
@@ -1579,7 +1675,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                    aligned_bytes(sizeof(T) * (size_t)std::max(nbi, nbv * d)) + aligned_bytes(sizeof(T) * d) +
                    aligned_bytes(sizeof(int64_t) * k) + 1024;
     char* aux;
-    int32_t rc = aux_workspace(bytes, &aux);
+    int32_t rc = aux_workspace(bytes, s, &aux);
     if (rc) return rc;
     Carver cv(aux);
     uint32_t* lab[2] = {cv.take<uint32_t>(n), cv.take<uint32_t>(n)};
@@ -1790,10 +1886,18 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                 // reference's select_nth_unstable_by + sort_by, :1347-1359)
                 std::vector<int64_t> order((size_t)n);
                 for (int64_t i = 0; i < n; ++i) order[i] = i;
+                // A total order (std::nth_element / std::sort need one): a NaN
+                // distance ranks above every number, NaNs and equal values by
+                // index.  On numbers it is the reference's (distance desc,
+                // index asc).
                 auto by_rank = [&](int64_t a, int64_t b) {
                     const double da = (double)dist_h[a], db = (double)dist_h[b];
-                    if (db < da) return true;
-                    if (da < db) return false;
+                    const bool na = da != da, nb = db != db;
+                    if (na != nb) return na;
+                    if (!na) {
+                        if (db < da) return true;
+                        if (da < db) return false;
+                    }
                     return a < b;
                 };
                 const int64_t m_top = std::min<int64_t>(8 * empties + 64, n);

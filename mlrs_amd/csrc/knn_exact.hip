@@ -2,7 +2,7 @@
 // the per-row (value, index) top-k selection over a materialized matrix.
 //
 // Together the last two are the engine's generic path -- any d, any k up to
-// select_rows_max_k(), any arm, f32 or f64 -- the MI355X counterpart of the
+// the row length, any arm, f32 or f64 -- the MI355X counterpart of the
 // reference's two-kernel distance_direct -> top_k composition
 // (crates/mlrs-algos/src/neighbors/nearest.rs:1117-1343,
 // crates/mlrs-backend/src/prims/distance.rs:428-551, prims/topk.rs:62-186).
@@ -265,117 +265,161 @@ template <> struct KeyOf<double> {
     }
 };
 
+// LDS-resident selection serves k up to SEL_MAXK; larger k collects into the
+// output rows and sorts there (select_collect_kernel and below).
 constexpr int SEL_MAXK = 256;
 
+// Shared state of one row's radix select (one 256-thread workgroup per row).
+template <typename K>
+struct RadixShared {
+    uint32_t hist[256];
+    uint32_t cnt_less, cnt_eq, nvalid;
+    uint32_t wave_less[4], wave_eq[4];
+    K prefix;
+    uint32_t want;
+};
+
+// Number of admissible (non-NaN) values of the row.
+template <typename T>
+__device__ uint32_t row_count_valid(const T* __restrict__ dr, int64_t cols, RadixShared<typename KeyOf<T>::K>& sh) {
+    const int tid = threadIdx.x;
+    if (tid == 0) sh.nvalid = 0;
+    __syncthreads();
+    uint32_t local = 0;
+    for (int64_t c = tid; c < cols; c += 256) {
+        const T v = dr[c];
+        local += (v == v) ? 1u : 0u;
+    }
+    atomicAdd(&sh.nvalid, local);
+    __syncthreads();
+    return sh.nvalid;
+}
+
+// Radix select, 8 bits per pass from the top: `prefix` becomes the kk-th
+// smallest key of the row (NaN excluded) and `want` how many of its copies
+// belong to the kk smallest (the lowest-index ones).
+template <typename T>
+__device__ void row_radix_kth(const T* __restrict__ dr, int64_t cols, uint32_t kk,
+                              RadixShared<typename KeyOf<T>::K>& sh, typename KeyOf<T>::K& prefix,
+                              uint32_t& want) {
+    typedef typename KeyOf<T>::K K;
+    const int tid = threadIdx.x;
+    K pmask = 0;
+    prefix = 0;
+    want = kk;
+    for (int shift = KeyOf<T>::BITS - 8; shift >= 0; shift -= 8) {
+        sh.hist[tid] = 0;
+        __syncthreads();
+        for (int64_t c = tid; c < cols; c += 256) {
+            const T v = dr[c];
+            if (v != v) continue;
+            const K key = KeyOf<T>::key(v);
+            if ((key & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t w = want;
+            int b = 0;
+            for (; b < 255; ++b) {
+                if (sh.hist[b] >= w) break;
+                w -= sh.hist[b];
+            }
+            sh.prefix = prefix | ((K)b << shift);
+            sh.want = w;
+        }
+        __syncthreads();
+        prefix = sh.prefix;
+        want = sh.want;
+        pmask |= ((K)255 << shift);
+        __syncthreads();
+    }
+}
+
+// The kk smallest pairs of the row, in ascending column order within each
+// class: every key below `prefix` goes to slot [0, kk - want) and the first
+// `want` copies of `prefix` to [kk - want, kk).  put(slot, key, column).
+template <typename T, typename Put>
+__device__ void row_collect(const T* __restrict__ dr, int64_t cols, uint32_t kk, typename KeyOf<T>::K prefix,
+                            uint32_t want, RadixShared<typename KeyOf<T>::K>& sh, Put put) {
+    typedef typename KeyOf<T>::K K;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t n_less = kk - want;
+    if (tid == 0) {
+        sh.cnt_less = 0;
+        sh.cnt_eq = 0;
+    }
+    __syncthreads();
+    for (int64_t base = 0; base < cols; base += 256) {
+        const int64_t c = base + tid;
+        bool is_less = false, is_eq = false;
+        K key = 0;
+        if (c < cols) {
+            const T v = dr[c];
+            if (v == v) {
+                key = KeyOf<T>::key(v);
+                is_less = key < prefix;
+                is_eq = key == prefix;
+            }
+        }
+        const uint64_t bl = __builtin_amdgcn_ballot_w64(is_less);
+        const uint64_t be = __builtin_amdgcn_ballot_w64(is_eq);
+        if (lane == 0) {
+            sh.wave_less[wv] = (uint32_t)__builtin_popcountll(bl);
+            sh.wave_eq[wv] = (uint32_t)__builtin_popcountll(be);
+        }
+        __syncthreads();
+        uint32_t before_l = sh.cnt_less, before_e = sh.cnt_eq;
+        for (int w2 = 0; w2 < wv; ++w2) {
+            before_l += sh.wave_less[w2];
+            before_e += sh.wave_eq[w2];
+        }
+        if (is_less) {
+            const uint32_t r = before_l + (uint32_t)__builtin_popcountll(bl & below);
+            if (r < n_less) put(r, key, (uint32_t)c);  // always true: kk - want keys lie below prefix
+        }
+        if (is_eq) {
+            const uint32_t r = before_e + (uint32_t)__builtin_popcountll(be & below);
+            if (r < want) put(n_less + r, key, (uint32_t)c);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            sh.cnt_less += sh.wave_less[0] + sh.wave_less[1] + sh.wave_less[2] + sh.wave_less[3];
+            sh.cnt_eq += sh.wave_eq[0] + sh.wave_eq[1] + sh.wave_eq[2] + sh.wave_eq[3];
+        }
+        __syncthreads();
+    }
+}
+
+// k <= SEL_MAXK: the kk pairs are collected and bitonic-sorted in LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void select_rows_kernel(const T* __restrict__ dist, int64_t rows,
                                                           int64_t cols, int64_t ld, int k, int mode,
                                                           T* __restrict__ out_val,
                                                           uint32_t* __restrict__ out_idx) {
     typedef typename KeyOf<T>::K K;
-    __shared__ uint32_t hist[256];
+    __shared__ RadixShared<K> sh;
     __shared__ K skey[SEL_MAXK];
     __shared__ uint32_t sidx[SEL_MAXK];
-    __shared__ uint32_t s_cnt_less, s_cnt_eq, s_nvalid;
-    __shared__ uint32_t s_wave_eq[4];
-    __shared__ K s_prefix;
-    __shared__ uint32_t s_want;
 
     const int64_t row = blockIdx.x;
     if (row >= rows) return;
     const T* dr = dist + row * ld;
     const int tid = threadIdx.x;
 
-    // 1. count admissible (non-NaN) values
-    if (tid == 0) s_nvalid = 0;
-    __syncthreads();
-    uint32_t local = 0;
-    for (int64_t c = tid; c < cols; c += 256) {
-        T v = dr[c];
-        local += (v == v) ? 1u : 0u;
-    }
-    atomicAdd(&s_nvalid, local);
-    __syncthreads();
-    const uint32_t nvalid = s_nvalid;
+    const uint32_t nvalid = row_count_valid<T>(dr, cols, sh);
     const int kk = (int)((uint32_t)k < nvalid ? (uint32_t)k : nvalid);
 
     if (kk > 0) {
-        // 2. radix select of the kk-th smallest key
-        K prefix = 0, pmask = 0;
-        uint32_t want = (uint32_t)kk;
-        for (int shift = KeyOf<T>::BITS - 8; shift >= 0; shift -= 8) {
-            hist[tid] = 0;
-            __syncthreads();
-            for (int64_t c = tid; c < cols; c += 256) {
-                T v = dr[c];
-                if (v != v) continue;
-                K key = KeyOf<T>::key(v);
-                if ((key & pmask) == prefix) atomicAdd(&hist[(uint32_t)(key >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            if (tid == 0) {
-                uint32_t w = want;
-                int b = 0;
-                for (; b < 255; ++b) {
-                    if (hist[b] >= w) break;
-                    w -= hist[b];
-                }
-                s_prefix = prefix | ((K)b << shift);
-                s_want = w;
-            }
-            __syncthreads();
-            prefix = s_prefix;
-            want = s_want;
-            pmask |= ((K)255 << shift);
-            __syncthreads();
-        }
-        // prefix = kk-th smallest key; `want` of its copies are taken, lowest index first.
-        // 3. collect
-        if (tid == 0) {
-            s_cnt_less = 0;
-            s_cnt_eq = 0;
-        }
-        __syncthreads();
-        const uint32_t n_less = (uint32_t)kk - want;
-        for (int64_t base = 0; base < cols; base += 256) {
-            int64_t c = base + tid;
-            bool is_less = false, is_eq = false;
-            K key = 0;
-            if (c < cols) {
-                T v = dr[c];
-                if (v == v) {
-                    key = KeyOf<T>::key(v);
-                    is_less = key < prefix;
-                    is_eq = key == prefix;
-                }
-            }
-            if (is_less) {
-                uint32_t p = atomicAdd(&s_cnt_less, 1u);
-                if (p < n_less) {  // always true; keeps every store inside skey
-                    skey[p] = key;
-                    sidx[p] = (uint32_t)c;
-                }
-            }
-            // index-ordered rank among equal keys in this chunk
-            uint64_t bal = __builtin_amdgcn_ballot_w64(is_eq);
-            int lane = tid & 63, wv = tid >> 6;
-            uint32_t below = (uint32_t)__builtin_popcountll(bal & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-            if (lane == 0) s_wave_eq[wv] = (uint32_t)__builtin_popcountll(bal);
-            __syncthreads();
-            uint32_t before = s_cnt_eq;
-            for (int w2 = 0; w2 < wv; ++w2) before += s_wave_eq[w2];
-            if (is_eq) {
-                uint32_t r = before + below;
-                if (r < want && n_less + r < (uint32_t)kk) {
-                    skey[n_less + r] = key;
-                    sidx[n_less + r] = (uint32_t)c;
-                }
-            }
-            __syncthreads();
-            if (tid == 0) s_cnt_eq += s_wave_eq[0] + s_wave_eq[1] + s_wave_eq[2] + s_wave_eq[3];
-            __syncthreads();
-        }
-        // 4. bitonic sort of the kk kept pairs by (key, index)
+        K prefix;
+        uint32_t want;
+        row_radix_kth<T>(dr, cols, (uint32_t)kk, sh, prefix, want);
+        row_collect<T>(dr, cols, (uint32_t)kk, prefix, want, sh, [&](uint32_t slot, K key, uint32_t c) {
+            skey[slot] = key;
+            sidx[slot] = c;
+        });
+        // bitonic sort of the kk kept pairs by (key, index)
         int n2 = 1;
         while (n2 < kk) n2 <<= 1;
         for (int e = kk + tid; e < n2; e += 256) {
@@ -404,7 +448,7 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const T* __restrict__ 
             }
         }
     }
-    // 5. emit (value recovered from the key: exact, since the key map is a bijection)
+    // emit (value recovered from the key: exact, since the key map is a bijection)
     for (int s = tid; s < k; s += 256) {
         T v;
         uint32_t ix;
@@ -419,6 +463,169 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const T* __restrict__ 
         out_val[row * k + s] = v;
         out_idx[row * k + s] = ix;
     }
+}
+
+// ---------------------------------------------------------------------------
+// k > SEL_MAXK (any k up to the row length, the reference's top_k contract,
+// crates/mlrs-backend/src/prims/topk.rs:208-212): the same radix select, the
+// kk pairs collected straight into the row's output slots (keys in the value
+// slots, which have the key's width), then sorted by (key, index) -- in LDS
+// when kk fits one chunk, else chunk sorts in LDS followed by merge passes
+// through a scratch copy -- and finally mapped back to values.  (key, index)
+// pairs are distinct, so every step is a total order with no ties.
+// ---------------------------------------------------------------------------
+template <typename T> struct SortChunk;
+template <> struct SortChunk<float> { static constexpr int N = 8192; };   // 64 KB of (key, index)
+template <> struct SortChunk<double> { static constexpr int N = 4096; };  // 48 KB
+
+template <typename K>
+__device__ __forceinline__ bool pair_gt(K ka, uint32_t ia, K kb, uint32_t ib) {
+    return (ka > kb) || (ka == kb && ia > ib);
+}
+
+// One workgroup per row: kk = min(k, admissible values) pairs into
+// okey/oidx[row*k + 0..kk), and nk[row] = kk.
+template <typename T>
+__global__ __launch_bounds__(256) void select_collect_kernel(const T* __restrict__ dist, int64_t rows,
+                                                             int64_t cols, int64_t ld, int k,
+                                                             typename KeyOf<T>::K* __restrict__ okey,
+                                                             uint32_t* __restrict__ oidx, uint32_t* __restrict__ nk) {
+    typedef typename KeyOf<T>::K K;
+    __shared__ RadixShared<K> sh;
+    const int64_t row = blockIdx.x;
+    if (row >= rows) return;
+    const T* dr = dist + row * ld;
+    const uint32_t nvalid = row_count_valid<T>(dr, cols, sh);
+    const uint32_t kk = (uint32_t)k < nvalid ? (uint32_t)k : nvalid;
+    if (threadIdx.x == 0) nk[row] = kk;
+    if (kk == 0) return;
+    K prefix;
+    uint32_t want;
+    row_radix_kth<T>(dr, cols, kk, sh, prefix, want);
+    K* rk = okey + row * (int64_t)k;
+    uint32_t* ri = oidx + row * (int64_t)k;
+    row_collect<T>(dr, cols, kk, prefix, want, sh, [&](uint32_t slot, K key, uint32_t c) {
+        rk[slot] = key;
+        ri[slot] = c;
+    });
+}
+
+// Sort chunk `ch` ([ch*N, min((ch+1)*N, kk)) of row r) in LDS, in place.
+// Workgroup b = r * nchunks + ch.
+template <typename T>
+__global__ __launch_bounds__(512) void select_sort_chunk_kernel(typename KeyOf<T>::K* __restrict__ key,
+                                                                uint32_t* __restrict__ idx,
+                                                                const uint32_t* __restrict__ nk, int64_t rows,
+                                                                int k, int nchunks) {
+    typedef typename KeyOf<T>::K K;
+    constexpr int N = SortChunk<T>::N;
+    __shared__ K sk[N];
+    __shared__ uint32_t si[N];
+    const int64_t r = (int64_t)blockIdx.x / nchunks;
+    const int ch = (int)((int64_t)blockIdx.x - r * nchunks);
+    if (r >= rows) return;
+    const int64_t kk = nk[r];
+    const int64_t lo = (int64_t)ch * N;
+    if (lo >= kk) return;
+    const int n = (int)((kk - lo) < N ? (kk - lo) : N);
+    int n2 = 1;
+    while (n2 < n) n2 <<= 1;
+    K* rk = key + r * (int64_t)k + lo;
+    uint32_t* ri = idx + r * (int64_t)k + lo;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < n2; e += 512) {
+        sk[e] = e < n ? rk[e] : ~(K)0;
+        si[e] = e < n ? ri[e] : kSentinelIdx;
+    }
+    __syncthreads();
+    for (int size = 2; size <= n2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int e = tid; e < n2; e += 512) {
+                const int p = e ^ stride;
+                if (p > e) {
+                    const bool up = (e & size) == 0;
+                    const K ka = sk[e], kb = sk[p];
+                    const uint32_t ia = si[e], ib = si[p];
+                    if (pair_gt<K>(ka, ia, kb, ib) == up) {
+                        sk[e] = kb;
+                        sk[p] = ka;
+                        si[e] = ib;
+                        si[p] = ia;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int e = tid; e < n; e += 512) {
+        rk[e] = sk[e];
+        ri[e] = si[e];
+    }
+}
+
+// One merge pass: sorted runs of length L within [0, kk) of every row are
+// merged pairwise into runs of 2L (src -> dst).  An element's place is its
+// rank in its own run plus the number of smaller elements of the partner run
+// (binary search).  Workgroup b covers elements [c*256, c*256+256) of row
+// b / nblk, c = b % nblk.
+template <typename K>
+__global__ __launch_bounds__(256) void select_merge_kernel(const K* __restrict__ skey, const uint32_t* __restrict__ sidx,
+                                                           K* __restrict__ dkey, uint32_t* __restrict__ didx,
+                                                           const uint32_t* __restrict__ nk, int64_t rows, int k,
+                                                           int64_t L, int64_t nblk) {
+    const int64_t r = (int64_t)blockIdx.x / nblk;
+    const int64_t c = (int64_t)blockIdx.x - r * nblk;
+    if (r >= rows) return;
+    const int64_t kk = nk[r];
+    const int64_t i = c * 256 + threadIdx.x;
+    if (i >= kk) return;
+    const K* rk = skey + r * (int64_t)k;
+    const uint32_t* ri = sidx + r * (int64_t)k;
+    const K ek = rk[i];
+    const uint32_t ei = ri[i];
+    const int64_t s = (i / (2 * L)) * (2 * L);
+    const bool in_a = i < s + L;
+    // the partner run [plo, phi)
+    const int64_t plo = in_a ? s + L : s;
+    int64_t phi = in_a ? s + 2 * L : s + L;
+    if (phi > kk) phi = kk;
+    int64_t lo = plo, hi = phi > plo ? phi : plo;  // first partner element greater than (ek, ei)
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (pair_gt<K>(ek, ei, rk[mid], ri[mid])) lo = mid + 1;
+        else hi = mid;
+    }
+    const int64_t own = in_a ? i - s : i - s - L;
+    const int64_t pos = s + own + (lo - plo);
+    dkey[r * (int64_t)k + pos] = ek;
+    didx[r * (int64_t)k + pos] = ei;
+}
+
+// Keys back to values with the output transform; slots past kk get (+inf, 0).
+template <typename T>
+__global__ __launch_bounds__(256) void select_finish_kernel(const typename KeyOf<T>::K* __restrict__ skey,
+                                                            const uint32_t* __restrict__ sidx,
+                                                            const uint32_t* __restrict__ nk, int64_t rows, int k,
+                                                            int mode, int64_t nblk, T* __restrict__ out_val,
+                                                            uint32_t* __restrict__ out_idx) {
+    const int64_t r = (int64_t)blockIdx.x / nblk;
+    const int64_t c = (int64_t)blockIdx.x - r * nblk;
+    if (r >= rows) return;
+    const int64_t i = c * 256 + threadIdx.x;
+    if (i >= k) return;
+    const int64_t o = r * (int64_t)k + i;
+    T v;
+    uint32_t ix;
+    if (i < (int64_t)nk[r]) {
+        v = KeyOf<T>::val(skey[o]);
+        ix = sidx[o];
+    } else {
+        v = FloatTraits<T>::inf();
+        ix = 0;
+    }
+    if (mode == EMIT_SQRT) v = FloatTraits<T>::sqrt_(v);
+    out_val[o] = v;
+    out_idx[o] = ix;
 }
 
 // argmin_dist_rows (crates/mlrs-kernels/src/kmeans.rs:284-310) over a
@@ -620,20 +827,71 @@ hipError_t launch_pow_inplace(T* v, int64_t n, T e, hipStream_t s) {
     return hipGetLastError();
 }
 
-int select_rows_max_k() { return SEL_MAXK; }
+size_t select_rows_scratch_bytes(int64_t rows, int k, int elem_bytes) {
+    if (k <= SEL_MAXK || rows <= 0) return 0;
+    const int chunk = elem_bytes == 4 ? SortChunk<float>::N : SortChunk<double>::N;
+    size_t b = ((size_t)rows * 4 + 255) & ~(size_t)255;
+    if (k > chunk) {
+        b += (((size_t)rows * k * elem_bytes + 255) & ~(size_t)255);
+        b += (((size_t)rows * k * 4 + 255) & ~(size_t)255);
+    }
+    return b;
+}
 
 template <typename T>
 hipError_t launch_select_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, int k, int mode,
-                              T* out_val, uint32_t* out_idx, hipStream_t s) {
+                              T* out_val, uint32_t* out_idx, void* scratch, hipStream_t s) {
+    typedef typename KeyOf<T>::K K;
     if (rows == 0) return hipSuccess;
-    if (k < 1 || k > SEL_MAXK) return hipErrorInvalidValue;
+    if (k < 1) return hipErrorInvalidValue;
     if (k <= 64) {
         hipLaunchKernelGGL((select_small_kernel<T>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, dist, rows,
                            cols, ld, k, mode, out_val, out_idx);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((select_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, s, dist, rows, cols,
-                       ld, k, mode, out_val, out_idx);
+    if (k <= SEL_MAXK) {
+        hipLaunchKernelGGL((select_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, s, dist, rows, cols,
+                           ld, k, mode, out_val, out_idx);
+        return hipGetLastError();
+    }
+    // k > SEL_MAXK: collect into the outputs (keys in the value slots), sort, finish
+    if (!scratch) return hipErrorInvalidValue;
+    constexpr int N = SortChunk<T>::N;
+    char* sp = static_cast<char*>(scratch);
+    uint32_t* nk = reinterpret_cast<uint32_t*>(sp);
+    sp += ((size_t)rows * 4 + 255) & ~(size_t)255;
+    K* okey = reinterpret_cast<K*>(out_val);
+    hipLaunchKernelGGL((select_collect_kernel<T>), dim3((unsigned)rows), dim3(256), 0, s, dist, rows, cols, ld, k,
+                       okey, out_idx, nk);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nchunks = (k + N - 1) / N;
+    hipLaunchKernelGGL((select_sort_chunk_kernel<T>), dim3((unsigned)(rows * nchunks)), dim3(512), 0, s, okey,
+                       out_idx, nk, rows, k, nchunks);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t nblk = (k + 255) / 256;
+    const K* src_k = okey;
+    const uint32_t* src_i = out_idx;
+    if (nchunks > 1) {
+        K* tk = reinterpret_cast<K*>(sp);
+        sp += ((size_t)rows * k * sizeof(K) + 255) & ~(size_t)255;
+        uint32_t* ti = reinterpret_cast<uint32_t*>(sp);
+        K* bufk[2] = {okey, tk};
+        uint32_t* bufi[2] = {out_idx, ti};
+        int cur = 0;
+        for (int64_t L = N; L < k; L *= 2) {
+            hipLaunchKernelGGL((select_merge_kernel<K>), dim3((unsigned)(rows * nblk)), dim3(256), 0, s, bufk[cur],
+                               bufi[cur], bufk[cur ^ 1], bufi[cur ^ 1], nk, rows, k, L, nblk);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            cur ^= 1;
+        }
+        src_k = bufk[cur];
+        src_i = bufi[cur];
+    }
+    hipLaunchKernelGGL((select_finish_kernel<T>), dim3((unsigned)(rows * nblk)), dim3(256), 0, s, src_k, src_i, nk,
+                       rows, k, mode, nblk, out_val, out_idx);
     return hipGetLastError();
 }
 
@@ -650,8 +908,8 @@ template hipError_t launch_pairwise_tile<double>(const double*, int64_t, const d
                                                  int, const double*, const double*, double*, int64_t, int,
                                                  hipStream_t, double, int, double);
 template hipError_t launch_select_rows<float>(const float*, int64_t, int64_t, int64_t, int, int, float*,
-                                              uint32_t*, hipStream_t);
+                                              uint32_t*, void*, hipStream_t);
 template hipError_t launch_select_rows<double>(const double*, int64_t, int64_t, int64_t, int, int, double*,
-                                               uint32_t*, hipStream_t);
+                                               uint32_t*, void*, hipStream_t);
 
 }  // namespace mlrs

@@ -184,11 +184,14 @@ template <typename T>
 hipError_t launch_pow_inplace(T* v, int64_t n, T e, hipStream_t s);
 
 // Generic exact path: per-row (value, index) top-k over a materialized
-// rows x cols matrix, NaN never admitted, sentinel-padded.
+// rows x cols matrix, NaN never admitted, sentinel-padded; any k >= 1.  For k
+// above 256 the pairs are collected into the output rows and sorted there,
+// with select_rows_scratch_bytes(rows, k, sizeof(T)) bytes of `scratch`
+// (256-byte aligned; unused, and may be null, for k <= 256).
 template <typename T>
 hipError_t launch_select_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, int k,
-                              int mode, T* out_val, uint32_t* out_idx, hipStream_t s);
-int select_rows_max_k();
+                              int mode, T* out_val, uint32_t* out_idx, void* scratch, hipStream_t s);
+size_t select_rows_scratch_bytes(int64_t rows, int k, int elem_bytes);
 
 // argmin_dist_rows semantics over a materialized block (generic k-means path).
 template <typename T>

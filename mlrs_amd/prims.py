@@ -61,6 +61,34 @@ def _dev_check(*ts):
             raise ValueError("mlrs_amd prims take device tensors (got a %s tensor)" % t.device)
         if not t.is_contiguous():
             raise ValueError("mlrs_amd prims take contiguous row-major tensors")
+    if any(t.device != ts[0].device for t in ts[1:]):
+        raise ValueError("mlrs_amd prims take operands on one device (got %s)" % sorted({str(t.device) for t in ts}))
+    # the library works on the current HIP device
+    if ts and ts[0].device.index != torch.cuda.current_device():
+        raise ValueError("operands are on %s but the current device is cuda:%d (use torch.cuda.device(...))"
+                         % (ts[0].device, torch.cuda.current_device()))
+
+
+# Index / label buffers hold uint32 values; int32 (and uint32 where torch has
+# it) tensors have that width.
+_IDX_DTYPES = tuple(d for d in (torch.int32, getattr(torch, "uint32", None)) if d is not None)
+
+
+def _check_out(t, name, dtypes, numel, device):
+    """A caller-supplied output buffer: the C ABI counts elements, not bytes,
+    and writes through the raw pointer, so the buffer must be a contiguous
+    tensor on the operands' device with the element type and count the call
+    writes.  Raises before anything is launched."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError("%s must be a tensor, got %s" % (name, type(t).__name__))
+    if t.device != device:
+        raise ValueError("%s must be on %s (got %s)" % (name, device, t.device))
+    if t.dtype not in dtypes:
+        raise TypeError("%s must be %s, got %s" % (name, " or ".join(str(d) for d in dtypes), t.dtype))
+    if not t.is_contiguous():
+        raise ValueError("%s must be contiguous" % name)
+    if t.numel() != numel:
+        raise ValueError("%s must hold %d elements, got %d" % (name, numel, t.numel()))
 
 
 _PATHS = {"auto": 0, "fused": 1, "lowd": 2, "generic": 3}
@@ -95,6 +123,8 @@ def knn_topk(xq, x_train, k, metric="euclidean", p=2.0, out=None):
         widen = True
     else:
         dist, idx = out
+        _check_out(dist, "out distances", (xq.dtype,), nq * int(k), xq.device)
+        _check_out(idx, "out indices", _IDX_DTYPES, nq * int(k), xq.device)
         widen = False
     lib = _lib.load()
     rc = getattr(lib, "mlrs_knn_topk_" + s)(
@@ -111,9 +141,15 @@ def knn_topk(xq, x_train, k, metric="euclidean", p=2.0, out=None):
 def kmeans_assign(x, centers, labels=None, sqdist=None):
     """Nearest centre of every row: ``(labels int64, squared distances)``."""
     _dev_check(x, centers)
+    if centers.dtype != x.dtype:
+        raise TypeError("points and centres dtypes differ")
     s = _suffix(x)
     n, d = x.shape
     kc = centers.shape[0]
+    if labels is not None:
+        _check_out(labels, "labels", _IDX_DTYPES, n, x.device)
+    if sqdist is not None:
+        _check_out(sqdist, "sqdist", (x.dtype,), n, x.device)
     lab = torch.empty(n, dtype=torch.int32, device=x.device) if labels is None else labels
     dist = torch.empty(n, dtype=x.dtype, device=x.device) if sqdist is None else sqdist
     lib = _lib.load()
@@ -130,9 +166,13 @@ def pairwise_distance(x, y, metric="euclidean", sqrt=False, out=None, p=2.0):
     """Full ``rows_x x rows_y`` distance matrix (squared Euclidean unless
     ``sqrt``; ``p`` is the Minkowski exponent)."""
     _dev_check(x, y)
+    if y.dtype != x.dtype:
+        raise TypeError("x and y dtypes differ")
     s = _suffix(x)
     rx, cx = x.shape
     ry, cy = y.shape
+    if out is not None:
+        _check_out(out, "out", (x.dtype,), rx * ry, x.device)
     o = torch.empty((rx, ry), dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     rc = getattr(lib, "mlrs_pairwise_distance_" + s)(
@@ -146,6 +186,8 @@ def row_sqnorms(x, out=None):
     _dev_check(x)
     s = _suffix(x)
     n, d = x.shape
+    if out is not None:
+        _check_out(out, "out", (x.dtype,), n, x.device)
     o = torch.empty(n, dtype=x.dtype, device=x.device) if out is None else out
     lib = _lib.load()
     rc = getattr(lib, "mlrs_row_sqnorms_" + s)(_ptr(x), x.numel(), n, d, _ptr(o), o.numel(),

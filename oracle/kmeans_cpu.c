@@ -85,16 +85,24 @@ static uint64_t km_next_below(km_rng *r, uint64_t bound)
     }
 }
 
-/* ---- relocation ranking: (distance desc, index asc) ---- */
+/* ---- relocation ranking: (distance desc, index asc) ----
+ * A total order for qsort: a NaN distance ranks above every number, NaNs and
+ * equal values by index.  On numbers it is the reference's
+ * (prims/kmeans.rs:1347-1359). */
 static const double *km_rank_dist;
 static int km_rank_cmp(const void *pa, const void *pb)
 {
     int64_t a = *(const int64_t *)pa, b = *(const int64_t *)pb;
     double da = km_rank_dist[a], db = km_rank_dist[b];
-    if (db < da)
-        return -1;
-    if (da < db)
-        return 1;
+    int na = da != da, nb = db != db;
+    if (na != nb)
+        return na ? -1 : 1;
+    if (!na) {
+        if (db < da)
+            return -1;
+        if (da < db)
+            return 1;
+    }
     return (a < b) ? -1 : (a > b);
 }
 

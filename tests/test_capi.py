@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib.load()
-    assert lib.mlrs_abi_version() == 3
+    assert lib.mlrs_abi_version() == 4
     assert lib.mlrs_status_string(0) == b"ok"
     assert lib.mlrs_status_string(-7) == b"invalid parameter value"
     assert lib.mlrs_status_string(-1) == b"shape mismatch"
@@ -240,3 +240,7 @@ def test_kmeans_fit_validation():
     assert call(tol=-1.0) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"tol"
     assert call(c_len=8) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"centers"
     assert call(l_len=9) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"labels"
+
+
+def test_every_k_up_to_n_train_is_served():
+    assert _lib.load().mlrs_knn_max_k(4, 128, 0) == 2**31 - 1

@@ -94,6 +94,23 @@ def test_fit_relocation_walks_past_the_selected_prefix():
     assert len(set(got[1].cpu().tolist())) == ini.shape[0]
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_fit_relocation_with_a_nan_distance(dtype):
+    """A NaN row reaches the relocation ranking (the C ABI does not check
+    finiteness, as the reference's Rust fit does not): the ranking is a total
+    order, NaN first, and the fit matches the oracle's bits."""
+    X = _blobs(7, 600, 3, 3, spread=0.8, dtype=dtype)
+    X[37] = np.nan
+    ini = np.array([X[0], X[1], [500.0, 500.0, 500.0], [-400.0, 0.0, 0.0]], dtype=dtype)
+    wc, wl, wi, wn = oracle.kmeans_fit(X, 4, "array", ini, max_iter=1)
+    gc, gl, gi, gn = prims.kmeans_fit(_t(X), 4, "array", _t(ini), max_iter=1)
+    np.testing.assert_array_equal(gl.cpu().numpy(), wl.astype(np.int64))
+    np.testing.assert_array_equal(gc.cpu().numpy(), wc)
+    assert (gi == wi) or (np.isnan(gi) and np.isnan(wi))
+    assert gn == wn
+    assert np.isnan(gc.cpu().numpy()[2]).all()
+
+
 @pytest.mark.parametrize("s", ["f32", "f64"])
 def test_estimator_fixture(s):
     z = load_golden("kmeans_%s_seed42" % s)

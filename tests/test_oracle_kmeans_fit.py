@@ -124,3 +124,22 @@ def test_restarts_keep_the_lowest_inertia():
     assert inertia == best
     winner = [r for r in runs if r[2] == best][0]
     np.testing.assert_array_equal(c, winner[0])
+
+
+def test_relocation_ranks_a_nan_distance_first():
+    """A NaN row (distance NaN to its centre) during the empty-cluster
+    relocation: the ranking is a total order with NaN above every number, so
+    the NaN row moves first (its new centre is NaN) and the farthest finite
+    row next (its new centre is that row)."""
+    X = _blobs(7, 600, 3, 3, spread=0.8)
+    X[37] = np.nan
+    init = np.array([X[0], X[1], [500.0, 500.0, 500.0], [-400.0, 0.0, 0.0]])
+    first = oracle.kmeans_fit(X, 4, "array", init, max_iter=1)
+    again = oracle.kmeans_fit(X, 4, "array", init, max_iter=1)
+    np.testing.assert_array_equal(first[0], again[0])
+    np.testing.assert_array_equal(first[1], again[1])
+    c = first[0]
+    assert np.isnan(c[2]).all()
+    _, dist = oracle.kmeans_assign(X, init)
+    far = int(np.nanargmax(np.where(np.isnan(dist), -np.inf, dist)))
+    np.testing.assert_array_equal(c[3], X[far])
