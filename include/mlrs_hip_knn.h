@@ -118,6 +118,30 @@ int32_t mlrs_knn_topk_f64(const double *xq, int64_t xq_len, int64_t n_query, int
  * every k up to n_train (the arguments are kept for ABI stability). */
 int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric);
 
+/*
+ * mlrs_knn_topk_f32 for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, validation,
+ * kernels and bits as mlrs_knn_topk_f32; the only difference is where the
+ * kernels' scratch (norms, per-segment lists, queued screen values, exact
+ * tiles) lives: in a static device array of MLRS_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends, instead of the library's cached
+ * workspace.  The call makes no hipMalloc / hipFree / allocating library
+ * call; its first call on a device looks the array's device address up once
+ * (hipGetSymbolAddress).  A search whose scratch would exceed the array
+ * returns MLRS_ERR_UNSUPPORTED, operand "scratch" {rows = bytes needed,
+ * len = MLRS_NOALLOC_SCRATCH_BYTES}, before any launch (the exact-tile path
+ * sizes its tiles to fit; the Gram path at n_train = 1M, d = 128, k = 32
+ * needs ~64 MiB for 10k queries).  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, no ordering between
+ * them) RACE -- order them yourself.  Not ordered against the other entry
+ * points' calls (they use other memory), and no timing events are recorded.
+ */
+#define MLRS_NOALLOC_SCRATCH_BYTES 134217728 /* 128 MiB */
+int32_t mlrs_knn_topk_f32_noalloc(const float *xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                                  const float *x_train, int64_t xt_len, int64_t n_train, int32_t k,
+                                  int32_t metric, double p, float *out_dist, uint32_t *out_idx,
+                                  int64_t out_len, void *stream);
 
 /*
  * Nearest-centre assignment (the k-means assignment step, k = 1 search).

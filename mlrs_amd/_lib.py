@@ -18,6 +18,9 @@ MLRS_ERR_HIP = -5
 MLRS_ERR_ALLOC = -6
 MLRS_ERR_INVALID_PARAM = -7
 
+# Size of the allocation-free entry point's static scratch (MLRS_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 128 << 20
+
 METRIC_EUCLIDEAN = 0
 METRIC_COSINE = 1
 METRIC_MANHATTAN = 2
@@ -79,6 +82,8 @@ SIGNATURES = {
     "mlrs_knn_topk_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _i32, _f64, _vp, _vp, _i64, _vp]),
     "mlrs_knn_topk_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _i32, _f64, _vp, _vp, _i64, _vp]),
     "mlrs_knn_max_k": (_i32, [_i32, _i64, _i32]),
+    "mlrs_knn_topk_f32_noalloc": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _i32, _f64, _vp, _vp, _i64,
+                                         _vp]),
     "mlrs_kmeans_assign_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mlrs_kmeans_assign_f64": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "mlrs_pairwise_distance_f32": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _f64, _vp, _i64,

@@ -17,6 +17,12 @@
 
 using namespace mlrs;
 
+// Scratch of the allocation-free entry point (mlrs_knn_topk_f32_noalloc): one
+// copy per GPU, held until the process ends.  Host code never uses this name
+// as an address -- it takes the device address hipGetSymbolAddress returns
+// for the current device (g_scratch_dev) and passes that to the kernels.
+static __device__ __align__(256) char scratch[MLRS_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 // ---------------------------------------------------------------------------
@@ -121,6 +127,11 @@ struct CallState {
 };
 CallState* g_call = nullptr;  // the running entry-point call (under g_mu)
 
+// The allocation-free variant runs with the static scratch in place of the
+// arenas (set for the duration of such a call, under g_mu).
+bool g_noalloc = false;
+char* g_noalloc_base = nullptr;
+
 // Holds the process-wide lock for one entry-point call; records the call's
 // end on its stream when the call touched a cached buffer.
 struct CallGuard {
@@ -143,7 +154,7 @@ struct CallGuard {
 
 // Before the running call first touches a cached buffer of `dev`.
 int32_t order_after_last_call(int dev, hipStream_t s) {
-    if (!g_call || g_call->armed) return MLRS_OK;
+    if (!g_call || g_call->armed || g_noalloc) return MLRS_OK;
     DevOrder& O = g_order[dev];
     hipError_t e;
     if (!O.ev) {
@@ -171,6 +182,10 @@ int32_t current_device(int* dev) {
     return MLRS_OK;
 }
 
+// Bytes a call may carve from the workspace (the static scratch's size in the
+// allocation-free variant, else unbounded).
+size_t workspace_limit() { return g_noalloc ? (size_t)MLRS_NOALLOC_SCRATCH_BYTES : SIZE_MAX; }
+
 // Growing a cached buffer synchronizes the whole device (the old buffer may
 // still be read by earlier work on any stream, and hipFree synchronizes the
 // device anyway).
@@ -188,6 +203,14 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
     }
     *cus = A.cus;
     if (bytes == 0) bytes = 256;
+    if (g_noalloc) {
+        if (bytes > (size_t)MLRS_NOALLOC_SCRATCH_BYTES)
+            return set_err(MLRS_ERR_UNSUPPORTED, "scratch", (int64_t)bytes, 0, (int64_t)MLRS_NOALLOC_SCRATCH_BYTES, 0,
+                           "this search needs %zu bytes of scratch; the allocation-free entry point holds %zu",
+                           bytes, (size_t)MLRS_NOALLOC_SCRATCH_BYTES);
+        *out = g_noalloc_base;
+        return MLRS_OK;
+    }
     rc = order_after_last_call(dev, s);
     if (rc) return rc;
     if (A.cap < bytes) {
@@ -225,7 +248,7 @@ struct KernelTimer {
     hipStream_t s;
     TimedLaunch t{nullptr, nullptr};
     KernelTimer(hipStream_t st, const char* name) : s(st) {
-        if (!g_timing) return;
+        if (!g_timing || g_noalloc) return;
         if (hipEventCreate(&t.a) != hipSuccess || hipEventCreate(&t.b) != hipSuccess) {
             t.a = t.b = nullptr;
             return;
@@ -320,7 +343,9 @@ int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d,
     // per query row of a tile: its exact values plus the selection's scratch
     const size_t fixed = 4 * aligned_bytes(sizeof(T) * (nq + nt)) + 4096;
     const size_t per_row = sizeof(T) * (size_t)std::max<int64_t>(nt, 1) + select_rows_scratch_bytes(1, k, sizeof(T));
-    const size_t tile_budget = (size_t)256 << 20;
+    size_t tile_budget = (size_t)256 << 20;
+    const size_t limit = workspace_limit();
+    if (limit != SIZE_MAX) tile_budget = std::min(tile_budget, limit > fixed ? limit - fixed : 0);
     int64_t qt = (int64_t)(tile_budget / per_row);
     qt = std::max<int64_t>(1, std::min<int64_t>(qt, nq));
     const size_t sel_bytes = select_rows_scratch_bytes(qt, k, sizeof(T));
@@ -703,6 +728,21 @@ int32_t knn_topk_f32_validate(const float* xq, int64_t xq_len, int64_t n_query, 
         return set_err(MLRS_ERR_UNSUPPORTED, "p", 0, 0, 0, 0, "minkowski p must be >= 1");
     return MLRS_OK;
 }
+
+// The allocation-free variant's device address of the static scratch, per
+// device, taken once with that device current.
+char* g_scratch_dev[kMaxDevices];
+
+struct NoAllocScope {
+    NoAllocScope(char* base) {
+        g_noalloc = true;
+        g_noalloc_base = base;
+    }
+    ~NoAllocScope() {
+        g_noalloc = false;
+        g_noalloc_base = nullptr;
+    }
+};
 }  // namespace
 
 extern "C" {
@@ -715,6 +755,28 @@ int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int6
                                        out_dist, out_idx, out_len);
     if (rc) return rc;
     if (n_query == 0) return MLRS_OK;
+    return knn_topk_f32_dispatch(xq, n_query, n_features, x_train, n_train, k, metric, p, out_dist, out_idx,
+                                 (hipStream_t)stream);
+}
+
+int32_t mlrs_knn_topk_f32_noalloc(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
+                                  const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
+                                  double p, float* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
+    CallGuard cg;
+    int32_t rc = knn_topk_f32_validate(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric, p,
+                                       out_dist, out_idx, out_len);
+    if (rc) return rc;
+    if (n_query == 0) return MLRS_OK;
+    int dev = 0;
+    rc = current_device(&dev);
+    if (rc) return rc;
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return hip_err(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress");
+        g_scratch_dev[dev] = static_cast<char*>(ptr);
+    }
+    NoAllocScope scope(g_scratch_dev[dev]);
     return knn_topk_f32_dispatch(xq, n_query, n_features, x_train, n_train, k, metric, p, out_dist, out_idx,
                                  (hipStream_t)stream);
 }

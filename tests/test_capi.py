@@ -242,5 +242,19 @@ def test_kmeans_fit_validation():
     assert call(l_len=9) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"labels"
 
 
+def test_noalloc_entry_validates_like_the_allocating_one():
+    lib = _lib.load()
+    for name in ("mlrs_knn_topk_f32", "mlrs_knn_topk_f32_noalloc"):
+        f = getattr(lib, name)
+        assert f(P, 39, 10, 4, P, 80, 20, 3, 0, 2.0, P, P, 30, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+        assert _info().operand == b"x"
+        assert f(P, 40, 10, 4, P, 80, 20, 21, 0, 2.0, P, P, 210, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+        e = _info()
+        assert (e.operand, e.rows, e.cols, e.len) == (b"k", 1, 21, 20)
+        assert f(P, 40, 10, 4, P, 80, 20, 3, 9, 2.0, P, P, 30, None) == _lib.MLRS_ERR_UNSUPPORTED
+        # no queries: nothing to do, no device touched
+        assert f(P, 0, 0, 4, P, 80, 20, 3, 0, 2.0, P, P, 0, None) == _lib.MLRS_OK
+
+
 def test_every_k_up_to_n_train_is_served():
     assert _lib.load().mlrs_knn_max_k(4, 128, 0) == 2**31 - 1
