@@ -13,10 +13,20 @@ arithmetic) timed on a bounded sample of the same workload on this host.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
   python bench.py --radius R [--config c2]    # radius_neighbors on the same data
+  python bench.py --config c5 --fit [--fit-iters N]   # k-means fit at c5 scale
 
 With --radius a step is one radius_neighbors call (count pass, row offsets,
 fill pass, boundary transform) of all queries against the index; its parity
-is checked against the CPU oracle on a few query rows.
+is checked against the CPU oracle on a few query rows.  With --fit a step is
+one k-means fit of the c5 points into 1,024 clusters from a seeded random
+init (SplitMix64, as the reference draws it), tol 0, at most N Lloyd
+iterations (assignment, centroid sums, relocation, host update), reported per
+iteration; its parity is a fit of a 200k-row prefix against the CPU oracle's.
+
+The CPU baseline runs the oracle on every CPU this process may use, capped
+by OMP_NUM_THREADS where the host sets it (the GPU box gives one GPU's job a
+16-thread CPU share that way); the line records the affinity count, the
+threads used, the CPU model and the oracle's compile flags.
 """
 import argparse
 import ctypes
@@ -43,11 +53,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "d256"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--radius", type=float, default=None,
                     help="measure radius_neighbors with this radius instead of the k-nearest search")
+    ap.add_argument("--fit", action="store_true", help="k-means fit at c5 scale (with --config c5)")
+    ap.add_argument("--fit-iters", type=int, default=10, help="Lloyd iterations per fit step (--fit)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel "
                          "of known traffic, the scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -79,10 +91,18 @@ def main():
     if radius is not None and kmeans:
         print("--radius needs a k-nearest configuration (c1-c4)", file=sys.stderr)
         sys.exit(2)
+    if args.fit and not kmeans:
+        print("--fit needs --config c5", file=sys.stderr)
+        sys.exit(2)
+    fit_iters = []
 
     def step():
         if radius is not None:
             return prims.radius_neighbors(ta, tb, radius, metric)
+        if args.fit:
+            r = prims.kmeans_fit(ta, n_index, "random", seed=7, max_iter=args.fit_iters, tol=0.0)
+            fit_iters.append(r[3])
+            return r
         if kmeans:
             return prims.kmeans_assign(ta, tb)
         return prims.knn_topk(ta, tb, k, metric)
@@ -106,8 +126,11 @@ def main():
     _lib.check(lib.mlrs_timing_enable(0))
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
     kern_ms = tot_ms.value / max(1, launches.value)
-    log("timed %d steps: %.3f ms/step, %s avg %.3f ms over %d launches"
-        % (args.steps, ms_per_step, name.value.decode(), kern_ms, launches.value))
+    # the dominant kernel's time within one step (a step may launch it more
+    # than once: exact tiles, one assignment per Lloyd iteration)
+    kern_ms_step = tot_ms.value / args.steps
+    log("timed %d steps: %.3f ms/step, %s avg %.3f ms over %d launches (%.3f ms per step)"
+        % (args.steps, ms_per_step, name.value.decode(), kern_ms, launches.value, kern_ms_step))
 
     if args.calib_copy_mib:
         n = args.calib_copy_mib * (1 << 20) // 4
@@ -120,9 +143,19 @@ def main():
         del src, dst
 
     # ---- parity of the measured run against the committed golden subset ----
-    g = np.load(os.path.join(ROOT, "tests", "golden", "%s_golden.npz" % args.config))
-    sub = g["subset"]
-    if radius is not None:
+    gpath = os.path.join(ROOT, "tests", "golden", "%s_golden.npz" % args.config)
+    g = np.load(gpath) if os.path.exists(gpath) else None
+    sub = g["subset"] if g is not None else np.unique(np.linspace(0, n_query - 1, 64).astype(np.int64))
+    if args.fit:
+        import oracle
+        fc, fl, finert, fit_n = out
+        npre = 200_000
+        wc, wl, wi, wn = oracle.kmeans_fit(a[:npre], n_index, "random", seed=7, max_iter=3, tol=0.0)
+        gc, gl, gi, gn = prims.kmeans_fit(ta[:npre].contiguous(), n_index, "random", seed=7, max_iter=3, tol=0.0)
+        ok = (np.array_equal(gl.cpu().numpy(), wl.astype(np.int64)) and np.array_equal(gc.cpu().numpy(), wc)
+              and gi == wi and gn == wn)
+        sub = np.arange(npre)
+    elif radius is not None:
         import oracle
         dist, idx, cnt = out
         cnt = cnt.cpu().numpy()
@@ -139,17 +172,35 @@ def main():
         lab, sq = out
         ok = (np.array_equal(lab.cpu().numpy()[sub], g["labels"].astype(np.int64))
               and np.array_equal(sq.cpu().numpy()[sub], g["sqdist"]))
-    else:
+    elif g is not None:
         dist, idx = out
         ok = (np.array_equal(idx.cpu().numpy()[sub], g["idx"].astype(np.int64))
               and np.array_equal(dist.cpu().numpy()[sub], g["dist"]))
-    parity = ("bitwise-equal to the CPU oracle on %d %s rows" % (len(sub), "sampled" if radius is not None else "golden")
-              if ok else "MISMATCH vs the CPU oracle")
+    else:
+        import oracle
+        dist, idx = out
+        wd, wi = oracle.knn_topk(a[sub], b, k, metric)
+        ok = (np.array_equal(idx.cpu().numpy()[sub], wi.astype(np.int64))
+              and np.array_equal(dist.cpu().numpy()[sub], wd))
+    if args.fit:
+        parity = ("3-iteration fit of the first 200000 points bitwise-equal to the CPU oracle's (centres, labels, "
+                  "inertia, n_iter)" if ok else "MISMATCH vs the CPU oracle")
+    else:
+        kind = "golden" if (g is not None and radius is None) else "sampled"
+        parity = ("bitwise-equal to the CPU oracle on %d %s rows" % (len(sub), kind) if ok
+                  else "MISMATCH vs the CPU oracle")
     log(parity)
 
     evals = float(n_query) * float(n_index)
-    value = evals / (ms_per_step / 1000.0)
-    flops = 2.0 * d * evals
+    if args.fit:
+        # one assignment per Lloyd iteration plus the final one
+        iters = float(np.mean(fit_iters[-args.steps:]))
+        ms_per_iter = ms_per_step / max(iters, 1.0)
+        evals_step = evals * (iters + 1.0)
+        value = evals_step / (ms_per_step / 1000.0)
+    else:
+        value = evals / (ms_per_step / 1000.0)
+    flops = 2.0 * d * (evals_step if args.fit else evals)
     kname = name.value.decode()
     f64 = cfg["dtype"] == "f64"
     if radius is not None and kname.startswith("radius_gram"):
@@ -168,7 +219,7 @@ def main():
         # the low-d ALU kernel and the exact tiles of small searches: vector
         # units without packed math (an FMA counts two flops)
         bound, peak, unit = "valu", PEAKS["valu_f64" if f64 else "valu_f32"], "TFLOP/s"
-    achieved = flops / (kern_ms / 1000.0) / 1e12
+    achieved = flops / (kern_ms_step / 1000.0) / 1e12
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "traffic_%s%s.json" % ("radius_" if radius is not None else "",
                                                                    args.config))
@@ -178,17 +229,27 @@ def main():
     cpu = None
     if not args.no_cpu:
         import oracle
-        threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+        affinity = len(os.sched_getaffinity(0))
+        omp = os.environ.get("OMP_NUM_THREADS", "")
+        threads = args.cpu_threads or (min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity)
+        info = oracle.build_info()
         # bounded sample: a prefix of the queries against the full index, run
         # repeatedly until about 10 s of CPU work has been timed
-        sample = {"c1": n_query, "c2": 2000, "c3": 256, "c4": 20000, "c5": 400000}[args.config]
+        sample = {"c1": n_query, "c2": 2000, "c3": 256, "c4": 20000, "c5": 400000, "d256": 1000}[args.config]
         if radius is not None:
-            sample = {"c1": n_query, "c2": 512, "c3": 128, "c4": 20000}[args.config]
-        log("CPU baseline: %d of %d queries, %d threads" % (sample, n_query, threads))
+            sample = {"c1": n_query, "c2": 512, "c3": 128, "c4": 20000, "d256": 256}[args.config]
+        if args.fit:
+            sample = 100_000
+        log("CPU baseline: %d of %d queries, %d threads (affinity %d, OMP_NUM_THREADS=%s), %s, %s"
+            % (sample, n_query, threads, affinity, omp or "unset", info["cpu_model"], info["flags"]))
+        cpu_iters = [0]
 
         def cpu_pass():
             if radius is not None:
                 oracle.radius_neighbors(a[:sample], b, radius, metric, nthreads=threads)
+            elif args.fit:
+                r = oracle.kmeans_fit(a[:sample], n_index, "random", seed=7, max_iter=2, tol=0.0)
+                cpu_iters[0] += r[3] + 1
             elif kmeans:
                 oracle.kmeans_assign(a[:sample], b, nthreads=threads)
             else:
@@ -200,22 +261,37 @@ def main():
             cpu_pass()
             dt += time.perf_counter() - tc
             reps += 1
-        cpu = {"value": float(sample) * n_index * reps / dt, "unit": "dist-evals/s", "cores": threads, "kind": "port",
-               "sample": "first %d of %d queries vs the full %d-row index, %d passes in %.1f s"
-                         % (sample, n_query, n_index, reps, dt)}
+        n_evals = float(sample) * n_index * (cpu_iters[0] if args.fit else reps)
+        what = ("k-means fits (random init, 2 iterations) of the first %d of %d points" if args.fit
+                else "first %d of %d queries vs the full %d-row index" % (sample, n_query, n_index))
+        if args.fit:
+            what = what % (sample, n_query)
+        cpu = {"value": n_evals / dt, "unit": "dist-evals/s", "cores": threads, "kind": "port",
+               "sample": "%s, %d passes in %.1f s" % (what, reps, dt),
+               "affinity_cpus": affinity, "omp_num_threads": omp or None, "cpu_model": info["cpu_model"],
+               "oracle_build": info["flags"]}
         log("CPU baseline %.3g evals/s" % cpu["value"])
 
     wl = {"c1": "c1: 10k x 1k, d=64, k=10, f32 N(0,1)",
           "c2": "c2: 1M index x 10k queries, d=128, k=32, f32, 100-comp GMM",
           "c3": "c3: 200k x 5k, d=256, k=16, f64 cosine, U[0,1)",
           "c4": "c4: 500k self-kNN, d=3, k=8, f32, 5% exact duplicates",
-          "c5": "c5: k-means assign, 5M points x 1024 centroids, d=64, f32"}[args.config]
+          "c5": "c5: k-means assign, 5M points x 1024 centroids, d=64, f32",
+          "d256": "d256: 200k index x 5k queries, d=256, k=32, f32, 100-comp GMM"}[args.config]
+    if args.fit:
+        wl = ("k-means fit at c5 scale: 5M points into 1024 clusters, d=64, f32, seeded random init, tol 0, "
+              "at most %d Lloyd iterations per step" % args.fit_iters)
     if radius is not None:
         wl = "radius_neighbors, radius %g, on %s (%d matches, %.1f per query)" % (radius, wl, matches,
                                                                                  matches / n_query)
+    if args.fit:
+        metric_name = "k-means fit assignment dist-evals/s (c5 scale)"
+    elif radius is not None:
+        metric_name = "radius_neighbors dist-evals/s (%s)" % args.config
+    else:
+        metric_name = METRIC if args.config == "c2" else "dist-evals/s (%s)" % args.config
     line = {
-        "metric": (METRIC if args.config == "c2" else "dist-evals/s (%s)" % args.config) if radius is None
-        else "radius_neighbors dist-evals/s (%s)" % args.config,
+        "metric": metric_name,
         "value": value,
         "unit": "dist-evals/s",
         "n_gpus": 1,
@@ -230,8 +306,14 @@ def main():
         "config": {"workload": wl, "n_index": n_index, "n_query": n_query, "d": d,
                    "k": k if radius is None else None, "radius": radius, "metric": metric,
                    "queries_per_s": n_query / (ms_per_step / 1000.0), "parity": parity},
+        "fit": ({"iterations": float(np.mean(fit_iters[-args.steps:])), "ms_per_iteration": ms_per_iter}
+                if args.fit else None),
         "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
-                     "traffic": traffic, "kernel": name.value.decode(), "kernel_ms": kern_ms},
+                     "traffic": traffic, "kernel": name.value.decode(), "kernel_ms": kern_ms,
+                     "kernel_launches_per_step": launches.value / args.steps, "kernel_ms_per_step": kern_ms_step,
+                     "basis": {"mfma": "dense MFMA peak, 2*d flops per distance evaluation",
+                               "valu": "non-packed FP32/FP64 VALU peak (an FMA = 2 flops; packed FP32 is off in "
+                                       "this build), 2*d flops per distance evaluation"}[bound]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

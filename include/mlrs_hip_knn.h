@@ -392,6 +392,44 @@ int32_t mlrs_kmeans_fit_f64(const double *x, int64_t x_len, int64_t n, int64_t n
                             uint32_t *out_labels, int64_t labels_len, double *out_inertia, int64_t *out_n_iter,
                             void *stream);
 
+/*
+ * Fit-time ownership copy: dst[0..len) = src[0..len) on `stream` (device
+ * pointers, any alignment; 16-byte vectors when both are 16-byte aligned).
+ * Replaces: device_copy (crates/mlrs-backend/src/prims/knn.rs:358-386) with
+ *   its copy_elem / copy_elem_cpu_chunked kernels (crates/mlrs-kernels/src/
+ *   elementwise.rs:71-125), which NearestNeighbors' Rust Fit::fit runs to own
+ *   the training matrix.  The reference's u32 element ceiling (a CubeCL launch
+ *   limit) does not apply.
+ * Errors: ShapeMismatch "src" (len < 0), "dst" {len, 1, dst_len} when
+ *   dst_len != len; NullPointer when len > 0 and a pointer is NULL.
+ */
+int32_t mlrs_device_copy_f32(const float *src, int64_t len, float *dst, int64_t dst_len, void *stream);
+int32_t mlrs_device_copy_f64(const double *src, int64_t len, double *dst, int64_t dst_len, void *stream);
+
+/*
+ * Buffer counters of the current device: PoolStats (crates/mlrs-backend/src/
+ * pool.rs:27-56) over the library's cached device buffers (the main and
+ * auxiliary workspaces and the radius plan memory).  allocations: buffers
+ * grown with hipMalloc; reuses: requests the held buffer already covered;
+ * live_bytes: capacity currently held; peak_bytes: its high-water mark;
+ * read_backs: device-to-host copies the library made (radius totals and
+ * flags, the consumers' error checks, the k-means fit's per-iteration state)
+ * -- the search, assignment, pairwise, norm and graph paths make none, so a
+ * memory gate can assert read_backs does not move across them.
+ * mlrs_pool_stats_reset zeroes allocations, reuses and read_backs and sets
+ * peak_bytes to live_bytes.  The allocation-free entry point's static
+ * scratch is not a cached buffer and is not counted.
+ */
+typedef struct mlrs_pool_stats {
+    uint64_t allocations;
+    uint64_t reuses;
+    uint64_t peak_bytes;
+    uint64_t live_bytes;
+    uint64_t read_backs;
+} mlrs_pool_stats;
+int32_t mlrs_pool_stats_get(mlrs_pool_stats *out);
+int32_t mlrs_pool_stats_reset(void);
+
 /* Release the cached device workspace of the current device. */
 int32_t mlrs_release_workspace(void);
 

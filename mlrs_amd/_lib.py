@@ -40,6 +40,18 @@ class ErrorInfo(ctypes.Structure):
     ]
 
 
+class PoolStats(ctypes.Structure):
+    """mlrs_pool_stats: the reference's PoolStats counters over the library's
+    cached device buffers (crates/mlrs-backend/src/pool.rs:27-56)."""
+    _fields_ = [
+        ("allocations", ctypes.c_uint64),
+        ("reuses", ctypes.c_uint64),
+        ("peak_bytes", ctypes.c_uint64),
+        ("live_bytes", ctypes.c_uint64),
+        ("read_backs", ctypes.c_uint64),
+    ]
+
+
 class PrimError(ValueError):
     """A geometry violation rejected before any launch (mlrs_core::PrimError)."""
 
@@ -111,6 +123,10 @@ SIGNATURES = {
     "mlrs_kmeans_fit_f64": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, ctypes.c_uint64, _i64, _i64, _f64,
                                    _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
     "mlrs_release_workspace": (_i32, []),
+    "mlrs_device_copy_f32": (_i32, [_vp, _i64, _vp, _i64, _vp]),
+    "mlrs_device_copy_f64": (_i32, [_vp, _i64, _vp, _i64, _vp]),
+    "mlrs_pool_stats_get": (_i32, [ctypes.POINTER(PoolStats)]),
+    "mlrs_pool_stats_reset": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
     "mlrs_force_path": (_i32, [_i32]),
     "mlrs_timing_read": (_i32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, _i32]),

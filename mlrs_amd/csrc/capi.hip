@@ -182,6 +182,31 @@ int32_t current_device(int* dev) {
     return MLRS_OK;
 }
 
+// PoolStats (crates/mlrs-backend/src/pool.rs:27-56) over the library's cached
+// device buffers (main and auxiliary workspaces, radius plan memory), per
+// device: an allocation is a buffer grown with hipMalloc, a reuse a request
+// the held buffer already covers; live bytes are the held capacities;
+// read-backs count the device-to-host copies the library makes (a total, a
+// flag, k-means sums) -- 0 for the search, assignment and pairwise paths.
+mlrs_pool_stats g_pool[kMaxDevices];
+
+void pool_note_grow(int dev, size_t old_cap, size_t new_cap) {
+    mlrs_pool_stats& P = g_pool[dev];
+    P.allocations += 1;
+    P.live_bytes = P.live_bytes - old_cap + new_cap;
+    if (P.live_bytes > P.peak_bytes) P.peak_bytes = P.live_bytes;
+}
+
+void pool_note_release(int dev, size_t cap) { g_pool[dev].live_bytes -= cap; }
+
+// Counted before each device-to-host copy of the running call.
+void note_read_back() {
+    int dev = -1;
+    if (g_call && g_call->armed) dev = g_call->dev;
+    else if (hipGetDevice(&dev) != hipSuccess) return;
+    if (dev >= 0 && dev < kMaxDevices) g_pool[dev].read_backs += 1;
+}
+
 // Bytes a call may carve from the workspace (the static scratch's size in the
 // allocation-free variant, else unbounded).
 size_t workspace_limit() { return g_noalloc ? (size_t)MLRS_NOALLOC_SCRATCH_BYTES : SIZE_MAX; }
@@ -214,6 +239,7 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
     rc = order_after_last_call(dev, s);
     if (rc) return rc;
     if (A.cap < bytes) {
+        const size_t old_cap = A.cap;
         if (A.base) {
             e = hipDeviceSynchronize();
             if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
@@ -225,10 +251,14 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
         e = hipMalloc((void**)&A.base, want);
         if (e != hipSuccess) {
             A.base = nullptr;
+            pool_note_release(dev, old_cap);
             return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)want, 0, 0, (int)e,
                            "device workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
         }
         A.cap = want;
+        pool_note_grow(dev, old_cap, want);
+    } else {
+        g_pool[dev].reuses += 1;
     }
     *out = A.base;
     return MLRS_OK;
@@ -955,6 +985,7 @@ extern "C++" {
 // point, as in the reference, whose host raises right after its gather.
 static int32_t read_first_bad(const unsigned long long* dev_word, hipStream_t s, int64_t* row) {
     unsigned long long h = ~0ull;
+    note_read_back();
     hipError_t e = hipMemcpyAsync(&h, dev_word, sizeof(h), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_err(e, "first_bad read-back");
@@ -1033,6 +1064,7 @@ static int32_t classify_impl(const int32_t* y_class, int64_t n_train, int32_t n_
     if (rc) return rc;
     if (row >= 0) {
         int64_t rec[3] = {0, 0, 0};
+        note_read_back();
         e = hipMemcpy(rec, err + 3 * row, sizeof(rec), hipMemcpyDeviceToHost);
         if (e != hipSuccess) return hip_err(e, "knn_classify error read-back");
         // classifier.rs:850-875: the first bad (query, neighbour) in row order
@@ -1152,7 +1184,12 @@ static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int ns
 }
 
 static int32_t radius_plan_memory(RadiusPlan& P, size_t bytes) {
-    if (P.cap >= bytes) return MLRS_OK;
+    const int dev = (int)(&P - g_rplan);
+    if (P.cap >= bytes) {
+        g_pool[dev].reuses += 1;
+        return MLRS_OK;
+    }
+    const size_t old_cap = P.cap;
     P.valid = false;
     if (P.base) {
         hipError_t e = hipDeviceSynchronize();
@@ -1165,14 +1202,17 @@ static int32_t radius_plan_memory(RadiusPlan& P, size_t bytes) {
     hipError_t e = hipMalloc((void**)&P.base, want);
     if (e != hipSuccess) {
         P.base = nullptr;
+        pool_note_release(dev, old_cap);
         return set_err(MLRS_ERR_ALLOC, "radius", (int64_t)want, 0, 0, (int)e,
                        "device allocation of %zu bytes for the radius scan failed: %s", want, hipGetErrorString(e));
     }
     P.cap = want;
+    pool_note_grow(dev, old_cap, want);
     return MLRS_OK;
 }
 
 static int32_t read_u64(const unsigned long long* dev, hipStream_t s, unsigned long long* out) {
+    note_read_back();
     hipError_t e = hipMemcpyAsync(out, dev, sizeof(*out), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_err(e, "radius read-back");
@@ -1377,6 +1417,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         hipError_t e2 = launch_fill_u32(B.mismatch, 1, 0u, s);
         if (e2 == hipSuccess) e2 = scan(RADIUS_FILL);
         if (e2 != hipSuccess) return hip_err(e2, "radius fill");
+        note_read_back();
         e2 = hipMemcpyAsync(bad, B.mismatch, sizeof(*bad), hipMemcpyDeviceToHost, s);
         if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
         if (e2 != hipSuccess) return hip_err(e2, "radius read-back");
@@ -1400,6 +1441,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
         counted_now = true;
         if (stage_cap > 0 && P.total <= (unsigned long long)capacity) {
             unsigned int over = 1;
+            note_read_back();
             hipError_t e2 = hipMemcpyAsync(&over, B.stage_over, sizeof(over), hipMemcpyDeviceToHost, s);
             if (e2 == hipSuccess) e2 = hipStreamSynchronize(s);
             if (e2 != hipSuccess) return hip_err(e2, "radius read-back");
@@ -1477,6 +1519,7 @@ static int32_t aux_workspace(size_t bytes, hipStream_t s, char** out) {
     hipError_t e;
     Arena& A = g_aux[dev];
     if (A.cap < bytes) {
+        const size_t old_cap = A.cap;
         if (A.base) {
             e = hipDeviceSynchronize();
             if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
@@ -1488,10 +1531,14 @@ static int32_t aux_workspace(size_t bytes, hipStream_t s, char** out) {
         e = hipMalloc((void**)&A.base, want);
         if (e != hipSuccess) {
             A.base = nullptr;
+            pool_note_release(dev, old_cap);
             return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)want, 0, 0, (int)e,
                            "device allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
         }
         A.cap = want;
+        pool_note_grow(dev, old_cap, want);
+    } else {
+        g_pool[dev].reuses += 1;
     }
     *out = A.base;
     return MLRS_OK;
@@ -1694,6 +1741,7 @@ struct KmRng {
 
 template <typename T>
 static int32_t km_d2h(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    note_read_back();
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     return e == hipSuccess ? MLRS_OK : hip_err(e, "kmeans read-back");
@@ -1922,6 +1970,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                 KernelTimer kt(s, "km_centroid_sums");
                 e = launch_km_centroid_sums<T>(x, lab[cur], n, d, k, nb, rpb, w, s);
             }
+            note_read_back();
             if (e == hipSuccess) e = hipMemcpyAsync(sums_h.data(), w.sums, sizeof(T) * (size_t)kd,
                                                     hipMemcpyDeviceToHost, s);
             if (e == hipSuccess) e = hipMemcpyAsync(counts_h.data(), w.counts, sizeof(uint32_t) * (size_t)k,
@@ -2126,6 +2175,55 @@ int32_t mlrs_timing_read(double* total_ms, int64_t* launches, char* kernel_name,
     return MLRS_OK;
 }
 
+}  // extern "C"
+
+namespace {
+template <typename T>
+int32_t device_copy_impl(const T* src, int64_t len, T* dst, int64_t dst_len, void* stream) {
+    CallGuard cg;
+    if (len < 0) return shape_err("src", len, 1, len);
+    if (dst_len != len) return shape_err("dst", len, 1, dst_len);
+    if (len == 0) return MLRS_OK;
+    if (!src || !dst) return set_err(MLRS_ERR_NULL_POINTER, "src", 0, 0, 0, 0, "null pointer");
+    const hipError_t e = launch_device_copy<T>(src, dst, len, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_err(e, "device_copy");
+    return MLRS_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t mlrs_device_copy_f32(const float* src, int64_t len, float* dst, int64_t dst_len, void* stream) {
+    return device_copy_impl<float>(src, len, dst, dst_len, stream);
+}
+int32_t mlrs_device_copy_f64(const double* src, int64_t len, double* dst, int64_t dst_len, void* stream) {
+    return device_copy_impl<double>(src, len, dst, dst_len, stream);
+}
+
+int32_t mlrs_pool_stats_get(mlrs_pool_stats* out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!out) return set_err(MLRS_ERR_NULL_POINTER, "out", 0, 0, 0, 0, "null pointer");
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        std::memset(out, 0, sizeof(*out));
+        return MLRS_OK;
+    }
+    *out = g_pool[dev];
+    return MLRS_OK;
+}
+
+int32_t mlrs_pool_stats_reset(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MLRS_OK;
+    mlrs_pool_stats& P = g_pool[dev];
+    P.allocations = 0;
+    P.reuses = 0;
+    P.read_backs = 0;
+    P.peak_bytes = P.live_bytes;
+    return MLRS_OK;
+}
+
 int32_t mlrs_release_workspace(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     int dev = 0;
@@ -2139,16 +2237,19 @@ int32_t mlrs_release_workspace(void) {
     }
     if (A.base) {
         (void)hipFree(A.base);
+        pool_note_release(dev, A.cap);
         A.base = nullptr;
         A.cap = 0;
     }
     if (X.base) {
         (void)hipFree(X.base);
+        pool_note_release(dev, X.cap);
         X.base = nullptr;
         X.cap = 0;
     }
     if (P.base) {
         (void)hipFree(P.base);
+        pool_note_release(dev, P.cap);
         P.base = nullptr;
         P.cap = 0;
         P.valid = false;

@@ -7,6 +7,8 @@
 // (crates/mlrs-algos/src/neighbors/nearest.rs:1117-1343,
 // crates/mlrs-backend/src/prims/distance.rs:428-551, prims/topk.rs:62-186).
 // The pairwise kernel alone is the pairwise-distance entry point.
+#include <algorithm>
+
 #include "knn_common.hpp"
 #include "knn_kernels.hpp"
 
@@ -819,6 +821,57 @@ __global__ void pow_inplace_kernel(T* __restrict__ v, int64_t n, T e) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) v[i] = FloatTraits<T>::pow_(v[i], e);
 }
+
+// copy_elem (crates/mlrs-kernels/src/elementwise.rs:71-125): dst = src.
+// 16-byte vectors when both pointers are 16-byte aligned, each thread moving
+// four of them per pass; the remainder (fewer than 16 bytes) and unaligned
+// buffers go element by element.
+__global__ __launch_bounds__(256) void copy_vec16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                         int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * 1024;
+    for (int64_t b = (int64_t)blockIdx.x * 1024 + threadIdx.x; b < n16; b += stride) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (b + 256 * u < n16) v[u] = src[b + 256 * u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (b + 256 * u < n16) dst[b + 256 * u] = v[u];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void copy_elems_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+template <typename T>
+hipError_t launch_device_copy(const T* src, T* dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    int64_t done = 0;
+    if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
+        const int64_t n16 = (n * (int64_t)sizeof(T)) / 16;
+        if (n16 > 0) {
+            const int64_t blocks = std::min<int64_t>((n16 + 1023) / 1024, 8192);
+            hipLaunchKernelGGL(copy_vec16_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                               reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), n16);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            done = n16 * 16 / (int64_t)sizeof(T);
+        }
+    }
+    if (done < n) {
+        const int64_t rest = n - done;
+        const int64_t blocks = std::min<int64_t>((rest + 255) / 256, 8192);
+        hipLaunchKernelGGL((copy_elems_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, src + done, dst + done,
+                           rest);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+template hipError_t launch_device_copy<float>(const float*, float*, int64_t, hipStream_t);
+template hipError_t launch_device_copy<double>(const double*, double*, int64_t, hipStream_t);
 
 template <typename T>
 hipError_t launch_pow_inplace(T* v, int64_t n, T e, hipStream_t s) {

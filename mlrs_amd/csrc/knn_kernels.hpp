@@ -182,6 +182,9 @@ hipError_t launch_pairwise_tile(const T* x, int64_t nx, const T* y, int64_t ny, 
                                 hipStream_t s, T pexp = T(0), int pint = 0, T root_exp = T(0));
 template <typename T>
 hipError_t launch_pow_inplace(T* v, int64_t n, T e, hipStream_t s);
+// dst[0..n) = src[0..n) (the fit-time ownership copy).
+template <typename T>
+hipError_t launch_device_copy(const T* src, T* dst, int64_t n, hipStream_t s);
 
 // Generic exact path: per-row (value, index) top-k over a materialized
 // rows x cols matrix, NaN never admitted, sentinel-padded; any k >= 1.  For k

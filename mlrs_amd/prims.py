@@ -19,6 +19,8 @@ Geometry is validated by the C ABI before any launch; a violation raises
 | ``kmeans_fit``      | KMeans::fit, crates/mlrs-algos/src/cluster/kmeans.rs:1353-1580 |
 | ``knn_regress``     | knn_regress_mean / knn_regress_gather, crates/mlrs-kernels/src/knn.rs:95-316 |
 | ``knn_classify``    | KNeighborsClassifier's host vote, crates/mlrs-algos/src/neighbors/classifier.rs:782-930 |
+| ``device_copy``     | device_copy, crates/mlrs-backend/src/prims/knn.rs:358-386         |
+| ``pool_stats``      | BufferPool::stats (PoolStats), crates/mlrs-backend/src/pool.rs:27-56,97 |
 """
 import ctypes
 
@@ -194,6 +196,33 @@ def row_sqnorms(x, out=None):
                                                _stream(x.device))
     _lib.check(rc)
     return o
+
+
+def device_copy(x, out=None):
+    """The fit-time ownership copy (mlrs_device_copy_*, the reference's
+    device_copy): a new device tensor holding ``x``'s values, or ``out``
+    filled with them."""
+    _dev_check(x)
+    s = _suffix(x)
+    if out is not None:
+        _check_out(out, "out", (x.dtype,), x.numel(), x.device)
+    o = torch.empty_like(x) if out is None else out
+    rc = getattr(_lib.load(), "mlrs_device_copy_" + s)(_ptr(x), x.numel(), _ptr(o), o.numel(), _stream(x.device))
+    _lib.check(rc)
+    return o
+
+
+def pool_stats():
+    """The library's buffer counters on the current device (mlrs_pool_stats_get):
+    a dict with allocations, reuses, peak_bytes, live_bytes, read_backs."""
+    st = _lib.PoolStats()
+    _lib.check(_lib.load().mlrs_pool_stats_get(ctypes.byref(st)))
+    return {name: int(getattr(st, name)) for name, _ in _lib.PoolStats._fields_}
+
+
+def pool_stats_reset():
+    """Zero the allocation, reuse and read-back counters (peak := live)."""
+    _lib.check(_lib.load().mlrs_pool_stats_reset())
 
 
 # Last match total per search shape (device, dtype, sizes, metric, p, radius):

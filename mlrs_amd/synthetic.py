@@ -14,6 +14,12 @@ c4  500,000 x 3 points U[0,1)^3, 5% of rows overwritten by exact copies of
 c5  5,000,000 x 64 points from a 1,024-component mixture (centres N(0, 25 I),
     unit std) against 1,024 centroids = centres + N(0, 0.01 I) (variance 0.01,
     i.e. std 0.1), f32, k=1 (nearest-centre assignment)
+
+and one more shape outside the five, an embedding-sized search:
+
+d256 index 200,000 x 256 and queries 5,000 x 256 from c2's generator at
+     d = 256 (100-component mixture, centres U[-10,10]^256, unit std), f32,
+     Euclidean, k=32
 """
 import numpy as np
 
@@ -25,6 +31,7 @@ CONFIGS = {
     "c3": dict(n_index=200_000, n_query=5_000, d=256, k=16, metric="cosine", dtype="f64"),
     "c4": dict(n_index=500_000, n_query=500_000, d=3, k=8, metric="euclidean", dtype="f32"),
     "c5": dict(n_index=1_024, n_query=5_000_000, d=64, k=1, metric="euclidean", dtype="f32"),
+    "d256": dict(n_index=200_000, n_query=5_000, d=256, k=32, metric="euclidean", dtype="f32"),
 }
 
 
@@ -79,7 +86,11 @@ def gen_c5(seed=SEED, n_points=5_000_000, n_centres=1_024, d=64):
     return x, centroids
 
 
-GENERATORS = {"c1": gen_c1, "c2": gen_c2, "c3": gen_c3, "c4": gen_c4, "c5": gen_c5}
+def gen_d256(seed=SEED, n_index=200_000, n_query=5_000, d=256):
+    return gen_c2(seed=seed, n_index=n_index, n_query=n_query, d=d)
+
+
+GENERATORS = {"c1": gen_c1, "c2": gen_c2, "c3": gen_c3, "c4": gen_c4, "c5": gen_c5, "d256": gen_d256}
 
 
 def generate(name, **kw):

@@ -17,7 +17,48 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libmlrs_oracle.so")
+_LIB_PATHS = {"x86-64-v3": os.path.join(_HERE, "libmlrs_oracle.so"),
+              "x86-64-v4": os.path.join(_HERE, "libmlrs_oracle_v4.so")}
+_V4_FLAGS = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
+
+
+def host_isa():
+    """The widest oracle build this CPU runs: x86-64-v4 when /proc/cpuinfo
+    lists the AVX-512 subsets it needs, else x86-64-v3.  MLRS_ORACLE_ISA
+    overrides."""
+    forced = os.environ.get("MLRS_ORACLE_ISA")
+    if forced in _LIB_PATHS:
+        return forced
+    try:
+        flags = set()
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    break
+        if all(x in flags for x in _V4_FLAGS):
+            return "x86-64-v4"
+    except OSError:
+        pass
+    return "x86-64-v3"
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def build_info():
+    """What the loaded oracle is: {"isa", "flags", "cpu_model"}."""
+    from . import build as _build
+    isa = host_isa()
+    return {"isa": isa, "flags": _build.flags_of(isa), "cpu_model": cpu_model()}
 
 METRIC_EUCLIDEAN = 0
 METRIC_COSINE = 1
@@ -38,10 +79,11 @@ def _load():
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(_LIB_PATH):
+    path = _LIB_PATHS[host_isa()]
+    if not os.path.exists(path):
         from . import build as _build  # noqa: F401  (oracle/build.py)
         _build.build()
-    lib = ctypes.CDLL(_LIB_PATH)
+    lib = ctypes.CDLL(path)
     i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
     lib.orc_knn_arm.argtypes = [i64, i64, i32]
     lib.orc_knn_arm.restype = i32

@@ -258,3 +258,20 @@ def test_noalloc_entry_validates_like_the_allocating_one():
 
 def test_every_k_up_to_n_train_is_served():
     assert _lib.load().mlrs_knn_max_k(4, 128, 0) == 2**31 - 1
+
+
+def test_device_copy_validation():
+    lib = _lib.load()
+    for f in (lib.mlrs_device_copy_f32, lib.mlrs_device_copy_f64):
+        assert f(P, 10, P, 9, None) == _lib.MLRS_ERR_SHAPE_MISMATCH
+        e = _info()
+        assert (e.operand, e.rows, e.cols, e.len) == (b"dst", 10, 1, 9)
+        assert f(P, -1, P, -1, None) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"src"
+        assert f(None, 4, P, 4, None) == _lib.MLRS_ERR_NULL_POINTER
+        assert f(None, 0, None, 0, None) == _lib.MLRS_OK
+
+
+def test_pool_stats_without_a_device():
+    st = _lib.PoolStats()
+    assert _lib.load().mlrs_pool_stats_get(ctypes.byref(st)) == _lib.MLRS_OK
+    assert _lib.load().mlrs_pool_stats_get(None) == _lib.MLRS_ERR_NULL_POINTER

@@ -4,17 +4,21 @@ Each configuration's full synthetic data is regenerated (mlrs_amd.synthetic,
 seeded) and checked against the generator fingerprints stored with the golden
 subsets; the engine then answers the WHOLE query set and
 
+* every row must equal the CPU oracle's answer, computed here on the host's
+  cores over the whole query set (about 20 s of CPU for c1-c5 together on 16
+  threads), bit for bit;
 * the golden subset (CPU-oracle answers against the full index, written by
-  tests/golden/gen_golden.py) must match bit for bit, and
+  tests/golden/gen_golden.py when the fixtures were made) must match too --
+  it guards against the generator or the oracle drifting between hosts;
 * every row must satisfy the size-independent properties of the reference's
   output contract: ascending values (index order on equal cosine values),
   indices in range and distinct per row, finite values; self-kNN rows start
-  at distance 0; k-means
-  labels in range with the label's squared distance the row minimum over a
-  sampled recomputation.
+  at distance 0; k-means labels in range with the label's squared distance
+  the row minimum over a sampled recomputation.
 """
 import os
 import sys
+import time
 
 import numpy as np
 import pytest
@@ -70,6 +74,14 @@ def test_config_knn_full_size(cfg):
     np.testing.assert_array_equal(idx[sub], z["idx"].astype(np.int64))
     np.testing.assert_array_equal(dist[sub], z["dist"])
     _row_properties(dist, idx, b.shape[0], c["metric"] == "cosine")
+    import oracle
+    t0 = time.time()
+    wd, wi = oracle.knn_topk(a, b, c["k"], c["metric"])
+    print("%s: oracle answered all %d rows in %.1f s" % (cfg, a.shape[0], time.time() - t0), flush=True)
+    bad = np.argwhere(idx != wi.astype(np.int64))
+    assert bad.size == 0, "%s: %d index mismatches, first %s" % (cfg, len(bad), bad[:3].tolist())
+    bad = np.argwhere(dist != wd)
+    assert bad.size == 0, "%s: %d distance mismatches, first %s" % (cfg, len(bad), bad[:3].tolist())
     if cfg == "c4":  # self-kNN: every point finds itself (or an exact duplicate) at distance 0
         assert np.all(dist[:, 0] == 0)
 
@@ -91,6 +103,14 @@ def test_config_kmeans_full_size():
     np.testing.assert_array_equal(sq[sub], z["sqdist"])
     assert np.all((labels >= 0) & (labels < b.shape[0]))
     assert np.all(np.isfinite(sq)) and np.all(sq >= 0)
+    import oracle
+    t0 = time.time()
+    wl, ws = oracle.kmeans_assign(a, b)
+    print("c5: oracle answered all %d rows in %.1f s" % (a.shape[0], time.time() - t0), flush=True)
+    bad = np.argwhere(labels != wl.astype(np.int64))
+    assert bad.size == 0, "c5: %d label mismatches, first %s" % (len(bad), bad[:3].tolist())
+    bad = np.argwhere(sq != ws)
+    assert bad.size == 0, "c5: %d distance mismatches, first %s" % (len(bad), bad[:3].tolist())
     # a sampled recomputation in float64: no centroid is clearly closer than the label's
     rng = np.random.default_rng(7)
     rows = rng.choice(a.shape[0], 4096, replace=False)

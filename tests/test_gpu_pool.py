@@ -1,0 +1,55 @@
+"""The fit-time device copy (mlrs_device_copy_*) and the buffer counters
+(mlrs_pool_stats_*): the search, assignment, pairwise and graph paths read
+nothing back to the host (the reference's memory gate asserts read_backs == 0
+across device-resident prims, e.g. crates/mlrs-backend/tests/laplacian_test.rs:
+266-276), the radius search reads back its total, and cached buffers are
+reused rather than reallocated across calls of one shape."""
+import numpy as np
+import pytest
+import torch
+
+from mlrs_amd import prims
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n,offset", [(1, 0), (3, 0), (1000003, 0), (1000003, 1), (777, 3), (4096, 2)])
+def test_device_copy(dtype, n, offset):
+    g = torch.Generator(device="cpu").manual_seed(n + offset)
+    base = torch.randn(n + offset + 5, generator=g, dtype=dtype).to(DEV)
+    src = base[offset:offset + n]
+    dst_base = torch.full((n + 7,), -7.0, dtype=dtype, device=DEV)
+    dst = dst_base[2:2 + n] if offset else dst_base[:n]
+    prims.device_copy(src, out=dst)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+    # nothing past the destination is touched
+    rest = torch.cat([dst_base[:2], dst_base[2 + n:]]) if offset else dst_base[n:]
+    assert torch.all(rest == -7.0)
+    c = prims.device_copy(src)
+    assert torch.equal(c, src) and c.data_ptr() != src.data_ptr()
+
+
+def test_search_paths_read_nothing_back():
+    g = torch.Generator(device="cpu").manual_seed(1)
+    xt = torch.randn((20000, 64), generator=g).to(DEV)
+    xq = torch.randn((500, 64), generator=g).to(DEV)
+    c = torch.randn((40, 64), generator=g).to(DEV)
+    prims.knn_topk(xq, xt, 16)                    # grows the buffers once
+    torch.cuda.synchronize()
+    prims.pool_stats_reset()
+    before = prims.pool_stats()
+    for _ in range(3):
+        prims.knn_topk(xq, xt, 16)
+    prims.kmeans_assign(xt, c)
+    prims.pairwise_distance(xq, c, "cosine")
+    prims.knn_graph(xq.double(), 5)
+    torch.cuda.synchronize()
+    after = prims.pool_stats()
+    assert after["read_backs"] == before["read_backs"] == 0
+    assert after["reuses"] >= 3
+    assert after["live_bytes"] > 0 and after["peak_bytes"] >= after["live_bytes"]
+    prims.radius_neighbors(xq, xt, 9.0)
+    assert prims.pool_stats()["read_backs"] > 0

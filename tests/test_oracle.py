@@ -19,13 +19,14 @@ for the fused multiply-add (one rounding of the exact a*b+c), so it is an
 independent restatement of the reference's operation order, not a copy of
 the C code.
 """
+import os
 from fractions import Fraction
 
 import numpy as np
 import pytest
 
 import oracle
-from conftest import assert_topk_matches, load_golden
+from conftest import ROOT, assert_topk_matches, load_golden
 
 
 # ---------------------------------------------------------------------------
@@ -401,6 +402,34 @@ def test_oracle_vs_sklearn(dtype, metric):
     assert_topk_matches(d, i, wd, wi, _brute(xq, xt, metric), atol_rel=1e-5 if dtype == np.float32 else 1e-12)
 
 
+@pytest.mark.parametrize("d", [129, 256])
+@pytest.mark.parametrize("metric", ["cosine", "euclidean"])
+def test_host_arm_f64_against_numpy_brute_force(d, metric):
+    """The knn_host arm (d > 128: reciprocal-norm cosine clamped to [0, 2],
+    crates/mlrs-backend/src/prims/knn_host.rs:382-397 and :749-760; mul+add
+    Euclidean) in f64 against an independent numpy f64 brute force (BLAS
+    products, another summation order) at the north star's 1e-12 relative
+    bar; indices equal except where the two picks' values tie within it.
+    Inputs as config c3: iid U[0,1), rows not normalised."""
+    assert oracle.knn_arm(d, 16, metric) == oracle.ARM_HOST
+    rng = np.random.default_rng(d)
+    xq, xt = rng.random((60, d)), rng.random((4000, d))
+    k = 16
+    got_d, got_i = oracle.knn_topk(xq, xt, k, metric)
+    if metric == "cosine":
+        nq_, nt_ = np.linalg.norm(xq, axis=1), np.linalg.norm(xt, axis=1)
+        full = np.clip(1.0 - (xq @ xt.T) / np.outer(nq_, nt_), 0.0, 2.0)
+    else:
+        full = np.sqrt(np.maximum(((xq[:, None, :] - xt[None, :, :]) ** 2).sum(-1), 0.0))
+    order = np.lexsort((np.broadcast_to(np.arange(xt.shape[0]), full.shape), full), axis=1)[:, :k]
+    want_d = np.take_along_axis(full, order, axis=1)
+    rel = np.abs(got_d - want_d) / np.abs(want_d)
+    assert rel.max() <= 1e-12, rel.max()
+    for r, c in np.argwhere(got_i != order):
+        picked = full[r, got_i[r, c]]
+        assert abs(picked - want_d[r, c]) <= 1e-12 * abs(want_d[r, c]), (r, c)
+
+
 def test_oracle_kmeans_vs_sklearn():
     from sklearn.cluster import KMeans
     rng = np.random.default_rng(8)
@@ -458,3 +487,48 @@ def test_metric_family_matches_exact_model(dtype, metric, p):
             np.testing.assert_allclose(d[r], np.array(want_v, dtype=dtype), rtol=4 * np.finfo(dtype).eps, atol=0)
         else:
             assert np.array_equal(d[r], np.array(want_v, dtype=dtype))
+
+
+_ISA_SCRIPT = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[2])
+import oracle
+assert oracle.host_isa() == sys.argv[3]
+rng = np.random.default_rng(0)
+out = {}
+for d, dt, metric in [(3, np.float32, "euclidean"), (64, np.float32, "euclidean"), (64, np.float32, "cosine"),
+                      (131, np.float64, "cosine"), (40, np.float64, "manhattan")]:
+    xq = rng.standard_normal((50, d)).astype(dt)
+    xt = rng.standard_normal((3000, d)).astype(dt)
+    dd, ii = oracle.knn_topk(xq, xt, 9, metric)
+    out["d_%d_%s" % (d, metric)], out["i_%d_%s" % (d, metric)] = dd, ii
+x = rng.standard_normal((5000, 16)).astype(np.float32)
+c = rng.standard_normal((33, 16)).astype(np.float32)
+out["lab"], out["sq"] = oracle.kmeans_assign(x, c)
+out["pw"] = oracle.pairwise(x[:100], c, "euclidean", sqrt=True)
+gi, gd = oracle.knn_graph(x[:800].astype(np.float64), 7, "cosine")
+out["gi"], out["gd"] = gi, gd
+fit = oracle.kmeans_fit(x, 8, "k-means++", seed=3, max_iter=5)
+out["fc"], out["fl"] = fit[0], fit[1]
+np.savez(sys.argv[1], **out)
+"""
+
+
+def test_isa_builds_return_the_same_bits(tmp_path):
+    """The x86-64-v3 and x86-64-v4 builds of the oracle (the box loads the
+    widest its CPU runs) agree bit for bit: -ffp-contract=off and no
+    reassociation leave vectorisation nothing to change."""
+    import subprocess
+    import sys
+    if oracle.host_isa() != "x86-64-v4":
+        pytest.skip("this host cannot run the AVX-512 build")
+    res = {}
+    for isa in ("x86-64-v3", "x86-64-v4"):
+        f = str(tmp_path / (isa + ".npz"))
+        env = dict(os.environ, MLRS_ORACLE_ISA=isa)
+        subprocess.run([sys.executable, "-c", _ISA_SCRIPT, f, ROOT, isa], check=True, env=env)
+        res[isa] = np.load(f)
+    a, b = res["x86-64-v3"], res["x86-64-v4"]
+    for key in a.files:
+        assert np.array_equal(a[key], b[key], equal_nan=True), key
