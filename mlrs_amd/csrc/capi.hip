@@ -471,9 +471,10 @@ static int pick_path(bool lowd_ok, bool gram_ok) {
 
 int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
                    int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
-    const bool cos = (arm == ARM_COS_FOLD);
+    const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
+    const bool host_cos = arm == ARM_COS_HOST;
     // sizes that do not depend on the strip count
-    size_t fixed = aligned_bytes(sizeof(float) * nq) + 2 * aligned_bytes(sizeof(float) * nt) +
+    size_t fixed = 2 * aligned_bytes(sizeof(float) * nq) + 3 * aligned_bytes(sizeof(float) * nt) +
                    aligned_bytes(sizeof(NormStats)) + 1024;
     char* ws;
     int cus;
@@ -495,12 +496,14 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     GramArgs32 a;
     std::memset(&a, 0, sizeof(a));
     float* qsq = cv.take<float>(nq);
+    float* qinv = cv.take<float>(nq);
     float* xsq = cv.take<float>(nt);
+    float* xinv = cv.take<float>(nt);
     float* xscale = cv.take<float>(nt);
     NormStats* stats = cv.take<NormStats>(1);
-    hipError_t e = launch_row_norms<float>(xq, nq, d, qsq, nullptr, nullptr, nullptr, s);
+    hipError_t e = launch_row_norms<float>(xq, nq, d, qsq, host_cos ? qinv : nullptr, nullptr, nullptr, s);
     if (e == hipSuccess)
-        e = launch_row_norms<float>(xt, nt, d, xsq, nullptr, cos ? xscale : nullptr, stats, s);
+        e = launch_row_norms<float>(xt, nt, d, xsq, host_cos ? xinv : nullptr, cos ? xscale : nullptr, stats, s);
     if (e != hipSuccess) return hip_err(e, "row_norms");
     a.q = xq;
     a.nq = nq;
@@ -512,6 +515,8 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     a.qsq = qsq;
     a.xsq = xsq;
     a.xscale = xscale;
+    a.qinv = host_cos ? qinv : nullptr;
+    a.xinv = host_cos ? xinv : nullptr;
     a.stats = stats;
     // Screen bounds (see knn_gram_f32.hip): with u = 2^-23 (covers any
     // rounding mode of the matrix core) the expansion's and the reference's
@@ -528,6 +533,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     }
     a.grid_wgs = grid_wgs;
     a.nslots = nslots;
+    a.qpb = gram_f32_queries_per_block(d);
     a.part_val = cv.take<float>(parts);
     a.part_idx = cv.take<uint32_t>(parts);
     if (qvals) a.qval = cv.take<float>(qvals);
@@ -735,7 +741,10 @@ int32_t knn_topk_f32_dispatch(const float* xq, int64_t n_query, int64_t n_featur
     const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
     const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
-    const bool gram_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD || arm == ARM_COS_FOLD) &&
+    // the knn_host cosine arm on the matrix cores in the wide shape only (it
+    // serves d > 128, where the wide shape runs)
+    const bool gram_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD || arm == ARM_COS_FOLD ||
+                          (arm == ARM_COS_HOST && n_features > 128)) &&
                          n_features <= gram_f32_max_d() && k <= gram_f32_max_k();
     int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)

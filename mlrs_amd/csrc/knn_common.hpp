@@ -387,4 +387,23 @@ __device__ __forceinline__ float pick16(const f32x16_t& a, int r) {
     return __uint_as_float(v);
 }
 
+// Element r (0..7) of the pair (a0, a1) = (a0[0..3], a1[0..3]), by the same
+// v_bfi_b32 select tree as pick16.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float pick8(const f32x4_t& a0, const f32x4_t& a1, int r) {
+    const uint32_t s0 = 0u - ((uint32_t)r & 1u), s1 = 0u - (((uint32_t)r >> 1) & 1u),
+                   s2 = 0u - (((uint32_t)r >> 2) & 1u);
+    const float e[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    uint32_t l1[4], l2[2], v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l1[i]) : "v"(s0), "v"(__float_as_uint(e[2 * i + 1])),
+            "v"(__float_as_uint(e[2 * i])));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l2[i]) : "v"(s1), "v"(l1[2 * i + 1]), "v"(l1[2 * i]));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(v) : "v"(s2), "v"(l2[1]), "v"(l2[0]));
+    return __uint_as_float(v);
+}
+
 }  // namespace mlrs

@@ -3,7 +3,7 @@
 // Replaces the GPU arm euclidean_topk_fused{,_dot,_dot_vec,_dot_vec8}
 // (crates/mlrs-kernels/src/knn.rs:377-2112) and the two-kernel
 // distance_direct -> top_k fallback (crates/mlrs-algos/src/neighbors/
-// nearest.rs:1058-1343) for f32, d <= 128, k <= 64, Euclidean and cosine.
+// nearest.rs:1058-1343) for f32, d <= 256, k <= 64, Euclidean and cosine.
 //
 // Shape of one workgroup: 4 waves x 32 queries = 128 queries, walking one
 // strip of index rows 32 at a time.
@@ -45,11 +45,8 @@ namespace mlrs {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kQpw = 32;                 // queries per wave (MFMA N dimension)
-constexpr int kQpb = kWaves * kQpw;      // queries per workgroup
-constexpr int kBn = 32;                  // index rows per tile (MFMA M dimension)
+constexpr int kBn = 32;                  // index rows per tile
 constexpr int kKcap = 64;                // largest k this kernel keeps
-constexpr int kQcap = 64;                // queued candidates per query
 constexpr int kQcapK1 = 48;              // k = 1: the screen tightens every tile, queues stay short
 constexpr int kShareEvery = 64;          // tiles between reads of the shared thresholds
 constexpr int kSumSlots = 16;            // segment summaries read per refresh (k > 1)
@@ -58,18 +55,38 @@ constexpr int kSumSlots = 16;            // segment summaries read per refresh (
 #endif
 constexpr int64_t kSeedRows = MLRS_SEED_ROWS;  // index rows sampled for the initial bound (k > 1)
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+// The two register shapes of a wave's block of (row, query) values.
+//  d <= 128 (W16 = false): 32 queries per wave, v_mfma_f32_32x32x2f32 over
+//    the 32-row tile; lane (h = lane / 32, jl = lane % 32) holds 16 of query
+//    jl's rows, and the query operand is d/2 VGPRs.
+//  128 < d <= 256 (W16 = true): 16 queries per wave, v_mfma_f32_16x16x4f32
+//    on the tile's two 16-row halves; lane (g = lane / 16, jl = lane % 16)
+//    holds 8 of query jl's rows, and lane group g contracts the g-th quarter
+//    of the feature axis, so the query operand is d/4 VGPRs (64 at d = 256).
+template <bool W16>
+struct GramShape {
+    static constexpr int qpw = W16 ? 16 : 32;      // queries per wave
+    static constexpr int qpb = kWaves * qpw;       // queries per workgroup
+    static constexpr int vals = W16 ? 8 : 16;      // tile values per lane
+    static constexpr int qcap = W16 ? 48 : 64;     // queued candidates per query (k > 1)
+};
+constexpr int kQpbNarrow = GramShape<false>::qpb;
+constexpr int kQpbWide = GramShape<true>::qpb;
+constexpr int kQvalPerWave = 32 * 64;             // screen values a wave may queue (either shape)
 
-template <int QCAP>
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int QCAP, int QPW>
 struct WaveLds {
-    uint32_t qidx[kQpw][QCAP];
-    float thr[kQpw];
-    float qa[kQpw];   // exact arm's query operand (row_sumsq for the fold arm)
-    float qs[kQpw];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
-    float eps[kQpw];  // screen error bound
-    uint32_t off[kQpw];                 // k = 1: queue offsets of the batched flush
-    uint32_t mode[kQpw];                // k > 1: 0 = screen-value list, 1 = exact list
-    unsigned long long best[kQpw];      // k = 1: (value bits << 32 | index) of the kept pair
+    uint32_t qidx[QPW][QCAP];
+    float thr[QPW];
+    float qa[QPW];   // exact arm's query operand (row_sumsq for the fold arm)
+    float qs[QPW];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
+    float eps[QPW];  // screen error bound
+    uint32_t off[QPW];                 // k = 1: queue offsets of the batched flush
+    uint32_t mode[QPW];                // k > 1: 0 = screen-value list, 1 = exact list
+    unsigned long long best[QPW];      // k = 1: (value bits << 32 | index) of the kept pair
 };
 
 // (value, index) packed so that unsigned order is the (value, index) order
@@ -92,6 +109,18 @@ __device__ __forceinline__ float screen_threshold(float R, float qs, float eps) 
         if (qs == 0.0f) return inf;
         return round_up_f(((double)R + (double)eps - 1.0) * (double)qs);
     }
+}
+
+// The arms' per-row and per-query operands of the exact evaluation: the
+// squared norm (cosine fold: sqrt(||q||^2 ||x||^2)), the reciprocal norm
+// (knn_host cosine) or nothing (Euclidean).
+template <int ARM>
+__device__ __forceinline__ float row_operand(const GramArgs32& a, int64_t t) {
+    return (ARM == ARM_COS_FOLD) ? a.xsq[t] : (ARM == ARM_COS_HOST) ? a.xinv[t] : 0.0f;
+}
+template <int ARM>
+__device__ __forceinline__ float query_operand(const GramArgs32& a, int64_t q) {
+    return (ARM == ARM_COS_FOLD) ? a.qsq[q] : (ARM == ARM_COS_HOST) ? a.qinv[q] : 0.0f;
 }
 
 // Exact value of one (query, row) pair in the arm's operation order, loads
@@ -126,6 +155,11 @@ __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const fl
                 acc = acc + d1 * d1;
                 acc = acc + d2 * d2;
                 acc = acc + d3 * d3;
+            } else if (ARM == ARM_COS_HOST) {  // mul + add dot
+                acc = acc + a[u].x * b[u].x;
+                acc = acc + a[u].y * b[u].y;
+                acc = acc + a[u].z * b[u].z;
+                acc = acc + a[u].w * b[u].w;
             } else {  // ARM_COS_FOLD: fma dot
                 acc = __builtin_fmaf(a[u].x, b[u].x, acc);
                 acc = __builtin_fmaf(a[u].y, b[u].y, acc);
@@ -148,6 +182,11 @@ __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const fl
             acc = acc + d1 * d1;
             acc = acc + d2 * d2;
             acc = acc + d3 * d3;
+        } else if (ARM == ARM_COS_HOST) {
+            acc = acc + a.x * b.x;
+            acc = acc + a.y * b.y;
+            acc = acc + a.z * b.z;
+            acc = acc + a.w * b.w;
         } else {
             acc = __builtin_fmaf(a.x, b.x, acc);
             acc = __builtin_fmaf(a.y, b.y, acc);
@@ -160,6 +199,9 @@ __device__ __forceinline__ float exact_f32(const float* __restrict__ q, const fl
         float sim = (denom > 0.0f) ? acc / denom : 0.0f;
         return clamp02<float>(1.0f - sim);
     }
+    // knn_host cosine (crates/mlrs-backend/src/prims/knn_host.rs:749-760):
+    // reciprocal norms, 1 - dot * (1/||q||) * (1/||x||), clamped
+    if (ARM == ARM_COS_HOST) return clamp02<float>(1.0f - acc * qa * ya);
     return acc;
 }
 
@@ -199,16 +241,27 @@ struct GramOcc {
 
 template <int NG, int ARM, bool COS, bool VEC4, bool K1>
 __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kernel(GramArgs32 a) {
+    constexpr bool W16 = NG > 16;     // the wide shape (GramShape)
+    typedef GramShape<W16> SH;
+    constexpr int QPW = SH::qpw;
+    constexpr int QPB = SH::qpb;
     constexpr int DP = NG * 8;        // padded feature count
-    constexpr int STRIDE = DP + 4;    // LDS row stride (floats)
+    // LDS row stride (floats).  Narrow: rows 4 banks apart, so the A-operand
+    // ds_read_b128 of 16 consecutive rows do not conflict.  Wide: no padding
+    // (two 64 KB tiles must leave room for a second workgroup); instead each
+    // row's 16-byte chunks are XOR-swizzled by the row's low four bits, with
+    // the same effect (DP is a multiple of 64 there, so chunks stay in their row).
+    constexpr int STRIDE = W16 ? DP : DP + 4;
     constexpr int TILE_F4 = kBn * DP / 4;
     constexpr int PF = (TILE_F4 + 255) / 256;
+    constexpr int QQ = DP / 4;        // wide: features per lane-group quarter
+    constexpr int NQR = W16 ? QQ / 4 : NG;  // 16-byte query-operand chunks per lane
 
     __shared__ __attribute__((aligned(16))) float tile[2][kBn][STRIDE];
     __shared__ __attribute__((aligned(16))) float tnorm[2][kBn];
-    constexpr int QCAP = K1 ? kQcapK1 : kQcap;
+    constexpr int QCAP = K1 ? kQcapK1 : SH::qcap;
     constexpr int kFlushAt = QCAP - kBn;  // flush when a queue may overflow next tile
-    __shared__ WaveLds<QCAP> wl[kWaves];
+    __shared__ WaveLds<QCAP, QPW> wl[kWaves];
 
     // Kernel arguments as locals: they stay in SGPRs.
     const float* __restrict__ Q = a.q;
@@ -223,18 +276,28 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
-    const int h = lane >> 5;
-    const int jl = lane & 31;
-    WaveLds<QCAP>& L = wl[w];
+    // narrow: h = lane / 32 picks the 4-row group of each 8-row slab;
+    // wide: g = lane / 16 picks the 4-row group of each 16-row half and the
+    // feature quarter.  jl: the lane's query within the wave.
+    const int h = W16 ? (lane >> 4) : (lane >> 5);
+    const int jl = lane & (QPW - 1);
+    WaveLds<QCAP, QPW>& L = wl[w];
     const float inf = __builtin_huge_valf();
     // screen values of this wave's queued pairs, [queue position][query]
-    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * (kQpw * kQcap);
+    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * kQvalPerWave;
+
+    // Tile row of value r of this lane.
+    auto row_of = [&](int r) -> int {
+        return W16 ? 16 * (r >> 2) + 4 * h + (r & 3) : 8 * (r >> 2) + 4 * h + (r & 3);
+    };
+    // LDS float offset of 16-byte chunk c of tile row r.
+    auto chunk_at = [&](int r, int c) -> int { return r * STRIDE + 4 * (W16 ? (c ^ (r & 15)) : c); };
 
     // ---- work split (StreamSplit): this workgroup's range of (query block,
     //      tile) units, panel-major; each piece of a job in the range is a
     //      segment with its own exact lists [slot][nq][k], merged at the end
     //      by knn_merge_f32_kernel. ----
-    const StreamSplit sp(nq, nt, kQpb, kBn, a.grid_wgs);
+    const StreamSplit sp(nq, nt, QPB, kBn, a.grid_wgs);
     const int64_t wg = xcd_grouped_wg(blockIdx.x, gridDim.x);
     const int64_t u_hi = ((wg + 1) * sp.P < sp.T) ? (wg + 1) * sp.P : sp.T;
     for (int64_t u = wg * sp.P; u < u_hi;) {
@@ -251,12 +314,17 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     const int64_t nsum = SUMM ? (sp.slots_of(qblock) < kSumSlots ? sp.slots_of(qblock) : kSumSlots) : 0;
     const int rk1 = (k + 3) / 4, rk2 = (k + 1) / 2, rk3 = (3 * k + 3) / 4;
 
-    const int64_t qwave = qblock * kQpb + w * kQpw;  // first query of this wave
+    const int64_t qwave = qblock * QPB + w * QPW;  // first query of this wave
     const int64_t qmine = qwave + jl;
     const bool qvalid = qmine < nq;
     const int64_t t_begin = tile0 * kBn;
     int64_t t_end = tile1 * kBn;
     if (t_end > nt) t_end = nt;
+
+    // Feature of chunk element e of the lane's query-operand chunk i.
+    auto qfeat = [&](int i, int e) -> int64_t {
+        return W16 ? (int64_t)h * QQ + 4 * i + e : (int64_t)8 * i + 4 * h + e;
+    };
 
     // ---- segment start: the loads first, from clamped rows so that they are
     //      unconditional and all in flight together (a segment of k-means
@@ -266,12 +334,12 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     const int64_t qrow = qvalid ? qmine : nq - 1;
     const float qsq_l = QSQ[qrow];
     const float r0_l = SHARED_R ? __uint_as_float(SHARED_R[qrow]) : inf;
-    float4 qreg[NG];
+    float4 qreg[NQR];
     if (VEC4 && kEarlyQ) {
         const float* qp = Q + qrow * d;
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            const int64_t c = 8 * g + 4 * h;
+        for (int g = 0; g < NQR; ++g) {
+            const int64_t c = qfeat(g, 0);
             const float4 v = *reinterpret_cast<const float4*>(qp + (c < d ? c : d - 4));
             qreg[g] = (qvalid && c < d) ? v : make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -279,7 +347,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 
     // ---- per-query constants, lists, queues ----
     uint32_t cntr = 0u;  // queued candidates of query jl
-    if (lane < kQpw) {
+    if (lane < QPW) {
         const float qsq = qvalid ? qsq_l : 0.0f;
         L.thr[lane] = qvalid ? inf : -inf;
         if (!COS) {
@@ -288,7 +356,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             L.eps[lane] = (float)(a.eps_rel * ((double)qsq + (double)a.stats->xsq_max) + a.eps_abs);
         } else {
             L.qs[lane] = __builtin_sqrtf(qsq);
-            L.qa[lane] = qsq;
+            L.qa[lane] = (ARM == ARM_COS_HOST) ? (qvalid ? a.qinv[qrow] : 0.0f) : qsq;
             L.eps[lane] = (float)a.eps_abs;
         }
         // Screen-value lists need |screen distance - exact| <= eps for every
@@ -300,9 +368,9 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         L.mode[lane] = sv ? 0u : 1u;
     }
     if (K1) {
-        if (lane < kQpw) L.best[lane] = kBestEmpty;
+        if (lane < QPW) L.best[lane] = kBestEmpty;
     } else {
-        for (int j = 0; j < kQpw; ++j) {
+        for (int j = 0; j < QPW; ++j) {
             const int64_t qg = qwave + j;
             if (qg < nq && lane < K2) {
                 LV[qg * K2 + lane] = inf;
@@ -311,25 +379,25 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         }
     }
     // Strips that start late begin from the bound earlier strips have reached.
-    if (SHARED_R && lane < kQpw && qvalid)
+    if (SHARED_R && lane < QPW && qvalid)
         L.thr[lane] = fminf(L.thr[lane], screen_threshold<COS>(r0_l, L.qs[lane], L.eps[lane]));
 
-    // ---- query operand: qreg[g] = scale * q[8g+4h .. 8g+4h+3] (aligned rows:
-    //      loaded above, one 16-byte load per group) ----
+    // ---- query operand: qreg[i] = scale * q[qfeat(i, 0..3)] (aligned rows:
+    //      one 16-byte load per chunk) ----
     {
         const float scale = COS ? 1.0f : -2.0f;
         const float* qp = Q + qmine * d;
         if (VEC4) {
             if (!kEarlyQ) {
 #pragma unroll
-                for (int g = 0; g < NG; ++g) {
-                    const int64_t c = 8 * g + 4 * h;
+                for (int g = 0; g < NQR; ++g) {
+                    const int64_t c = qfeat(g, 0);
                     qreg[g] = (qvalid && c < d) ? *reinterpret_cast<const float4*>(qp + c)
                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
 #pragma unroll
-            for (int g = 0; g < NG; ++g) {
+            for (int g = 0; g < NQR; ++g) {
                 qreg[g].x *= scale;
                 qreg[g].y *= scale;
                 qreg[g].z *= scale;
@@ -337,11 +405,11 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             }
         } else {
 #pragma unroll
-            for (int g = 0; g < NG; ++g) {
+            for (int g = 0; g < NQR; ++g) {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    int64_t c = 8 * g + 4 * h + e;
+                    const int64_t c = qfeat(g, e);
                     v[e] = (qvalid && c < d) ? qp[c] * scale : 0.0f;
                 }
                 qreg[g] = make_float4(v[0], v[1], v[2], v[3]);
@@ -361,25 +429,32 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         const int f = tid + 256 * p;
         pf_r[p] = f / (DP / 4);
         const int c4 = f % (DP / 4);
-        pf_on[p] = (f < TILE_F4) && (VEC4 ? (4 * c4 < d) : (4 * c4 < d));
+        pf_on[p] = (f < TILE_F4) && (4 * c4 < d);
         pf_src[p] = X + (t_begin + pf_r[p]) * d + 4 * c4;
     }
     // Whole tiles of rows without padded columns load unconditionally.
     const bool pf_fast = VEC4 && (PF * 256 == TILE_F4) && (d == DP);
+    // Wide rows: a thread's chunks lie in one column, PF_RPP rows apart, so one
+    // pointer and uniform offsets address them (eight live 64-bit pointers
+    // would not fit next to the 64-register query operand).
+    constexpr int PF_RPP = (256 % (DP / 4) == 0) ? 256 / (DP / 4) : 0;
+    constexpr bool PF_ONE_PTR = W16 && PF_RPP > 0;
+    // The address, row and on-flag of prefetch chunk p (wide rows: derived
+    // from chunk 0's).
+#define MLRS_PF_SRC(p) (PF_ONE_PTR ? pf_src[0] + (int64_t)(p) * PF_RPP * d : pf_src[p])
+#define MLRS_PF_ROW(p) (PF_ONE_PTR ? pf_r[0] + (p) * PF_RPP : pf_r[p])
+#define MLRS_PF_ON(p) (PF_ONE_PTR ? pf_on[0] : pf_on[p])
 #define MLRS_PREFETCH(T0)                                                                    \
     do {                                                                                     \
         const uint32_t t0_ = (uint32_t)(T0);                                                 \
         if (pf_fast && t0_ + (uint32_t)kBn <= t_end32) {                                     \
-            _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                 \
-                pf[p] = gload4(pf_src[p]);                                                   \
-                pf_src[p] += kBn * d;                                                        \
-            }                                                                                \
+            _Pragma("unroll") for (int p = 0; p < PF; ++p) pf[p] = gload4(MLRS_PF_SRC(p));   \
         } else {                                                                             \
         _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);                                      \
-            const uint32_t t = t0_ + (uint32_t)pf_r[p];                                      \
-            if (pf_on[p] && t < t_end32) {                                                   \
-                const float* src = pf_src[p];                                                \
+            const uint32_t t = t0_ + (uint32_t)MLRS_PF_ROW(p);                               \
+            if (MLRS_PF_ON(p) && t < t_end32) {                                              \
+                const float* src = MLRS_PF_SRC(p);                                           \
                 if (VEC4) {                                                                  \
                     v = gload4(src);                                                         \
                 } else {                                                                     \
@@ -391,9 +466,9 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
                 }                                                                            \
             }                                                                                \
             pf[p] = v;                                                                       \
-            pf_src[p] += kBn * d;                                                            \
         }                                                                                    \
         }                                                                                    \
+        _Pragma("unroll") for (int p = 0; p < (PF_ONE_PTR ? 1 : PF); ++p) pf_src[p] += kBn * d; \
         if (tid < kBn) {                                                                     \
             const uint32_t t = t0_ + (uint32_t)tid;                                          \
             if (COS)                                                                         \
@@ -413,8 +488,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     //      among the k best), the old list and the queue are re-evaluated
     //      exactly and the query's list stays exact from then on. ----
 #define MLRS_EXACT_AT(T_)                                                                    \
-    exact_f32<ARM, VEC4>(Q + qg_ * d, X + (int64_t)(T_) * d, d, L.qa[j_],                    \
-                         (ARM == ARM_COS_FOLD) ? XSQ[(T_)] : 0.0f)
+    exact_f32<ARM, VEC4>(Q + qg_ * d, X + (int64_t)(T_) * d, d, L.qa[j_], row_operand<ARM>(a, (T_)))
 #define MLRS_FLUSH(J)                                                                        \
     do {                                                                                     \
         const int j_ = (J);                                                                  \
@@ -427,7 +501,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
             t_ = L.qidx[j_][lane];                                                           \
-            const float s_ = exact_ ? 0.0f : QVw[lane * kQpw + j_];                          \
+            const float s_ = exact_ ? 0.0f : QVw[lane * QPW + j_];                           \
             if (exact_ || s_ != s_)                                                          \
                 e_ = MLRS_EXACT_AT(t_);                                                      \
             else                                                                             \
@@ -495,22 +569,22 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     //      batches, kept with a 64-bit LDS atomicMin on (value, index) ----
 #define MLRS_FLUSH_K1()                                                                      \
     do {                                                                                     \
-        const uint32_t c_ = (lane < kQpw) ? cntr : 0u;                                       \
+        const uint32_t c_ = (lane < QPW) ? cntr : 0u;                                        \
         uint32_t incl_ = c_;                                                                 \
-        _Pragma("unroll") for (int m_ = 1; m_ < kQpw; m_ <<= 1) {                            \
+        _Pragma("unroll") for (int m_ = 1; m_ < QPW; m_ <<= 1) {                             \
             const uint32_t o_ = (uint32_t)__shfl_up((int)incl_, m_, 64);                     \
-            if ((lane & 31) >= m_) incl_ += o_;                                              \
+            if ((lane & (QPW - 1)) >= m_) incl_ += o_;                                       \
         }                                                                                    \
-        const uint32_t total_ = (uint32_t)__shfl((int)incl_, kQpw - 1, 64);                  \
-        if (lane < kQpw) L.off[lane] = incl_ - c_;                                           \
+        const uint32_t total_ = (uint32_t)__shfl((int)incl_, QPW - 1, 64);                   \
+        if (lane < QPW) L.off[lane] = incl_ - c_;                                            \
         for (uint32_t base_ = 0; base_ < total_; base_ += 64) {                              \
             const uint32_t e_ = base_ + (uint32_t)lane;                                      \
             if (e_ < total_) {                                                               \
                 int j_ = 0;                                                                  \
-                _Pragma("unroll") for (int m_ = 16; m_ >= 1; m_ >>= 1) if (L.off[j_ + m_] <= e_) \
+                _Pragma("unroll") for (int m_ = QPW / 2; m_ >= 1; m_ >>= 1) if (L.off[j_ + m_] <= e_) \
                     j_ += m_;                                                                \
                 const uint32_t t_ = L.qidx[j_][e_ - L.off[j_]];                              \
-                const float ya_ = (ARM == ARM_COS_FOLD) ? XSQ[t_] : 0.0f;                    \
+                const float ya_ = row_operand<ARM>(a, t_);                                   \
                 const float v_ = exact_f32<ARM, VEC4>(Q + (qwave + j_) * d, X + (int64_t)t_ * d, d, \
                                                        L.qa[j_], ya_);                       \
                 if (v_ == v_)                                                                \
@@ -518,7 +592,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             }                                                                                \
         }                                                                                    \
         cntr = 0u;                                                                           \
-        if (lane < kQpw) {                                                                   \
+        if (lane < QPW) {                                                                    \
             float R_ = __uint_as_float((uint32_t)(L.best[lane] >> 32));                      \
             if (SHARED_R && qvalid && R_ < inf) {                                            \
                 const unsigned int old_ = atomicMin(&SHARED_R[qmine], __float_as_uint(R_));  \
@@ -544,107 +618,173 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             if (f < TILE_F4) {
                 const int r = f / (DP / 4);
                 const int c4 = f % (DP / 4);
-                *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = pf[p];
+                *reinterpret_cast<float4*>(&tile[buf][0][0] + chunk_at(r, c4)) = pf[p];
             }
         }
         if (tid < kBn) tnorm[buf][tid] = pfn;
         __syncthreads();
         if (t0 + kBn < t_end) MLRS_PREFETCH(t0 + kBn);
 
+        // The lane's tile values: narrow, acc[r] = row row_of(r); wide, r < 4
+        // in acc0 (the first 16-row half) and r >= 4 in acc1.
         f32x16 acc;
-        if (!COS) {
+        f32x4 acc0, acc1;
+        if constexpr (!W16) {
+            if (!COS) {
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                float4 n4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
-                acc[4 * g4 + 0] = n4.x;
-                acc[4 * g4 + 1] = n4.y;
-                acc[4 * g4 + 2] = n4.z;
-                acc[4 * g4 + 3] = n4.w;
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    float4 n4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                    acc[4 * g4 + 0] = n4.x;
+                    acc[4 * g4 + 1] = n4.y;
+                    acc[4 * g4 + 2] = n4.z;
+                    acc[4 * g4 + 3] = n4.w;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+            }
+            // A operands double-buffered: the next group's LDS read is issued
+            // before the current group's four MFMAs (the scheduling barriers keep
+            // that order), so its latency hides under ~256 MFMA cycles.
+            const float* arow = &tile[buf][jl][4 * h];
+            float4 av = *reinterpret_cast<const float4*>(arow);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                float4 an = av;
+                if (g + 1 < NG) an = *reinterpret_cast<const float4*>(arow + 8 * (g + 1));
+                __builtin_amdgcn_sched_barrier(0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qreg[g].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qreg[g].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qreg[g].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                av = an;
+            }
+            if (COS) {
+                // rows scaled by -1/||x_t|| after the contraction (the scales ride
+                // in tnorm), so the prefetched loads need no arithmetic before the
+                // next tile's LDS store
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const float4 s4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                    acc[4 * g4 + 0] *= s4.x;
+                    acc[4 * g4 + 1] *= s4.y;
+                    acc[4 * g4 + 2] *= s4.z;
+                    acc[4 * g4 + 3] *= s4.w;
+                }
             }
         } else {
+            const float4 n0 = *reinterpret_cast<const float4*>(&tnorm[buf][4 * h]);
+            const float4 n1 = *reinterpret_cast<const float4*>(&tnorm[buf][16 + 4 * h]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-        }
-        // A operands double-buffered: the next group's LDS read is issued
-        // before the current group's four MFMAs (the scheduling barriers keep
-        // that order), so its latency hides under ~256 MFMA cycles.
-        const float* arow = &tile[buf][jl][4 * h];
-        float4 av = *reinterpret_cast<const float4*>(arow);
+            for (int r = 0; r < 4; ++r) {
+                acc0[r] = COS ? 0.0f : (&n0.x)[r];
+                acc1[r] = COS ? 0.0f : (&n1.x)[r];
+            }
+            // A operands: this lane's rows jl and 16 + jl, its quarter's chunk
+            // i, one group ahead; each chunk feeds eight MFMAs (four k-steps
+            // on each half).
+            const float* t0p = &tile[buf][0][0];
+            const int c0 = h * (QQ / 4);
+            float4 av0 = *reinterpret_cast<const float4*>(t0p + chunk_at(jl, c0));
+            float4 av1 = *reinterpret_cast<const float4*>(t0p + chunk_at(16 + jl, c0));
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            float4 an = av;
-            if (g + 1 < NG) an = *reinterpret_cast<const float4*>(arow + 8 * (g + 1));
-            __builtin_amdgcn_sched_barrier(0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qreg[g].x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qreg[g].y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qreg[g].z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            av = an;
-        }
-        if (COS) {
-            // rows scaled by -1/||x_t|| after the contraction (the scales ride
-            // in tnorm), so the prefetched loads need no arithmetic before the
-            // next tile's LDS store
+            for (int i = 0; i < NQR; ++i) {
+                float4 an0 = av0, an1 = av1;
+                if (i + 1 < NQR) {
+                    an0 = *reinterpret_cast<const float4*>(t0p + chunk_at(jl, c0 + i + 1));
+                    an1 = *reinterpret_cast<const float4*>(t0p + chunk_at(16 + jl, c0 + i + 1));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av0.x, qreg[i].x, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av1.x, qreg[i].x, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av0.y, qreg[i].y, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av1.y, qreg[i].y, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av0.z, qreg[i].z, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av1.z, qreg[i].z, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av0.w, qreg[i].w, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av1.w, qreg[i].w, acc1, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                av0 = an0;
+                av1 = an1;
+            }
+            if (COS) {
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                const float4 s4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
-                acc[4 * g4 + 0] *= s4.x;
-                acc[4 * g4 + 1] *= s4.y;
-                acc[4 * g4 + 2] *= s4.z;
-                acc[4 * g4 + 3] *= s4.w;
+                for (int r = 0; r < 4; ++r) {
+                    acc0[r] *= (&n0.x)[r];
+                    acc1[r] *= (&n1.x)[r];
+                }
             }
         }
+        auto val = [&](int r) -> float {
+            if constexpr (W16) return r < 4 ? acc0[r] : acc1[r - 4];
+            else return acc[r];
+        };
 
         // ---- k = 1: tighten with this tile's smallest expansion value ----
         if (!COS && k == 1) {
             float m = inf;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) m = fminf(m, acc[r]);  // NaN ignored; past-end rows are +inf
+            for (int r = 0; r < SH::vals; ++r) m = fminf(m, val(r));  // NaN ignored; past-end rows are +inf
+            if (W16) m = fminf(m, shfl_xor_f(m, 16));
             m = fminf(m, shfl_xor_f(m, 32));
             if (m < inf) thr = fminf(thr, round_up_f((double)m + 2.0 * (double)L.eps[jl]));
         }
 
-        // ---- screen: lane (jl, h) holds rows 8*(r/4) + 4h + (r%4) of the tile
-        //      for query jl.  Passing rows are appended to the query's queue at
-        //      cntr (kept in registers, equal in lanes jl and jl + 32); the h = 1
-        //      lane writes after the h = 0 lane's entries. ----
+        // ---- screen: value r of the lane is tile row row_of(r) for query jl.
+        //      Passing rows are appended to the query's queue at cntr (kept in
+        //      registers, equal in every lane of the query); the lanes of a
+        //      query write in lane order, each after the earlier lanes' entries. ----
         uint32_t m = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) m |= (uint32_t)!(acc[r] > thr) << r;
+        for (int r = 0; r < SH::vals; ++r) m |= (uint32_t)!(val(r) > thr) << r;
         if (!qvalid) m = 0;
         if (t0 + kBn > t_end) {  // partial tile: rows past the segment are not candidates
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if ((uint32_t)t0 + (uint32_t)(8 * (r >> 2) + 4 * h + (r & 3)) >= t_end32) m &= ~(1u << r);
+            for (int r = 0; r < SH::vals; ++r)
+                if ((uint32_t)t0 + (uint32_t)row_of(r) >= t_end32) m &= ~(1u << r);
         }
         if (__builtin_amdgcn_ballot_w64(m != 0)) {
             const uint32_t c = (uint32_t)__builtin_popcount(m);
-            const uint32_t co = shfl_xor_u(c, 32);
-            uint32_t pos = cntr + (h ? co : 0u);
-            const uint32_t tb = (uint32_t)t0 + 4u * (uint32_t)h;
+            uint32_t before, total;
+            if constexpr (W16) {
+                // exclusive prefix and total over the query's four lanes (h = 0..3)
+                const uint32_t u1 = (uint32_t)__shfl_up((int)c, 16, 64);
+                const uint32_t s1 = c + (h >= 1 ? u1 : 0u);
+                const uint32_t u2 = (uint32_t)__shfl_up((int)s1, 32, 64);
+                const uint32_t incl = s1 + (h >= 2 ? u2 : 0u);
+                before = incl - c;
+                total = (uint32_t)__shfl((int)incl, 48 + jl, 64);
+            } else {
+                const uint32_t co = shfl_xor_u(c, 32);
+                before = h ? co : 0u;
+                total = c + co;
+            }
+            uint32_t pos = cntr + before;
+            const uint32_t tb = (uint32_t)t0;
             if (K1) {
                 while (m) {
                     const int r = __builtin_ctz(m);
                     m &= m - 1;
-                    L.qidx[jl][pos++] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
+                    L.qidx[jl][pos++] = tb + (uint32_t)row_of(r);
                 }
             } else {
                 // one iteration per admitted row of the lane (usually one)
                 while (m) {
                     const int r = __builtin_ctz(m);
                     m &= m - 1;
-                    L.qidx[jl][pos] = tb + (uint32_t)(8 * (r >> 2) + (r & 3));
-                    QVw[pos * kQpw + jl] = pick16(acc, r);
+                    L.qidx[jl][pos] = tb + (uint32_t)row_of(r);
+                    if constexpr (W16) QVw[pos * QPW + jl] = pick8(acc0, acc1, r);
+                    else QVw[pos * QPW + jl] = pick16(acc, r);
                     ++pos;
                 }
             }
-            cntr += c + co;
+            cntr += total;
         }
         // ---- flush queries whose queue could overflow on the next tile ----
-        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > (uint32_t)kFlushAt);
+        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < QPW && cntr > (uint32_t)kFlushAt);
         if (mask) {
-            if (lane < kQpw) L.thr[lane] = fminf(L.thr[lane], thr);
+            if (lane < QPW) L.thr[lane] = fminf(L.thr[lane], thr);
             if (K1) {
                 MLRS_FLUSH_K1();
             } else {
@@ -661,7 +801,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         }
         // ---- pick up thresholds tightened by other strips of these queries ----
         if (SHARED_R && (++tiles % kShareEvery) == 0) {
-            if (lane < kQpw && qvalid) {
+            if (lane < QPW && qvalid) {
                 float R = __uint_as_float(SHARED_R[qmine]);
                 if (nsum > 0) {
                     // the smallest T with at least k pairs <= T over the
@@ -720,7 +860,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 
     // ---- final flush of every non-empty queue ----
     {
-        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > 0u);
+        uint64_t mask = __builtin_amdgcn_ballot_w64(lane < QPW && cntr > 0u);
         if (K1) {
             if (mask) MLRS_FLUSH_K1();
         } else {
@@ -737,9 +877,12 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 #undef MLRS_FLUSH
 #undef MLRS_EXACT_AT
 #undef MLRS_PREFETCH
+#undef MLRS_PF_SRC
+#undef MLRS_PF_ROW
+#undef MLRS_PF_ON
 
     // ---- k = 1: the kept pair becomes this segment's one-entry list ----
-    if (K1 && lane < kQpw && qvalid) {
+    if (K1 && lane < QPW && qvalid) {
         const unsigned long long b = L.best[lane];
         LV[qmine] = __uint_as_float((uint32_t)(b >> 32));
         LI[qmine] = (uint32_t)b;
@@ -759,7 +902,7 @@ __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t
     if (qg >= a.nq) return;
     const int64_t d = a.d;
     const float inf = __builtin_huge_valf();
-    const float qa = (ARM == ARM_COS_FOLD) ? a.qsq[qg] : 0.0f;
+    const float qa = query_operand<ARM>(a, qg);
     float lv = inf;
     uint32_t li = kSentinelIdx;
     for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
@@ -768,7 +911,7 @@ __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t
         uint32_t t = kSentinelIdx;
         if (s < nsamp) {
             t = (uint32_t)((s * a.nt) / nsamp);
-            const float ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f;
+            const float ya = row_operand<ARM>(a, t);
             e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
             if (e != e) {
                 e = inf;
@@ -801,8 +944,8 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
     const int K2 = gram_list_cap(k);
     const int64_t d = a.d;
     const float inf = __builtin_huge_valf();
-    const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
-    const int64_t nsl = sp.slots_of(qg / kQpb);
+    const StreamSplit sp(a.nq, a.nt, a.qpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / a.qpb);
     // the k-th smallest value over the union of the lists
     float uv = inf;
     uint32_t ui = kSentinelIdx;
@@ -817,7 +960,7 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
         wave_merge64<float>(uv, ui, v, ix, lane);
     }
     const float qsq = a.qsq[qg];
-    const float eps = (ARM == ARM_COS_FOLD)
+    const float eps = (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST)
                           ? (float)a.eps_abs
                           : (float)(a.eps_rel * ((double)qsq + (double)a.stats->xsq_max) + a.eps_abs);
     double W = (double)bcast_f(uv, k - 1) + 2.0 * (double)eps;
@@ -831,8 +974,8 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
         uint32_t t = kSentinelIdx;
         if ((uint32_t)lane < count) {
             t = cand[wv][lane];
-            e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qsq,
-                                     (ARM == ARM_COS_FOLD) ? a.xsq[t] : 0.0f);
+            e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, query_operand<ARM>(a, qg),
+                                        row_operand<ARM>(a, t));
             if (e != e) {
                 e = inf;
                 t = kSentinelIdx;
@@ -872,8 +1015,8 @@ __global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
     if (qg >= a.nq) return;
     float lv = a.part_val[qg];
     uint32_t li = a.part_idx[qg];
-    const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
-    const int64_t nsl = sp.slots_of(qg / kQpb);
+    const StreamSplit sp(a.nq, a.nt, a.qpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / a.qpb);
     for (int64_t s = 1; s < nsl; ++s) {
         const float v = a.part_val[s * a.nq + qg];
         const uint32_t ix = a.part_idx[s * a.nq + qg];
@@ -893,7 +1036,7 @@ __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
 
 template <int NG, int ARM, bool COS, bool VEC4>
 hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
-    dim3 grid((unsigned)StreamSplit(a.nq, a.nt, kQpb, kBn, a.grid_wgs).G);
+    dim3 grid((unsigned)StreamSplit(a.nq, a.nt, a.qpb, kBn, a.grid_wgs).G);
     (void)nblocks;
     if (a.k == 1)
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true>), grid, dim3(256), 0, s, a);
@@ -905,11 +1048,23 @@ hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
 template <int ARM, bool COS, bool VEC4>
 hipError_t launch_arm(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     const int ng = (int)((a.d + 7) / 8);
+    // the split and the merge must see the query-block size of the shape
+    if (a.qpb != (ng > 16 ? kQpbWide : kQpbNarrow)) return hipErrorInvalidValue;
     if (ng <= 2) return launch_ng<2, ARM, COS, VEC4>(a, nblocks, s);
     if (ng <= 4) return launch_ng<4, ARM, COS, VEC4>(a, nblocks, s);
     if (ng <= 8) return launch_ng<8, ARM, COS, VEC4>(a, nblocks, s);
     if (ng <= 12) return launch_ng<12, ARM, COS, VEC4>(a, nblocks, s);
-    return launch_ng<16, ARM, COS, VEC4>(a, nblocks, s);
+    if (ng <= 16) return launch_ng<16, ARM, COS, VEC4>(a, nblocks, s);
+    if (ng <= 24) return launch_ng<24, ARM, COS, VEC4>(a, nblocks, s);
+    return launch_ng<32, ARM, COS, VEC4>(a, nblocks, s);
+}
+
+template <int ARM, bool COS, bool VEC4>
+hipError_t launch_wide(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
+    const int ng = (int)((a.d + 7) / 8);
+    if (ng <= 16 || a.qpb != kQpbWide) return hipErrorInvalidValue;
+    if (ng <= 24) return launch_ng<24, ARM, COS, VEC4>(a, nblocks, s);
+    return launch_ng<32, ARM, COS, VEC4>(a, nblocks, s);
 }
 
 template <int ARM, bool VEC4>
@@ -921,8 +1076,11 @@ hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
 
 }  // namespace
 
+int gram_f32_queries_per_block(int64_t d) { return d > 128 ? kQpbWide : kQpbNarrow; }
+
 void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots) {
-    const StreamSplit full(nq, nt, kQpb, kBn, 1);
+    const int64_t qpb = gram_f32_queries_per_block(d);
+    const StreamSplit full(nq, nt, qpb, kBn, 1);
     // one resident round (two workgroups per CU, three for k = 1 at d <= 64:
     // GramOcc), but at least 16 tiles each
     const int per_cu = (k == 1 && d <= 64) ? 3 : 2;
@@ -930,12 +1088,11 @@ void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* 
     if (g0 > full.T / 16) g0 = full.T / 16;
     if (g0 < 1) g0 = 1;
     *grid_wgs = g0;
-    *nslots = (int)StreamSplit(nq, nt, kQpb, kBn, g0).nslots();
+    *nslots = (int)StreamSplit(nq, nt, qpb, kBn, g0).nslots();
 }
 
 int gram_f32_max_k() { return kKcap; }
-int gram_f32_max_d() { return 128; }
-int gram_f32_queries_per_block() { return kQpb; }
+int gram_f32_max_d() { return 256; }
 int gram_f32_rows_per_tile() { return kBn; }
 
 hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
@@ -958,6 +1115,8 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
                         : launch_seed<ARM_EUCLID_MULADD, false>(a, nsamp, s);
         if (arm == ARM_COS_FOLD)
             return vec4 ? launch_seed<ARM_COS_FOLD, true>(a, nsamp, s) : launch_seed<ARM_COS_FOLD, false>(a, nsamp, s);
+        if (arm == ARM_COS_HOST)
+            return vec4 ? launch_seed<ARM_COS_HOST, true>(a, nsamp, s) : launch_seed<ARM_COS_HOST, false>(a, nsamp, s);
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r, a.nq);
@@ -983,11 +1142,13 @@ hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s) {
         return vec4 ? launch_merge<ARM_EUCLID_MULADD, true>(a, s) : launch_merge<ARM_EUCLID_MULADD, false>(a, s);
     if (arm == ARM_COS_FOLD)
         return vec4 ? launch_merge<ARM_COS_FOLD, true>(a, s) : launch_merge<ARM_COS_FOLD, false>(a, s);
+    if (arm == ARM_COS_HOST)
+        return vec4 ? launch_merge<ARM_COS_HOST, true>(a, s) : launch_merge<ARM_COS_HOST, false>(a, s);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
-    const int64_t nblocks = (a.nq + kQpb - 1) / kQpb;
+    const int64_t nblocks = (a.nq + a.qpb - 1) / a.qpb;
     const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
     hipError_t e;
@@ -1000,6 +1161,9 @@ hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s) {
     else if (arm == ARM_COS_FOLD)
         e = vec4 ? launch_arm<ARM_COS_FOLD, true, true>(a, nblocks, s)
                  : launch_arm<ARM_COS_FOLD, true, false>(a, nblocks, s);
+    else if (arm == ARM_COS_HOST)  // the knn_host arm serves cosine above d = 128 only: wide shapes
+        e = vec4 ? launch_wide<ARM_COS_HOST, true, true>(a, nblocks, s)
+                 : launch_wide<ARM_COS_HOST, true, false>(a, nblocks, s);
     else
         return hipErrorInvalidValue;
     return e;

@@ -97,14 +97,17 @@ struct GramArgs32 {
     const float* qsq;  // query row_sumsq
     const float* xsq;  // index row_sumsq
     const float* xscale;  // cosine: -1/||x_t|| (0 for zero rows)
+    const float* qinv;    // knn_host cosine: query reciprocal norms (0 for zero rows)
+    const float* xinv;    // knn_host cosine: index reciprocal norms
     const NormStats* stats;
     double eps_rel;    // Euclidean screen bound: eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
     double eps_abs;    // cosine screen bound (absolute)
     int64_t grid_wgs;  // the G0 the StreamSplit is built from (<= one resident round)
     int nslots;        // list slots per query (StreamSplit::nslots)
+    int qpb;           // queries per workgroup: gram_f32_queries_per_block(d)
     float* part_val;   // [nslots][nq][gram_list_cap(k)] lists, one per (segment, query)
     uint32_t* part_idx;
-    float* qval;       // [grid_wgs][4 waves][32 queries][64]: screen values of the queued pairs (k > 1)
+    float* qval;       // [grid_wgs][4 waves][2048]: screen values of the queued pairs (k > 1)
     float4* summ;      // [nslots][nq]: per-(segment, query) list summaries (k > 1), or null
     float* out_val;    // [nq][k]
     uint32_t* out_idx;
@@ -131,7 +134,8 @@ hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
 hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s);
 int gram_f32_max_k();
 int gram_f32_max_d();
-int gram_f32_queries_per_block();
+// 128 queries per workgroup for d <= 128 (32 per wave), 64 above (16 per wave)
+int gram_f32_queries_per_block(int64_t d);
 int gram_f32_rows_per_tile();
 
 struct GramArgs64 {

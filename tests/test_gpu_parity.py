@@ -64,11 +64,16 @@ LOWD = [(300, 2000, 3, 8), (257, 1000, 1, 1), (100, 3000, 16, 32), (1000, 5000, 
 # Gram-MFMA path (f32, 16 < d <= 128, k <= 64)
 GRAM = [(300, 3000, 64, 10), (129, 1000, 17, 5), (500, 4000, 128, 32), (77, 600, 100, 64),
         (1000, 70000, 128, 32), (5, 100, 33, 1), (200, 2048, 24, 20), (1, 31, 40, 31), (130, 5000, 96, 7)]
-# generic exact path (k > 64, d > 128)
-GENERIC = [(50, 500, 64, 100), (20, 300, 64, 200), (30, 400, 200, 10)]
+# Gram-MFMA path, wide shape (f32, 128 < d <= 256: 16 queries per wave on
+# 16x16x4 MFMAs; d not a multiple of 4 takes the element-wise loads)
+GRAM_WIDE = [(300, 3000, 256, 10), (129, 1000, 129, 5), (500, 4000, 192, 32), (77, 600, 200, 64),
+             (1000, 30000, 256, 32), (5, 100, 160, 1), (200, 2048, 255, 20), (1, 31, 136, 31),
+             (130, 5000, 250, 7), (65, 3000, 256, 1), (70, 9000, 176, 16)]
+# generic exact path (k > 64, d > 256)
+GENERIC = [(50, 500, 64, 100), (20, 300, 64, 200), (30, 400, 300, 10)]
 
 
-@pytest.mark.parametrize("case", LOWD + GRAM + GENERIC)
+@pytest.mark.parametrize("case", LOWD + GRAM + GRAM_WIDE + GENERIC)
 def test_f32_euclidean_bitwise(case):
     nq, nt, d, k = case
     xq, xt = _data(100 + d, nq, nt, d)
@@ -76,7 +81,8 @@ def test_f32_euclidean_bitwise(case):
 
 
 @pytest.mark.parametrize("case", [(300, 3000, 64, 10), (100, 2000, 5, 7), (50, 500, 130, 8), (40, 400, 64, 80),
-                                  (600, 20000, 128, 32)])
+                                  (600, 20000, 128, 32), (300, 5000, 256, 16), (50, 2000, 150, 32),
+                                  (129, 3000, 200, 1), (64, 1000, 193, 64)])
 def test_f32_cosine_bitwise(case):
     nq, nt, d, k = case
     xq, xt = _data(200 + d, nq, nt, d)
@@ -101,7 +107,7 @@ def test_f64_bitwise(case, metric):
     check_knn(xq, xt, k, metric, str(case))
 
 
-@pytest.mark.parametrize("d", [3, 64])
+@pytest.mark.parametrize("d", [3, 64, 256])
 def test_duplicates_and_boundary_ties(d):
     """100 identical rows around the k-th slot: membership and order are
     decided by index alone (knn_metric_kernel_test.rs:269-289)."""
@@ -114,7 +120,7 @@ def test_duplicates_and_boundary_ties(d):
     assert np.all(gd[0] == 0)
 
 
-@pytest.mark.parametrize("d,k", [(3, 8), (48, 24)])
+@pytest.mark.parametrize("d,k", [(3, 8), (48, 24), (208, 24)])
 def test_quantized_data_many_ties(d, k):
     rng = np.random.default_rng(6)
     xt = rng.integers(-3, 4, size=(4000, d)).astype(np.float32)
@@ -123,7 +129,7 @@ def test_quantized_data_many_ties(d, k):
     check_knn(xq, xt, k, "cosine", "quantized cosine")
 
 
-@pytest.mark.parametrize("d", [4, 64])
+@pytest.mark.parametrize("d", [4, 64, 200])
 def test_nan_rows(d):
     xq, xt = _data(8, 200, 1500, d)
     xt[[3, 700, 1499]] = np.nan
@@ -136,14 +142,14 @@ def test_nan_rows(d):
     check_knn(xq[:20], small, 8, "euclidean", "nan sentinel")
 
 
+@pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("perturb", [0.0, 1e-4])
-def test_near_ties_across_segments(perturb):
+def test_near_ties_across_segments(perturb, d):
     """Copies of each query (exact, or perturbed far inside the screen's error
     window) spread through a large index, so they fall in different segments
     of the fused split: each segment's list and the final merge must resolve
     them by exact value, then index."""
     rng = np.random.default_rng(31)
-    d = 64
     xt = rng.standard_normal((80000, d)).astype(np.float32)
     xq = rng.standard_normal((12, d)).astype(np.float32)
     for j in range(12):
@@ -166,11 +172,24 @@ def test_cosine_nan_rows():
     assert gi[0, :3].tolist() == [2, 1500, 2999] and np.all(gd[0, :3] == 1.0)
 
 
-def test_cosine_zero_rows():
-    xq, xt = _data(9, 100, 1000, 40)
+@pytest.mark.parametrize("d", [40, 200])
+def test_cosine_zero_rows(d):
+    xq, xt = _data(9, 100, 1000, d)
     xt[[0, 5, 999]] = 0.0
     xq[3] = 0.0
     check_knn(xq, xt, 10, "cosine", "zero rows")
+
+
+def test_cosine_host_arm_nan_rows():
+    """Above d = 128 cosine is the knn_host arm: a NaN row's value is NaN and
+    never admitted (the fold arm scores it 1 instead)."""
+    rng = np.random.default_rng(33)
+    xt = rng.standard_normal((3000, 144)).astype(np.float32)
+    xq = rng.standard_normal((64, 144)).astype(np.float32)
+    xt[[2, 1500, 2999]] = np.nan
+    xq[7] = np.nan
+    gd, gi = check_knn(xq, xt, 16, "cosine", "host cosine nan")
+    assert not np.isin(gi[np.arange(64) != 7], [2, 1500, 2999]).any()
 
 
 @pytest.mark.parametrize("d", [5, 200])
@@ -200,10 +219,11 @@ def test_f64_nonaligned_pointer():
     assert_same(d_.cpu().numpy(), i_.cpu().numpy(), wd, wi, "f64 offset")
 
 
-def test_huge_values_overflow_norms():
+@pytest.mark.parametrize("d", [64, 240])
+def test_huge_values_overflow_norms(d):
     """Squared norms overflow f32: the screen bound becomes infinite and every
     row is evaluated exactly; results still match the reference arithmetic."""
-    xq, xt = _data(10, 40, 500, 64, scale=1e18)
+    xq, xt = _data(10, 40, 500, d, scale=1e18)
     xt[:5] *= 1e2
     check_knn(xq, xt, 6, "euclidean", "huge")
 
@@ -214,9 +234,10 @@ def test_k_equals_n_train_and_tiny_index():
     check_knn(xq, xt[:1], 1, "euclidean", "n_train=1")
 
 
-def test_nonaligned_pointer_and_odd_d():
-    xq, xt = _data(12, 70, 900, 37)
-    tq = _t(np.concatenate([np.zeros((1, 37), np.float32), xq]))[1:]  # 148-byte offset -> not 16-aligned
+@pytest.mark.parametrize("d", [37, 137])
+def test_nonaligned_pointer_and_odd_d(d):
+    xq, xt = _data(12, 70, 900, d)
+    tq = _t(np.concatenate([np.zeros((1, d), np.float32), xq]))[1:]  # 4*d-byte offset -> not 16-aligned
     tq = tq.contiguous()
     d_, i_ = prims.knn_topk(tq, _t(xt), 9)
     torch.cuda.synchronize()
@@ -269,7 +290,7 @@ def test_kmeans_ties_and_nan(d):
     assert lab[30].item() == 0 and np.isnan(sq[30].item())
 
 
-@pytest.mark.parametrize("d", [8, 33, 64, 100])
+@pytest.mark.parametrize("d", [8, 33, 64, 100, 200])
 def test_kmeans_queue_overflow_ties(d):
     """500 identical centres: every row of a tile passes the k = 1 screen, so
     the candidate queues overflow and flush inside the tile loop many times;
@@ -288,7 +309,7 @@ def test_kmeans_queue_overflow_ties(d):
     assert lab[0].item() == 3 and sq[0].item() == 0.0
 
 
-@pytest.mark.parametrize("d", [24, 64])
+@pytest.mark.parametrize("d", [24, 64, 160])
 def test_k1_search_all_duplicates(d):
     """k = 1 search over an index of mostly identical rows (every query's queue
     overflows on every tile): the lowest index of the tied rows wins."""
