@@ -54,8 +54,22 @@ def build(verbose=False, jobs=4):
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n%s%s" % (r.stdout, r.stderr))
+    _check_resolved(tmp)
     os.replace(tmp, OUT)
     return OUT
+
+
+def _check_resolved(lib):
+    """A shared library links with undefined symbols; one of the engine's own
+    (e.g. a kernel launch stub the host pass dropped) would only fail when the
+    library is loaded.  Fail the build instead."""
+    r = subprocess.run(["nm", "-u", "-C", lib], capture_output=True, text=True)
+    if r.returncode != 0:
+        return  # no nm: nothing to check with
+    own = [l.strip() for l in r.stdout.splitlines() if "mlrs" in l]
+    if own:
+        os.unlink(lib)
+        raise RuntimeError("the engine library leaves its own symbols undefined:\n  " + "\n  ".join(own[:20]))
 
 
 if __name__ == "__main__":

@@ -613,7 +613,7 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     a.shared_r = cv.take<unsigned long long>(nq);
     a.out_val = out_v;
     a.out_idx = out_i;
-    e = launch_gram_f64_prep(a, s);
+    e = launch_gram_f64_prep(a, arm, s);
     if (e == hipSuccess) {
         KernelTimer timer(s, "knn_gram_f64_kernel");
         e = launch_gram_f64(a, arm, s);

@@ -134,6 +134,63 @@ __device__ __forceinline__ T exact_pair(const T* __restrict__ q, const T* __rest
     }
 }
 
+// Exact values of QS (query, row) pairs that share one row, each in the
+// arm's operation order (exact_pair's): the row's elements are read once for
+// all QS queries.  VEC: d a multiple of the 16-byte vector and every row
+// 16-byte aligned.
+template <typename T, int ARM, int QS, bool VEC>
+__device__ __forceinline__ void exact_pairs_shared_row(const T* const (&q)[QS], const T* __restrict__ y, int64_t d,
+                                                       const T (&qa)[QS], T ya, T (&out)[QS]) {
+    using F = FloatTraits<T>;
+    T acc[QS];
+#pragma unroll
+    for (int j = 0; j < QS; ++j) acc[j] = T(0);
+    auto step = [&](T qv, T yv, T& a) {
+        if (ARM == ARM_EUCLID_FMA) {
+            const T diff = qv - yv;
+            a = F::fma_(diff, diff, a);
+        } else if (ARM == ARM_EUCLID_MULADD) {
+            const T diff = qv - yv;
+            a = a + diff * diff;
+        } else if (ARM == ARM_COS_FOLD) {
+            a = F::fma_(qv, yv, a);
+        } else {  // ARM_COS_HOST
+            a = a + qv * yv;
+        }
+    };
+    constexpr int W = 16 / (int)sizeof(T);  // elements per 16-byte vector
+    typedef T vec_t __attribute__((ext_vector_type(W)));
+    int64_t c = 0;
+    if (VEC) {
+        for (; c + W <= d; c += W) {
+            const vec_t yv = *reinterpret_cast<const vec_t*>(y + c);
+#pragma unroll
+            for (int j = 0; j < QS; ++j) {
+                const vec_t qv = *reinterpret_cast<const vec_t*>(q[j] + c);
+#pragma unroll
+                for (int e = 0; e < W; ++e) step(qv[e], yv[e], acc[j]);
+            }
+        }
+    }
+    for (; c < d; ++c) {
+        const T yv = y[c];
+#pragma unroll
+        for (int j = 0; j < QS; ++j) step(q[j][c], yv, acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < QS; ++j) {
+        if (ARM == ARM_COS_FOLD) {
+            const T denom = F::sqrt_(qa[j] * ya);
+            const T sim = (denom > T(0)) ? acc[j] / denom : T(0);
+            out[j] = clamp02<T>(T(1) - sim);
+        } else if (ARM == ARM_COS_HOST) {
+            out[j] = clamp02<T>(T(1) - acc[j] * qa[j] * ya);
+        } else {
+            out[j] = acc[j];
+        }
+    }
+}
+
 // Smallest float >= t (screen thresholds are rounded up, never down).
 __device__ __forceinline__ float round_up_f(double t) {
     float f = (float)t;
@@ -385,6 +442,21 @@ __device__ __forceinline__ float pick16(const f32x16_t& a, int r) {
         asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l3[i]) : "v"(s2), "v"(l2[2 * i + 1]), "v"(l2[2 * i]));
     asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(v) : "v"(s3), "v"(l3[1]), "v"(l3[0]));
     return __uint_as_float(v);
+}
+
+// 16 bytes per lane from global memory straight into LDS (gfx950's
+// global_load_lds_dwordx4, counted by vmcnt): lane i's bytes land at
+// lds_wave_base + 16 i, lds_wave_base uniform over the wave.  The builtin
+// exists only for the device target; the host pass, which never runs a
+// kernel body, compiles the call away (it would otherwise drop the kernel's
+// launch stub).
+__device__ __forceinline__ void global_to_lds16(const void* g, void* lds_wave_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+#else
+    (void)g;
+    (void)lds_wave_base;
+#endif
 }
 
 // Element r (0..7) of the pair (a0, a1) = (a0[0..3], a1[0..3]), by the same

@@ -894,34 +894,53 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 
 // Initial per-query bound: the k-th smallest exact value over an evenly
 // spaced sample of index rows.  Any k distinct rows bound the final k-th
-// value from above, so the screen starts tight instead of at +inf.
+// value from above, so the screen starts tight instead of at +inf.  A wave
+// seeds kSeedQpw queries: lane l evaluates sample row l of each batch of 64
+// against all of them, so every sampled row is read once per wave.
+constexpr int kSeedQpw = 4;
 template <int ARM, bool VEC4>
 __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t nsamp) {
     const int lane = threadIdx.x & 63;
-    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (qg >= a.nq) return;
+    const int64_t q0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kSeedQpw;
+    if (q0 >= a.nq) return;
     const int64_t d = a.d;
     const float inf = __builtin_huge_valf();
-    const float qa = query_operand<ARM>(a, qg);
-    float lv = inf;
-    uint32_t li = kSentinelIdx;
+    const float* qp[kSeedQpw];
+    float qa[kSeedQpw], lv[kSeedQpw];
+    uint32_t li[kSeedQpw];
+#pragma unroll
+    for (int j = 0; j < kSeedQpw; ++j) {
+        const int64_t qg = (q0 + j < a.nq) ? q0 + j : a.nq - 1;  // past the end: repeats a query, not written
+        qp[j] = a.q + qg * d;
+        qa[j] = query_operand<ARM>(a, qg);
+        lv[j] = inf;
+        li[j] = kSentinelIdx;
+    }
     for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
         const int64_t s = s0 + lane;
-        float e = inf;
+        float e[kSeedQpw];
         uint32_t t = kSentinelIdx;
+#pragma unroll
+        for (int j = 0; j < kSeedQpw; ++j) e[j] = inf;
         if (s < nsamp) {
             t = (uint32_t)((s * a.nt) / nsamp);
-            const float ya = row_operand<ARM>(a, t);
-            e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
-            if (e != e) {
-                e = inf;
-                t = kSentinelIdx;
-            }
+            exact_pairs_shared_row<float, ARM, kSeedQpw, VEC4>(qp, a.x + (int64_t)t * d, d, qa, row_operand<ARM>(a, t),
+                                                              e);
         }
-        wave_sort64<float>(e, t, lane);
-        wave_merge64<float>(lv, li, e, t, lane);
+#pragma unroll
+        for (int j = 0; j < kSeedQpw; ++j) {
+            uint32_t tj = t;
+            if (e[j] != e[j]) {
+                e[j] = inf;
+                tj = kSentinelIdx;
+            }
+            wave_sort64<float>(e[j], tj, lane);
+            wave_merge64<float>(lv[j], li[j], e[j], tj, lane);
+        }
     }
-    if (lane == a.k - 1) a.shared_r[qg] = __float_as_uint(lv);
+#pragma unroll
+    for (int j = 0; j < kSeedQpw; ++j)
+        if (lane == a.k - 1 && q0 + j < a.nq) a.shared_r[q0 + j] = __float_as_uint(lv[j]);
 }
 
 // Merge the per-segment lists of one query per wave and emit the output
@@ -1069,8 +1088,9 @@ hipError_t launch_wide(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
 
 template <int ARM, bool VEC4>
 hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
-    hipLaunchKernelGGL((knn_seed_f32_kernel<ARM, VEC4>), dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a,
-                       nsamp);
+    const int64_t per_block = 4 * kSeedQpw;
+    hipLaunchKernelGGL((knn_seed_f32_kernel<ARM, VEC4>), dim3((unsigned)((a.nq + per_block - 1) / per_block)),
+                       dim3(256), 0, s, a, nsamp);
     return hipGetLastError();
 }
 

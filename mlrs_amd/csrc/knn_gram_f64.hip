@@ -35,7 +35,7 @@ constexpr int kQpw = 16;               // queries per wave (MFMA N dimension)
 constexpr int kQpb = kWaves * kQpw;    // queries per workgroup
 constexpr int kBn = 16;                // index rows per tile (MFMA M dimension)
 constexpr int kKcap = 64;              // largest k kept
-constexpr int kQcap = 32;              // queued candidates per query
+constexpr int kQcap = 48;              // queued candidates per query (two workgroups still fit a CU's LDS)
 constexpr int kFlushAt = kQcap - kBn;  // flush when a queue may overflow on the next tile
 constexpr int kShareEvery = 32;        // tiles between reads of the shared bound
 constexpr int kMaxD = 256;
@@ -125,9 +125,21 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     constexpr int RPG = 256 / CPT;         // tile rows one pass of the workgroup loads
     constexpr int PF = kBn / RPG;          // passes per tile
     static_assert(RPG >= 1 && kBn % RPG == 0, "tile fill shape");
+    // Rows of whole kilobytes (d padded to 128 or 256) with 16-byte aligned
+    // operands load the next tile straight into LDS (global_load_lds_dwordx4:
+    // each wave instruction fills one contiguous kilobyte, half or all of a
+    // row), so no registers hold it in flight; other shapes stage it through
+    // registers.
+    constexpr bool DIRECT = VEC2 && (DP % 128 == 0);
+    constexpr int KB_PER_ROW = DP >= 128 ? DP / 128 : 1;  // 1 KB wave loads per tile row (DIRECT)
+    constexpr int LOADS_PER_WAVE = kBn * KB_PER_ROW / kWaves;
 
-    __shared__ __attribute__((aligned(16))) double tile[2][kBn][STRIDE];
-    __shared__ __attribute__((aligned(16))) double tnorm[2][kBn];
+    // The two tile buffers are distinct objects, so the compiler can tell the
+    // direct loads into one from the reads of the other.
+    __shared__ __attribute__((aligned(16))) double tileA[kBn][STRIDE];
+    __shared__ __attribute__((aligned(16))) double tileB[kBn][STRIDE];
+    __shared__ __attribute__((aligned(16))) double tnA[kBn];
+    __shared__ __attribute__((aligned(16))) double tnB[kBn];
     __shared__ WaveLds64 wl[kWaves];
 
     const double* __restrict__ Q = a.q;
@@ -338,57 +350,120 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
         if (jl == j_) cntr = 0u;                                                             \
     } while (0)
 
-#define MLRS_STORE64(B)                                                                      \
+#define MLRS_STORE64(DST, TN)                                                                \
     do {                                                                                     \
         if (pr0 < RPG) {                                                                     \
-            double* dst_ = &tile[(B)][pr0][2 * pc2];                                         \
+            double* dst_ = &(DST)[pr0][2 * pc2];                                             \
             _Pragma("unroll") for (int p = 0; p < PF; ++p)                                   \
                 *reinterpret_cast<double2*>(dst_ + p * RPG * STRIDE) = pf[p];                \
         }                                                                                    \
-        if (tid < kBn) tnorm[(B)][tid] = pfn;                                                \
+        if (tid < kBn) (TN)[tid] = pfn;                                                      \
     } while (0)
 
-    // The next tile is loaded into registers before this tile's MFMAs and
-    // stored into the other LDS buffer right after them, so the prefetch
-    // registers are free again during the screen and the rescoring.
+    // Direct loads of tile T0's rows into DST: wave w fills kilobytes
+    // w*LOADS_PER_WAVE + i of the tile (row kb / KB_PER_ROW, its half kb %
+    // KB_PER_ROW); a row past the segment is not loaded (its values are masked
+    // out of the screen).  The row norms go through a register as in the
+    // staged path.
+    auto direct_load = [&](double (&dst)[kBn][STRIDE], uint32_t t0) {
+        if constexpr (DIRECT) {
+#pragma unroll
+        for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+            const int kb = w * LOADS_PER_WAVE + i;
+            const int r = kb / KB_PER_ROW, half = kb % KB_PER_ROW;
+            const uint32_t t = t0 + (uint32_t)r;
+            const int c = half * 128 + 2 * lane;
+            if (t < t_end32 && c < d)
+                global_to_lds16(X + (int64_t)t * d + c, &dst[r][half * 128]);
+        }
+        }
+        if (tid < kBn) {
+            const uint32_t t = t0 + (uint32_t)tid;
+            if (COS)
+                pfn = (t < t_end32) ? XSCALE[t] : 0.0;
+            else
+                pfn = (t < t_end32) ? XSQ[t] : inf;
+        }
+    };
+    if (DIRECT && d < DP) {
+        // columns past d are never loaded: zero them once in both buffers
+        // (they meet the query operand's zeros, and garbage could be NaN)
+        const int pad = (int)(DP - d);
+        for (int e = tid; e < kBn * pad; e += 256) {
+            tileA[e / pad][d + e % pad] = 0.0;
+            tileB[e / pad][d + e % pad] = 0.0;
+        }
+    }
+
+    // The next tile is loaded (into registers, or straight into the other LDS
+    // buffer) before this tile's MFMAs; staged registers are stored into the
+    // other buffer right after them, so they are free again during the screen
+    // and the rescoring.
     if (t_begin < t_end) {
-        MLRS_PREFETCH64(t_begin);
-        MLRS_STORE64(0);
+        if (DIRECT) {
+            direct_load(tileA, (uint32_t)t_begin);
+            if (tid < kBn) tnA[tid] = pfn;
+        } else {
+            MLRS_PREFETCH64(t_begin);
+            MLRS_STORE64(tileA, tnA);
+        }
     }
 
     double thr = L.thr[jl];
-    int buf = 0;
     int tiles = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, buf ^= 1) {
-        __syncthreads();  // tile[buf] written; every wave is done with tile[buf ^ 1]
+    auto tile_step = [&](double (&cur)[kBn][STRIDE], double* tncur, double (&nxt)[kBn][STRIDE], double* tnnxt,
+                         int64_t t0) {
+        // this wave's direct loads into cur are done; the barrier makes every
+        // wave's visible and ends every wave's reads of nxt
+        if (DIRECT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
         const bool more = t0 + kBn < t_end;
-        if (more) MLRS_PREFETCH64(t0 + kBn);
+        if (more) {
+            if (DIRECT)
+                direct_load(nxt, (uint32_t)(t0 + kBn));
+            else
+                MLRS_PREFETCH64(t0 + kBn);
+        }
 
-        f64x4 acc;
+        // two accumulator chains (even and odd k-steps): one dependent chain
+        // of f64 MFMAs leaves the matrix unit idle between its instructions
+        f64x4 acc0, acc1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = COS ? 0.0 : tnorm[buf][g + 4 * r];
+        for (int r = 0; r < 4; ++r) {
+            acc0[r] = COS ? 0.0 : tncur[g + 4 * r];
+            acc1[r] = 0.0;
+        }
         // A operand: this lane's tile row jl, columns g*NS + s; one 16-byte
         // read feeds two k-steps, the next pair is read one step ahead.
-        const double* arow = &tile[buf][jl][g * NS];
+        const double* arow = &cur[jl][g * NS];
         double2 av = *reinterpret_cast<const double2*>(arow);
 #pragma unroll
         for (int p = 0; p < NS / 2; ++p) {
             double2 an = av;
             if (p + 1 < NS / 2) an = *reinterpret_cast<const double2*>(arow + 2 * (p + 1));
             __builtin_amdgcn_sched_barrier(0);
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av.x, qreg[2 * p], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av.y, qreg[2 * p + 1], acc, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(av.x, qreg[2 * p], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(av.y, qreg[2 * p + 1], acc1, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             av = an;
         }
+        f64x4 acc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = acc0[r] + acc1[r];
         if (COS) {
             // rows scaled by -1/||x_t|| after the contraction (the scales ride
             // in tnorm), so the prefetched loads need no arithmetic until the
             // LDS store after the MFMAs
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] *= tnorm[buf][g + 4 * r];
+            for (int r = 0; r < 4; ++r) acc[r] *= tncur[g + 4 * r];
         }
-        if (more) MLRS_STORE64(buf ^ 1);
+        if (more) {
+            if (DIRECT) {
+                if (tid < kBn) tnnxt[tid] = pfn;
+            } else {
+                MLRS_STORE64(nxt, tnnxt);
+            }
+        }
 
         // ---- screen: lane holds tile rows g + 4r for query jl ----
         uint32_t m = 0;
@@ -440,6 +515,13 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
             }
             thr = L.thr[jl];
         }
+    };
+    for (int64_t t0 = t_begin; t0 < t_end;) {
+        tile_step(tileA, tnA, tileB, tnB, t0);
+        t0 += kBn;
+        if (t0 >= t_end) break;
+        tile_step(tileB, tnB, tileA, tnA, t0);
+        t0 += kBn;
     }
     {
         uint64_t mask = __builtin_amdgcn_ballot_w64(lane < kQpw && cntr > 0u);
@@ -556,6 +638,58 @@ __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
     }
 }
 
+// Initial per-query bound: the k-th smallest exact value over an evenly
+// spaced sample of index rows (any k distinct rows bound the final k-th value
+// from above), so each segment's screen starts tight instead of at +inf.  A
+// wave seeds kSeedQpw64 queries: lane l evaluates sample row l of each batch
+// of 64 against all of them, so every sampled row is read once per wave.
+constexpr int64_t kSeedRows64 = 512;
+constexpr int kSeedQpw64 = 4;
+template <int ARM, bool VEC2>
+__global__ __launch_bounds__(256) void knn_seed_f64_kernel(GramArgs64 a, int64_t nsamp) {
+    const int lane = threadIdx.x & 63;
+    const int64_t q0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kSeedQpw64;
+    if (q0 >= a.nq) return;
+    const int64_t d = a.d;
+    const double inf = __builtin_huge_val();
+    const double* qp[kSeedQpw64];
+    double qa[kSeedQpw64], lv[kSeedQpw64];
+    uint32_t li[kSeedQpw64];
+#pragma unroll
+    for (int j = 0; j < kSeedQpw64; ++j) {
+        const int64_t qg = (q0 + j < a.nq) ? q0 + j : a.nq - 1;  // past the end: repeats a query, not written
+        qp[j] = a.q + qg * d;
+        qa[j] = (ARM == ARM_COS_FOLD) ? a.qsq[qg] : (ARM == ARM_COS_HOST) ? a.qinv[qg] : 0.0;
+        lv[j] = inf;
+        li[j] = kSentinelIdx;
+    }
+    for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
+        const int64_t s = s0 + lane;
+        double e[kSeedQpw64];
+        uint32_t t = kSentinelIdx;
+#pragma unroll
+        for (int j = 0; j < kSeedQpw64; ++j) e[j] = inf;
+        if (s < nsamp) {
+            t = (uint32_t)((s * a.nt) / nsamp);
+            const double ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : (ARM == ARM_COS_HOST) ? a.xinv[t] : 0.0;
+            exact_pairs_shared_row<double, ARM, kSeedQpw64, VEC2>(qp, a.x + (int64_t)t * d, d, qa, ya, e);
+        }
+#pragma unroll
+        for (int j = 0; j < kSeedQpw64; ++j) {
+            uint32_t tj = t;
+            if (e[j] != e[j]) {
+                e[j] = inf;
+                tj = kSentinelIdx;
+            }
+            wave_sort64<double>(e[j], tj, lane);
+            wave_merge64<double>(lv[j], li[j], e[j], tj, lane);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kSeedQpw64; ++j)
+        if (lane == a.k - 1 && q0 + j < a.nq) a.shared_r[q0 + j] = (unsigned long long)__double_as_longlong(lv[j]);
+}
+
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -597,8 +731,29 @@ void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nsl
 int gram_f64_max_k() { return kKcap; }
 int gram_f64_max_d() { return kMaxD; }
 
-hipError_t launch_gram_f64_prep(const GramArgs64& a, hipStream_t s) {
+template <int ARM>
+hipError_t launch_seed64(const GramArgs64& a, bool vec2, int64_t nsamp, hipStream_t s) {
+    const int64_t per_block = 4 * kSeedQpw64;
+    const dim3 grid((unsigned)((a.nq + per_block - 1) / per_block));
+    if (vec2)
+        hipLaunchKernelGGL((knn_seed_f64_kernel<ARM, true>), grid, dim3(256), 0, s, a, nsamp);
+    else
+        hipLaunchKernelGGL((knn_seed_f64_kernel<ARM, false>), grid, dim3(256), 0, s, a, nsamp);
+    return hipGetLastError();
+}
+
+hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s) {
     if (!a.shared_r) return hipSuccess;
+    const int64_t nsamp = a.nt < kSeedRows64 ? a.nt : kSeedRows64;
+    if (nsamp >= a.k) {
+        const bool vec2 = (a.d % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                          ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+        if (arm == ARM_EUCLID_FMA) return launch_seed64<ARM_EUCLID_FMA>(a, vec2, nsamp, s);
+        if (arm == ARM_EUCLID_MULADD) return launch_seed64<ARM_EUCLID_MULADD>(a, vec2, nsamp, s);
+        if (arm == ARM_COS_FOLD) return launch_seed64<ARM_COS_FOLD>(a, vec2, nsamp, s);
+        if (arm == ARM_COS_HOST) return launch_seed64<ARM_COS_HOST>(a, vec2, nsamp, s);
+        return hipErrorInvalidValue;
+    }
     hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r, a.nq,
                        kInfBits64);
     return hipGetLastError();

@@ -121,7 +121,7 @@ __host__ __device__ inline int gram_list_cap(int k) { return k == 1 ? 1 : (k + 3
 
 // Screen values kept per workgroup while pairs wait in the queues (k > 1).
 inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64; }
-inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 32; }
+inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
 // G0, launched workgroups and per-query list slots of the Gram kernel's split.
 void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots);
@@ -158,14 +158,16 @@ struct GramArgs64 {
     int nslots;
     double* part_val;     // [nslots][nq][gram_list_cap(k)]
     uint32_t* part_idx;
-    double* qval;         // [grid_wgs][4 waves][16 queries][32]: screen values of the queued pairs (k > 1)
+    double* qval;         // [grid_wgs][4 waves][16 queries][48]: screen values of the queued pairs
     double* out_val;      // [nq][k]
     uint32_t* out_idx;
     unsigned long long* shared_r;  // [nq] best known exact k-th value per query (double bits)
 };
 
 void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
-hipError_t launch_gram_f64_prep(const GramArgs64& a, hipStream_t s);
+// prep: the shared per-query bound, seeded with the k-th exact value over a
+// row sample (arm: the exact arithmetic)
+hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s);
 hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s);
 hipError_t launch_gram_f64_merge(const GramArgs64& a, int arm, hipStream_t s);
 int gram_f64_max_k();
