@@ -134,63 +134,6 @@ __device__ __forceinline__ T exact_pair(const T* __restrict__ q, const T* __rest
     }
 }
 
-// Exact values of QS (query, row) pairs that share one row, each in the
-// arm's operation order (exact_pair's): the row's elements are read once for
-// all QS queries.  VEC: d a multiple of the 16-byte vector and every row
-// 16-byte aligned.
-template <typename T, int ARM, int QS, bool VEC>
-__device__ __forceinline__ void exact_pairs_shared_row(const T* const (&q)[QS], const T* __restrict__ y, int64_t d,
-                                                       const T (&qa)[QS], T ya, T (&out)[QS]) {
-    using F = FloatTraits<T>;
-    T acc[QS];
-#pragma unroll
-    for (int j = 0; j < QS; ++j) acc[j] = T(0);
-    auto step = [&](T qv, T yv, T& a) {
-        if (ARM == ARM_EUCLID_FMA) {
-            const T diff = qv - yv;
-            a = F::fma_(diff, diff, a);
-        } else if (ARM == ARM_EUCLID_MULADD) {
-            const T diff = qv - yv;
-            a = a + diff * diff;
-        } else if (ARM == ARM_COS_FOLD) {
-            a = F::fma_(qv, yv, a);
-        } else {  // ARM_COS_HOST
-            a = a + qv * yv;
-        }
-    };
-    constexpr int W = 16 / (int)sizeof(T);  // elements per 16-byte vector
-    typedef T vec_t __attribute__((ext_vector_type(W)));
-    int64_t c = 0;
-    if (VEC) {
-        for (; c + W <= d; c += W) {
-            const vec_t yv = *reinterpret_cast<const vec_t*>(y + c);
-#pragma unroll
-            for (int j = 0; j < QS; ++j) {
-                const vec_t qv = *reinterpret_cast<const vec_t*>(q[j] + c);
-#pragma unroll
-                for (int e = 0; e < W; ++e) step(qv[e], yv[e], acc[j]);
-            }
-        }
-    }
-    for (; c < d; ++c) {
-        const T yv = y[c];
-#pragma unroll
-        for (int j = 0; j < QS; ++j) step(q[j][c], yv, acc[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < QS; ++j) {
-        if (ARM == ARM_COS_FOLD) {
-            const T denom = F::sqrt_(qa[j] * ya);
-            const T sim = (denom > T(0)) ? acc[j] / denom : T(0);
-            out[j] = clamp02<T>(T(1) - sim);
-        } else if (ARM == ARM_COS_HOST) {
-            out[j] = clamp02<T>(T(1) - acc[j] * qa[j] * ya);
-        } else {
-            out[j] = acc[j];
-        }
-    }
-}
-
 // Smallest float >= t (screen thresholds are rounded up, never down).
 __device__ __forceinline__ float round_up_f(double t) {
     float f = (float)t;
@@ -476,6 +419,121 @@ __device__ __forceinline__ float pick8(const f32x4_t& a0, const f32x4_t& a1, int
         asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(l2[i]) : "v"(s1), "v"(l1[2 * i + 1]), "v"(l1[2 * i]));
     asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(v) : "v"(s2), "v"(l2[1]), "v"(l2[0]));
     return __uint_as_float(v);
+}
+
+// The Gram kernels' seed: for the kSeedQpb queries of one workgroup (four
+// waves, kSeedQpw each), the k-th smallest EXACT value (the arm's operation
+// order) over nsamp evenly spaced index rows, stored as the bits of its type
+// into shared_r; any k rows bound the final k-th value from above.  Each
+// batch of 64 sampled rows is staged through LDS in column chunks of 512
+// bytes (coalesced loads, each row read once per workgroup); lane l of every
+// wave continues its row's running sums, one per query, chunk by chunk, in
+// ascending column order.  qop / yop: the arm's per-query / per-row operand
+// arrays (squared norms for the fold arm, reciprocal norms for the knn_host
+// arm, unused for Euclidean).
+constexpr int kSeedQpw = 4;
+constexpr int kSeedQpb = 4 * kSeedQpw;
+template <typename T, int ARM, typename Bits>
+__device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T* __restrict__ X, int64_t nq,
+                                               int64_t nt, int64_t d, int k, int64_t nsamp,
+                                               const T* __restrict__ qop, const T* __restrict__ yop,
+                                               Bits* __restrict__ shared_r) {
+    using F = FloatTraits<T>;
+    constexpr int CH = 512 / (int)sizeof(T);  // columns per chunk (a power of two)
+    constexpr int CH_LOG = sizeof(T) == 4 ? 7 : 6;
+    constexpr int STR = CH + 1;                // LDS row stride: lane l reads row l, no bank conflicts
+    __shared__ T rows[64][STR];
+    __shared__ T qch[kSeedQpb][CH];            // the workgroup's queries, same columns
+    __shared__ uint32_t srow[64];              // the batch's sampled index rows
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const T inf = F::inf();
+    const int64_t qb0 = (int64_t)blockIdx.x * kSeedQpb;
+    const int64_t q0 = qb0 + (int64_t)w * kSeedQpw;
+    T qa[kSeedQpw], lv[kSeedQpw];
+    uint32_t li[kSeedQpw];
+#pragma unroll
+    for (int j = 0; j < kSeedQpw; ++j) {
+        const int64_t qg = (q0 + j < nq) ? q0 + j : nq - 1;  // past the end: repeats a query, not written
+        qa[j] = (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST) ? qop[qg] : T(0);
+        lv[j] = inf;
+        li[j] = kSentinelIdx;
+    }
+    for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
+        const int64_t s = s0 + lane;
+        const bool on = s < nsamp;
+        const uint32_t t = on ? (uint32_t)((s * nt) / nsamp) : kSentinelIdx;
+        __syncthreads();  // the previous batch's rows are no longer read
+        if (tid < 64) srow[tid] = t;
+        T acc[kSeedQpw];
+#pragma unroll
+        for (int j = 0; j < kSeedQpw; ++j) acc[j] = T(0);
+        for (int64_t c0 = 0; c0 < d; c0 += CH) {
+            const int cw = (d - c0 < CH) ? (int)(d - c0) : CH;
+            __syncthreads();  // srow written; the previous chunk is no longer read
+            // rows s0 .. s0+63 of the sample, columns c0 .. c0+CH: thread i
+            // copies elements i, i+256, ... of the 64 x CH block (row-major;
+            // consecutive threads read consecutive columns of one row)
+            for (int e = tid; e < 64 * CH; e += 256) {
+                const int r = e >> CH_LOG, c = e & (CH - 1);
+                const uint32_t tr = srow[r];
+                rows[r][c] = (tr != kSentinelIdx && c < cw) ? X[(int64_t)tr * d + c0 + c] : T(0);
+            }
+            for (int e = tid; e < kSeedQpb * CH; e += 256) {
+                const int j = e >> CH_LOG, c = e & (CH - 1);
+                const int64_t qg = (qb0 + j < nq) ? qb0 + j : nq - 1;
+                qch[j][c] = (c < cw) ? Q[qg * d + c0 + c] : T(0);
+            }
+            __syncthreads();
+#pragma unroll 4
+            for (int c = 0; c < cw; ++c) {
+                const T yv = rows[lane][c];
+#pragma unroll
+                for (int j = 0; j < kSeedQpw; ++j) {
+                    const T qv = qch[w * kSeedQpw + j][c];  // the same address in every lane
+                    if (ARM == ARM_EUCLID_FMA) {
+                        const T diff = qv - yv;
+                        acc[j] = F::fma_(diff, diff, acc[j]);
+                    } else if (ARM == ARM_EUCLID_MULADD) {
+                        const T diff = qv - yv;
+                        acc[j] = acc[j] + diff * diff;
+                    } else if (ARM == ARM_COS_FOLD) {
+                        acc[j] = F::fma_(qv, yv, acc[j]);
+                    } else {  // ARM_COS_HOST
+                        acc[j] = acc[j] + qv * yv;
+                    }
+                }
+            }
+        }
+        const T ya = (on && (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST)) ? yop[t] : T(0);
+#pragma unroll
+        for (int j = 0; j < kSeedQpw; ++j) {
+            T e = acc[j];
+            if (ARM == ARM_COS_FOLD) {
+                const T denom = F::sqrt_(qa[j] * ya);
+                const T sim = (denom > T(0)) ? e / denom : T(0);
+                e = clamp02<T>(T(1) - sim);
+            } else if (ARM == ARM_COS_HOST) {
+                e = clamp02<T>(T(1) - e * qa[j] * ya);
+            }
+            uint32_t tj = t;
+            if (!on || e != e) {
+                e = inf;
+                tj = kSentinelIdx;
+            }
+            wave_sort64<T>(e, tj, lane);
+            wave_merge64<T>(lv[j], li[j], e, tj, lane);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kSeedQpw; ++j) {
+        if (lane == k - 1 && q0 + j < nq) {
+            if (sizeof(T) == 4)
+                shared_r[q0 + j] = (Bits)__float_as_uint((float)lv[j]);
+            else
+                shared_r[q0 + j] = (Bits)__double_as_longlong((double)lv[j]);
+        }
+    }
 }
 
 }  // namespace mlrs

@@ -893,54 +893,13 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 }
 
 // Initial per-query bound: the k-th smallest exact value over an evenly
-// spaced sample of index rows.  Any k distinct rows bound the final k-th
-// value from above, so the screen starts tight instead of at +inf.  A wave
-// seeds kSeedQpw queries: lane l evaluates sample row l of each batch of 64
-// against all of them, so every sampled row is read once per wave.
-constexpr int kSeedQpw = 4;
-template <int ARM, bool VEC4>
+// spaced sample of index rows (seed_kth_block).  Any k distinct rows bound the
+// final k-th value from above, so the screen starts tight instead of at +inf.
+template <int ARM>
 __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t nsamp) {
-    const int lane = threadIdx.x & 63;
-    const int64_t q0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kSeedQpw;
-    if (q0 >= a.nq) return;
-    const int64_t d = a.d;
-    const float inf = __builtin_huge_valf();
-    const float* qp[kSeedQpw];
-    float qa[kSeedQpw], lv[kSeedQpw];
-    uint32_t li[kSeedQpw];
-#pragma unroll
-    for (int j = 0; j < kSeedQpw; ++j) {
-        const int64_t qg = (q0 + j < a.nq) ? q0 + j : a.nq - 1;  // past the end: repeats a query, not written
-        qp[j] = a.q + qg * d;
-        qa[j] = query_operand<ARM>(a, qg);
-        lv[j] = inf;
-        li[j] = kSentinelIdx;
-    }
-    for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
-        const int64_t s = s0 + lane;
-        float e[kSeedQpw];
-        uint32_t t = kSentinelIdx;
-#pragma unroll
-        for (int j = 0; j < kSeedQpw; ++j) e[j] = inf;
-        if (s < nsamp) {
-            t = (uint32_t)((s * a.nt) / nsamp);
-            exact_pairs_shared_row<float, ARM, kSeedQpw, VEC4>(qp, a.x + (int64_t)t * d, d, qa, row_operand<ARM>(a, t),
-                                                              e);
-        }
-#pragma unroll
-        for (int j = 0; j < kSeedQpw; ++j) {
-            uint32_t tj = t;
-            if (e[j] != e[j]) {
-                e[j] = inf;
-                tj = kSentinelIdx;
-            }
-            wave_sort64<float>(e[j], tj, lane);
-            wave_merge64<float>(lv[j], li[j], e[j], tj, lane);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < kSeedQpw; ++j)
-        if (lane == a.k - 1 && q0 + j < a.nq) a.shared_r[q0 + j] = __float_as_uint(lv[j]);
+    const float* qop = (ARM == ARM_COS_FOLD) ? a.qsq : a.qinv;
+    const float* yop = (ARM == ARM_COS_FOLD) ? a.xsq : a.xinv;
+    seed_kth_block<float, ARM>(a.q, a.x, a.nq, a.nt, a.d, a.k, nsamp, qop, yop, a.shared_r);
 }
 
 // Merge the per-segment lists of one query per wave and emit the output
@@ -1086,11 +1045,10 @@ hipError_t launch_wide(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     return launch_ng<32, ARM, COS, VEC4>(a, nblocks, s);
 }
 
-template <int ARM, bool VEC4>
+template <int ARM>
 hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
-    const int64_t per_block = 4 * kSeedQpw;
-    hipLaunchKernelGGL((knn_seed_f32_kernel<ARM, VEC4>), dim3((unsigned)((a.nq + per_block - 1) / per_block)),
-                       dim3(256), 0, s, a, nsamp);
+    hipLaunchKernelGGL((knn_seed_f32_kernel<ARM>), dim3((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb)), dim3(256), 0, s,
+                       a, nsamp);
     return hipGetLastError();
 }
 
@@ -1126,17 +1084,10 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
     }
     if (a.k > 1 && kSeedRows > 0) {
         const int64_t nsamp = a.nt < kSeedRows ? a.nt : kSeedRows;
-        const bool vec4 = (a.d % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
-                          ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
-        if (arm == ARM_EUCLID_FMA)
-            return vec4 ? launch_seed<ARM_EUCLID_FMA, true>(a, nsamp, s) : launch_seed<ARM_EUCLID_FMA, false>(a, nsamp, s);
-        if (arm == ARM_EUCLID_MULADD)
-            return vec4 ? launch_seed<ARM_EUCLID_MULADD, true>(a, nsamp, s)
-                        : launch_seed<ARM_EUCLID_MULADD, false>(a, nsamp, s);
-        if (arm == ARM_COS_FOLD)
-            return vec4 ? launch_seed<ARM_COS_FOLD, true>(a, nsamp, s) : launch_seed<ARM_COS_FOLD, false>(a, nsamp, s);
-        if (arm == ARM_COS_HOST)
-            return vec4 ? launch_seed<ARM_COS_HOST, true>(a, nsamp, s) : launch_seed<ARM_COS_HOST, false>(a, nsamp, s);
+        if (arm == ARM_EUCLID_FMA) return launch_seed<ARM_EUCLID_FMA>(a, nsamp, s);
+        if (arm == ARM_EUCLID_MULADD) return launch_seed<ARM_EUCLID_MULADD>(a, nsamp, s);
+        if (arm == ARM_COS_FOLD) return launch_seed<ARM_COS_FOLD>(a, nsamp, s);
+        if (arm == ARM_COS_HOST) return launch_seed<ARM_COS_HOST>(a, nsamp, s);
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(fill_inf_bits_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r, a.nq);

@@ -639,55 +639,15 @@ __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
 }
 
 // Initial per-query bound: the k-th smallest exact value over an evenly
-// spaced sample of index rows (any k distinct rows bound the final k-th value
-// from above), so each segment's screen starts tight instead of at +inf.  A
-// wave seeds kSeedQpw64 queries: lane l evaluates sample row l of each batch
-// of 64 against all of them, so every sampled row is read once per wave.
+// spaced sample of index rows (seed_kth_block): any k distinct rows bound the
+// final k-th value from above, so each segment's screen starts tight instead
+// of at +inf.
 constexpr int64_t kSeedRows64 = 512;
-constexpr int kSeedQpw64 = 4;
-template <int ARM, bool VEC2>
+template <int ARM>
 __global__ __launch_bounds__(256) void knn_seed_f64_kernel(GramArgs64 a, int64_t nsamp) {
-    const int lane = threadIdx.x & 63;
-    const int64_t q0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kSeedQpw64;
-    if (q0 >= a.nq) return;
-    const int64_t d = a.d;
-    const double inf = __builtin_huge_val();
-    const double* qp[kSeedQpw64];
-    double qa[kSeedQpw64], lv[kSeedQpw64];
-    uint32_t li[kSeedQpw64];
-#pragma unroll
-    for (int j = 0; j < kSeedQpw64; ++j) {
-        const int64_t qg = (q0 + j < a.nq) ? q0 + j : a.nq - 1;  // past the end: repeats a query, not written
-        qp[j] = a.q + qg * d;
-        qa[j] = (ARM == ARM_COS_FOLD) ? a.qsq[qg] : (ARM == ARM_COS_HOST) ? a.qinv[qg] : 0.0;
-        lv[j] = inf;
-        li[j] = kSentinelIdx;
-    }
-    for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
-        const int64_t s = s0 + lane;
-        double e[kSeedQpw64];
-        uint32_t t = kSentinelIdx;
-#pragma unroll
-        for (int j = 0; j < kSeedQpw64; ++j) e[j] = inf;
-        if (s < nsamp) {
-            t = (uint32_t)((s * a.nt) / nsamp);
-            const double ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : (ARM == ARM_COS_HOST) ? a.xinv[t] : 0.0;
-            exact_pairs_shared_row<double, ARM, kSeedQpw64, VEC2>(qp, a.x + (int64_t)t * d, d, qa, ya, e);
-        }
-#pragma unroll
-        for (int j = 0; j < kSeedQpw64; ++j) {
-            uint32_t tj = t;
-            if (e[j] != e[j]) {
-                e[j] = inf;
-                tj = kSentinelIdx;
-            }
-            wave_sort64<double>(e[j], tj, lane);
-            wave_merge64<double>(lv[j], li[j], e[j], tj, lane);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < kSeedQpw64; ++j)
-        if (lane == a.k - 1 && q0 + j < a.nq) a.shared_r[q0 + j] = (unsigned long long)__double_as_longlong(lv[j]);
+    const double* qop = (ARM == ARM_COS_FOLD) ? a.qsq : a.qinv;
+    const double* yop = (ARM == ARM_COS_FOLD) ? a.xsq : a.xinv;
+    seed_kth_block<double, ARM>(a.q, a.x, a.nq, a.nt, a.d, a.k, nsamp, qop, yop, a.shared_r);
 }
 
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
@@ -732,13 +692,9 @@ int gram_f64_max_k() { return kKcap; }
 int gram_f64_max_d() { return kMaxD; }
 
 template <int ARM>
-hipError_t launch_seed64(const GramArgs64& a, bool vec2, int64_t nsamp, hipStream_t s) {
-    const int64_t per_block = 4 * kSeedQpw64;
-    const dim3 grid((unsigned)((a.nq + per_block - 1) / per_block));
-    if (vec2)
-        hipLaunchKernelGGL((knn_seed_f64_kernel<ARM, true>), grid, dim3(256), 0, s, a, nsamp);
-    else
-        hipLaunchKernelGGL((knn_seed_f64_kernel<ARM, false>), grid, dim3(256), 0, s, a, nsamp);
+hipError_t launch_seed64(const GramArgs64& a, int64_t nsamp, hipStream_t s) {
+    hipLaunchKernelGGL((knn_seed_f64_kernel<ARM>), dim3((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb)), dim3(256), 0,
+                       s, a, nsamp);
     return hipGetLastError();
 }
 
@@ -746,12 +702,10 @@ hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s) {
     if (!a.shared_r) return hipSuccess;
     const int64_t nsamp = a.nt < kSeedRows64 ? a.nt : kSeedRows64;
     if (nsamp >= a.k) {
-        const bool vec2 = (a.d % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
-                          ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
-        if (arm == ARM_EUCLID_FMA) return launch_seed64<ARM_EUCLID_FMA>(a, vec2, nsamp, s);
-        if (arm == ARM_EUCLID_MULADD) return launch_seed64<ARM_EUCLID_MULADD>(a, vec2, nsamp, s);
-        if (arm == ARM_COS_FOLD) return launch_seed64<ARM_COS_FOLD>(a, vec2, nsamp, s);
-        if (arm == ARM_COS_HOST) return launch_seed64<ARM_COS_HOST>(a, vec2, nsamp, s);
+        if (arm == ARM_EUCLID_FMA) return launch_seed64<ARM_EUCLID_FMA>(a, nsamp, s);
+        if (arm == ARM_EUCLID_MULADD) return launch_seed64<ARM_EUCLID_MULADD>(a, nsamp, s);
+        if (arm == ARM_COS_FOLD) return launch_seed64<ARM_COS_FOLD>(a, nsamp, s);
+        if (arm == ARM_COS_HOST) return launch_seed64<ARM_COS_HOST>(a, nsamp, s);
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(fill_u64_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a.shared_r, a.nq,
