@@ -1788,8 +1788,10 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     km_layout(n, std::max<int64_t>(((int64_t)4 << 20) / d, 64), &nbv, &rpbv);  // feature_mean_var
     km_layout(n, 256, &nbi, &rpbi);                                            // sum_device
 
+    const int64_t nsub = km_sub_blocks(nb, rpb, k);
     size_t bytes = 4 * aligned_bytes(sizeof(uint32_t) * (size_t)n) + 2 * aligned_bytes(sizeof(T) * (size_t)n) +
-                   3 * aligned_bytes(sizeof(uint32_t) * (size_t)(nb * k)) + 2 * aligned_bytes(sizeof(uint32_t) * k) +
+                   2 * aligned_bytes(sizeof(uint32_t) * (size_t)(nb * k)) +
+                   aligned_bytes(sizeof(uint32_t) * (size_t)(nb * nsub * k)) + 2 * aligned_bytes(sizeof(uint32_t) * k) +
                    aligned_bytes(sizeof(T) * (size_t)(nb * kd)) + 2 * aligned_bytes(sizeof(T) * (size_t)kd) +
                    aligned_bytes(sizeof(T) * (size_t)std::max(nbi, nbv * d)) + aligned_bytes(sizeof(T) * d) +
                    aligned_bytes(sizeof(int64_t) * k) + 1024;
@@ -1805,7 +1807,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     KmScratch<T> w;
     w.pcount = cv.take<uint32_t>(nb * k);
     w.seg = cv.take<uint32_t>(nb * k);
-    w.cursor = cv.take<uint32_t>(nb * k);
+    w.cursor = cv.take<uint32_t>(nb * nsub * k);
     w.counts = cv.take<uint32_t>(k);
     w.starts = cv.take<uint32_t>(k);
     w.perm = perm;

@@ -12,11 +12,17 @@
 // numbers -- so the thread of (b, c, j) walks exactly the rows of its bucket,
 // in ascending order: the same sums in the same order for O(n*d) work.
 //
-//   km_hist_kernel          pcount[b][c]: one workgroup per block (LDS histogram)
+// Each block is cut into S sub-blocks of consecutive rows, one wave each, so
+// the scatter fills the chip whatever the block count:
+//   km_subhist_kernel       cursor[b][s][c]: label counts of sub-block (b, s)
+//   km_subprefix_kernel     per (b, c): counts -> exclusive prefix over s, and
+//                           pcount[b][c], the bucket size
 //   km_label_totals_kernel  per label: its total and each (b, c) bucket's
 //   km_label_starts_kernel  start in the label-major permutation (a prefix
 //   km_add_starts_kernel    over blocks, then over labels)
-//   km_scatter_kernel       stable scatter of the block's rows into their buckets
+//   km_scatter_kernel       stable scatter of each sub-block's rows: row i of
+//                           label c goes to seg[b][c] + cursor[b][s][c] + its
+//                           rank among the sub-block's earlier rows of c
 //   km_psum_kernel          psum[b][c][j] over the bucket, ascending rows
 //   km_reduce_kernel        sums[c][j] = sum over b in order
 //
@@ -33,7 +39,17 @@ namespace mlrs {
 
 namespace {
 
-constexpr int kLdsLabels = 8192;  // labels an LDS histogram / cursor array holds
+// The lanes of the wave whose label equals this lane's (a label-match ballot
+// over the label bits), among the lanes in `active`.
+__device__ __forceinline__ uint64_t same_label_lanes(uint32_t lab, int nbits, uint64_t active) {
+    uint64_t m = active;
+    for (int bit = 0; bit < nbits; ++bit) {
+        const bool one = (lab >> bit) & 1u;
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(one);
+        m &= one ? bal : ~bal;
+    }
+    return m;
+}
 
 // acc + p[0] + p[stride] + ... in order; the loads are issued 16 at a time
 // ahead of the dependent adds, so a long strided sum is not latency-bound.
@@ -52,23 +68,49 @@ __device__ __forceinline__ T ordered_sum(const T* __restrict__ p, int64_t count,
     return acc;
 }
 
-__global__ __launch_bounds__(256) void km_hist_kernel(const uint32_t* __restrict__ labels, int64_t n, int64_t rpb,
-                                                      int64_t k, uint32_t* __restrict__ pcount) {
-    __shared__ uint32_t h[kLdsLabels];
-    const int64_t b = blockIdx.x;
-    const int64_t start = b * rpb;
-    const int64_t end = (start + rpb) < n ? start + rpb : n;
-    uint32_t* out = pcount + b * k;
-    if (k <= kLdsLabels) {
-        for (int64_t c = threadIdx.x; c < k; c += 256) h[c] = 0u;
-        __syncthreads();
-        for (int64_t i = start + threadIdx.x; i < end; i += 256) atomicAdd(&h[labels[i]], 1u);
-        __syncthreads();
-        for (int64_t c = threadIdx.x; c < k; c += 256) out[c] = h[c];
-    } else {
-        // out[] was zeroed by the caller
-        for (int64_t i = start + threadIdx.x; i < end; i += 256) atomicAdd(&out[labels[i]], 1u);
+// One wave per sub-block (b, s): its label counts into cursor[b][s][.]
+// (zeroed by the caller).  Each chunk of 64 rows adds one count per distinct
+// label, from the group's lowest lane; the wave owns the counts, so the adds
+// need no atomics.
+__global__ __launch_bounds__(256) void km_subhist_kernel(const uint32_t* __restrict__ labels, int64_t n,
+                                                         int64_t rpb, int64_t k, int64_t nsub, int64_t srows,
+                                                         int nbits, uint32_t* __restrict__ cursor) {
+    const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t b = wv / nsub, sb = wv - b * nsub;
+    const int64_t bend = ((b + 1) * rpb < n) ? (b + 1) * rpb : n;
+    const int64_t start = b * rpb + sb * srows;
+    const int64_t end = (start + srows < bend) ? start + srows : bend;
+    if (b * rpb >= n || start >= end) return;
+    uint32_t* cur = cursor + wv * k;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int64_t i0 = start; i0 < end; i0 += 64) {
+        const int64_t i = i0 + lane;
+        const bool on = i < end;
+        const uint32_t lab = on ? labels[i] : 0u;
+        const uint64_t grp = same_label_lanes(lab, nbits, __builtin_amdgcn_ballot_w64(on));
+        if (on && (grp & below) == 0) cur[lab] += (uint32_t)__builtin_popcountll(grp);
+        // the next chunk may read a count another lane just wrote
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
+}
+
+// One thread per (b, c): the sub-blocks' counts become their exclusive prefix
+// (the label's rows before sub-block s within the block), and the total is the
+// (b, c) bucket's size.
+__global__ __launch_bounds__(256) void km_subprefix_kernel(uint32_t* __restrict__ cursor, int64_t nb, int64_t k,
+                                                           int64_t nsub, uint32_t* __restrict__ pcount) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= nb * k) return;
+    const int64_t b = t / k, c = t - b * k;
+    uint32_t run = 0;
+    for (int64_t sb = 0; sb < nsub; ++sb) {
+        uint32_t* p = cursor + ((b * nsub + sb) * k + c);
+        const uint32_t v = *p;
+        *p = run;
+        run += v;
+    }
+    pcount[t] = run;
 }
 
 // One thread per label: counts[c], and seg[b][c] = the bucket's first slot
@@ -130,42 +172,37 @@ __global__ __launch_bounds__(256) void km_add_starts_kernel(uint32_t* __restrict
     for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < nb * k; t += stride) seg[t] += starts[t % k];
 }
 
-// One workgroup per block: rows in chunks of 256, each row placed after the
-// rows of its label earlier in the block.  cursor[b][c] starts as the bucket
-// start and advances chunk by chunk.
-__global__ __launch_bounds__(256) void km_scatter_kernel(const uint32_t* __restrict__ labels, int64_t n, int64_t rpb,
-                                                         int64_t k, uint32_t* __restrict__ cursor,
-                                                         uint32_t* __restrict__ perm) {
-    __shared__ uint32_t lab[256];
-    __shared__ uint32_t cur[kLdsLabels];
-    const int64_t b = blockIdx.x;
-    const int64_t start = b * rpb;
-    const int64_t end = (start + rpb) < n ? start + rpb : n;
-    uint32_t* gcur = cursor + b * k;
-    const bool lds = k <= kLdsLabels;
-    uint32_t* cp = lds ? cur : gcur;
-    if (lds) {
-        for (int64_t c = threadIdx.x; c < k; c += 256) cur[c] = gcur[c];
-    }
-    __syncthreads();
-    for (int64_t i0 = start; i0 < end; i0 += 256) {
-        const int t = threadIdx.x;
-        const int64_t i = i0 + t;
-        const int cnt = (end - i0) < 256 ? (int)(end - i0) : 256;
-        if (t < cnt) lab[t] = labels[i];
-        __syncthreads();
-        uint32_t rank = 0, after = 0, c = 0, base = 0;
-        if (t < cnt) {
-            c = lab[t];
-            for (int u = 0; u < t; ++u) rank += (lab[u] == c) ? 1u : 0u;
-            for (int u = t + 1; u < cnt; ++u) after += (lab[u] == c) ? 1u : 0u;
-            base = cp[c];
-            perm[base + rank] = (uint32_t)i;
+// One wave per sub-block (b, s), its rows in order, 64 at a time: a row goes
+// to its bucket's start seg[b][c], plus the label's rows in earlier
+// sub-blocks and earlier chunks (cursor[b][s][c], advanced by the group's
+// highest lane), plus its rank among the chunk's earlier rows of the label.
+__global__ __launch_bounds__(256) void km_scatter_kernel(const uint32_t* __restrict__ labels, int64_t n,
+                                                         int64_t rpb, int64_t k, int64_t nsub, int64_t srows,
+                                                         int nbits, const uint32_t* __restrict__ seg,
+                                                         uint32_t* __restrict__ cursor, uint32_t* __restrict__ perm) {
+    const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t b = wv / nsub, sb = wv - b * nsub;
+    const int64_t bend = ((b + 1) * rpb < n) ? (b + 1) * rpb : n;
+    const int64_t start = b * rpb + sb * srows;
+    const int64_t end = (start + srows < bend) ? start + srows : bend;
+    if (b * rpb >= n || start >= end) return;
+    uint32_t* cur = cursor + wv * k;
+    const uint32_t* bseg = seg + b * k;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int64_t i0 = start; i0 < end; i0 += 64) {
+        const int64_t i = i0 + lane;
+        const bool on = i < end;
+        const uint32_t lab = on ? labels[i] : 0u;
+        const uint64_t grp = same_label_lanes(lab, nbits, __builtin_amdgcn_ballot_w64(on));
+        if (on) {
+            const uint32_t rank = (uint32_t)__builtin_popcountll(grp & below);
+            const uint32_t base = cur[lab];
+            perm[bseg[lab] + base + rank] = (uint32_t)i;
+            if ((grp >> lane) == 1ull) cur[lab] = base + (uint32_t)__builtin_popcountll(grp);  // highest lane
         }
-        __syncthreads();
-        if (t < cnt && after == 0) cp[c] = base + rank + 1u;  // the label's last row in this chunk
-        __threadfence_block();
-        __syncthreads();
+        // the next chunk may read a cursor another lane just wrote
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
 }
 
@@ -179,8 +216,22 @@ __global__ __launch_bounds__(256) void km_psum_kernel(const T* __restrict__ x, i
     for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
         const int64_t bc = t / d, j = t - bc * d;
         const uint32_t s0 = seg[bc], m = pcount[bc];
+        const uint32_t* __restrict__ pp = perm + s0;
+        // the bucket's rows in ascending order; eight row numbers, then eight
+        // elements, are loaded ahead of the dependent adds
         T acc = T(0);
-        for (uint32_t p = 0; p < m; ++p) acc = acc + x[(int64_t)perm[s0 + p] * d + j];
+        uint32_t p = 0;
+        for (; p + 8 <= m; p += 8) {
+            uint32_t r[8];
+            T v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) r[u] = pp[p + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = x[(int64_t)r[u] * d + j];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = acc + v[u];
+        }
+        for (; p < m; ++p) acc = acc + x[(int64_t)pp[p] * d + j];
         psum[t] = acc;
     }
 }
@@ -286,21 +337,37 @@ unsigned blocks_for(int64_t n, int64_t cap) {
 
 }  // namespace
 
+int64_t km_sub_blocks(int64_t nb, int64_t rpb, int64_t k) {
+    // about 2,048 waves in all, at least 64 rows each, and the per-(sub-block,
+    // label) cursors within 256 MB
+    int64_t sb = (2048 + nb - 1) / nb;
+    const int64_t by_rows = (rpb + 63) / 64;
+    if (sb > by_rows) sb = by_rows;
+    const int64_t by_mem = ((int64_t)64 << 20) / (nb * (k > 0 ? k : 1));
+    if (sb > by_mem) sb = by_mem;
+    return sb < 1 ? 1 : sb;
+}
+
 template <typename T>
 hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n, int64_t d, int64_t k, int64_t nb,
                                    int64_t rpb, const KmScratch<T>& w, hipStream_t s) {
-    if (k > kLdsLabels) {
-        hipError_t e = launch_fill_u32(w.pcount, nb * k, 0u, s);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(km_hist_kernel, dim3((unsigned)nb), dim3(256), 0, s, labels, n, rpb, k, w.pcount);
+    const int64_t nsub = km_sub_blocks(nb, rpb, k);
+    const int64_t srows = (rpb + nsub - 1) / nsub;
+    int nbits = 0;
+    while (nbits < 32 && ((int64_t)1 << nbits) < k) ++nbits;
+    const int64_t waves = nb * nsub;
+    hipError_t e = launch_fill_u32(w.cursor, waves * k, 0u, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(km_subhist_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, labels, n, rpb, k, nsub,
+                       srows, nbits, w.cursor);
+    hipLaunchKernelGGL(km_subprefix_kernel, dim3(blocks_for(nb * k, 1 << 30)), dim3(256), 0, s, w.cursor, nb, k, nsub,
+                       w.pcount);
     hipLaunchKernelGGL(km_label_totals_kernel, dim3(blocks_for(k, 1 << 20)), dim3(256), 0, s, w.pcount, nb, k, w.seg,
                        w.counts);
     hipLaunchKernelGGL(km_label_starts_kernel, dim3(1), dim3(256), 0, s, w.counts, k, w.starts);
     hipLaunchKernelGGL(km_add_starts_kernel, dim3(blocks_for(nb * k, 4096)), dim3(256), 0, s, w.seg, nb, k, w.starts);
-    hipError_t e = hipMemcpyAsync(w.cursor, w.seg, sizeof(uint32_t) * (size_t)(nb * k), hipMemcpyDeviceToDevice, s);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(km_scatter_kernel, dim3((unsigned)nb), dim3(256), 0, s, labels, n, rpb, k, w.cursor, w.perm);
+    hipLaunchKernelGGL(km_scatter_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, labels, n, rpb, k, nsub,
+                       srows, nbits, w.seg, w.cursor, w.perm);
     hipLaunchKernelGGL((km_psum_kernel<T>), dim3(blocks_for(nb * k * d, 65536)), dim3(256), 0, s, x, d, nb, k,
                        w.pcount, w.seg, w.perm, w.psum);
     hipLaunchKernelGGL((km_reduce_kernel<T>), dim3(blocks_for(k * d, 1 << 20)), dim3(256), 0, s, w.psum, nb, k * d,

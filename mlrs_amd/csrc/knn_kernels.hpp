@@ -332,13 +332,15 @@ template <typename T>
 struct KmScratch {
     uint32_t* pcount;  // [nb][k] rows of label c in block b
     uint32_t* seg;     // [nb][k] first slot of bucket (b, c) in perm
-    uint32_t* cursor;  // [nb][k] scatter cursors
+    uint32_t* cursor;  // [nb][km_sub_blocks(nb, rpb, k)][k] sub-block counts, then scatter cursors
     uint32_t* counts;  // [k]
     uint32_t* starts;  // [k]
     uint32_t* perm;    // [n] row numbers, bucket by bucket
     T* psum;           // [nb][k][d]
     T* sums;           // [k][d]
 };
+// Sub-blocks per reference block in the centroid-sum scatter (sizes KmScratch::cursor).
+int64_t km_sub_blocks(int64_t nb, int64_t rpb, int64_t k);
 template <typename T>
 hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n, int64_t d, int64_t k, int64_t nb,
                                    int64_t rpb, const KmScratch<T>& w, hipStream_t s);
