@@ -437,9 +437,11 @@ int32_t mlrs_release_workspace(void);
  * Measurement hook (no counterpart in the reference; for benchmarks).
  * While enabled, every call records a pair of HIP events on its own stream
  * around the launch of its dominant kernel (the Gram-MFMA kernel, the low-d
- * ALU kernel, or the generic path's distance tile).  mlrs_timing_read waits
- * for the recorded events and returns the summed kernel time, the number of
- * timed launches and the kernel's name; enabling again clears the records.
+ * ALU kernel, or the generic path's distance tile; k-means fit also times
+ * its centroid-sum pass).  mlrs_timing_read waits for the recorded events,
+ * picks the name with the largest summed time, and returns that sum, the
+ * number of launches timed under the name and the name; enabling again
+ * clears the records.
  */
 int32_t mlrs_timing_enable(int32_t on);
 int32_t mlrs_timing_read(double *total_ms, int64_t *launches, char *kernel_name, int32_t name_len);

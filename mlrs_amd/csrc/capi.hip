@@ -269,21 +269,21 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
 // ---------------------------------------------------------------------------
 struct TimedLaunch {
     hipEvent_t a, b;
+    const char* name;  // a string literal: the timed kernel (or region)
 };
 bool g_timing = false;
 std::vector<TimedLaunch> g_timed;
-char g_timed_name[64] = "";
 
 struct KernelTimer {
     hipStream_t s;
-    TimedLaunch t{nullptr, nullptr};
+    TimedLaunch t{nullptr, nullptr, nullptr};
     KernelTimer(hipStream_t st, const char* name) : s(st) {
         if (!g_timing || g_noalloc) return;
         if (hipEventCreate(&t.a) != hipSuccess || hipEventCreate(&t.b) != hipSuccess) {
             t.a = t.b = nullptr;
             return;
         }
-        std::snprintf(g_timed_name, sizeof(g_timed_name), "%s", name);
+        t.name = name;
         (void)hipEventRecord(t.a, s);
     }
     ~KernelTimer() {
@@ -2165,24 +2165,38 @@ int32_t mlrs_timing_enable(int32_t on) {
     std::lock_guard<std::mutex> lk(g_mu);
     clear_timed();
     g_timing = on != 0;
-    g_timed_name[0] = 0;
     return MLRS_OK;
 }
 
 int32_t mlrs_timing_read(double* total_ms, int64_t* launches, char* kernel_name, int32_t name_len) {
     std::lock_guard<std::mutex> lk(g_mu);
-    double tot = 0.0;
+    // per-name totals; the name with the largest summed time is reported
+    std::vector<const char*> names;
+    std::vector<double> tot;
+    std::vector<int64_t> cnt;
     for (auto& t : g_timed) {
         hipError_t e = hipEventSynchronize(t.b);
         if (e != hipSuccess) return hip_err(e, "hipEventSynchronize");
         float ms = 0.0f;
         e = hipEventElapsedTime(&ms, t.a, t.b);
         if (e != hipSuccess) return hip_err(e, "hipEventElapsedTime");
-        tot += ms;
+        size_t i = 0;
+        while (i < names.size() && std::strcmp(names[i], t.name) != 0) ++i;
+        if (i == names.size()) {
+            names.push_back(t.name);
+            tot.push_back(0.0);
+            cnt.push_back(0);
+        }
+        tot[i] += ms;
+        ++cnt[i];
     }
-    if (total_ms) *total_ms = tot;
-    if (launches) *launches = (int64_t)g_timed.size();
-    if (kernel_name && name_len > 0) std::snprintf(kernel_name, (size_t)name_len, "%s", g_timed_name);
+    size_t best = 0;
+    for (size_t i = 1; i < names.size(); ++i)
+        if (tot[i] > tot[best]) best = i;
+    const bool any = !names.empty();
+    if (total_ms) *total_ms = any ? tot[best] : 0.0;
+    if (launches) *launches = any ? cnt[best] : 0;
+    if (kernel_name && name_len > 0) std::snprintf(kernel_name, (size_t)name_len, "%s", any ? names[best] : "");
     return MLRS_OK;
 }
 

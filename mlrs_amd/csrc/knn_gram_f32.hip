@@ -5,36 +5,47 @@
 // distance_direct -> top_k fallback (crates/mlrs-algos/src/neighbors/
 // nearest.rs:1058-1343) for f32, d <= 256, k <= 64, Euclidean and cosine.
 //
-// Shape of one workgroup: 4 waves x 32 queries = 128 queries, walking one
+// Two register shapes (GramShape below): d <= 128, 4 waves x 32 queries =
+// 128 queries per workgroup on v_mfma_f32_32x32x2f32; 128 < d <= 256, 4 waves
+// x 16 queries = 64 per workgroup on v_mfma_f32_16x16x4f32.  Either walks one
 // strip of index rows 32 at a time.
-//  * Each wave keeps its 32 query rows in VGPRs as the B operand of
-//    v_mfma_f32_32x32x2f32 (pre-scaled by -2 for Euclidean), loaded once.
-//  * The 32-row index tile is staged in LDS (row stride d_pad+4 floats: rows
-//    land 4 banks apart, so the ds_read_b128 A-operand reads do not conflict),
+//  * Each wave keeps its query rows in VGPRs as the B operand (pre-scaled by
+//    -2 for Euclidean), loaded once per segment.
+//  * The 32-row index tile is staged in LDS (narrow: row stride d_pad+4
+//    floats, rows 4 banks apart; wide: 16-byte chunks XOR-swizzled by row),
 //    double-buffered and prefetched into registers one tile ahead.
 //  * Euclidean: the accumulator starts at ||x_t||^2, so after the contraction
 //    acc = ||x_t||^2 - 2 x_t.q_j, the expansion minus the per-query constant.
 //    Cosine: the contraction is scaled by -1/||x_t|| per row afterwards,
 //    acc = -x_t.q_j/||x_t||.
 //  * Screen: acc is compared against a per-query threshold derived from the
-//    best exact k-th value known for the query (its own list, or any strip's,
-//    shared through a per-query word in global memory) plus a rigorous bound
-//    on the expansion's rounding error and the reference's own.  A pair that
-//    can still enter the exact top-k always passes; the comparison is
-//    !(acc > thr), so NaN passes too.  For k = 1 the bound is tightened every
-//    tile with the tile's smallest expansion value.
-//  * For k > 1 the per-query bound starts from a prep launch: the k-th
-//    smallest exact value over an evenly spaced sample of index rows.
+//    best bound known on the query's k-th exact value (its own list, any
+//    segment's, shared through a per-query word and per-segment list
+//    summaries in global memory) plus a rigorous bound eps on the expansion's
+//    rounding error and the reference's own.  A pair that can still enter the
+//    exact top-k always passes; the comparison is !(acc > thr), so NaN passes
+//    too.  For k = 1 the bound is tightened every tile with the tile's
+//    smallest expansion value.
+//  * For k > 1 the per-query bound starts from a seed launch: the k-th
+//    smallest exact value over 512 evenly spaced index rows.
 //  * Passing (query, row) pairs are queued in LDS (queue lengths live in
-//    registers; a lane pair appends with a popcount prefix, no atomics).
-//    When a query's queue is half full the wave evaluates the queued pairs
-//    EXACTLY, in the reference arm's operation order, sorts them and merges
-//    them into the query's exact top-k list with the (value, index) order.
-//    The lists live in global memory (one per query and segment): keeping
-//    only the queues in LDS (~70 KB per workgroup) lets two workgroups share
-//    a CU, so one workgroup's selection work overlaps the other's MFMAs.
-//  * Work split: StreamSplit (knn_kernels.hpp), panel-major, so the
-//    workgroups on one index panel stream its rows in lockstep.
+//    registers; the lanes screening a query append with a popcount prefix,
+//    no atomics); their screen values wait in a per-wave global array.
+//    Before a queue could overflow, the wave sorts it and merges it into the
+//    query's list for this segment (global memory, one per query and
+//    segment): a queued pair enters with its screen value mapped back to a
+//    distance, which is within eps of its exact value, and the list keeps
+//    the k + 32 (at most 64) smallest.  No pair is evaluated exactly during
+//    the scan, except in the rare lists that turn exact (a dropped pair
+//    inside the 2 eps window of the k-th, NaN screen values, norms that could
+//    overflow).  k = 1 keeps one exact (value, index) pair per query in LDS.
+//  * The merge kernel takes each query's lists from all segments, finds the
+//    k-th value V of their union and evaluates EXACTLY, in the reference
+//    arm's operation order, every listed pair whose screen value is within
+//    2 eps of V (window rescoring), then ranks by (exact value, index).
+//  * Work split: StreamSplit (knn_kernels.hpp), panel-major, with XCD-grouped
+//    workgroup numbering, so the workgroups on one XCD stream the same index
+//    panel in lockstep.
 // The kept lists are therefore the reference's own top-k: the full distance
 // matrix never reaches HBM and no tolerance is involved.
 #include "knn_common.hpp"

@@ -147,6 +147,11 @@ class _NeighborsBase:
             raise NotImplementedError("metric %r is not served by the HIP engine" % eff)
         t, _ = _as_device_matrix(X)
         _check_finite(t)
+        if isinstance(X, torch.Tensor) and t.data_ptr() == X.data_ptr():
+            # Fit::fit keeps its own copy of the training rows
+            # (crates/mlrs-backend/src/prims/knn.rs:358-386 device_copy): a
+            # device tensor of the caller is copied, not aliased
+            t = prims.device_copy(t)
         self._fit_X_dev = t
         self._engine_metric = engine_metric
         self._engine_p = float(eff_p) if engine_metric == "minkowski" else 2.0

@@ -53,3 +53,21 @@ def test_search_paths_read_nothing_back():
     assert after["live_bytes"] > 0 and after["peak_bytes"] >= after["live_bytes"]
     prims.radius_neighbors(xq, xt, 9.0)
     assert prims.pool_stats()["read_backs"] > 0
+
+
+def test_estimator_fit_owns_its_rows():
+    # Fit::fit copies the training rows (prims/knn.rs:358-386): writing into
+    # the caller's tensor afterwards changes nothing the estimator answers
+    import oracle
+    from mlrs_amd.neighbors import NearestNeighbors
+    rng = np.random.default_rng(5)
+    xt = rng.standard_normal((3000, 24)).astype(np.float32)
+    xq = rng.standard_normal((200, 24)).astype(np.float32)
+    dt = torch.from_numpy(xt).to(DEV)
+    nn = NearestNeighbors(n_neighbors=7).fit(dt)
+    assert nn._fit_X_dev.data_ptr() != dt.data_ptr()
+    dt.fill_(0.0)
+    dist, idx = nn.kneighbors(xq)
+    wd, wi = oracle.knn_topk(xq, xt, 7)
+    np.testing.assert_array_equal(np.asarray(idx), wi.astype(np.int32))
+    np.testing.assert_array_equal(np.asarray(dist), wd)
