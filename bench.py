@@ -56,7 +56,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "d256"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "d256", "c2k128"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--radius", type=float, default=None,
@@ -238,9 +238,10 @@ def main():
         info = oracle.build_info()
         # bounded sample: a prefix of the queries against the full index, run
         # repeatedly until about 10 s of CPU work has been timed
-        sample = {"c1": n_query, "c2": 2000, "c3": 256, "c4": 20000, "c5": 400000, "d256": 1000}[args.config]
+        sample = {"c1": n_query, "c2": 2000, "c3": 256, "c4": 20000, "c5": 400000, "d256": 1000,
+                  "c2k128": 2000}[args.config]
         if radius is not None:
-            sample = {"c1": n_query, "c2": 512, "c3": 128, "c4": 20000, "d256": 256}[args.config]
+            sample = {"c1": n_query, "c2": 512, "c3": 128, "c4": 20000, "d256": 256, "c2k128": 512}[args.config]
         if args.fit:
             sample = 100_000
         log("CPU baseline: %d of %d queries, %d threads (affinity %d, OMP_NUM_THREADS=%s), %s, %s"
@@ -280,7 +281,8 @@ def main():
           "c3": "c3: 200k x 5k, d=256, k=16, f64 cosine, U[0,1)",
           "c4": "c4: 500k self-kNN, d=3, k=8, f32, 5% exact duplicates",
           "c5": "c5: k-means assign, 5M points x 1024 centroids, d=64, f32",
-          "d256": "d256: 200k index x 5k queries, d=256, k=32, f32, 100-comp GMM"}[args.config]
+          "d256": "d256: 200k index x 5k queries, d=256, k=32, f32, 100-comp GMM",
+          "c2k128": "c2k128: c2's data (1M index x 10k queries, d=128) with k=128, f32"}[args.config]
     if args.fit:
         wl = ("k-means fit at c5 scale: 5M points into 1024 clusters, d=64, f32, seeded random init, tol 0, "
               "at most %d Lloyd iterations per step" % args.fit_iters)

@@ -354,6 +354,93 @@ __device__ __forceinline__ void wave_merge64_key(unsigned long long& lv, unsigne
     for (int m = 32; m > 0; m >>= 1) bitonic_step_key(lv, lane, m, true);
 }
 
+// ---------------------------------------------------------------------------
+// Lists longer than a wave: NB blocks, element 64 r + lane in block r, the
+// whole list ascending.  A sorted 64-lane sequence is merged in block by
+// block: the 64 smallest of (block r, carry) stay in block r and the 64
+// largest carry on into block r + 1 (every element of block r + 1 is >= all
+// of block r, so the smallest 64 of everything from block r on lie in block r
+// or the carry).  Each step is a half-cleaner of the bitonic union.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned long long reverse_key(unsigned long long v) {
+    return ((unsigned long long)reverse_lane_u((uint32_t)(v >> 32)) << 32) | reverse_lane_u((uint32_t)v);
+}
+__device__ __forceinline__ void bitonic_clean_key(unsigned long long& v, int lane) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) bitonic_step_key(v, lane, m, true);
+}
+__device__ __forceinline__ uint32_t key_hi_u(unsigned long long v) { return (uint32_t)(v >> 32); }
+
+// Merge the ascending 64-lane sequence v into the NB-block list lv; the
+// 64 NB smallest keys stay, ascending, and the smallest discarded key is
+// returned (kKeyEmpty-like keys when only empties are discarded).  A block
+// whose largest key is below the carry's smallest is left as it is.
+template <int NB>
+__device__ __forceinline__ unsigned long long wave_merge_blocks_key_drop(unsigned long long (&lv)[NB],
+                                                                         unsigned long long v, int lane) {
+    unsigned long long carry = v;
+#pragma unroll
+    for (int r = 0; r < NB; ++r) {
+        if (NB > 1) {
+            // both keys are wave-uniform after the readlanes: a uniform branch
+            const unsigned long long cmin = ((unsigned long long)bcast_u(key_hi_u(carry), 0) << 32) |
+                                            bcast_u((uint32_t)carry, 0);
+            const unsigned long long bmax = ((unsigned long long)bcast_u(key_hi_u(lv[r]), 63) << 32) |
+                                            bcast_u((uint32_t)lv[r], 63);
+            if (bmax < cmin) continue;
+        }
+        const unsigned long long rc = reverse_key(carry);
+        const bool t = rc < lv[r];
+        const unsigned long long lo = t ? rc : lv[r];
+        carry = t ? lv[r] : rc;
+        lv[r] = lo;
+        bitonic_clean_key(lv[r], lane);
+        if (r + 1 < NB) bitonic_clean_key(carry, lane);
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        const unsigned long long o = xor_lane_key(carry, m);
+        carry = (o < carry) ? o : carry;
+    }
+    return carry;
+}
+
+// The order bits of list element `pos` (wave-uniform pos), from its block.
+template <int NB>
+__device__ __forceinline__ uint32_t list_hi_at(const unsigned long long (&lv)[NB], int pos) {
+    const int b = pos >> 6;
+    uint32_t v = key_hi_u(lv[0]);
+#pragma unroll
+    for (int r = 1; r < NB; ++r)
+        if (b == r) v = key_hi_u(lv[r]);
+    return bcast_u(v, pos & 63);
+}
+
+// The same block merge on (value, index) pairs (the seed's list).
+template <typename T, int NB>
+__device__ __forceinline__ void wave_merge_blocks(T (&lv)[NB], uint32_t (&li)[NB], T v, uint32_t ix, int lane) {
+    T cv = v;
+    uint32_t ci = ix;
+#pragma unroll
+    for (int r = 0; r < NB; ++r) {
+        const T rv = reverse_f(cv);
+        const uint32_t ri = reverse_u(ci);
+        const bool t = pair_less<T>(rv, ri, lv[r], li[r]);
+        const T lov = t ? rv : lv[r];
+        const uint32_t loi = t ? ri : li[r];
+        cv = t ? lv[r] : rv;
+        ci = t ? li[r] : ri;
+        lv[r] = lov;
+        li[r] = loi;
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1) bitonic_step<T>(lv[r], li[r], lane, m, true);
+        if (r + 1 < NB) {
+#pragma unroll
+            for (int m = 32; m > 0; m >>= 1) bitonic_step<T>(cv, ci, lane, m, true);
+        }
+    }
+}
+
 // A 16-byte load through the global address space.  A pointer the compiler
 // cannot prove global (one walked in a register array) is otherwise loaded
 // with a flat instruction, which also counts against the LDS wait counter:
@@ -433,7 +520,7 @@ __device__ __forceinline__ float pick8(const f32x4_t& a0, const f32x4_t& a1, int
 // arm, unused for Euclidean).
 constexpr int kSeedQpw = 4;
 constexpr int kSeedQpb = 4 * kSeedQpw;
-template <typename T, int ARM, typename Bits>
+template <typename T, int ARM, typename Bits, int SB = 1>
 __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T* __restrict__ X, int64_t nq,
                                                int64_t nt, int64_t d, int k, int64_t nsamp,
                                                const T* __restrict__ qop, const T* __restrict__ yop,
@@ -450,14 +537,17 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
     const T inf = F::inf();
     const int64_t qb0 = (int64_t)blockIdx.x * kSeedQpb;
     const int64_t q0 = qb0 + (int64_t)w * kSeedQpw;
-    T qa[kSeedQpw], lv[kSeedQpw];
-    uint32_t li[kSeedQpw];
+    T qa[kSeedQpw], lv[kSeedQpw][SB];
+    uint32_t li[kSeedQpw][SB];
 #pragma unroll
     for (int j = 0; j < kSeedQpw; ++j) {
         const int64_t qg = (q0 + j < nq) ? q0 + j : nq - 1;  // past the end: repeats a query, not written
         qa[j] = (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST) ? qop[qg] : T(0);
-        lv[j] = inf;
-        li[j] = kSentinelIdx;
+#pragma unroll
+        for (int b = 0; b < SB; ++b) {
+            lv[j][b] = inf;
+            li[j][b] = kSentinelIdx;
+        }
     }
     for (int64_t s0 = 0; s0 < nsamp; s0 += 64) {
         const int64_t s = s0 + lane;
@@ -522,16 +612,24 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
                 tj = kSentinelIdx;
             }
             wave_sort64<T>(e, tj, lane);
-            wave_merge64<T>(lv[j], li[j], e, tj, lane);
+            if (SB == 1)
+                wave_merge64<T>(lv[j][0], li[j][0], e, tj, lane);
+            else
+                wave_merge_blocks<T, SB>(lv[j], li[j], e, tj, lane);
         }
     }
 #pragma unroll
     for (int j = 0; j < kSeedQpw; ++j) {
-        if (lane == k - 1 && q0 + j < nq) {
+        // element k - 1 of the list: block (k - 1) / 64, lane (k - 1) % 64
+        T kv = lv[j][0];
+#pragma unroll
+        for (int b = 1; b < SB; ++b)
+            if (((k - 1) >> 6) == b) kv = lv[j][b];
+        if (lane == ((k - 1) & 63) && q0 + j < nq) {
             if (sizeof(T) == 4)
-                shared_r[q0 + j] = (Bits)__float_as_uint((float)lv[j]);
+                shared_r[q0 + j] = (Bits)__float_as_uint((float)kv);
             else
-                shared_r[q0 + j] = (Bits)__double_as_longlong((double)lv[j]);
+                shared_r[q0 + j] = (Bits)__double_as_longlong((double)kv);
         }
     }
 }

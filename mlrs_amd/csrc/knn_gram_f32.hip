@@ -3,7 +3,7 @@
 // Replaces the GPU arm euclidean_topk_fused{,_dot,_dot_vec,_dot_vec8}
 // (crates/mlrs-kernels/src/knn.rs:377-2112) and the two-kernel
 // distance_direct -> top_k fallback (crates/mlrs-algos/src/neighbors/
-// nearest.rs:1058-1343) for f32, d <= 256, k <= 64, Euclidean and cosine.
+// nearest.rs:1058-1343) for f32, d <= 256, k <= 128, Euclidean and cosine.
 //
 // Two register shapes (GramShape below): d <= 128, 4 waves x 32 queries =
 // 128 queries per workgroup on v_mfma_f32_32x32x2f32; 128 < d <= 256, 4 waves
@@ -57,7 +57,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kBn = 32;                  // index rows per tile
-constexpr int kKcap = 64;                // largest k this kernel keeps
+constexpr int kKcap = 128;               // largest k this kernel keeps
 constexpr int kQcapK1 = 48;              // k = 1: the screen tightens every tile, queues stay short
 constexpr int kShareEvery = 64;          // tiles between reads of the shared thresholds
 constexpr int kSumSlots = 16;            // segment summaries read per refresh (k > 1)
@@ -250,7 +250,9 @@ struct GramOcc {
     static constexpr int wgs = (K1 && NG <= 8) ? 3 : 2;
 };
 
-template <int NG, int ARM, bool COS, bool VEC4, bool K1>
+// KL: 64-entry blocks of a (segment, query) list in registers during a flush
+// (1 for k <= 64, 3 for k <= 128: k + 32 entries).
+template <int NG, int ARM, bool COS, bool VEC4, bool K1, int KL>
 __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kernel(GramArgs32 a) {
     constexpr bool W16 = NG > 16;     // the wide shape (GramShape)
     typedef GramShape<W16> SH;
@@ -383,9 +385,13 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     } else {
         for (int j = 0; j < QPW; ++j) {
             const int64_t qg = qwave + j;
-            if (qg < nq && lane < K2) {
-                LV[qg * K2 + lane] = inf;
-                LI[qg * K2 + lane] = kSentinelIdx;
+#pragma unroll
+            for (int r = 0; r < KL; ++r) {
+                const int p = 64 * r + lane;
+                if (qg < nq && p < K2) {
+                    LV[qg * K2 + p] = inf;
+                    LI[qg * K2 + p] = kSentinelIdx;
+                }
             }
         }
     }
@@ -506,8 +512,12 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         const int64_t qg_ = qwave + j_;                                                      \
         const uint32_t n_ = bcast_u(cntr, j_);                                               \
         const bool exact_ = L.mode[j_] != 0u;                                                \
-        unsigned long long lk_ = kKeyEmpty;                                                  \
-        if (lane < K2) lk_ = pair_key(LV[qg_ * K2 + lane], LI[qg_ * K2 + lane]);             \
+        unsigned long long lk_[KL];                                                          \
+        _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) {                                  \
+            const int p_ = 64 * r_ + lane;                                                   \
+            lk_[r_] = kKeyEmpty;                                                             \
+            if (p_ < K2) lk_[r_] = pair_key(LV[qg_ * K2 + p_], LI[qg_ * K2 + p_]);           \
+        }                                                                                    \
         float e_ = inf;                                                                      \
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
@@ -524,15 +534,21 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         }                                                                                    \
         unsigned long long ek_ = pair_key(e_, t_);                                           \
         wave_sort64_key(ek_, lane);                                                          \
-        const unsigned long long ok_ = lk_;                                                  \
-        const unsigned long long dk_ = wave_merge64_key_drop(lk_, ek_, lane);                \
-        float R_ = f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), k - 1));               \
+        const unsigned long long ok_ = lk_[0];                                               \
+        unsigned long long dk_;                                                              \
+        if constexpr (KL == 1)                                                               \
+            dk_ = wave_merge64_key_drop(lk_[0], ek_, lane);                                  \
+        else                                                                                 \
+            dk_ = wave_merge_blocks_key_drop<KL>(lk_, ek_, lane);                            \
+        float R_ = f32_from_order_bits(list_hi_at<KL>(lk_, k - 1));                          \
         if (!exact_) {                                                                       \
-            const float dr_ = (K2 < 64) ? f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), K2)) \
-                                        : key_value(dk_);                                    \
+            const float dr_ = (K2 < 64 * KL) ? f32_from_order_bits(list_hi_at<KL>(lk_, K2))  \
+                                             : key_value(dk_);                               \
             double w_ = (double)R_ + 2.0 * (double)L.eps[j_];                                \
             w_ += __builtin_fabs(w_) * 0x1p-40;                                              \
             if (dr_ < inf && (double)dr_ <= w_) {                                            \
+              if constexpr (KL == 1) {                                                       \
+                /* the old list and the queue, exactly */                                    \
                 float x1_ = inf, x2_ = inf;                                                  \
                 uint32_t i1_ = key_index(ok_), i2_ = key_index(ek_);                         \
                 if (i1_ != kSentinelIdx) x1_ = MLRS_EXACT_AT(i1_);                           \
@@ -543,23 +559,45 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
                 wave_sort64_key(k1_, lane);                                                  \
                 wave_sort64_key(k2_, lane);                                                  \
                 wave_merge64_key(k1_, k2_, lane);                                            \
-                lk_ = k1_;                                                                   \
-                R_ = f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), k - 1));             \
+                lk_[0] = k1_;                                                                \
+              } else {                                                                       \
+                /* the old list (still in memory) and the queue, exactly */                  \
+                _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) lk_[r_] = kKeyEmpty;       \
+                _Pragma("unroll") for (int r_ = 0; r_ <= KL; ++r_) {                         \
+                    uint32_t i_ = kSentinelIdx;                                              \
+                    if (r_ < KL) {                                                           \
+                        const int p_ = 64 * r_ + lane;                                       \
+                        if (p_ < K2) i_ = LI[qg_ * K2 + p_];                                 \
+                    } else if ((uint32_t)lane < n_) {                                        \
+                        i_ = L.qidx[j_][lane];                                               \
+                    }                                                                        \
+                    float x_ = inf;                                                          \
+                    if (i_ != kSentinelIdx) x_ = MLRS_EXACT_AT(i_);                          \
+                    if (x_ != x_) { x_ = inf; i_ = kSentinelIdx; }                           \
+                    unsigned long long b_ = pair_key(x_, i_);                                \
+                    wave_sort64_key(b_, lane);                                               \
+                    (void)wave_merge_blocks_key_drop<KL>(lk_, b_, lane);                     \
+                }                                                                            \
+              }                                                                              \
+                R_ = f32_from_order_bits(list_hi_at<KL>(lk_, k - 1));                        \
                 if (lane == 0) L.mode[j_] = 1u;                                              \
             } else if (R_ < inf) {                                                           \
                 R_ = round_up_f((double)R_ + (double)L.eps[j_]);                             \
             }                                                                                \
         }                                                                                    \
-        if (lane < K2) {                                                                     \
-            LV[qg_ * K2 + lane] = key_value(lk_);                                            \
-            LI[qg_ * K2 + lane] = key_index(lk_);                                            \
+        _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) {                                  \
+            const int p_ = 64 * r_ + lane;                                                   \
+            if (p_ < K2) {                                                                   \
+                LV[qg_ * K2 + p_] = key_value(lk_[r_]);                                      \
+                LI[qg_ * K2 + p_] = key_index(lk_[r_]);                                      \
+            }                                                                                \
         }                                                                                    \
         if (SUMM) {                                                                          \
             const bool sv_ = !exact_ && L.mode[j_] == 0u;                                    \
-            float p_[4] = {f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), rk1 - 1)),    \
-                           f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), rk2 - 1)),    \
-                           f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), rk3 - 1)),    \
-                           f32_from_order_bits(bcast_u((uint32_t)(lk_ >> 32), k - 1))};     \
+            float p_[4] = {f32_from_order_bits(list_hi_at<KL>(lk_, rk1 - 1)),                \
+                           f32_from_order_bits(list_hi_at<KL>(lk_, rk2 - 1)),                \
+                           f32_from_order_bits(list_hi_at<KL>(lk_, rk3 - 1)),                \
+                           f32_from_order_bits(list_hi_at<KL>(lk_, k - 1))};                 \
             if (lane == 0) {                                                                 \
                 _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                             \
                     if (sv_ && p_[i_] < inf) p_[i_] = round_up_f((double)p_[i_] + (double)L.eps[j_]); \
@@ -906,11 +944,12 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 // Initial per-query bound: the k-th smallest exact value over an evenly
 // spaced sample of index rows (seed_kth_block).  Any k distinct rows bound the
 // final k-th value from above, so the screen starts tight instead of at +inf.
-template <int ARM>
+// SB: 64-entry blocks of the running sample list (k <= 64 SB).
+template <int ARM, int SB>
 __global__ __launch_bounds__(256) void knn_seed_f32_kernel(GramArgs32 a, int64_t nsamp) {
     const float* qop = (ARM == ARM_COS_FOLD) ? a.qsq : a.qinv;
     const float* yop = (ARM == ARM_COS_FOLD) ? a.xsq : a.xinv;
-    seed_kth_block<float, ARM>(a.q, a.x, a.nq, a.nt, a.d, a.k, nsamp, qop, yop, a.shared_r);
+    seed_kth_block<float, ARM, unsigned int, SB>(a.q, a.x, a.nq, a.nt, a.d, a.k, nsamp, qop, yop, a.shared_r);
 }
 
 // Merge the per-segment lists of one query per wave and emit the output
@@ -997,6 +1036,102 @@ __global__ __launch_bounds__(256) void knn_merge_f32_kernel(GramArgs32 a) {
     if (lane < k) emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, k, qg, lane, lv, li, a.out_val, a.out_idx);
 }
 
+// 64 < k <= 128: the same merge over lists of up to three 64-entry blocks
+// (k + 32 entries).  The union and the result are kept as two-block lists
+// (the k smallest fit in 128 entries), merged block by block on 64-bit
+// (value bits, index) keys.
+template <int ARM, bool VEC4>
+__global__ __launch_bounds__(256) void knn_merge_blocks_f32_kernel(GramArgs32 a) {
+    constexpr int SLB = 3;  // blocks of a segment list
+    constexpr int UB = 2;   // blocks of the union and of the result
+    __shared__ uint32_t cand[4][128];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + wv;
+    if (qg >= a.nq) return;
+    const int k = a.k;
+    const int K2 = gram_list_cap(k);
+    const int64_t d = a.d;
+    const StreamSplit sp(a.nq, a.nt, a.qpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / a.qpb);
+    // the k-th smallest value over the union of the lists
+    unsigned long long u[UB];
+#pragma unroll
+    for (int r = 0; r < UB; ++r) u[r] = kKeyEmpty;
+    for (int64_t s = 0; s < nsl; ++s) {
+#pragma unroll
+        for (int r = 0; r < SLB; ++r) {
+            if (64 * r >= K2) break;
+            const int p = 64 * r + lane;
+            unsigned long long key = kKeyEmpty;
+            if (p < K2) {
+                const int64_t o = (s * a.nq + qg) * K2 + p;
+                key = pair_key(a.part_val[o], a.part_idx[o]);
+            }
+            (void)wave_merge_blocks_key_drop<UB>(u, key, lane);
+        }
+    }
+    const float qsq = a.qsq[qg];
+    const float eps = (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST)
+                          ? (float)a.eps_abs
+                          : (float)(a.eps_rel * ((double)qsq + (double)a.stats->xsq_max) + a.eps_abs);
+    double W = (double)f32_from_order_bits(list_hi_at<UB>(u, k - 1)) + 2.0 * (double)eps;
+    W += __builtin_fabs(W) * 0x1p-40;
+    // exact evaluation of the window's pairs, compacted 64 at a time
+    unsigned long long res[UB];
+#pragma unroll
+    for (int r = 0; r < UB; ++r) res[r] = kKeyEmpty;
+    uint32_t nc = 0;
+    auto evaluate = [&](uint32_t count) {
+        float e = __builtin_huge_valf();
+        uint32_t t = kSentinelIdx;
+        if ((uint32_t)lane < count) {
+            t = cand[wv][lane];
+            e = exact_f32<ARM, VEC4, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, query_operand<ARM>(a, qg),
+                                        row_operand<ARM>(a, t));
+            if (e != e) {
+                e = __builtin_huge_valf();
+                t = kSentinelIdx;
+            }
+        }
+        unsigned long long ek = pair_key(e, t);
+        wave_sort64_key(ek, lane);
+        (void)wave_merge_blocks_key_drop<UB>(res, ek, lane);
+    };
+    for (int64_t s = 0; s < nsl; ++s) {
+        for (int r = 0; r < SLB; ++r) {
+            if (64 * r >= K2) break;
+            const int p = 64 * r + lane;
+            bool in = false;
+            uint32_t ix = kSentinelIdx;
+            if (p < K2) {
+                const int64_t o = (s * a.nq + qg) * K2 + p;
+                ix = a.part_idx[o];
+                in = (ix != kSentinelIdx) && !((double)a.part_val[o] > W);
+            }
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+            const uint32_t pre = (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull));
+            if (in) cand[wv][nc + pre] = ix;
+            nc += (uint32_t)__builtin_popcountll(bal);
+            if (nc >= 64) {
+                evaluate(64);
+                const uint32_t rest = nc - 64;
+                const uint32_t mv = ((uint32_t)lane < rest) ? cand[wv][64 + lane] : 0u;
+                if ((uint32_t)lane < rest) cand[wv][lane] = mv;
+                nc = rest;
+            }
+        }
+    }
+    if (nc > 0) evaluate(nc);
+#pragma unroll
+    for (int r = 0; r < UB; ++r) {
+        const int slot = 64 * r + lane;
+        if (slot < k)
+            emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, k, qg, slot, key_value(res[r]), key_index(res[r]),
+                      a.out_val, a.out_idx);
+    }
+}
+
 // k = 1: the same merge with one lane per query (the segment lists are one
 // pair each, so the merge is a (value, index) minimum).
 __global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
@@ -1028,9 +1163,11 @@ hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     dim3 grid((unsigned)StreamSplit(a.nq, a.nt, a.qpb, kBn, a.grid_wgs).G);
     (void)nblocks;
     if (a.k == 1)
-        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true, 1>), grid, dim3(256), 0, s, a);
+    else if (a.k <= 64)
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 1>), grid, dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 3>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1058,8 +1195,11 @@ hipError_t launch_wide(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
 
 template <int ARM>
 hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
-    hipLaunchKernelGGL((knn_seed_f32_kernel<ARM>), dim3((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb)), dim3(256), 0, s,
-                       a, nsamp);
+    const dim3 grid((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb));
+    if (a.k <= 64)
+        hipLaunchKernelGGL((knn_seed_f32_kernel<ARM, 1>), grid, dim3(256), 0, s, a, nsamp);
+    else
+        hipLaunchKernelGGL((knn_seed_f32_kernel<ARM, 2>), grid, dim3(256), 0, s, a, nsamp);
     return hipGetLastError();
 }
 
@@ -1107,7 +1247,11 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
 
 template <int ARM, bool VEC4>
 hipError_t launch_merge(const GramArgs32& a, hipStream_t s) {
-    hipLaunchKernelGGL((knn_merge_f32_kernel<ARM, VEC4>), dim3((unsigned)((a.nq + 3) / 4)), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)((a.nq + 3) / 4));
+    if (a.k <= 64)
+        hipLaunchKernelGGL((knn_merge_f32_kernel<ARM, VEC4>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((knn_merge_blocks_f32_kernel<ARM, VEC4>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

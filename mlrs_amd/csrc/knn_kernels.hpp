@@ -116,8 +116,11 @@ struct GramArgs32 {
 
 // Entries of one (segment, query) list of the Gram kernels: the k best plus
 // room for the pairs whose screen values lie within the error window of the
-// k-th (k = 1 keeps the single best pair, exactly).
-__host__ __device__ inline int gram_list_cap(int k) { return k == 1 ? 1 : (k + 32 < 64 ? k + 32 : 64); }
+// k-th (k = 1 keeps the single best pair, exactly): one 64-entry block for
+// k <= 64, k + 32 (at most 160, three blocks) above.
+__host__ __device__ inline int gram_list_cap(int k) {
+    return k == 1 ? 1 : k <= 64 ? (k + 32 < 64 ? k + 32 : 64) : k + 32;
+}
 
 // Screen values kept per workgroup while pairs wait in the queues (k > 1).
 inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64; }

@@ -20,6 +20,10 @@ and one more shape outside the five, an embedding-sized search:
 d256 index 200,000 x 256 and queries 5,000 x 256 from c2's generator at
      d = 256 (100-component mixture, centres U[-10,10]^256, unit std), f32,
      Euclidean, k=32
+
+and c2 at the top of the reference's metric-arm k range:
+
+c2k128 c2's data with k=128
 """
 import numpy as np
 
@@ -32,6 +36,7 @@ CONFIGS = {
     "c4": dict(n_index=500_000, n_query=500_000, d=3, k=8, metric="euclidean", dtype="f32"),
     "c5": dict(n_index=1_024, n_query=5_000_000, d=64, k=1, metric="euclidean", dtype="f32"),
     "d256": dict(n_index=200_000, n_query=5_000, d=256, k=32, metric="euclidean", dtype="f32"),
+    "c2k128": dict(n_index=1_000_000, n_query=10_000, d=128, k=128, metric="euclidean", dtype="f32"),
 }
 
 
@@ -90,7 +95,8 @@ def gen_d256(seed=SEED, n_index=200_000, n_query=5_000, d=256):
     return gen_c2(seed=seed, n_index=n_index, n_query=n_query, d=d)
 
 
-GENERATORS = {"c1": gen_c1, "c2": gen_c2, "c3": gen_c3, "c4": gen_c4, "c5": gen_c5, "d256": gen_d256}
+GENERATORS = {"c1": gen_c1, "c2": gen_c2, "c3": gen_c3, "c4": gen_c4, "c5": gen_c5, "d256": gen_d256,
+              "c2k128": gen_c2}
 
 
 def generate(name, **kw):

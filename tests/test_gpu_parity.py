@@ -69,11 +69,17 @@ GRAM = [(300, 3000, 64, 10), (129, 1000, 17, 5), (500, 4000, 128, 32), (77, 600,
 GRAM_WIDE = [(300, 3000, 256, 10), (129, 1000, 129, 5), (500, 4000, 192, 32), (77, 600, 200, 64),
              (1000, 30000, 256, 32), (5, 100, 160, 1), (200, 2048, 255, 20), (1, 31, 136, 31),
              (130, 5000, 250, 7), (65, 3000, 256, 1), (70, 9000, 176, 16)]
-# generic exact path (k > 64, d > 256)
+# Gram-MFMA path with 64 < k <= 128 (lists of k + 32 entries in three
+# 64-entry blocks), both shapes; large enough that the automatic choice takes
+# the fused kernel too
+GRAM_K128 = [(300, 20000, 64, 100), (500, 40000, 128, 128), (77, 9000, 100, 65), (130, 9000, 96, 96),
+             (64, 5000, 200, 128), (200, 20000, 256, 80), (1, 300, 40, 128), (129, 1000, 17, 127),
+             (40, 129, 33, 128)]
+# generic exact path (k > 128, d > 256)
 GENERIC = [(50, 500, 64, 100), (20, 300, 64, 200), (30, 400, 300, 10)]
 
 
-@pytest.mark.parametrize("case", LOWD + GRAM + GRAM_WIDE + GENERIC)
+@pytest.mark.parametrize("case", LOWD + GRAM + GRAM_WIDE + GRAM_K128 + GENERIC)
 def test_f32_euclidean_bitwise(case):
     nq, nt, d, k = case
     xq, xt = _data(100 + d, nq, nt, d)
@@ -82,7 +88,8 @@ def test_f32_euclidean_bitwise(case):
 
 @pytest.mark.parametrize("case", [(300, 3000, 64, 10), (100, 2000, 5, 7), (50, 500, 130, 8), (40, 400, 64, 80),
                                   (600, 20000, 128, 32), (300, 5000, 256, 16), (50, 2000, 150, 32),
-                                  (129, 3000, 200, 1), (64, 1000, 193, 64)])
+                                  (129, 3000, 200, 1), (64, 1000, 193, 64), (300, 20000, 128, 100),
+                                  (64, 5000, 193, 128), (100, 8000, 48, 65)])
 def test_f32_cosine_bitwise(case):
     nq, nt, d, k = case
     xq, xt = _data(200 + d, nq, nt, d)
@@ -108,19 +115,20 @@ def test_f64_bitwise(case, metric):
 
 
 @pytest.mark.parametrize("d", [3, 64, 256])
-def test_duplicates_and_boundary_ties(d):
+@pytest.mark.parametrize("k", [32, 100])
+def test_duplicates_and_boundary_ties(d, k):
     """100 identical rows around the k-th slot: membership and order are
     decided by index alone (knn_metric_kernel_test.rs:269-289)."""
     rng = np.random.default_rng(5)
     xt = rng.standard_normal((3000, d)).astype(np.float32)
     xt[500:600] = xt[7]            # 101 copies of row 7
     xq = np.concatenate([xt[7:8], xt[:50], rng.standard_normal((20, d)).astype(np.float32)])
-    gd, gi = check_knn(xq, xt, 32, "euclidean", "dups d=%d" % d)
-    assert gi[0].tolist() == [7] + list(range(500, 531))
+    gd, gi = check_knn(xq, xt, k, "euclidean", "dups d=%d k=%d" % (d, k))
+    assert gi[0].tolist() == [7] + list(range(500, 500 + k - 1))
     assert np.all(gd[0] == 0)
 
 
-@pytest.mark.parametrize("d,k", [(3, 8), (48, 24), (208, 24)])
+@pytest.mark.parametrize("d,k", [(3, 8), (48, 24), (208, 24), (48, 100), (208, 128)])
 def test_quantized_data_many_ties(d, k):
     rng = np.random.default_rng(6)
     xt = rng.integers(-3, 4, size=(4000, d)).astype(np.float32)
@@ -144,7 +152,8 @@ def test_nan_rows(d):
 
 @pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("perturb", [0.0, 1e-4])
-def test_near_ties_across_segments(perturb, d):
+@pytest.mark.parametrize("k", [32, 120])
+def test_near_ties_across_segments(perturb, d, k):
     """Copies of each query (exact, or perturbed far inside the screen's error
     window) spread through a large index, so they fall in different segments
     of the fused split: each segment's list and the final merge must resolve
@@ -155,8 +164,8 @@ def test_near_ties_across_segments(perturb, d):
     for j in range(12):
         rows = np.arange(40) * 1999 + 17 * j + 5
         xt[rows] = xq[j] + perturb * rng.standard_normal((40, d)).astype(np.float32)
-    check_knn(xq, xt, 32, "euclidean", "near ties %g" % perturb)
-    check_knn(xq, xt, 32, "cosine", "near ties cosine %g" % perturb)
+    check_knn(xq, xt, k, "euclidean", "near ties %g" % perturb)
+    check_knn(xq, xt, k, "cosine", "near ties cosine %g" % perturb)
 
 
 def test_cosine_nan_rows():
