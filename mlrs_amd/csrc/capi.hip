@@ -7,6 +7,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
+#include <unordered_map>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -1756,6 +1758,71 @@ static int32_t km_d2h(void* dst, const void* src, size_t bytes, hipStream_t s) {
     return e == hipSuccess ? MLRS_OK : hip_err(e, "kmeans read-back");
 }
 
+// The top m rows by (distance desc, index asc) -- the prefix of the
+// relocation's ranking (prims/kmeans.rs:1347-1359) -- selected on the device
+// from the keys -distance (ascending (key, index) is that order), with their
+// labels.  *ranked stays false when a distance is NaN: the reference ranks
+// NaN above every number, which the keys cannot express, so the host ranks.
+// The selection runs one workgroup per row, so a long array is cut into
+// chunks of C keys (padded with +inf): each chunk's m smallest are selected
+// in parallel, then the m smallest of those.  The candidates lie chunk by
+// chunk, each chunk's equal keys in index order, so candidate order breaks
+// ties as the row number does.
+template <typename T>
+static int32_t km_rank_device(const T* dist, const uint32_t* labels, int64_t n, int64_t m,
+                              std::vector<uint32_t>& rows, std::vector<uint32_t>& labs, bool* ranked,
+                              hipStream_t s) {
+    *ranked = false;
+    int64_t C = 8192;
+    while (C < 4 * m || C * C < n * m) C <<= 1;
+    const int64_t R = (n + C - 1) / C;
+    const bool two = R > 1;
+    const int64_t padded = two ? R * C : n;
+    const int64_t cand = two ? R * m : 0;
+    const size_t sel = std::max(select_rows_scratch_bytes(two ? R : 1, (int)m, (int)sizeof(T)),
+                                select_rows_scratch_bytes(1, (int)m, (int)sizeof(T)));
+    const size_t bytes = aligned_bytes(sizeof(T) * (size_t)padded) + aligned_bytes(sizeof(T) * (size_t)cand) +
+                         2 * aligned_bytes(sizeof(uint32_t) * (size_t)cand) + aligned_bytes(sizeof(T) * (size_t)m) +
+                         3 * aligned_bytes(sizeof(uint32_t) * (size_t)m) + aligned_bytes(sizeof(uint32_t)) +
+                         aligned_bytes(sel) + 256;
+    char* ws;
+    int cus;
+    int32_t rc = workspace(bytes, s, &ws, &cus);
+    if (rc) return rc;
+    Carver cv(ws);
+    T* neg = cv.take<T>((size_t)padded);
+    T* v1 = cv.take<T>((size_t)cand);
+    uint32_t* i1 = cv.take<uint32_t>((size_t)cand);
+    uint32_t* g1 = cv.take<uint32_t>((size_t)cand);
+    T* v2 = cv.take<T>((size_t)m);
+    uint32_t* i2 = cv.take<uint32_t>((size_t)m);
+    uint32_t* orow = cv.take<uint32_t>((size_t)m);
+    uint32_t* olab = cv.take<uint32_t>((size_t)m);
+    unsigned int* nans = cv.take<unsigned int>(1);
+    void* scratch = sel ? static_cast<void*>(cv.take<char>(sel)) : nullptr;
+    hipError_t e = launch_km_neg<T>(dist, n, padded, neg, nans, s);
+    if (two) {
+        if (e == hipSuccess) e = launch_select_rows<T>(neg, R, C, C, (int)m, EMIT_IDENTITY, v1, i1, scratch, s);
+        if (e == hipSuccess) e = launch_km_chunk_rows(i1, R, m, C, g1, s);
+        if (e == hipSuccess) e = launch_select_rows<T>(v1, 1, cand, cand, (int)m, EMIT_IDENTITY, v2, i2, scratch, s);
+        if (e == hipSuccess) e = launch_km_take_u32(g1, cand, i2, m, orow, s);
+    } else if (e == hipSuccess) {
+        e = launch_select_rows<T>(neg, 1, n, n, (int)m, EMIT_IDENTITY, v2, orow, scratch, s);
+    }
+    if (e == hipSuccess) e = launch_km_take_u32(labels, n, orow, m, olab, s);
+    if (e != hipSuccess) return hip_err(e, "kmeans relocation ranking");
+    unsigned int nn = 0;
+    rc = km_d2h<T>(&nn, nans, sizeof(nn), s);
+    if (rc || nn) return rc;
+    rows.resize((size_t)m);
+    labs.resize((size_t)m);
+    rc = km_d2h<T>(rows.data(), orow, sizeof(uint32_t) * (size_t)m, s);
+    if (!rc) rc = km_d2h<T>(labs.data(), olab, sizeof(uint32_t) * (size_t)m, s);
+    if (rc) return rc;
+    *ranked = true;
+    return MLRS_OK;
+}
+
 template <typename T>
 static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, int64_t k, int32_t init_kind,
                                const T* init, int64_t init_len, uint64_t seed, int64_t n_init, int64_t max_iter,
@@ -1861,13 +1928,23 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
             chosen.clear();
             chosen.reserve((size_t)k);
             if (init_kind == 2) {  // random_sample (prims/kmeans.rs:1769-1786)
-                std::vector<int64_t> ids((size_t)n);
-                for (int64_t i = 0; i < n; ++i) ids[i] = i;
+                // the partial Fisher-Yates shuffle of 0..n over the positions
+                // it touches only: a position absent from the map still holds
+                // its own number (the same draws and swaps as a full array)
+                std::unordered_map<int64_t, int64_t> ids;
+                ids.reserve((size_t)(2 * k));
+                auto at = [&](int64_t p) {
+                    const auto it = ids.find(p);
+                    return it == ids.end() ? p : it->second;
+                };
                 for (int64_t i = 0; i < k; ++i) {
                     const int64_t j = i + (int64_t)rng.next_below((uint64_t)(n - i));
-                    std::swap(ids[i], ids[j]);
+                    const int64_t vi = at(i), vj = at(j);
+                    ids[i] = vj;
+                    ids[j] = vi;
                 }
-                chosen.assign(ids.begin(), ids.begin() + k);
+                chosen.resize((size_t)k);
+                for (int64_t i = 0; i < k; ++i) chosen[i] = at(i);
             } else {  // kmeanspp_sample (prims/kmeans.rs:381-491)
                 std::vector<char> is_chosen((size_t)n, 0);
                 // the D^2 weights come back every draw: pinned host memory
@@ -1996,66 +2073,106 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
             if (empties) {
                 // relocate_empty_clusters (prims/kmeans.rs:1323-1410): the
                 // farthest rows by (distance desc, index asc) into the empty
-                // clusters, never emptying their donor
-                lab_h.resize((size_t)n);
-                dist_h.resize((size_t)n);
-                rc = km_d2h<T>(lab_h.data(), lab[cur], sizeof(uint32_t) * (size_t)n, s);
-                if (!rc) rc = km_d2h<T>(dist_h.data(), dist, sizeof(T) * (size_t)n, s);
-                if (rc) return rc;
-                // the ranking is only needed over a prefix: the top
-                // m = 8 * empties + 64 rows are selected in O(n) and sorted,
-                // the rest sorted only if the walk runs past them (the
-                // reference's select_nth_unstable_by + sort_by, :1347-1359)
-                std::vector<int64_t> order((size_t)n);
-                for (int64_t i = 0; i < n; ++i) order[i] = i;
-                // A total order (std::nth_element / std::sort need one): a NaN
-                // distance ranks above every number, NaNs and equal values by
-                // index.  On numbers it is the reference's (distance desc,
-                // index asc).
-                auto by_rank = [&](int64_t a, int64_t b) {
-                    const double da = (double)dist_h[a], db = (double)dist_h[b];
-                    const bool na = da != da, nb = db != db;
-                    if (na != nb) return na;
-                    if (!na) {
-                        if (db < da) return true;
-                        if (da < db) return false;
-                    }
-                    return a < b;
-                };
+                // clusters, never emptying their donor.  The walk records the
+                // moves (target, row, donor) in its order; they are applied
+                // afterwards in that order, so the sums see the same
+                // operations as a walk that applies them as it goes.
                 const int64_t m_top = std::min<int64_t>(8 * empties + 64, n);
-                if (m_top < n) std::nth_element(order.begin(), order.begin() + m_top, order.end(), by_rank);
-                std::sort(order.begin(), order.begin() + m_top, by_rank);
-                int64_t ranked = m_top;
-                std::vector<char> moved((size_t)n, 0);
-                std::vector<T> row((size_t)d);
-                int64_t cursor = 0;
-                for (int64_t c = 0; c < k; ++c) {
-                    if (cnt[c] != 0) continue;
-                    bool ok_move = false;
-                    while (cursor < n) {
-                        if (cursor == ranked) {  // past the selected prefix: rank the rest
-                            std::sort(order.begin() + ranked, order.end(), by_rank);
-                            ranked = n;
+                std::vector<int64_t> moves;  // (target, row, donor) triples
+                std::vector<int64_t> cnt_w;
+                // the walk over a ranked prefix: false when it runs past it
+                auto walk = [&](int64_t len, const std::function<int64_t(int64_t)>& row_at,
+                                const std::function<int64_t(int64_t)>& label_at) -> bool {
+                    moves.clear();
+                    cnt_w = cnt;
+                    int64_t cursor = 0;
+                    for (int64_t c = 0; c < k; ++c) {
+                        if (cnt_w[c] != 0) continue;
+                        bool ok_move = false;
+                        while (cursor < len) {
+                            const int64_t pos = cursor++;
+                            const int64_t donor = label_at(pos);
+                            if (cnt_w[donor] <= 1) continue;
+                            moves.push_back(c);
+                            moves.push_back(row_at(pos));
+                            moves.push_back(donor);
+                            ++cnt_w[c];
+                            --cnt_w[donor];
+                            ok_move = true;
+                            break;
                         }
-                        const int64_t i = order[cursor++];
-                        if (moved[i]) continue;
-                        const int64_t donor = lab_h[i];
-                        if (cnt[donor] <= 1) continue;
-                        rc = km_d2h<T>(row.data(), x + i * d, sizeof(T) * (size_t)d, s);
-                        if (rc) return rc;
-                        for (int64_t j = 0; j < d; ++j) {
-                            const double xij = (double)row[j];
-                            nc[c * d + j] += xij;
-                            nc[donor * d + j] -= xij;
-                        }
-                        ++cnt[c];
-                        --cnt[donor];
-                        moved[i] = 1;
-                        ok_move = true;
-                        break;
+                        if (!ok_move) return false;
                     }
-                    if (!ok_move) return shape_err("labels", n, k, empties);
+                    return true;
+                };
+                // (a) the top m_top rows ranked on the device: keys -distance
+                //     selected by (key, index), the labels of those rows
+                //     gathered; only they come back
+                bool walked = false;
+                if (m_top <= (int64_t)INT32_MAX) {
+                    bool ranked = false;
+                    std::vector<uint32_t> rows_r, labs_r;
+                    rc = km_rank_device<T>(dist, lab[cur], n, m_top, rows_r, labs_r, &ranked, s);
+                    if (rc) return rc;
+                    if (ranked)
+                        walked = walk(m_top, [&](int64_t p) { return (int64_t)rows_r[p]; },
+                                      [&](int64_t p) { return (int64_t)labs_r[p]; });
                 }
+                // (b) the host ranking over every row: a NaN distance (ranked
+                //     above every number, which the keys cannot express) or a
+                //     walk past the device's prefix
+                if (!walked) {
+                    lab_h.resize((size_t)n);
+                    dist_h.resize((size_t)n);
+                    rc = km_d2h<T>(lab_h.data(), lab[cur], sizeof(uint32_t) * (size_t)n, s);
+                    if (!rc) rc = km_d2h<T>(dist_h.data(), dist, sizeof(T) * (size_t)n, s);
+                    if (rc) return rc;
+                    std::vector<int64_t> order((size_t)n);
+                    for (int64_t i = 0; i < n; ++i) order[i] = i;
+                    // A total order (std::sort needs one): a NaN distance ranks
+                    // above every number, NaNs and equal values by index.  On
+                    // numbers it is the reference's (distance desc, index asc).
+                    auto by_rank = [&](int64_t a, int64_t b) {
+                        const double da = (double)dist_h[a], db = (double)dist_h[b];
+                        const bool na = da != da, nb = db != db;
+                        if (na != nb) return na;
+                        if (!na) {
+                            if (db < da) return true;
+                            if (da < db) return false;
+                        }
+                        return a < b;
+                    };
+                    std::sort(order.begin(), order.end(), by_rank);
+                    if (!walk(n, [&](int64_t p) { return order[p]; },
+                              [&](int64_t p) { return (int64_t)lab_h[order[p]]; }))
+                        return shape_err("labels", n, k, empties);
+                }
+                // the moved rows, gathered on the device and read back at once
+                const int64_t nm = (int64_t)moves.size() / 3;
+                std::vector<int64_t> mrow((size_t)nm);
+                for (int64_t q = 0; q < nm; ++q) mrow[q] = moves[3 * q + 1];
+                std::vector<T> rows_h((size_t)(nm * d));
+                {
+                    char* ws;
+                    int cus;
+                    rc = workspace(aligned_bytes(sizeof(T) * (size_t)(nm * d)) + 256, s, &ws, &cus);
+                    if (rc) return rc;
+                    T* rows_dev = reinterpret_cast<T*>(ws);
+                    e = hipMemcpyAsync(idx_dev, mrow.data(), sizeof(int64_t) * (size_t)nm, hipMemcpyHostToDevice, s);
+                    if (e == hipSuccess) e = launch_km_gather<T>(x, idx_dev, nm, d, rows_dev, s);
+                    if (e != hipSuccess) return hip_err(e, "kmeans relocation rows");
+                    rc = km_d2h<T>(rows_h.data(), rows_dev, sizeof(T) * (size_t)(nm * d), s);
+                    if (rc) return rc;
+                }
+                for (int64_t q = 0; q < nm; ++q) {
+                    const int64_t c = moves[3 * q], donor = moves[3 * q + 2];
+                    for (int64_t j = 0; j < d; ++j) {
+                        const double xij = (double)rows_h[q * d + j];
+                        nc[c * d + j] += xij;
+                        nc[donor * d + j] -= xij;
+                    }
+                }
+                cnt = cnt_w;
             }
             // mean divide in f64 and the centre shift (single_run :1010-1030)
             for (int64_t c = 0; c < k; ++c) {

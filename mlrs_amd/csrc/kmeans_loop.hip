@@ -413,6 +413,66 @@ hipError_t launch_km_gather(const T* x, const int64_t* idx, int64_t k, int64_t d
     return hipGetLastError();
 }
 
+// Relocation ranking (relocate_empty_clusters, prims/kmeans.rs:1323-1410):
+// the keys -distance, so that ascending (key, index) is the reference's
+// (distance desc, index asc) order, padded with +inf up to `padded` entries,
+// and the number of NaN distances (the reference ranks those first, which the
+// keys cannot express).
+template <typename T>
+__global__ __launch_bounds__(256) void km_neg_kernel(const T* __restrict__ dist, int64_t n, int64_t padded,
+                                                     T* __restrict__ neg, unsigned int* __restrict__ nans) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    bool nan = false;
+    if (i < n) {
+        const T v = dist[i];
+        neg[i] = -v;
+        nan = v != v;
+    } else if (i < padded) {
+        neg[i] = FloatTraits<T>::inf();
+    }
+    const uint64_t b = __builtin_amdgcn_ballot_w64(nan);
+    if (b != 0 && (int)(threadIdx.x & 63) == __builtin_ctzll(b)) atomicAdd(nans, (unsigned int)__builtin_popcountll(b));
+}
+
+// Global row numbers of the first stage's picks: pick j of chunk r (column
+// idx[r m + j] of the chunk) is row r C + idx.
+__global__ __launch_bounds__(256) void km_chunk_rows_kernel(const uint32_t* __restrict__ idx, int64_t nchunks,
+                                                            int64_t m, int64_t C, uint32_t* __restrict__ rows) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < nchunks * m) rows[i] = (uint32_t)((i / m) * C + idx[i]);
+}
+
+// out[i] = src[idx[i]], i < m (0 for an index past the n_src entries).
+__global__ __launch_bounds__(256) void km_take_u32_kernel(const uint32_t* __restrict__ src, int64_t n_src,
+                                                          const uint32_t* __restrict__ idx, int64_t m,
+                                                          uint32_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < m) out[i] = ((int64_t)idx[i] < n_src) ? src[idx[i]] : 0u;
+}
+
+template <typename T>
+hipError_t launch_km_neg(const T* dist, int64_t n, int64_t padded, T* neg, unsigned int* nans, hipStream_t s) {
+    hipError_t e = launch_fill_u32(nans, 1, 0u, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((km_neg_kernel<T>), dim3((unsigned)((padded + 255) / 256)), dim3(256), 0, s, dist, n, padded,
+                       neg, nans);
+    return hipGetLastError();
+}
+
+hipError_t launch_km_chunk_rows(const uint32_t* idx, int64_t nchunks, int64_t m, int64_t C, uint32_t* rows,
+                                hipStream_t s) {
+    hipLaunchKernelGGL(km_chunk_rows_kernel, dim3((unsigned)((nchunks * m + 255) / 256)), dim3(256), 0, s, idx,
+                       nchunks, m, C, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_km_take_u32(const uint32_t* src, int64_t n_src, const uint32_t* idx, int64_t m, uint32_t* out,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(km_take_u32_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, src, n_src, idx, m,
+                       out);
+    return hipGetLastError();
+}
+
 #define MLRS_KM_INST(T)                                                                                            \
     template hipError_t launch_km_centroid_sums<T>(const T*, const uint32_t*, int64_t, int64_t, int64_t, int64_t,   \
                                                    int64_t, const KmScratch<T>&, hipStream_t);                     \
@@ -421,7 +481,8 @@ hipError_t launch_km_gather(const T* x, const int64_t* idx, int64_t k, int64_t d
     template hipError_t launch_km_col_sums<T>(const T*, int64_t, int64_t, int64_t, int64_t, const T*, T*,           \
                                               hipStream_t);                                                        \
     template hipError_t launch_km_mind2<T>(const T*, int64_t, int64_t, int64_t, int, T*, hipStream_t);              \
-    template hipError_t launch_km_gather<T>(const T*, const int64_t*, int64_t, int64_t, T*, hipStream_t);
+    template hipError_t launch_km_gather<T>(const T*, const int64_t*, int64_t, int64_t, T*, hipStream_t);        \
+    template hipError_t launch_km_neg<T>(const T*, int64_t, int64_t, T*, unsigned int*, hipStream_t);
 MLRS_KM_INST(float)
 MLRS_KM_INST(double)
 #undef MLRS_KM_INST

@@ -359,5 +359,15 @@ template <typename T>
 hipError_t launch_km_mind2(const T* x, int64_t n, int64_t d, int64_t cidx, int first, T* mind2, hipStream_t s);
 template <typename T>
 hipError_t launch_km_gather(const T* x, const int64_t* idx, int64_t k, int64_t d, T* out, hipStream_t s);
+// neg[i] = -dist[i] (i < n), +inf up to `padded`; *nans = the number of NaN
+// distances (relocation ranking).
+template <typename T>
+hipError_t launch_km_neg(const T* dist, int64_t n, int64_t padded, T* neg, unsigned int* nans, hipStream_t s);
+// rows[r m + j] = r C + idx[r m + j]: chunk-local picks to row numbers.
+hipError_t launch_km_chunk_rows(const uint32_t* idx, int64_t nchunks, int64_t m, int64_t C, uint32_t* rows,
+                                hipStream_t s);
+// out[i] = src[idx[i]], i < m (0 for an index past the n_src entries).
+hipError_t launch_km_take_u32(const uint32_t* src, int64_t n_src, const uint32_t* idx, int64_t m, uint32_t* out,
+                              hipStream_t s);
 
 }  // namespace mlrs

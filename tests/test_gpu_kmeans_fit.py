@@ -95,6 +95,22 @@ def test_fit_relocation_walks_past_the_selected_prefix():
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_fit_relocation_ranked_in_chunks_with_ties(dtype):
+    """60,000 rows on an integer grid (many equal distances, spread over the
+    device ranking's chunks of 8,192 keys) and 40 empty clusters: the top
+    8 * 40 + 64 rows by (distance desc, index asc) come from the two-stage
+    device selection, and the fit matches the oracle's bits."""
+    rng = np.random.default_rng(9)
+    X = rng.integers(0, 10, size=(60000, 3)).astype(dtype)
+    far = np.zeros((40, 3), dtype=dtype)
+    far[:, 0] = 1000.0 + 10.0 * np.arange(40)
+    ini = np.concatenate([X[:6], far])
+    want = oracle.kmeans_fit(X, ini.shape[0], "array", ini, max_iter=2, tol=0.0)
+    got = prims.kmeans_fit(_t(X), ini.shape[0], "array", _t(ini), max_iter=2, tol=0.0)
+    _same(got, want)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_fit_relocation_with_a_nan_distance(dtype):
     """A NaN row reaches the relocation ranking (the C ABI does not check
     finiteness, as the reference's Rust fit does not): the ranking is a total
