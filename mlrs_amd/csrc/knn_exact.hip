@@ -271,6 +271,9 @@ template <> struct KeyOf<double> {
 // output rows and sorts there (select_collect_kernel and below).
 constexpr int SEL_MAXK = 256;
 
+// Loads in flight per thread in the row scans below.
+constexpr int kRadixBatch = 8;
+
 // Shared state of one row's radix select (one 256-thread workgroup per row).
 template <typename K>
 struct RadixShared {
@@ -288,9 +291,17 @@ __device__ uint32_t row_count_valid(const T* __restrict__ dr, int64_t cols, Radi
     if (tid == 0) sh.nvalid = 0;
     __syncthreads();
     uint32_t local = 0;
-    for (int64_t c = tid; c < cols; c += 256) {
-        const T v = dr[c];
-        local += (v == v) ? 1u : 0u;
+    // kRadixBatch loads in flight per thread (a long row read by one
+    // workgroup is bound by the load latency otherwise)
+    for (int64_t c0 = 0; c0 < cols; c0 += 256 * kRadixBatch) {
+        T v[kRadixBatch];
+#pragma unroll
+        for (int u = 0; u < kRadixBatch; ++u) {
+            const int64_t c = c0 + u * 256 + tid;
+            v[u] = (c < cols) ? dr[c] : T(0) / T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < kRadixBatch; ++u) local += (v[u] == v[u]) ? 1u : 0u;
     }
     atomicAdd(&sh.nvalid, local);
     __syncthreads();
@@ -312,11 +323,19 @@ __device__ void row_radix_kth(const T* __restrict__ dr, int64_t cols, uint32_t k
     for (int shift = KeyOf<T>::BITS - 8; shift >= 0; shift -= 8) {
         sh.hist[tid] = 0;
         __syncthreads();
-        for (int64_t c = tid; c < cols; c += 256) {
-            const T v = dr[c];
-            if (v != v) continue;
-            const K key = KeyOf<T>::key(v);
-            if ((key & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)(key >> shift) & 255u], 1u);
+        for (int64_t c0 = 0; c0 < cols; c0 += 256 * kRadixBatch) {
+            T v[kRadixBatch];
+#pragma unroll
+            for (int u = 0; u < kRadixBatch; ++u) {
+                const int64_t c = c0 + u * 256 + tid;
+                v[u] = (c < cols) ? dr[c] : T(0) / T(0);  // past the row: NaN, never counted
+            }
+#pragma unroll
+            for (int u = 0; u < kRadixBatch; ++u) {
+                if (v[u] != v[u]) continue;
+                const K key = KeyOf<T>::key(v[u]);
+                if ((key & pmask) == prefix) atomicAdd(&sh.hist[(uint32_t)(key >> shift) & 255u], 1u);
+            }
         }
         __syncthreads();
         if (tid == 0) {
@@ -353,44 +372,56 @@ __device__ void row_collect(const T* __restrict__ dr, int64_t cols, uint32_t kk,
         sh.cnt_eq = 0;
     }
     __syncthreads();
-    for (int64_t base = 0; base < cols; base += 256) {
-        const int64_t c = base + tid;
-        bool is_less = false, is_eq = false;
-        K key = 0;
-        if (c < cols) {
-            const T v = dr[c];
-            if (v == v) {
-                key = KeyOf<T>::key(v);
-                is_less = key < prefix;
-                is_eq = key == prefix;
+    // kRadixBatch chunks' values loaded together, then compacted in order
+    for (int64_t b0 = 0; b0 < cols; b0 += 256 * kRadixBatch) {
+        T vv[kRadixBatch];
+#pragma unroll
+        for (int u = 0; u < kRadixBatch; ++u) {
+            const int64_t c = b0 + (int64_t)u * 256 + tid;
+            vv[u] = (c < cols) ? dr[c] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < kRadixBatch; ++u) {
+            const int64_t base = b0 + (int64_t)u * 256;
+            if (base >= cols) break;  // uniform
+            const int64_t c = base + tid;
+            bool is_less = false, is_eq = false;
+            K key = 0;
+            if (c < cols) {
+                const T v = vv[u];
+                if (v == v) {
+                    key = KeyOf<T>::key(v);
+                    is_less = key < prefix;
+                    is_eq = key == prefix;
+                }
             }
+            const uint64_t bl = __builtin_amdgcn_ballot_w64(is_less);
+            const uint64_t be = __builtin_amdgcn_ballot_w64(is_eq);
+            if (lane == 0) {
+                sh.wave_less[wv] = (uint32_t)__builtin_popcountll(bl);
+                sh.wave_eq[wv] = (uint32_t)__builtin_popcountll(be);
+            }
+            __syncthreads();
+            uint32_t before_l = sh.cnt_less, before_e = sh.cnt_eq;
+            for (int w2 = 0; w2 < wv; ++w2) {
+                before_l += sh.wave_less[w2];
+                before_e += sh.wave_eq[w2];
+            }
+            if (is_less) {
+                const uint32_t r = before_l + (uint32_t)__builtin_popcountll(bl & below);
+                if (r < n_less) put(r, key, (uint32_t)c);  // always true: kk - want keys lie below prefix
+            }
+            if (is_eq) {
+                const uint32_t r = before_e + (uint32_t)__builtin_popcountll(be & below);
+                if (r < want) put(n_less + r, key, (uint32_t)c);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                sh.cnt_less += sh.wave_less[0] + sh.wave_less[1] + sh.wave_less[2] + sh.wave_less[3];
+                sh.cnt_eq += sh.wave_eq[0] + sh.wave_eq[1] + sh.wave_eq[2] + sh.wave_eq[3];
+            }
+            __syncthreads();
         }
-        const uint64_t bl = __builtin_amdgcn_ballot_w64(is_less);
-        const uint64_t be = __builtin_amdgcn_ballot_w64(is_eq);
-        if (lane == 0) {
-            sh.wave_less[wv] = (uint32_t)__builtin_popcountll(bl);
-            sh.wave_eq[wv] = (uint32_t)__builtin_popcountll(be);
-        }
-        __syncthreads();
-        uint32_t before_l = sh.cnt_less, before_e = sh.cnt_eq;
-        for (int w2 = 0; w2 < wv; ++w2) {
-            before_l += sh.wave_less[w2];
-            before_e += sh.wave_eq[w2];
-        }
-        if (is_less) {
-            const uint32_t r = before_l + (uint32_t)__builtin_popcountll(bl & below);
-            if (r < n_less) put(r, key, (uint32_t)c);  // always true: kk - want keys lie below prefix
-        }
-        if (is_eq) {
-            const uint32_t r = before_e + (uint32_t)__builtin_popcountll(be & below);
-            if (r < want) put(n_less + r, key, (uint32_t)c);
-        }
-        __syncthreads();
-        if (tid == 0) {
-            sh.cnt_less += sh.wave_less[0] + sh.wave_less[1] + sh.wave_less[2] + sh.wave_less[3];
-            sh.cnt_eq += sh.wave_eq[0] + sh.wave_eq[1] + sh.wave_eq[2] + sh.wave_eq[3];
-        }
-        __syncthreads();
     }
 }
 
