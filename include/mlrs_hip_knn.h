@@ -450,8 +450,8 @@ int32_t mlrs_timing_read(double *total_ms, int64_t *launches, char *kernel_name,
  * Kernel-family override (no counterpart in the reference; for tests and
  * benchmarks).  Every family returns the same bits, so this only changes
  * speed: 0 = automatic choice (default); 1 = the fused Gram-MFMA kernels
- * wherever they serve the shape (f32: d <= 256, k <= 128, the knn_host
- * cosine arm only at d > 128; f64: d <= 256, k <= 64; k-means: d <= 256);
+ * wherever they serve the shape (d <= 256, k <= 128; the f32 knn_host
+ * cosine arm only at d > 128; k-means: d <= 256);
  * 2 = the
  * low-d ALU kernel wherever it serves the shape (f32 Euclidean, d <= 16,
  * k <= 32); 3 = the generic exact-tile path.  A family that does not serve

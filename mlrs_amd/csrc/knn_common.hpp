@@ -416,13 +416,21 @@ __device__ __forceinline__ uint32_t list_hi_at(const unsigned long long (&lv)[NB
     return bcast_u(v, pos & 63);
 }
 
-// The same block merge on (value, index) pairs (the seed's list).
+// The same block merge on (value, index) pairs (the seeds' lists, the f64
+// kernel's lists); returns the smallest value discarded.  A block whose
+// largest pair is below the carry's smallest is left as it is (a uniform
+// test, NB > 1 only).
 template <typename T, int NB>
-__device__ __forceinline__ void wave_merge_blocks(T (&lv)[NB], uint32_t (&li)[NB], T v, uint32_t ix, int lane) {
+__device__ __forceinline__ T wave_merge_blocks_drop(T (&lv)[NB], uint32_t (&li)[NB], T v, uint32_t ix, int lane) {
     T cv = v;
     uint32_t ci = ix;
 #pragma unroll
     for (int r = 0; r < NB; ++r) {
+        if (NB > 1) {
+            const T cmin = bcast_f(cv, 0), bmax = bcast_f(lv[r], 63);
+            const uint32_t cmi = bcast_u(ci, 0), bmi = bcast_u(li[r], 63);
+            if (pair_less<T>(bmax, bmi, cmin, cmi)) continue;
+        }
         const T rv = reverse_f(cv);
         const uint32_t ri = reverse_u(ci);
         const bool t = pair_less<T>(rv, ri, lv[r], li[r]);
@@ -439,6 +447,27 @@ __device__ __forceinline__ void wave_merge_blocks(T (&lv)[NB], uint32_t (&li)[NB
             for (int m = 32; m > 0; m >>= 1) bitonic_step<T>(cv, ci, lane, m, true);
         }
     }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        const T o = shfl_xor_f(cv, m);
+        cv = (o < cv) ? o : cv;
+    }
+    return cv;
+}
+template <typename T, int NB>
+__device__ __forceinline__ void wave_merge_blocks(T (&lv)[NB], uint32_t (&li)[NB], T v, uint32_t ix, int lane) {
+    (void)wave_merge_blocks_drop<T, NB>(lv, li, v, ix, lane);
+}
+
+// Value of list element `pos` (wave-uniform pos), from its block.
+template <typename T, int NB>
+__device__ __forceinline__ T list_value_at(const T (&lv)[NB], int pos) {
+    const int b = pos >> 6;
+    T v = lv[0];
+#pragma unroll
+    for (int r = 1; r < NB; ++r)
+        if (b == r) v = lv[r];
+    return bcast_f(v, pos & 63);
 }
 
 // A 16-byte load through the global address space.  A pointer the compiler

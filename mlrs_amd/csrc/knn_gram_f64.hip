@@ -1,7 +1,7 @@
 // Fused f64 Gram-MFMA kNN with exact rescoring (gfx950).
 //
 // The f64 counterpart of knn_gram_f32.hip: serves every cpu arm
-// (direct / metric / knn_host, Euclidean and cosine) for d <= 256, k <= 64,
+// (direct / metric / knn_host, Euclidean and cosine) for d <= 256, k <= 128,
 // replacing the materialized-matrix paths tiled_distance_topk /
 // tiled_metric_distance_topk (crates/mlrs-algos/src/neighbors/nearest.rs:
 // 1058-1512) and the host scan of knn_host_topk (crates/mlrs-backend/src/
@@ -34,7 +34,7 @@ constexpr int kWaves = 4;
 constexpr int kQpw = 16;               // queries per wave (MFMA N dimension)
 constexpr int kQpb = kWaves * kQpw;    // queries per workgroup
 constexpr int kBn = 16;                // index rows per tile (MFMA M dimension)
-constexpr int kKcap = 64;              // largest k kept
+constexpr int kKcap = 128;             // largest k kept
 constexpr int kQcap = 48;              // queued candidates per query (two workgroups still fit a CU's LDS)
 constexpr int kFlushAt = kQcap - kBn;  // flush when a queue may overflow on the next tile
 constexpr int kShareEvery = 32;        // tiles between reads of the shared bound
@@ -117,7 +117,9 @@ __device__ __forceinline__ double exact_f64(const double* __restrict__ q, const 
     return acc;
 }
 
-template <int NS, int ARM, bool COS, bool VEC2>
+// KL: 64-entry blocks of a (segment, query) list during a flush (1 for
+// k <= 64, 3 for k <= 128: k + 32 entries).
+template <int NS, int ARM, bool COS, bool VEC2, int KL>
 __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     constexpr int DP = 4 * NS;             // padded feature count
     constexpr int STRIDE = DP + 2;         // LDS row stride (doubles): rows 16 bytes apart in the banks
@@ -205,9 +207,13 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     }
     for (int j = 0; j < kQpw; ++j) {
         const int64_t qg = qwave + j;
-        if (qg < nq && lane < K2) {
-            LV[qg * K2 + lane] = inf;
-            LI[qg * K2 + lane] = kSentinelIdx;
+#pragma unroll
+        for (int r = 0; r < KL; ++r) {
+            const int p = 64 * r + lane;
+            if (qg < nq && p < K2) {
+                LV[qg * K2 + p] = inf;
+                LI[qg * K2 + p] = kSentinelIdx;
+            }
         }
     }
     if (SHARED_R && lane < kQpw && qvalid) {
@@ -293,8 +299,13 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
         const int64_t qg_ = qwave + j_;                                                      \
         const uint32_t n_ = bcast_u(cntr, j_);                                                \
         const bool exact_ = L.mode[j_] != 0u;                                                \
-        double lv_ = (lane < K2) ? LV[qg_ * K2 + lane] : inf;                                \
-        uint32_t li_ = (lane < K2) ? LI[qg_ * K2 + lane] : kSentinelIdx;                     \
+        double lv_[KL];                                                                      \
+        uint32_t li_[KL];                                                                    \
+        _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) {                                  \
+            const int p_ = 64 * r_ + lane;                                                   \
+            lv_[r_] = (p_ < K2) ? LV[qg_ * K2 + p_] : inf;                                   \
+            li_[r_] = (p_ < K2) ? LI[qg_ * K2 + p_] : kSentinelIdx;                          \
+        }                                                                                    \
         double e_ = inf;                                                                     \
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
@@ -310,14 +321,19 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
             }                                                                                \
         }                                                                                    \
         wave_sort64<double>(e_, t_, lane);                                                   \
-        const uint32_t oi_ = li_;                                                            \
-        const double dm_ = wave_merge64_drop<double>(lv_, li_, e_, t_, lane);                \
-        double R_ = bcast_f(lv_, k - 1);                                                      \
+        const uint32_t oi_ = li_[0];                                                         \
+        double dm_;                                                                          \
+        if constexpr (KL == 1)                                                               \
+            dm_ = wave_merge64_drop<double>(lv_[0], li_[0], e_, t_, lane);                   \
+        else                                                                                 \
+            dm_ = wave_merge_blocks_drop<double, KL>(lv_, li_, e_, t_, lane);                \
+        double R_ = list_value_at<double, KL>(lv_, k - 1);                                   \
         if (!exact_) {                                                                       \
-            const double dr_ = (K2 < 64) ? bcast_f(lv_, K2) : dm_;                            \
+            const double dr_ = (K2 < 64 * KL) ? list_value_at<double, KL>(lv_, K2) : dm_;    \
             double w_ = R_ + 2.0 * L.eps[j_];                                                \
             w_ += __builtin_fabs(w_) * 0x1p-40;                                              \
             if (dr_ < inf && dr_ <= w_) {                                                    \
+              if constexpr (KL == 1) {                                                       \
                 double x1_ = inf, x2_ = inf;                                                 \
                 uint32_t i1_ = oi_, i2_ = t_;                                                \
                 if (i1_ != kSentinelIdx) x1_ = MLRS_EXACT64_AT(i1_);                         \
@@ -327,17 +343,41 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
                 wave_sort64<double>(x1_, i1_, lane);                                         \
                 wave_sort64<double>(x2_, i2_, lane);                                         \
                 wave_merge64<double>(x1_, i1_, x2_, i2_, lane);                              \
-                lv_ = x1_;                                                                   \
-                li_ = i1_;                                                                   \
-                R_ = bcast_f(lv_, k - 1);                                                     \
+                lv_[0] = x1_;                                                                \
+                li_[0] = i1_;                                                                \
+              } else {                                                                       \
+                /* the old list (still in memory) and the queue, exactly */                  \
+                _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) {                          \
+                    lv_[r_] = inf;                                                           \
+                    li_[r_] = kSentinelIdx;                                                  \
+                }                                                                            \
+                _Pragma("unroll") for (int r_ = 0; r_ <= KL; ++r_) {                         \
+                    uint32_t i_ = kSentinelIdx;                                              \
+                    if (r_ < KL) {                                                           \
+                        const int p_ = 64 * r_ + lane;                                       \
+                        if (p_ < K2) i_ = LI[qg_ * K2 + p_];                                 \
+                    } else if ((uint32_t)lane < n_) {                                        \
+                        i_ = L.qidx[j_][lane];                                               \
+                    }                                                                        \
+                    double x_ = inf;                                                         \
+                    if (i_ != kSentinelIdx) x_ = MLRS_EXACT64_AT(i_);                        \
+                    if (x_ != x_) { x_ = inf; i_ = kSentinelIdx; }                           \
+                    wave_sort64<double>(x_, i_, lane);                                       \
+                    wave_merge_blocks<double, KL>(lv_, li_, x_, i_, lane);                   \
+                }                                                                            \
+              }                                                                              \
+                R_ = list_value_at<double, KL>(lv_, k - 1);                                  \
                 if (lane == 0) L.mode[j_] = 1u;                                              \
             } else if (R_ < inf) {                                                           \
                 R_ = R_ + L.eps[j_];                                                         \
             }                                                                                \
         }                                                                                    \
-        if (lane < K2) {                                                                     \
-            LV[qg_ * K2 + lane] = lv_;                                                       \
-            LI[qg_ * K2 + lane] = li_;                                                       \
+        _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) {                                  \
+            const int p_ = 64 * r_ + lane;                                                   \
+            if (p_ < K2) {                                                                   \
+                LV[qg_ * K2 + p_] = lv_[r_];                                                 \
+                LI[qg_ * K2 + p_] = li_[r_];                                                 \
+            }                                                                                \
         }                                                                                    \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf && R_ >= 0.0) {                                         \
@@ -638,16 +678,124 @@ __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
     }
 }
 
+// 64 < k <= 128: the same merge over lists of up to three 64-entry blocks
+// (k + 32 entries); the union and the result are two-block lists (the k
+// smallest fit in 128 entries), merged block by block.  k-means assignment
+// (k = 1) never comes here, so the output transform is the root or identity.
+template <int ARM, bool VEC2>
+__global__ __launch_bounds__(256) void knn_merge_blocks_f64_kernel(GramArgs64 a) {
+    constexpr int SLB = 3;  // blocks of a segment list
+    constexpr int UB = 2;   // blocks of the union and of the result
+    __shared__ uint32_t cand[4][128];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + wv;
+    if (qg >= a.nq) return;
+    const int k = a.k;
+    const int K2 = gram_list_cap(k);
+    const int64_t d = a.d;
+    const double inf = __builtin_huge_val();
+    const StreamSplit sp(a.nq, a.nt, kQpb, kBn, a.grid_wgs);
+    const int64_t nsl = sp.slots_of(qg / kQpb);
+    double uv[UB];
+    uint32_t ui[UB];
+#pragma unroll
+    for (int r = 0; r < UB; ++r) {
+        uv[r] = inf;
+        ui[r] = kSentinelIdx;
+    }
+    for (int64_t s = 0; s < nsl; ++s) {
+#pragma unroll
+        for (int r = 0; r < SLB; ++r) {
+            if (64 * r >= K2) break;
+            const int p = 64 * r + lane;
+            double v = inf;
+            uint32_t ix = kSentinelIdx;
+            if (p < K2) {
+                const int64_t o = (s * a.nq + qg) * K2 + p;
+                v = a.part_val[o];
+                ix = a.part_idx[o];
+            }
+            wave_merge_blocks<double, UB>(uv, ui, v, ix, lane);
+        }
+    }
+    const double qsq = a.qsq[qg];
+    const bool cos = (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST);
+    const double eps = cos ? a.eps_abs : a.eps_rel * (qsq + a.stats->xsq_max64) + a.eps_abs;
+    double W = list_value_at<double, UB>(uv, k - 1) + 2.0 * eps;
+    W += __builtin_fabs(W) * 0x1p-40;
+    const double qa = (ARM == ARM_COS_HOST) ? a.qinv[qg] : qsq;
+    double lv[UB];
+    uint32_t li[UB];
+#pragma unroll
+    for (int r = 0; r < UB; ++r) {
+        lv[r] = inf;
+        li[r] = kSentinelIdx;
+    }
+    uint32_t nc = 0;
+    auto evaluate = [&](uint32_t count) {
+        double e = inf;
+        uint32_t t = kSentinelIdx;
+        if ((uint32_t)lane < count) {
+            t = cand[wv][lane];
+            const double ya = (ARM == ARM_COS_FOLD) ? a.xsq[t] : (ARM == ARM_COS_HOST) ? a.xinv[t] : 0.0;
+            e = exact_f64<ARM, VEC2, 8>(a.q + qg * d, a.x + (int64_t)t * d, d, qa, ya);
+            if (e != e) {
+                e = inf;
+                t = kSentinelIdx;
+            }
+        }
+        wave_sort64<double>(e, t, lane);
+        wave_merge_blocks<double, UB>(lv, li, e, t, lane);
+    };
+    for (int64_t s = 0; s < nsl; ++s) {
+        for (int r = 0; r < SLB; ++r) {
+            if (64 * r >= K2) break;
+            const int p = 64 * r + lane;
+            bool in = false;
+            uint32_t ix = kSentinelIdx;
+            if (p < K2) {
+                const int64_t o = (s * a.nq + qg) * K2 + p;
+                ix = a.part_idx[o];
+                in = (ix != kSentinelIdx) && !(a.part_val[o] > W);
+            }
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(in);
+            const uint32_t pre = (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull));
+            if (in) cand[wv][nc + pre] = ix;
+            nc += (uint32_t)__builtin_popcountll(bal);
+            if (nc >= 64) {
+                evaluate(64);
+                const uint32_t rest = nc - 64;
+                const uint32_t mv = ((uint32_t)lane < rest) ? cand[wv][64 + lane] : 0u;
+                if ((uint32_t)lane < rest) cand[wv][lane] = mv;
+                nc = rest;
+            }
+        }
+    }
+    if (nc > 0) evaluate(nc);
+#pragma unroll
+    for (int r = 0; r < UB; ++r) {
+        const int slot = 64 * r + lane;
+        if (slot < k) {
+            const int64_t o = qg * k + slot;
+            a.out_val[o] = (a.mode == EMIT_SQRT) ? __builtin_sqrt(lv[r]) : lv[r];
+            a.out_idx[o] = (li[r] == kSentinelIdx) ? 0u : li[r];
+        }
+    }
+}
+
 // Initial per-query bound: the k-th smallest exact value over an evenly
 // spaced sample of index rows (seed_kth_block): any k distinct rows bound the
 // final k-th value from above, so each segment's screen starts tight instead
 // of at +inf.
 constexpr int64_t kSeedRows64 = 512;
-template <int ARM>
+// SB: 64-entry blocks of the running sample list (k <= 64 SB).
+template <int ARM, int SB>
 __global__ __launch_bounds__(256) void knn_seed_f64_kernel(GramArgs64 a, int64_t nsamp) {
     const double* qop = (ARM == ARM_COS_FOLD) ? a.qsq : a.qinv;
     const double* yop = (ARM == ARM_COS_FOLD) ? a.xsq : a.xinv;
-    seed_kth_block<double, ARM>(a.q, a.x, a.nq, a.nt, a.d, a.k, nsamp, qop, yop, a.shared_r);
+    seed_kth_block<double, ARM, unsigned long long, SB>(a.q, a.x, a.nq, a.nt, a.d, a.k, nsamp, qop, yop,
+                                                        a.shared_r);
 }
 
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
@@ -658,10 +806,17 @@ __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long 
 template <int NS, int ARM, bool COS>
 hipError_t launch_ns(const GramArgs64& a, bool vec2, hipStream_t s) {
     dim3 grid((unsigned)StreamSplit(a.nq, a.nt, kQpb, kBn, a.grid_wgs).G);
-    if (vec2)
-        hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, true>), grid, dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, false>), grid, dim3(256), 0, s, a);
+    if (a.k <= 64) {
+        if (vec2)
+            hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, true, 1>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, false, 1>), grid, dim3(256), 0, s, a);
+    } else {
+        if (vec2)
+            hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, true, 3>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((knn_gram_f64_kernel<NS, ARM, COS, false, 3>), grid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -693,8 +848,11 @@ int gram_f64_max_d() { return kMaxD; }
 
 template <int ARM>
 hipError_t launch_seed64(const GramArgs64& a, int64_t nsamp, hipStream_t s) {
-    hipLaunchKernelGGL((knn_seed_f64_kernel<ARM>), dim3((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb)), dim3(256), 0,
-                       s, a, nsamp);
+    const dim3 grid((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb));
+    if (a.k <= 64)
+        hipLaunchKernelGGL((knn_seed_f64_kernel<ARM, 1>), grid, dim3(256), 0, s, a, nsamp);
+    else
+        hipLaunchKernelGGL((knn_seed_f64_kernel<ARM, 2>), grid, dim3(256), 0, s, a, nsamp);
     return hipGetLastError();
 }
 
@@ -726,10 +884,16 @@ hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s) {
 template <int ARM>
 hipError_t launch_merge64(const GramArgs64& a, bool vec2, hipStream_t s) {
     const dim3 grid((unsigned)((a.nq + 3) / 4));
-    if (vec2)
+    if (a.k > 64) {
+        if (vec2)
+            hipLaunchKernelGGL((knn_merge_blocks_f64_kernel<ARM, true>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((knn_merge_blocks_f64_kernel<ARM, false>), grid, dim3(256), 0, s, a);
+    } else if (vec2) {
         hipLaunchKernelGGL((knn_merge_f64_kernel<ARM, true>), grid, dim3(256), 0, s, a);
-    else
+    } else {
         hipLaunchKernelGGL((knn_merge_f64_kernel<ARM, false>), grid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 

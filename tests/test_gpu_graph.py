@@ -40,7 +40,7 @@ def _check(got_i, got_d, want_i, want_d, metric):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("metric,p", METRICS)
-@pytest.mark.parametrize("shape", [(1500, 8, 15), (700, 40, 5), (400, 300, 33)])
+@pytest.mark.parametrize("shape", [(1500, 8, 15), (700, 40, 5), (400, 300, 33), (3000, 24, 100)])
 @pytest.mark.parametrize("include_self", [False, True])
 def test_graph_matches_oracle(family, dtype, metric, p, shape, include_self):
     n, d, k = shape

@@ -97,12 +97,14 @@ def test_f32_cosine_bitwise(case):
     check_knn(xq, xt, k, "cosine", str(case))
 
 
-# f64: Gram-MFMA path for d <= 256, k <= 64 (direct, metric and knn_host arms),
-# generic exact path beyond
+# f64: Gram-MFMA path for d <= 256, k <= 128 (direct, metric and knn_host arms;
+# 64 < k <= 128 with lists in three 64-entry blocks), generic exact path beyond
 F64 = [((100, 2000, 64, 10), "euclidean"), ((50, 1000, 3, 8), "euclidean"), ((64, 2000, 256, 16), "cosine"),
        ((40, 700, 20, 5), "cosine"), ((300, 30000, 256, 16), "cosine"), ((200, 5000, 200, 12), "euclidean"),
        ((77, 3000, 129, 64), "euclidean"), ((65, 2500, 33, 1), "cosine"), ((129, 4000, 128, 40), "cosine"),
-       ((10, 400, 300, 7), "euclidean"), ((33, 900, 255, 3), "cosine"), ((1, 17, 17, 17), "euclidean")]
+       ((10, 400, 300, 7), "euclidean"), ((33, 900, 255, 3), "cosine"), ((1, 17, 17, 17), "euclidean"),
+       ((100, 5000, 64, 100), "euclidean"), ((64, 4000, 256, 128), "cosine"), ((50, 3000, 200, 65), "euclidean"),
+       ((30, 2000, 129, 127), "cosine"), ((300, 30000, 256, 96), "cosine"), ((40, 6000, 24, 128), "cosine")]
 
 
 @pytest.mark.parametrize("case,metric", F64)
@@ -202,7 +204,8 @@ def test_cosine_host_arm_nan_rows():
 
 
 @pytest.mark.parametrize("d", [5, 200])
-def test_f64_nan_zero_rows_and_ties(d):
+@pytest.mark.parametrize("k", [24, 110])
+def test_f64_nan_zero_rows_and_ties(d, k):
     rng = np.random.default_rng(15 + d)
     xt = rng.integers(-2, 3, size=(3000, d)).astype(np.float64)
     xq = rng.integers(-2, 3, size=(150, d)).astype(np.float64)
@@ -212,8 +215,8 @@ def test_f64_nan_zero_rows_and_ties(d):
     xq[5] = np.nan
     xt[100:140] = xt[3]                   # duplicates around the k-th slot
     xq[10] = xt[3]
-    check_knn(xq, xt, 24, "euclidean", "f64 ties/nan")
-    check_knn(xq, xt, 24, "cosine", "f64 cosine ties/nan/zero")
+    check_knn(xq, xt, k, "euclidean", "f64 ties/nan")
+    check_knn(xq, xt, k, "cosine", "f64 cosine ties/nan/zero")
 
 
 def test_f64_nonaligned_pointer():
