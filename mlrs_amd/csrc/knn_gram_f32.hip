@@ -11,9 +11,12 @@
 // strip of index rows 32 at a time.
 //  * Each wave keeps its query rows in VGPRs as the B operand (pre-scaled by
 //    -2 for Euclidean), loaded once per segment.
-//  * The 32-row index tile is staged in LDS (narrow: row stride d_pad+4
-//    floats, rows 4 banks apart; wide: 16-byte chunks XOR-swizzled by row),
-//    double-buffered and prefetched into registers one tile ahead.
+//  * The 32-row index tile is staged in LDS (row stride d_pad + 4 floats, so
+//    16 consecutive rows fall on distinct bank groups; rows of 128 floats in
+//    pairs that share one 1 KB slot), double-buffered in two distinct LDS
+//    objects.  Aligned rows of at least 64 floats are loaded one tile ahead
+//    straight from global memory into LDS (global_load_lds_dwordx4); other
+//    shapes, and k = 1, prefetch into registers.
 //  * Euclidean: the accumulator starts at ||x_t||^2, so after the contraction
 //    acc = ||x_t||^2 - 2 x_t.q_j, the expansion minus the per-query constant.
 //    Cosine: the contraction is scaled by -1/||x_t|| per row afterwards,
@@ -28,9 +31,10 @@
 //    smallest expansion value.
 //  * For k > 1 the per-query bound starts from a seed launch: the k-th
 //    smallest exact value over 512 evenly spaced index rows.
-//  * Passing (query, row) pairs are queued in LDS (queue lengths live in
-//    registers; the lanes screening a query append with a popcount prefix,
-//    no atomics); their screen values wait in a per-wave global array.
+//  * Passing (query, row) pairs are queued in a per-wave global array (index
+//    rows and screen values; queue lengths live in registers; the lanes
+//    screening a query append with a popcount prefix, no atomics), which
+//    leaves the LDS small enough for three workgroups per CU at d <= 128.
 //    Before a queue could overflow, the wave sorts it and merges it into the
 //    query's list for this segment (global memory, one per query and
 //    segment): a queued pair enters with its screen value mapped back to a
@@ -38,7 +42,8 @@
 //    the k + 32 (at most 64) smallest.  No pair is evaluated exactly during
 //    the scan, except in the rare lists that turn exact (a dropped pair
 //    inside the 2 eps window of the k-th, NaN screen values, norms that could
-//    overflow).  k = 1 keeps one exact (value, index) pair per query in LDS.
+//    overflow).  k = 1 queues index rows in LDS and keeps one exact
+//    (value, index) pair per query there.
 //  * The merge kernel takes each query's lists from all segments, finds the
 //    k-th value V of their union and evaluates EXACTLY, in the reference
 //    arm's operation order, every listed pair whose screen value is within
@@ -83,11 +88,16 @@ struct GramShape {
 };
 constexpr int kQpbNarrow = GramShape<false>::qpb;
 constexpr int kQpbWide = GramShape<true>::qpb;
-constexpr int kQvalPerWave = 32 * 64;             // screen values a wave may queue (either shape)
+constexpr int kQvalPerWave = 32 * 64;             // pairs a wave may queue (either shape), k > 1
+// Per wave in a.qval: kQvalPerWave screen values, then their kQvalPerWave
+// index-row numbers, both [queue position][query].
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Per-wave LDS state.  Only k = 1 queues its candidates' indices here (QCAP
+// per query); k > 1 queues them in global memory beside their screen values,
+// which leaves room for a third workgroup per CU.
 template <int QCAP, int QPW>
 struct WaveLds {
     uint32_t qidx[QPW][QCAP];
@@ -243,38 +253,62 @@ __device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q,
     out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
 }
 
-// k = 1 with d <= 64 fits three workgroups per CU (168 VGPRs, ~46 KB LDS):
-// the short segments of an assignment (one per query block) overlap better.
-template <int NG, bool K1>
+// Workgroups per CU.  Three (at most 168 VGPRs, 53 KB LDS) wherever they
+// fit: k = 1 with d <= 64 (its LDS queues allow no more), and the narrow
+// shape (d <= 128) with k <= 64, whose queues live in global memory.  A
+// third wave per SIMD keeps the matrix core fed while the other two wait at
+// a tile barrier or merge a queue into a list.
+__host__ __device__ constexpr int gram_f32_wgs_per_cu(int ng, bool k1, int kl) {
+    return (k1 && ng <= 8) || (!k1 && ng <= 16 && kl == 1) ? 3 : 2;
+}
+template <int NG, bool K1, int KL>
 struct GramOcc {
-    static constexpr int wgs = (K1 && NG <= 8) ? 3 : 2;
+    static constexpr int wgs = gram_f32_wgs_per_cu(NG, K1, KL);
 };
 
 // KL: 64-entry blocks of a (segment, query) list in registers during a flush
 // (1 for k <= 64, 3 for k <= 128: k + 32 entries).
 template <int NG, int ARM, bool COS, bool VEC4, bool K1, int KL>
-__global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kernel(GramArgs32 a) {
+__global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_kernel(GramArgs32 a) {
     constexpr bool W16 = NG > 16;     // the wide shape (GramShape)
     typedef GramShape<W16> SH;
     constexpr int QPW = SH::qpw;
     constexpr int QPB = SH::qpb;
     constexpr int DP = NG * 8;        // padded feature count
-    // LDS row stride (floats).  Narrow: rows 4 banks apart, so the A-operand
-    // ds_read_b128 of 16 consecutive rows do not conflict.  Wide: no padding
-    // (two 64 KB tiles must leave room for a second workgroup); instead each
-    // row's 16-byte chunks are XOR-swizzled by the row's low four bits, with
-    // the same effect (DP is a multiple of 64 there, so chunks stay in their row).
-    constexpr int STRIDE = W16 ? DP : DP + 4;
+    constexpr int CPR = DP / 4;       // 16-byte chunks per tile row
+    // LDS row stride (floats): DP + 4, an odd number of 16-byte chunks, so
+    // the A-operand ds_read_b128 of 16 consecutive rows (one chunk column)
+    // hit 16 distinct groups of four banks.  Narrow rows of 128 floats are
+    // kept in pairs instead: slot s (0..15) holds rows s and s + 16 back to
+    // back (1 KB, one wave-wide direct load) and slots are 2 DP + 4 floats
+    // apart, so rows 0..15 (and 16..31) still fall on distinct bank groups.
+    constexpr int STRIDE = DP + 4;
+    constexpr bool PAIRS = !W16 && NG == 16;
+    constexpr int SLOT = 2 * DP + 4;
+    constexpr int TILE_FL = PAIRS ? 16 * SLOT : kBn * STRIDE;
     constexpr int TILE_F4 = kBn * DP / 4;
     constexpr int PF = (TILE_F4 + 255) / 256;
+    // 16-byte aligned rows of at least 64 floats go from global memory
+    // straight into LDS (gfx950's global_load_lds_dwordx4, one instruction per
+    // row, or per slot of two rows, with the first CPR (2 CPR) lanes active:
+    // lane i's 16 bytes land 16 i bytes after the row start), so no registers
+    // hold the next tile in flight and no ds_write stores it; other shapes
+    // stage it through registers.  The k = 1 kernel (short segments, three
+    // workgroups per CU already) runs faster staged.
+    constexpr bool DIRECT = VEC4 && NG >= 8 && !K1;
+    constexpr int RPW = kBn / kWaves;  // tile rows each wave fills (direct)
     constexpr int QQ = DP / 4;        // wide: features per lane-group quarter
     constexpr int NQR = W16 ? QQ / 4 : NG;  // 16-byte query-operand chunks per lane
 
-    __shared__ __attribute__((aligned(16))) float tile[2][kBn][STRIDE];
-    __shared__ __attribute__((aligned(16))) float tnorm[2][kBn];
+    // The two tile buffers are distinct objects, so the compiler can tell the
+    // direct loads into one from the reads of the other.
+    __shared__ __attribute__((aligned(16))) float tileA[TILE_FL];
+    __shared__ __attribute__((aligned(16))) float tileB[TILE_FL];
+    __shared__ __attribute__((aligned(16))) float tnA[kBn];
+    __shared__ __attribute__((aligned(16))) float tnB[kBn];
     constexpr int QCAP = K1 ? kQcapK1 : SH::qcap;
     constexpr int kFlushAt = QCAP - kBn;  // flush when a queue may overflow next tile
-    __shared__ WaveLds<QCAP, QPW> wl[kWaves];
+    __shared__ WaveLds<K1 ? QCAP : 1, QPW> wl[kWaves];
 
     // Kernel arguments as locals: they stay in SGPRs.
     const float* __restrict__ Q = a.q;
@@ -288,23 +322,37 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
     const int K2 = gram_list_cap(k);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     // narrow: h = lane / 32 picks the 4-row group of each 8-row slab;
     // wide: g = lane / 16 picks the 4-row group of each 16-row half and the
     // feature quarter.  jl: the lane's query within the wave.
     const int h = W16 ? (lane >> 4) : (lane >> 5);
     const int jl = lane & (QPW - 1);
-    WaveLds<QCAP, QPW>& L = wl[w];
+    WaveLds<K1 ? QCAP : 1, QPW>& L = wl[w];
     const float inf = __builtin_huge_valf();
-    // screen values of this wave's queued pairs, [queue position][query]
-    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * kQvalPerWave;
+    // screen values and index rows of this wave's queued pairs (k > 1),
+    // [queue position][query]
+    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * (2 * kQvalPerWave);
+    uint32_t* __restrict__ QIw = K1 ? nullptr : reinterpret_cast<uint32_t*>(QVw + kQvalPerWave);
 
     // Tile row of value r of this lane.
     auto row_of = [&](int r) -> int {
         return W16 ? 16 * (r >> 2) + 4 * h + (r & 3) : 8 * (r >> 2) + 4 * h + (r & 3);
     };
     // LDS float offset of 16-byte chunk c of tile row r.
-    auto chunk_at = [&](int r, int c) -> int { return r * STRIDE + 4 * (W16 ? (c ^ (r & 15)) : c); };
+    auto row_at = [&](int r) -> int { return PAIRS ? (r & 15) * SLOT + (r >> 4) * DP : r * STRIDE; };
+    auto chunk_at = [&](int r, int c) -> int { return row_at(r) + 4 * c; };
+
+    // Direct fills never write the columns past d (d < DP): zero them once in
+    // both buffers, as they meet the query operand's zeros and left alone
+    // could hold NaN.
+    if (DIRECT && d < DP) {
+        const int pad = (int)(DP - d);
+        for (int e = tid; e < kBn * pad; e += 256) {
+            tileA[row_at(e / pad) + d + e % pad] = 0.0f;
+            tileB[row_at(e / pad) + d + e % pad] = 0.0f;
+        }
+    }
 
     // ---- work split (StreamSplit): this workgroup's range of (query block,
     //      tile) units, panel-major; each piece of a job in the range is a
@@ -521,7 +569,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
         float e_ = inf;                                                                      \
         uint32_t t_ = kSentinelIdx;                                                          \
         if ((uint32_t)lane < n_) {                                                           \
-            t_ = L.qidx[j_][lane];                                                           \
+            t_ = QIw[lane * QPW + j_];                                                       \
             const float s_ = exact_ ? 0.0f : QVw[lane * QPW + j_];                           \
             if (exact_ || s_ != s_)                                                          \
                 e_ = MLRS_EXACT_AT(t_);                                                      \
@@ -569,7 +617,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
                         const int p_ = 64 * r_ + lane;                                       \
                         if (p_ < K2) i_ = LI[qg_ * K2 + p_];                                 \
                     } else if ((uint32_t)lane < n_) {                                        \
-                        i_ = L.qidx[j_][lane];                                               \
+                        i_ = QIw[lane * QPW + j_];                                           \
                     }                                                                        \
                     float x_ = inf;                                                          \
                     if (i_ != kSentinelIdx) x_ = MLRS_EXACT_AT(i_);                          \
@@ -653,26 +701,86 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
 
     float4 pf[PF];
     float pfn = 0.0f;
-    if (t_begin < t_end) MLRS_PREFETCH(t_begin);
+    // Direct fill of tile T0 into DST: wave w's instruction i fills chunks
+    // 64 (w PF + i) .. + 63 of the contiguous tile; chunk f is position f % CPR
+    // of row f / CPR, which holds the row's column chunk position ^ (row & 15).
+    // Rows past the segment are not loaded (their values are masked out of the
+    // screen); the row norms go through a register as in the staged path.
+    auto direct_load = [&](float (&dst)[TILE_FL], uint32_t t0) {
+        if constexpr (DIRECT && PAIRS) {
+            // slots 4w .. 4w + 3: lane l loads chunk l % 32 of row slot + 16 (l / 32)
+            const int rl = 16 * (lane >> 5);
+            const float* xw = X + (int64_t)(t0 + (uint32_t)(4 * w)) * d + (int64_t)rl * d + 4 * (lane & 31);
+            const int di = (int)d;
+            if (4 * (lane & 31) < di) {
+                if (t0 + (uint32_t)kBn <= t_end32) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (t0 + (uint32_t)(4 * w + i + rl) < t_end32) global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
+                }
+            }
+        } else if constexpr (DIRECT) {
+            // this wave's first row (wave-uniform) + the lane's chunk
+            const float* xw = X + (int64_t)(t0 + (uint32_t)(w * RPW)) * d + 4 * lane;
+            const int di = (int)d;
+            if (lane < CPR && 4 * lane < di) {
+                if (t0 + (uint32_t)kBn <= t_end32) {
+#pragma unroll
+                    for (int i = 0; i < RPW; ++i) global_to_lds16(xw + i * di, &dst[(w * RPW + i) * STRIDE]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < RPW; ++i)
+                        if (t0 + (uint32_t)(w * RPW + i) < t_end32)
+                            global_to_lds16(xw + i * di, &dst[(w * RPW + i) * STRIDE]);
+                }
+            }
+        }
+        if (tid < kBn) {
+            const uint32_t t = t0 + (uint32_t)tid;
+            if (COS)
+                pfn = (t < t_end32) ? XSCALE[t] : 0.0f;
+            else
+                pfn = (t < t_end32) ? XSQ[t] : inf;
+        }
+    };
+    // the tile at T0: into registers (staged) or straight into DST (direct)
+    auto load_tile = [&](float (&dst)[TILE_FL], int64_t t0) {
+        if constexpr (DIRECT)
+            direct_load(dst, (uint32_t)t0);
+        else
+            MLRS_PREFETCH(t0);
+    };
+    if (t_begin < t_end) load_tile(tileA, t_begin);
     __syncthreads();  // per-wave LDS init visible to the wave
 
     float thr = L.thr[jl];
-    int buf = 0;
     int tiles = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, buf ^= 1) {
-        // publish the prefetched tile
+    // One tile: CUR holds (or receives from the staging registers) the rows
+    // at T0, the next tile is loaded towards NXT.
+    auto tile_step = [&](float (&cur)[TILE_FL], float* __restrict__ tncur, float (&nxt)[TILE_FL],
+                         int64_t t0) {
+        // publish the tile: the staged registers are stored into CUR; the
+        // direct loads into CUR are waited for, and the barrier makes every
+        // wave's visible (and ends every wave's reads of NXT)
+        if constexpr (DIRECT) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        } else {
 #pragma unroll
-        for (int p = 0; p < PF; ++p) {
-            const int f = tid + 256 * p;
-            if (f < TILE_F4) {
-                const int r = f / (DP / 4);
-                const int c4 = f % (DP / 4);
-                *reinterpret_cast<float4*>(&tile[buf][0][0] + chunk_at(r, c4)) = pf[p];
+            for (int p = 0; p < PF; ++p) {
+                const int f = tid + 256 * p;
+                if (f < TILE_F4) {
+                    const int r = f / (DP / 4);
+                    const int c4 = f % (DP / 4);
+                    *reinterpret_cast<float4*>(&cur[0] + chunk_at(r, c4)) = pf[p];
+                }
             }
         }
-        if (tid < kBn) tnorm[buf][tid] = pfn;
+        if (tid < kBn) tncur[tid] = pfn;
         __syncthreads();
-        if (t0 + kBn < t_end) MLRS_PREFETCH(t0 + kBn);
+        if (t0 + kBn < t_end) load_tile(nxt, t0 + kBn);
 
         // The lane's tile values: narrow, acc[r] = row row_of(r); wide, r < 4
         // in acc0 (the first 16-row half) and r >= 4 in acc1.
@@ -682,7 +790,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             if (!COS) {
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
-                    float4 n4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                    float4 n4 = *reinterpret_cast<const float4*>(&tncur[8 * g4 + 4 * h]);
                     acc[4 * g4 + 0] = n4.x;
                     acc[4 * g4 + 1] = n4.y;
                     acc[4 * g4 + 2] = n4.z;
@@ -695,7 +803,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             // A operands double-buffered: the next group's LDS read is issued
             // before the current group's four MFMAs (the scheduling barriers keep
             // that order), so its latency hides under ~256 MFMA cycles.
-            const float* arow = &tile[buf][jl][4 * h];
+            const float* arow = &cur[row_at(jl) + 4 * h];
             float4 av = *reinterpret_cast<const float4*>(arow);
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
@@ -715,7 +823,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
                 // next tile's LDS store
 #pragma unroll
                 for (int g4 = 0; g4 < 4; ++g4) {
-                    const float4 s4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                    const float4 s4 = *reinterpret_cast<const float4*>(&tncur[8 * g4 + 4 * h]);
                     acc[4 * g4 + 0] *= s4.x;
                     acc[4 * g4 + 1] *= s4.y;
                     acc[4 * g4 + 2] *= s4.z;
@@ -723,8 +831,8 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
                 }
             }
         } else {
-            const float4 n0 = *reinterpret_cast<const float4*>(&tnorm[buf][4 * h]);
-            const float4 n1 = *reinterpret_cast<const float4*>(&tnorm[buf][16 + 4 * h]);
+            const float4 n0 = *reinterpret_cast<const float4*>(&tncur[4 * h]);
+            const float4 n1 = *reinterpret_cast<const float4*>(&tncur[16 + 4 * h]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 acc0[r] = COS ? 0.0f : (&n0.x)[r];
@@ -733,7 +841,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             // A operands: this lane's rows jl and 16 + jl, its quarter's chunk
             // i, one group ahead; each chunk feeds eight MFMAs (four k-steps
             // on each half).
-            const float* t0p = &tile[buf][0][0];
+            const float* t0p = &cur[0];
             const int c0 = h * (QQ / 4);
             float4 av0 = *reinterpret_cast<const float4*>(t0p + chunk_at(jl, c0));
             float4 av1 = *reinterpret_cast<const float4*>(t0p + chunk_at(16 + jl, c0));
@@ -822,7 +930,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
                 while (m) {
                     const int r = __builtin_ctz(m);
                     m &= m - 1;
-                    L.qidx[jl][pos] = tb + (uint32_t)row_of(r);
+                    QIw[pos * QPW + jl] = tb + (uint32_t)row_of(r);
                     if constexpr (W16) QVw[pos * QPW + jl] = pick8(acc0, acc1, r);
                     else QVw[pos * QPW + jl] = pick16(acc, r);
                     ++pos;
@@ -905,6 +1013,10 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1>::wgs)) void knn_gram_f32_kern
             }
             thr = L.thr[jl];
         }
+    };
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * kBn) {
+        tile_step(tileA, tnA, tileB, t0);
+        if (t0 + kBn < t_end) tile_step(tileB, tnB, tileA, t0 + kBn);
     }
 
     // ---- final flush of every non-empty queue ----
@@ -1210,9 +1322,9 @@ int gram_f32_queries_per_block(int64_t d) { return d > 128 ? kQpbWide : kQpbNarr
 void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots) {
     const int64_t qpb = gram_f32_queries_per_block(d);
     const StreamSplit full(nq, nt, qpb, kBn, 1);
-    // one resident round (two workgroups per CU, three for k = 1 at d <= 64:
-    // GramOcc), but at least 16 tiles each
-    const int per_cu = (k == 1 && d <= 64) ? 3 : 2;
+    // one resident round (gram_f32_wgs_per_cu workgroups per CU), but at
+    // least 16 tiles each
+    const int per_cu = gram_f32_wgs_per_cu((int)((d + 7) / 8), k == 1, k <= 64 ? 1 : 3);
     int64_t g0 = per_cu * (int64_t)(cus > 0 ? cus : 1);
     if (g0 > full.T / 16) g0 = full.T / 16;
     if (g0 < 1) g0 = 1;

@@ -107,7 +107,7 @@ struct GramArgs32 {
     int qpb;           // queries per workgroup: gram_f32_queries_per_block(d)
     float* part_val;   // [nslots][nq][gram_list_cap(k)] lists, one per (segment, query)
     uint32_t* part_idx;
-    float* qval;       // [grid_wgs][4 waves][2048]: screen values of the queued pairs (k > 1)
+    float* qval;       // [grid_wgs][4 waves][2][2048]: screen values, then index rows, of the queued pairs (k > 1)
     float4* summ;      // [nslots][nq]: per-(segment, query) list summaries (k > 1), or null
     float* out_val;    // [nq][k]
     uint32_t* out_idx;
@@ -122,8 +122,9 @@ __host__ __device__ inline int gram_list_cap(int k) {
     return k == 1 ? 1 : k <= 64 ? (k + 32 < 64 ? k + 32 : 64) : k + 32;
 }
 
-// Screen values kept per workgroup while pairs wait in the queues (k > 1).
-inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64; }
+// Screen values (f32: and their index rows) kept per workgroup while pairs
+// wait in the queues (k > 1).
+inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64 * 2; }
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
 // G0, launched workgroups and per-query list slots of the Gram kernel's split.
