@@ -512,7 +512,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
 #define MLRS_PREFETCH(T0)                                                                    \
     do {                                                                                     \
         const uint32_t t0_ = (uint32_t)(T0);                                                 \
-        if (pf_fast && t0_ + (uint32_t)kBn <= t_end32) {                                     \
+        if (pf_fast && t_end32 - t0_ >= (uint32_t)kBn) { /* not t0 + kBn: no wrap */        \
             _Pragma("unroll") for (int p = 0; p < PF; ++p) pf[p] = gload4(MLRS_PF_SRC(p));   \
         } else {                                                                             \
         _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                     \
@@ -654,8 +654,10 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
         }                                                                                    \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf) {                                                      \
-                unsigned int old_ = atomicMin(&SHARED_R[qg_], __float_as_uint(R_));          \
-                R_ = fminf(R_, __uint_as_float(old_));                                       \
+                /* published without waiting for the old value: other segments' */          \
+                /* bounds reach this one at its next refresh */                              \
+                __hip_atomic_fetch_min(&SHARED_R[qg_], __float_as_uint(R_), __ATOMIC_RELAXED,  \
+                                       __HIP_MEMORY_SCOPE_AGENT);                            \
             }                                                                                \
             L.thr[j_] = fminf(L.thr[j_], screen_threshold<COS>(R_, L.qs[j_], L.eps[j_]));    \
         }                                                                                    \
@@ -713,7 +715,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
             const float* xw = X + (int64_t)(t0 + (uint32_t)(4 * w)) * d + (int64_t)rl * d + 4 * (lane & 31);
             const int di = (int)d;
             if (4 * (lane & 31) < di) {
-                if (t0 + (uint32_t)kBn <= t_end32) {
+                if (t_end32 - t0 >= (uint32_t)kBn) {  // whole tile (t0 + kBn could wrap)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
                 } else {
@@ -727,7 +729,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
             const float* xw = X + (int64_t)(t0 + (uint32_t)(w * RPW)) * d + 4 * lane;
             const int di = (int)d;
             if (lane < CPR && 4 * lane < di) {
-                if (t0 + (uint32_t)kBn <= t_end32) {
+                if (t_end32 - t0 >= (uint32_t)kBn) {  // whole tile (t0 + kBn could wrap)
 #pragma unroll
                     for (int i = 0; i < RPW; ++i) global_to_lds16(xw + i * di, &dst[(w * RPW + i) * STRIDE]);
                 } else {
@@ -957,6 +959,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
             thr = L.thr[jl];
         }
         // ---- pick up thresholds tightened by other strips of these queries ----
+        rotate_wave_priority((uint32_t)tiles + 1u, GramOcc<NG, K1, KL>::wgs);
         if (SHARED_R && (++tiles % kShareEvery) == 0) {
             if (lane < QPW && qvalid) {
                 float R = __uint_as_float(SHARED_R[qmine]);

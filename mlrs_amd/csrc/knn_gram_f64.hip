@@ -548,6 +548,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
             }
             thr = L.thr[jl];
         }
+        rotate_wave_priority((uint32_t)tiles + 1u, 2);
         if (SHARED_R && (++tiles % kShareEvery) == 0) {
             if (lane < kQpw && qvalid) {
                 const double R = __longlong_as_double((long long)SHARED_R[qmine]);

@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a
 #define MLRS_RG_PREFETCH(T0)                                                                 \
     do {                                                                                     \
         const uint32_t t0_ = (uint32_t)(T0);                                                 \
-        if (pf_fast && t0_ + (uint32_t)kBn <= t_end32) {                                     \
+        if (pf_fast && t_end32 - t0_ >= (uint32_t)kBn) { /* not t0 + kBn: no wrap */        \
             _Pragma("unroll") for (int p = 0; p < PF; ++p) {                                 \
                 pf[p] = gload4(pf_src[p]);                                                   \
                 pf_src[p] += kBn * d;                                                        \
