@@ -782,7 +782,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
         }
         if (tid < kBn) tncur[tid] = pfn;
         __syncthreads();
-        if (t0 + kBn < t_end) load_tile(nxt, t0 + kBn);
+        if (t_end32 - (uint32_t)t0 > (uint32_t)kBn) load_tile(nxt, t0 + kBn);
 
         // The lane's tile values: narrow, acc[r] = row row_of(r); wide, r < 4
         // in acc0 (the first 16-row half) and r >= 4 in acc1.
@@ -898,7 +898,11 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
 #pragma unroll
         for (int r = 0; r < SH::vals; ++r) m |= (uint32_t)!(val(r) > thr) << r;
         if (!qvalid) m = 0;
-        if (t0 + kBn > t_end) {  // partial tile: rows past the segment are not candidates
+        // Partial tile (the segment's last): rows past the segment are not
+        // candidates.  Rows left are compared in 32 bits, a scalar branch; a
+        // 64-bit ordered compare is a vector instruction, and the compiler
+        // then computed this mask on every tile.
+        if (t_end32 - (uint32_t)t0 < (uint32_t)kBn) {
 #pragma unroll
             for (int r = 0; r < SH::vals; ++r)
                 if ((uint32_t)t0 + (uint32_t)row_of(r) >= t_end32) m &= ~(1u << r);
