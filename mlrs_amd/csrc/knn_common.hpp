@@ -579,9 +579,12 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
     using F = FloatTraits<T>;
     constexpr int CH = 512 / (int)sizeof(T);  // columns per chunk (a power of two)
     constexpr int CH_LOG = sizeof(T) == 4 ? 7 : 6;
-    constexpr int STR = CH + 1;                // LDS row stride: lane l reads row l, no bank conflicts
-    __shared__ T rows[64][STR];
-    __shared__ T qch[kSeedQpb][CH];            // the workgroup's queries, same columns
+    constexpr int V = 16 / (int)sizeof(T);     // elements per 16-byte LDS read
+    // LDS row stride: an odd number of 16-byte chunks, so the 16-byte reads of
+    // 64 lanes (lane l: row l) spread over the banks
+    constexpr int STR = CH + V;
+    __shared__ __attribute__((aligned(16))) T rows[64][STR];
+    __shared__ __attribute__((aligned(16))) T qch[kSeedQpb][CH];  // the workgroup's queries, same columns
     __shared__ uint32_t srow[64];              // the batch's sampled index rows
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -626,24 +629,38 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
                 qch[j][c] = (c < cw) ? Q[qg * d + c0 + c] : T(0);
             }
             __syncthreads();
-#pragma unroll 4
-            for (int c = 0; c < cw; ++c) {
-                const T yv = rows[lane][c];
+            // V columns per step, in ascending order (the arm's operation
+            // order), then the columns left over one at a time
+            auto step = [&](T& acc_j, T qv, T yv) {
+                if (ARM == ARM_EUCLID_FMA) {
+                    const T diff = qv - yv;
+                    acc_j = F::fma_(diff, diff, acc_j);
+                } else if (ARM == ARM_EUCLID_MULADD) {
+                    const T diff = qv - yv;
+                    acc_j = acc_j + diff * diff;
+                } else if (ARM == ARM_COS_FOLD) {
+                    acc_j = F::fma_(qv, yv, acc_j);
+                } else {  // ARM_COS_HOST
+                    acc_j = acc_j + qv * yv;
+                }
+            };
+            const int cfull = cw / V * V;
+#pragma unroll 2
+            for (int c = 0; c < cfull; c += V) {
+                T yv[V];
+                *reinterpret_cast<float4*>(yv) = *reinterpret_cast<const float4*>(&rows[lane][c]);
 #pragma unroll
                 for (int j = 0; j < kSeedQpw; ++j) {
-                    const T qv = qch[w * kSeedQpw + j][c];  // the same address in every lane
-                    if (ARM == ARM_EUCLID_FMA) {
-                        const T diff = qv - yv;
-                        acc[j] = F::fma_(diff, diff, acc[j]);
-                    } else if (ARM == ARM_EUCLID_MULADD) {
-                        const T diff = qv - yv;
-                        acc[j] = acc[j] + diff * diff;
-                    } else if (ARM == ARM_COS_FOLD) {
-                        acc[j] = F::fma_(qv, yv, acc[j]);
-                    } else {  // ARM_COS_HOST
-                        acc[j] = acc[j] + qv * yv;
-                    }
+                    T qv[V];  // the same address in every lane
+                    *reinterpret_cast<float4*>(qv) = *reinterpret_cast<const float4*>(&qch[w * kSeedQpw + j][c]);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) step(acc[j], qv[e], yv[e]);
                 }
+            }
+            for (int c = cfull; c < cw; ++c) {
+                const T yv = rows[lane][c];
+#pragma unroll
+                for (int j = 0; j < kSeedQpw; ++j) step(acc[j], qch[w * kSeedQpw + j][c], yv);
             }
         }
         const T ya = (on && (ARM == ARM_COS_FOLD || ARM == ARM_COS_HOST)) ? yop[t] : T(0);
@@ -662,6 +679,14 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
                 e = inf;
                 tj = kSentinelIdx;
             }
+            // Only the k-th value is kept: a batch with no value below the
+            // list's k-th (+inf until k rows are listed) cannot change it.
+            T kth = lv[j][0];
+#pragma unroll
+            for (int b = 1; b < SB; ++b)
+                if (((k - 1) >> 6) == b) kth = lv[j][b];
+            kth = bcast_f(kth, (k - 1) & 63);
+            if (!__builtin_amdgcn_ballot_w64(e < kth)) continue;
             wave_sort64<T>(e, tj, lane);
             if (SB == 1)
                 wave_merge64<T>(lv[j][0], li[j][0], e, tj, lane);

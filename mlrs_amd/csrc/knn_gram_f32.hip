@@ -30,7 +30,7 @@
 //    too.  For k = 1 the bound is tightened every tile with the tile's
 //    smallest expansion value.
 //  * For k > 1 the per-query bound starts from a seed launch: the k-th
-//    smallest exact value over 512 evenly spaced index rows.
+//    smallest exact value over evenly spaced index rows (gram_seed_rows).
 //  * Passing (query, row) pairs are queued in a per-wave global array (index
 //    rows and screen values; queue lengths live in registers; the lanes
 //    screening a query append with a popcount prefix, no atomics), which
@@ -66,10 +66,6 @@ constexpr int kKcap = 128;               // largest k this kernel keeps
 constexpr int kQcapK1 = 48;              // k = 1: the screen tightens every tile, queues stay short
 constexpr int kShareEvery = 64;          // tiles between reads of the shared thresholds
 constexpr int kSumSlots = 16;            // segment summaries read per refresh (k > 1)
-#ifndef MLRS_SEED_ROWS
-#define MLRS_SEED_ROWS 512
-#endif
-constexpr int64_t kSeedRows = MLRS_SEED_ROWS;  // index rows sampled for the initial bound (k > 1)
 
 // The two register shapes of a wave's block of (row, query) values.
 //  d <= 128 (W16 = false): 32 queries per wave, v_mfma_f32_32x32x2f32 over
@@ -255,11 +251,12 @@ __device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q,
 
 // Workgroups per CU.  Three (at most 168 VGPRs, 53 KB LDS) wherever they
 // fit: k = 1 with d <= 64 (its LDS queues allow no more), and the narrow
-// shape (d <= 128) with k <= 64, whose queues live in global memory.  A
+// shape (d <= 128) with k > 1, whose queues live in global memory (k <= 128:
+// the compiler spills a little of the three-block lists).  A
 // third wave per SIMD keeps the matrix core fed while the other two wait at
 // a tile barrier or merge a queue into a list.
 __host__ __device__ constexpr int gram_f32_wgs_per_cu(int ng, bool k1, int kl) {
-    return (k1 && ng <= 8) || (!k1 && ng <= 16 && kl == 1) ? 3 : 2;
+    return (k1 && ng <= 8) || (!k1 && ng <= 16) ? 3 : 2;
 }
 template <int NG, bool K1, int KL>
 struct GramOcc {
@@ -1326,6 +1323,7 @@ hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
 
 int gram_f32_queries_per_block(int64_t d) { return d > 128 ? kQpbWide : kQpbNarrow; }
 
+
 void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots) {
     const int64_t qpb = gram_f32_queries_per_block(d);
     const StreamSplit full(nq, nt, qpb, kBn, 1);
@@ -1352,8 +1350,8 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    if (a.k > 1 && kSeedRows > 0) {
-        const int64_t nsamp = a.nt < kSeedRows ? a.nt : kSeedRows;
+    if (a.k > 1) {
+        const int64_t nsamp = gram_seed_rows(a.nt, a.k);
         if (arm == ARM_EUCLID_FMA) return launch_seed<ARM_EUCLID_FMA>(a, nsamp, s);
         if (arm == ARM_EUCLID_MULADD) return launch_seed<ARM_EUCLID_MULADD>(a, nsamp, s);
         if (arm == ARM_COS_FOLD) return launch_seed<ARM_COS_FOLD>(a, nsamp, s);

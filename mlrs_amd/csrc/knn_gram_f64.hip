@@ -789,7 +789,6 @@ __global__ __launch_bounds__(256) void knn_merge_blocks_f64_kernel(GramArgs64 a)
 // spaced sample of index rows (seed_kth_block): any k distinct rows bound the
 // final k-th value from above, so each segment's screen starts tight instead
 // of at +inf.
-constexpr int64_t kSeedRows64 = 512;
 // SB: 64-entry blocks of the running sample list (k <= 64 SB).
 template <int ARM, int SB>
 __global__ __launch_bounds__(256) void knn_seed_f64_kernel(GramArgs64 a, int64_t nsamp) {
@@ -859,7 +858,7 @@ hipError_t launch_seed64(const GramArgs64& a, int64_t nsamp, hipStream_t s) {
 
 hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s) {
     if (!a.shared_r) return hipSuccess;
-    const int64_t nsamp = a.nt < kSeedRows64 ? a.nt : kSeedRows64;
+    const int64_t nsamp = gram_seed_rows(a.nt, a.k);
     if (nsamp >= a.k) {
         if (arm == ARM_EUCLID_FMA) return launch_seed64<ARM_EUCLID_FMA>(a, nsamp, s);
         if (arm == ARM_EUCLID_MULADD) return launch_seed64<ARM_EUCLID_MULADD>(a, nsamp, s);

@@ -127,6 +127,21 @@ __host__ __device__ inline int gram_list_cap(int k) {
 inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64 * 2; }
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
+// Index rows the seed launch samples for k > 1 (evenly spaced): 32 k, at
+// most 2048 and at most nt / 512 (the seed's exact vector work stays near
+// 0.2% of the scan's), but at least 512, so the k-th of the sample sits near
+// the same quantile for every k (at k = 128, 512 rows left the bound near the
+// 25% quantile).  Measured: c2 (1M rows, k = 32) steps fastest with 1024 rows,
+// k = 128 with 2048 (4096: the seed launch costs more than the scan saves),
+// d256 (200k rows) with 512; never more than the index.
+inline int64_t gram_seed_rows(int64_t nt, int k) {
+    int64_t n = 32 * (int64_t)k;
+    if (n > 2048) n = 2048;
+    if (n > nt / 512) n = nt / 512;
+    if (n < 512) n = 512;
+    return nt < n ? nt : n;
+}
+
 // G0, launched workgroups and per-query list slots of the Gram kernel's split.
 void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots);
 

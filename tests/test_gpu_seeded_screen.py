@@ -1,0 +1,64 @@
+"""GPU parity of the Gram kernels' seeded screen on a large index: for k > 1
+the seed launch takes the k-th exact value over an evenly spaced sample of
+the index (row s * n / m, m = 32 k, at most 2048 and n / 512, at least 512) and starts every
+query's screen there.  The bound only prunes, so the answer must stay the
+reference's own top-k, bit for bit against the CPU oracle -- checked with
+exact ties between a sampled row and unsampled copies of it (the seed's k-th
+value can then equal the final one), a query on that point, and a NaN row,
+for both register shapes (d <= 128 and 128 < d <= 256) and the Euclidean and
+cosine arms."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from mlrs_amd import prims
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+NT = 140_000
+
+
+def _nsamp(k):
+    """The seed launch's sample size (gram_seed_rows in knn_kernels.hpp)."""
+    return min(NT, max(512, min(2048, NT // 512, 32 * k)))
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _data(seed, nq, d, metric, k):
+    rng = np.random.default_rng(seed)
+    if metric == "cosine":
+        xq, xt = rng.random((nq, d), dtype=np.float32), rng.random((NT, d), dtype=np.float32)
+    else:
+        xq, xt = rng.standard_normal((nq, d), dtype=np.float32), rng.standard_normal((NT, d), dtype=np.float32)
+    s1 = 1 * NT // _nsamp(k)               # a sampled row
+    for r in (5, 6, 7, NT - 2):            # unsampled exact copies of it
+        xt[r] = xt[s1]
+    xt[9, 0] = np.nan                      # never admitted
+    xq[0] = xt[s1]                         # a query on the tied point
+    xq[1] = xt[s1] * 1.0000001             # and one next to it
+    return xq, xt
+
+
+@pytest.mark.parametrize("metric,d,k", [
+    ("euclidean", 64, 2), ("euclidean", 64, 16), ("euclidean", 64, 64), ("euclidean", 64, 100),
+    ("euclidean", 128, 128), ("euclidean", 200, 32), ("cosine", 64, 16), ("cosine", 128, 128),
+    ("cosine", 200, 16),
+])
+def test_seeded_screen_matches_oracle(metric, d, k):
+    nq = 256
+    xq, xt = _data(k * 1000 + d, nq, d, metric, k)
+    wd, wi = oracle.knn_topk(xq, xt, k, metric)
+    prims.force_path("fused")
+    try:
+        gd, gi = prims.knn_topk(_t(xq), _t(xt), k, metric)
+        torch.cuda.synchronize()
+    finally:
+        prims.force_path("auto")
+    gd, gi = gd.cpu().numpy(), gi.cpu().numpy()
+    bad = np.argwhere(gi != wi.astype(np.int64))
+    assert bad.size == 0, "%s d=%d k=%d: %d index mismatches, first %s" % (metric, d, k, len(bad), bad[:3].tolist())
+    assert np.array_equal(gd, wd), "%s d=%d k=%d: distance bits differ" % (metric, d, k)
