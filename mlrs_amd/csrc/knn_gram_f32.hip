@@ -60,7 +60,7 @@ namespace mlrs {
 
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;                // waves per workgroup, narrow shape (the wide shape: 6)
 constexpr int kBn = 32;                  // index rows per tile
 constexpr int kKcap = 128;               // largest k this kernel keeps
 constexpr int kQcapK1 = 48;              // k = 1: the screen tightens every tile, queues stay short
@@ -75,10 +75,17 @@ constexpr int kSumSlots = 16;            // segment summaries read per refresh (
 //    on the tile's two 16-row halves; lane (g = lane / 16, jl = lane % 16)
 //    holds 8 of query jl's rows, and lane group g contracts the g-th quarter
 //    of the feature axis, so the query operand is d/4 VGPRs (64 at d = 256).
+//  Both shapes run 4 waves per workgroup.  (For the wide shape, whose two
+//  33 KB tiles leave room for only two workgroups per CU, a third wave per
+//  SIMD from larger workgroups did not pay: two 6-wave workgroups are seldom
+//  placed so that both fit a CU (d256 7.0 ms), and one 12-wave workgroup runs
+//  its waves in lockstep behind one barrier (5.6 ms against 5.3-5.4).)
 template <bool W16>
 struct GramShape {
     static constexpr int qpw = W16 ? 16 : 32;      // queries per wave
-    static constexpr int qpb = kWaves * qpw;       // queries per workgroup
+    static constexpr int waves = kWaves;           // waves per workgroup
+    static constexpr int threads = 64 * waves;
+    static constexpr int qpb = waves * qpw;        // queries per workgroup
     static constexpr int vals = W16 ? 8 : 16;      // tile values per lane
     static constexpr int qcap = W16 ? 48 : 64;     // queued candidates per query (k > 1)
 };
@@ -266,11 +273,17 @@ struct GramOcc {
 // KL: 64-entry blocks of a (segment, query) list in registers during a flush
 // (1 for k <= 64, 3 for k <= 128: k + 32 entries).
 template <int NG, int ARM, bool COS, bool VEC4, bool K1, int KL>
-__global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_kernel(GramArgs32 a) {
+// (__launch_bounds__' second argument is waves per SIMD: workgroups per CU x
+// waves per workgroup / 4.)
+__global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
+                             (GramOcc<NG, K1, KL>::wgs * GramShape<(NG > 16)>::waves / 4)) void knn_gram_f32_kernel(
+    GramArgs32 a) {
     constexpr bool W16 = NG > 16;     // the wide shape (GramShape)
     typedef GramShape<W16> SH;
     constexpr int QPW = SH::qpw;
     constexpr int QPB = SH::qpb;
+    constexpr int WV = SH::waves;     // waves per workgroup
+    constexpr int NT = SH::threads;   // threads per workgroup
     constexpr int DP = NG * 8;        // padded feature count
     constexpr int CPR = DP / 4;       // 16-byte chunks per tile row
     // LDS row stride (floats): DP + 4, an odd number of 16-byte chunks, so
@@ -284,7 +297,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
     constexpr int SLOT = 2 * DP + 4;
     constexpr int TILE_FL = PAIRS ? 16 * SLOT : kBn * STRIDE;
     constexpr int TILE_F4 = kBn * DP / 4;
-    constexpr int PF = (TILE_F4 + 255) / 256;
+    constexpr int PF = (TILE_F4 + NT - 1) / NT;
     // 16-byte aligned rows of at least 64 floats go from global memory
     // straight into LDS (gfx950's global_load_lds_dwordx4, one instruction per
     // row, or per slot of two rows, with the first CPR (2 CPR) lanes active:
@@ -293,7 +306,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
     // stage it through registers.  The k = 1 kernel (short segments, three
     // workgroups per CU already) runs faster staged.
     constexpr bool DIRECT = VEC4 && NG >= 8 && !K1;
-    constexpr int RPW = kBn / kWaves;  // tile rows each wave fills (direct)
+    constexpr int RPW = (kBn + WV - 1) / WV;  // tile rows each wave fills (direct): w, w + WV, ...
     constexpr int QQ = DP / 4;        // wide: features per lane-group quarter
     constexpr int NQR = W16 ? QQ / 4 : NG;  // 16-byte query-operand chunks per lane
 
@@ -305,7 +318,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
     __shared__ __attribute__((aligned(16))) float tnB[kBn];
     constexpr int QCAP = K1 ? kQcapK1 : SH::qcap;
     constexpr int kFlushAt = QCAP - kBn;  // flush when a queue may overflow next tile
-    __shared__ WaveLds<K1 ? QCAP : 1, QPW> wl[kWaves];
+    __shared__ WaveLds<K1 ? QCAP : 1, QPW> wl[WV];
 
     // Kernel arguments as locals: they stay in SGPRs.
     const float* __restrict__ Q = a.q;
@@ -329,7 +342,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
     const float inf = __builtin_huge_valf();
     // screen values and index rows of this wave's queued pairs (k > 1),
     // [queue position][query]
-    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * kWaves + w) * (2 * kQvalPerWave);
+    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * WV + w) * (2 * kQvalPerWave);
     uint32_t* __restrict__ QIw = K1 ? nullptr : reinterpret_cast<uint32_t*>(QVw + kQvalPerWave);
 
     // Tile row of value r of this lane.
@@ -345,7 +358,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
     // could hold NaN.
     if (DIRECT && d < DP) {
         const int pad = (int)(DP - d);
-        for (int e = tid; e < kBn * pad; e += 256) {
+        for (int e = tid; e < kBn * pad; e += NT) {
             tileA[row_at(e / pad) + d + e % pad] = 0.0f;
             tileB[row_at(e / pad) + d + e % pad] = 0.0f;
         }
@@ -488,18 +501,18 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
     const float* pf_src[PF];
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
-        const int f = tid + 256 * p;
+        const int f = tid + NT * p;
         pf_r[p] = f / (DP / 4);
         const int c4 = f % (DP / 4);
         pf_on[p] = (f < TILE_F4) && (4 * c4 < d);
         pf_src[p] = X + (t_begin + pf_r[p]) * d + 4 * c4;
     }
     // Whole tiles of rows without padded columns load unconditionally.
-    const bool pf_fast = VEC4 && (PF * 256 == TILE_F4) && (d == DP);
+    const bool pf_fast = VEC4 && (PF * NT == TILE_F4) && (d == DP);
     // Wide rows: a thread's chunks lie in one column, PF_RPP rows apart, so one
     // pointer and uniform offsets address them (eight live 64-bit pointers
     // would not fit next to the 64-register query operand).
-    constexpr int PF_RPP = (256 % (DP / 4) == 0) ? 256 / (DP / 4) : 0;
+    constexpr int PF_RPP = (NT % (DP / 4) == 0) ? NT / (DP / 4) : 0;
     constexpr bool PF_ONE_PTR = W16 && PF_RPP > 0;
     // The address, row and on-flag of prefetch chunk p (wide rows: derived
     // from chunk 0's).
@@ -520,7 +533,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
                 if (VEC4) {                                                                  \
                     v = gload4(src);                                                         \
                 } else {                                                                     \
-                    const int c0_ = (int)((tid + 256 * p) % (DP / 4)) * 4;                   \
+                    const int c0_ = (int)((tid + NT * p) % (DP / 4)) * 4;                    \
                     float e4[4];                                                             \
                     _Pragma("unroll") for (int e = 0; e < 4; ++e) e4[e] =                    \
                         (c0_ + e < d) ? src[e] : 0.0f;                                       \
@@ -722,18 +735,21 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
                 }
             }
         } else if constexpr (DIRECT) {
-            // this wave's first row (wave-uniform) + the lane's chunk
-            const float* xw = X + (int64_t)(t0 + (uint32_t)(w * RPW)) * d + 4 * lane;
+            // rows w, w + WV, ... of the tile: this wave's first row
+            // (wave-uniform) + the lane's chunk
+            const float* xw = X + (int64_t)(t0 + (uint32_t)w) * d + 4 * lane;
             const int di = (int)d;
             if (lane < CPR && 4 * lane < di) {
                 if (t_end32 - t0 >= (uint32_t)kBn) {  // whole tile (t0 + kBn could wrap)
 #pragma unroll
-                    for (int i = 0; i < RPW; ++i) global_to_lds16(xw + i * di, &dst[(w * RPW + i) * STRIDE]);
+                    for (int i = 0; i < RPW; ++i)
+                        if (kBn % WV == 0 || w + WV * i < kBn)
+                            global_to_lds16(xw + (int64_t)WV * i * di, &dst[(w + WV * i) * STRIDE]);
                 } else {
 #pragma unroll
                     for (int i = 0; i < RPW; ++i)
-                        if (t0 + (uint32_t)(w * RPW + i) < t_end32)
-                            global_to_lds16(xw + i * di, &dst[(w * RPW + i) * STRIDE]);
+                        if ((kBn % WV == 0 || w + WV * i < kBn) && t0 + (uint32_t)(w + WV * i) < t_end32)
+                            global_to_lds16(xw + (int64_t)WV * i * di, &dst[(w + WV * i) * STRIDE]);
                 }
             }
         }
@@ -769,7 +785,7 @@ __global__ __launch_bounds__(256, (GramOcc<NG, K1, KL>::wgs)) void knn_gram_f32_
         } else {
 #pragma unroll
             for (int p = 0; p < PF; ++p) {
-                const int f = tid + 256 * p;
+                const int f = tid + NT * p;
                 if (f < TILE_F4) {
                     const int r = f / (DP / 4);
                     const int c4 = f % (DP / 4);
@@ -1277,13 +1293,14 @@ __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
 template <int NG, int ARM, bool COS, bool VEC4>
 hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     dim3 grid((unsigned)StreamSplit(a.nq, a.nt, a.qpb, kBn, a.grid_wgs).G);
+    const dim3 block(GramShape<(NG > 16)>::threads);
     (void)nblocks;
     if (a.k == 1)
-        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true, 1>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true, 1>), grid, block, 0, s, a);
     else if (a.k <= 64)
-        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 1>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 1>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 3>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 3>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 

@@ -123,7 +123,7 @@ __host__ __device__ inline int gram_list_cap(int k) {
 }
 
 // Screen values (f32: and their index rows) kept per workgroup while pairs
-// wait in the queues (k > 1).
+// wait in the queues (k > 1): 2 x 2048 per wave, 4 waves per workgroup.
 inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64 * 2; }
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
