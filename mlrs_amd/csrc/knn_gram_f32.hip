@@ -109,7 +109,7 @@ struct WaveLds {
     float qs[QPW];   // screen operand: ||q||^2 (Euclidean) or ||q|| (cosine)
     float eps[QPW];  // screen error bound
     uint32_t off[QPW];                 // k = 1: queue offsets of the batched flush
-    uint32_t mode[QPW];                // k > 1: 0 = screen-value list, 1 = exact list
+    uint32_t mode[QPW];                // 0: screen values lie within eps of exact values (k > 1: screen-value list); 1: not (exact list)
     unsigned long long best[QPW];      // k = 1: (value bits << 32 | index) of the kept pair
 };
 
@@ -701,6 +701,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             }                                                                                \
         }                                                                                    \
         cntr = 0u;                                                                           \
+        qlo = qlo0;                                                                          \
         if (lane < QPW) {                                                                    \
             float R_ = __uint_as_float((uint32_t)(L.best[lane] >> 32));                      \
             if (SHARED_R && qvalid && R_ < inf) {                                            \
@@ -772,6 +773,13 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     __syncthreads();  // per-wave LDS init visible to the wave
 
     float thr = L.thr[jl];
+    // k = 1: a lower bound on the screen values of the rows in query jl's
+    // queue.  A NaN screen value can hide a finite exact value only where a
+    // sum may overflow, so queries without screen-value mode (L.mode) keep
+    // -inf and never drop queued rows; with it, NaN screen values come from
+    // rows holding a NaN, whose exact values are NaN and never kept.
+    const float qlo0 = (L.mode[jl] == 0u) ? inf : -inf;
+    float qlo = qlo0;
     int tiles = 0;
     // One tile: CUR holds (or receives from the staging registers) the rows
     // at T0, the next tile is loaded towards NXT.
@@ -901,6 +909,18 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             if (W16) m = fminf(m, shfl_xor_f(m, 16));
             m = fminf(m, shfl_xor_f(m, 32));
             if (m < inf) thr = fminf(thr, round_up_f((double)m + 2.0 * (double)L.eps[jl]));
+            if constexpr (K1) {
+                // Rows queued on earlier tiles whose screen values all exceed
+                // the tightened threshold cannot be the nearest row (nor tie
+                // with it): the queue restarts before this tile's rows join it.
+                // Each new running minimum used to leave its predecessors queued
+                // (about ln(tiles) rows per query at each flush).
+                if (qlo > thr) {
+                    cntr = 0u;
+                    qlo = inf;
+                }
+                qlo = fminf(qlo, m);
+            }
         }
 
         // ---- screen: value r of the lane is tile row row_of(r) for query jl.
