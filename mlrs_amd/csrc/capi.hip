@@ -1298,8 +1298,13 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     const int64_t chunks = (nt + 63) / 64;
     int64_t want_strips;
     if (gram) {
+        // whole resident rounds on every XCD (a workgroup per (query block,
+        // strip), two per CU): at c2 the 26 strips of an even split left a
+        // fifth round of one or two workgroups per XCD
         const int64_t nqb = (nq + radius_gram_queries_per_block() - 1) / radius_gram_queries_per_block();
-        want_strips = ((int64_t)cus * 8 + nqb - 1) / std::max<int64_t>(1, nqb);
+        const int64_t old = ((int64_t)cus * 8 + nqb - 1) / std::max<int64_t>(1, nqb);
+        want_strips = pick_strips_xcd(nqb, nt, std::max<int64_t>(1, (int64_t)cus / 8 * radius_gram_wgs_per_cu()),
+                                      64, (int)std::min<int64_t>(2 * old, 65535));
     } else {
         want_strips = ((int64_t)cus * 16 + G - 1) / G;
     }

@@ -315,6 +315,7 @@ enum RadiusMode : int { RADIUS_COUNT = 0, RADIUS_FILL = 1, RADIUS_STAGE = 2 };
 bool radius_gram_serves(int arm, int64_t d);
 int64_t radius_gram_rows_per_tile();
 int64_t radius_gram_queries_per_block();
+int64_t radius_gram_wgs_per_cu();
 hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, int mode, hipStream_t s);
 // The staged matches of a STAGE pass copied into the outputs (after the offsets).
 hipError_t launch_radius_unstage(const RadiusArgs<float>& a, hipStream_t s);

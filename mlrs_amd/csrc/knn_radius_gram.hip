@@ -44,6 +44,7 @@ constexpr int kQpb = kWaves * kQpw;    // query rows per workgroup
 constexpr int kBn = 32;                // index rows per tile (MFMA M dimension)
 constexpr int kQcap = 64;              // queued pairs per query row
 constexpr int kFlushAt = kQcap - kBn;  // flush when a queue could overflow on the next tile
+constexpr int kWgsPerCu = 2;           // resident workgroups per CU (one wave per SIMD each)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -97,7 +98,7 @@ __device__ __forceinline__ float host_value(const float* __restrict__ q, const f
 }
 
 template <int NG, bool COS, bool VEC4, bool FILL, bool STAGE>
-__global__ __launch_bounds__(256, 2) void radius_gram_kernel(RadiusArgs<float> a, float* __restrict__ out_dist,
+__global__ __launch_bounds__(256, kWgsPerCu) void radius_gram_kernel(RadiusArgs<float> a, float* __restrict__ out_dist,
                                                              int32_t* __restrict__ out_idx) {
     constexpr int DP = NG * 8;        // padded feature count
     constexpr int STRIDE = DP + 4;    // LDS row stride (floats)
@@ -471,6 +472,7 @@ bool radius_gram_serves(int arm, int64_t d) {
 }
 int64_t radius_gram_rows_per_tile() { return kBn; }
 int64_t radius_gram_queries_per_block() { return kQpb; }
+int64_t radius_gram_wgs_per_cu() { return kWgsPerCu; }
 
 hipError_t launch_radius_gram(const RadiusArgs<float>& a, int arm, int mode, hipStream_t s) {
     if (a.nq == 0 || a.nstrips == 0) return hipSuccess;
