@@ -1299,8 +1299,9 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     int64_t want_strips;
     if (gram) {
         // whole resident rounds on every XCD (a workgroup per (query block,
-        // strip), two per CU): at c2 the 26 strips of an even split left a
-        // fifth round of one or two workgroups per XCD
+        // strip), radius_gram_wgs_per_cu() of them per CU): at c2 the 26
+        // strips of an even split left a fifth round of one or two
+        // workgroups per XCD
         const int64_t nqb = (nq + radius_gram_queries_per_block() - 1) / radius_gram_queries_per_block();
         const int64_t old = ((int64_t)cus * 8 + nqb - 1) / std::max<int64_t>(1, nqb);
         want_strips = pick_strips_xcd(nqb, nt, std::max<int64_t>(1, (int64_t)cus / 8 * radius_gram_wgs_per_cu()),

@@ -6,10 +6,13 @@
 // replaced by a screen.
 //
 // Shape: a workgroup is 4 waves x 32 query rows (128) and walks one strip of
-// index rows 32 at a time, exactly as the fused kNN kernel does
-// (knn_gram_f32.hip): the 32-row tile sits in LDS, double-buffered, the next
-// one prefetched into registers under the MFMAs, and each wave keeps its 32
-// query rows as the B operand of v_mfma_f32_32x32x2f32.
+// index rows 32 at a time, as the fused kNN kernel does (knn_gram_f32.hip):
+// the 32-row tile sits in LDS, the next one prefetched into registers under
+// the MFMAs, and each wave keeps its 32 query rows as the B operand of
+// v_mfma_f32_32x32x2f32.  One tile buffer (two barriers per tile) leaves room
+// for three workgroups per CU (52 KB LDS, 168 VGPRs): at c2 with radius 14.8
+// that ran the scan in 20.75 ms against 22.11 ms for two double-buffered
+// workgroups per CU.
 //  * Euclidean: acc = ||x||^2 - 2 x.q; a pair passes when
 //    acc <= th - ||q||^2 + eps.  Cosine: acc = x.q scaled by 1/||x|| after the
 //    contraction; a pair passes when 1 - acc/||q|| <= th + eps.  eps bounds
@@ -44,7 +47,7 @@ constexpr int kQpb = kWaves * kQpw;    // query rows per workgroup
 constexpr int kBn = 32;                // index rows per tile (MFMA M dimension)
 constexpr int kQcap = 64;              // queued pairs per query row
 constexpr int kFlushAt = kQcap - kBn;  // flush when a queue could overflow on the next tile
-constexpr int kWgsPerCu = 2;           // resident workgroups per CU (one wave per SIMD each)
+constexpr int kWgsPerCu = 3;           // resident workgroups per CU (one wave per SIMD each)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -105,8 +108,8 @@ __global__ __launch_bounds__(256, kWgsPerCu) void radius_gram_kernel(RadiusArgs<
     constexpr int TILE_F4 = kBn * DP / 4;
     constexpr int PF = (TILE_F4 + 255) / 256;
 
-    __shared__ __attribute__((aligned(16))) float tile[2][kBn][STRIDE];
-    __shared__ __attribute__((aligned(16))) float tnorm[2][kBn];
+    __shared__ __attribute__((aligned(16))) float tile[kBn][STRIDE];
+    __shared__ __attribute__((aligned(16))) float tnorm[kBn];
     __shared__ RgWaveLds wl[kWaves];
 
     const float* __restrict__ Q = a.q;
@@ -313,32 +316,32 @@ __global__ __launch_bounds__(256, kWgsPerCu) void radius_gram_kernel(RadiusArgs<
     __syncthreads();  // per-wave LDS state visible to the wave
 
     uint32_t cntr = 0u;  // queued pairs of query jl (equal in lanes jl and jl + 32)
-    int buf = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn, buf ^= 1) {
-        // publish the prefetched tile
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn) {
+        // publish the prefetched tile once every wave is done with the last one
+        __syncthreads();
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const int f = tid + 256 * p;
             if (f < TILE_F4) {
                 const int r = f / (DP / 4);
                 const int c4 = f % (DP / 4);
-                *reinterpret_cast<float4*>(&tile[buf][r][4 * c4]) = pf[p];
+                *reinterpret_cast<float4*>(&tile[r][4 * c4]) = pf[p];
             }
         }
-        if (tid < kBn) tnorm[buf][tid] = pfn;
+        if (tid < kBn) tnorm[tid] = pfn;
         __syncthreads();
         if (t0 + kBn < t_end) MLRS_RG_PREFETCH(t0 + kBn);
 
         f32x16 acc;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-            const float4 n4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+            const float4 n4 = *reinterpret_cast<const float4*>(&tnorm[8 * g4 + 4 * h]);
             acc[4 * g4 + 0] = COS ? 0.0f : n4.x;
             acc[4 * g4 + 1] = COS ? 0.0f : n4.y;
             acc[4 * g4 + 2] = COS ? 0.0f : n4.z;
             acc[4 * g4 + 3] = COS ? 0.0f : n4.w;
         }
-        const float* arow = &tile[buf][jl][4 * h];
+        const float* arow = &tile[jl][4 * h];
         float4 av = *reinterpret_cast<const float4*>(arow);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
@@ -359,7 +362,7 @@ __global__ __launch_bounds__(256, kWgsPerCu) void radius_gram_kernel(RadiusArgs<
         for (int g4 = 0; g4 < 4; ++g4) {
             float sc[4] = {1.f, 1.f, 1.f, 1.f};
             if (COS) {
-                const float4 s4 = *reinterpret_cast<const float4*>(&tnorm[buf][8 * g4 + 4 * h]);
+                const float4 s4 = *reinterpret_cast<const float4*>(&tnorm[8 * g4 + 4 * h]);
                 sc[0] = s4.x;
                 sc[1] = s4.y;
                 sc[2] = s4.z;
