@@ -484,7 +484,9 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     if (rc) return rc;
     int64_t grid_wgs = 1;
     int nslots = 1;
-    gram_f32_split(nq, nt, d, k, cus, &grid_wgs, &nslots);
+    const bool vec4 = (d % 4 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(xt) & 15) == 0);
+    gram_f32_split(nq, nt, d, k, cus, vec4, &grid_wgs, &nslots);
     // per-(segment slot, query) lists: the kernel's top-k state, merged at the end
     size_t parts = (size_t)nslots * nq * gram_list_cap(k);
     size_t qvals = (k > 1) ? gram_f32_qval_elems(grid_wgs) : 0;

@@ -257,17 +257,19 @@ __device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q,
 }
 
 // Workgroups per CU.  Three (at most 168 VGPRs, 53 KB LDS) wherever they
-// fit: k = 1 with d <= 64 (its LDS queues allow no more), and the narrow
-// shape (d <= 128) with k > 1, whose queues live in global memory (k <= 128:
-// the compiler spills a little of the three-block lists).  A
-// third wave per SIMD keeps the matrix core fed while the other two wait at
-// a tile barrier or merge a queue into a list.
-__host__ __device__ constexpr int gram_f32_wgs_per_cu(int ng, bool k1, int kl) {
-    return (k1 && ng <= 8) || (!k1 && ng <= 16) ? 3 : 2;
+// fit: k = 1 with d <= 64 (its LDS queues allow no more), the narrow shape
+// (d <= 128) with k > 1, whose queues live in global memory (k <= 128: the
+// compiler spills a little of the three-block lists), and the wide shape
+// with k > 1 and 16-byte rows, which then keeps one tile buffer (33 KB at
+// d = 256; two barriers per tile).  A third wave per SIMD keeps the matrix
+// core fed while the other two wait at a tile barrier or merge a queue into
+// a list.
+__host__ __device__ constexpr int gram_f32_wgs_per_cu(int ng, bool k1, int kl, bool vec4) {
+    return (k1 && ng <= 8) || (!k1 && (ng <= 16 || vec4)) ? 3 : 2;
 }
-template <int NG, bool K1, int KL>
+template <int NG, bool K1, int KL, bool VEC4>
 struct GramOcc {
-    static constexpr int wgs = gram_f32_wgs_per_cu(NG, K1, KL);
+    static constexpr int wgs = gram_f32_wgs_per_cu(NG, K1, KL, VEC4);
 };
 
 // KL: 64-entry blocks of a (segment, query) list in registers during a flush
@@ -276,7 +278,7 @@ template <int NG, int ARM, bool COS, bool VEC4, bool K1, int KL>
 // (__launch_bounds__' second argument is waves per SIMD: workgroups per CU x
 // waves per workgroup / 4.)
 __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
-                             (GramOcc<NG, K1, KL>::wgs * GramShape<(NG > 16)>::waves / 4)) void knn_gram_f32_kernel(
+                             (GramOcc<NG, K1, KL, VEC4>::wgs * GramShape<(NG > 16)>::waves / 4)) void knn_gram_f32_kernel(
     GramArgs32 a) {
     constexpr bool W16 = NG > 16;     // the wide shape (GramShape)
     typedef GramShape<W16> SH;
@@ -306,6 +308,9 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     // stage it through registers.  The k = 1 kernel (short segments, three
     // workgroups per CU already) runs faster staged.
     constexpr bool DIRECT = VEC4 && NG >= 8 && !K1;
+    // Wide shape, direct loads: one tile buffer, refilled once every wave's
+    // MFMA chain has read it, so that three workgroups fit a CU.
+    constexpr bool SINGLE = W16 && DIRECT;
     constexpr int RPW = (kBn + WV - 1) / WV;  // tile rows each wave fills (direct): w, w + WV, ...
     constexpr int QQ = DP / 4;        // wide: features per lane-group quarter
     constexpr int NQR = W16 ? QQ / 4 : NG;  // 16-byte query-operand chunks per lane
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     // The two tile buffers are distinct objects, so the compiler can tell the
     // direct loads into one from the reads of the other.
     __shared__ __attribute__((aligned(16))) float tileA[TILE_FL];
-    __shared__ __attribute__((aligned(16))) float tileB[TILE_FL];
+    __shared__ __attribute__((aligned(16))) float tileB[SINGLE ? 4 : TILE_FL];
     __shared__ __attribute__((aligned(16))) float tnA[kBn];
     __shared__ __attribute__((aligned(16))) float tnB[kBn];
     constexpr int QCAP = K1 ? kQcapK1 : SH::qcap;
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
         const int pad = (int)(DP - d);
         for (int e = tid; e < kBn * pad; e += NT) {
             tileA[row_at(e / pad) + d + e % pad] = 0.0f;
-            tileB[row_at(e / pad) + d + e % pad] = 0.0f;
+            if constexpr (!SINGLE) tileB[row_at(e / pad) + d + e % pad] = 0.0f;
         }
     }
 
@@ -803,7 +808,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
         }
         if (tid < kBn) tncur[tid] = pfn;
         __syncthreads();
-        if (t_end32 - (uint32_t)t0 > (uint32_t)kBn) load_tile(nxt, t0 + kBn);
+        if (!SINGLE && t_end32 - (uint32_t)t0 > (uint32_t)kBn) load_tile(nxt, t0 + kBn);
 
         // The lane's tile values: narrow, acc[r] = row row_of(r); wide, r < 4
         // in acc0 (the first 16-row half) and r >= 4 in acc1.
@@ -895,6 +900,12 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
                     acc1[r] *= (&n1.x)[r];
                 }
             }
+        }
+        if constexpr (SINGLE) {
+            // every wave's chain has read the tile (and its norms): refill it
+            // under this tile's screen
+            __syncthreads();
+            if (t_end32 - (uint32_t)t0 > (uint32_t)kBn) load_tile(nxt, t0 + kBn);
         }
         auto val = [&](int r) -> float {
             if constexpr (W16) return r < 4 ? acc0[r] : acc1[r - 4];
@@ -996,7 +1007,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             thr = L.thr[jl];
         }
         // ---- pick up thresholds tightened by other strips of these queries ----
-        rotate_wave_priority((uint32_t)tiles + 1u, GramOcc<NG, K1, KL>::wgs);
+        rotate_wave_priority((uint32_t)tiles + 1u, GramOcc<NG, K1, KL, VEC4>::wgs);
         if (SHARED_R && (++tiles % kShareEvery) == 0) {
             if (lane < QPW && qvalid) {
                 float R = __uint_as_float(SHARED_R[qmine]);
@@ -1054,9 +1065,13 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             thr = L.thr[jl];
         }
     };
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * kBn) {
-        tile_step(tileA, tnA, tileB, t0);
-        if (t0 + kBn < t_end) tile_step(tileB, tnB, tileA, t0 + kBn);
+    if constexpr (SINGLE) {
+        for (int64_t t0 = t_begin; t0 < t_end; t0 += kBn) tile_step(tileA, tnA, tileA, t0);
+    } else {
+        for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * kBn) {
+            tile_step(tileA, tnA, tileB, t0);
+            if (t0 + kBn < t_end) tile_step(tileB, tnB, tileA, t0 + kBn);
+        }
     }
 
     // ---- final flush of every non-empty queue ----
@@ -1361,12 +1376,12 @@ hipError_t launch_seed(const GramArgs32& a, int64_t nsamp, hipStream_t s) {
 int gram_f32_queries_per_block(int64_t d) { return d > 128 ? kQpbWide : kQpbNarrow; }
 
 
-void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots) {
+void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, bool vec4, int64_t* grid_wgs, int* nslots) {
     const int64_t qpb = gram_f32_queries_per_block(d);
     const StreamSplit full(nq, nt, qpb, kBn, 1);
     // one resident round (gram_f32_wgs_per_cu workgroups per CU), but at
     // least 16 tiles each
-    const int per_cu = gram_f32_wgs_per_cu((int)((d + 7) / 8), k == 1, k <= 64 ? 1 : 3);
+    const int per_cu = gram_f32_wgs_per_cu((int)((d + 7) / 8), k == 1, k <= 64 ? 1 : 3, vec4);
     int64_t g0 = per_cu * (int64_t)(cus > 0 ? cus : 1);
     if (g0 > full.T / 16) g0 = full.T / 16;
     if (g0 < 1) g0 = 1;

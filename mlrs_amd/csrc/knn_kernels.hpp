@@ -143,7 +143,9 @@ inline int64_t gram_seed_rows(int64_t nt, int k) {
 }
 
 // G0, launched workgroups and per-query list slots of the Gram kernel's split.
-void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, int64_t* grid_wgs, int* nslots);
+// vec4: the launch's 16-byte row test (d % 4 == 0, both bases 16-byte aligned),
+// which picks the kernel and with it the workgroups per CU the split assumes.
+void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, bool vec4, int64_t* grid_wgs, int* nslots);
 
 // Three launches per search: prep (the shared per-query bound: seeded from a
 // row sample for k > 1, else reset), the Gram kernel, the strip merge +
