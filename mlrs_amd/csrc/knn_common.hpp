@@ -571,6 +571,7 @@ __device__ __forceinline__ float pick8(const f32x4_t& a0, const f32x4_t& a1, int
 // arm, unused for Euclidean).
 constexpr int kSeedQpw = 4;
 constexpr int kSeedQpb = 4 * kSeedQpw;
+constexpr int kSeedInsertMax = 8;  // batches with at most this many rows below the k-th insert them one by one
 template <typename T, int ARM, typename Bits, int SB = 1>
 __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T* __restrict__ X, int64_t nq,
                                                int64_t nt, int64_t d, int k, int64_t nsamp,
@@ -591,6 +592,8 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
     const T inf = F::inf();
     const int64_t qb0 = (int64_t)blockIdx.x * kSeedQpb;
     const int64_t q0 = qb0 + (int64_t)w * kSeedQpw;
+    const bool vec = (d % V == 0) && ((reinterpret_cast<uintptr_t>(Q) & 15) == 0) &&
+                     ((reinterpret_cast<uintptr_t>(X) & 15) == 0);
     T qa[kSeedQpw], lv[kSeedQpw][SB];
     uint32_t li[kSeedQpw][SB];
 #pragma unroll
@@ -617,16 +620,43 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
             __syncthreads();  // srow written; the previous chunk is no longer read
             // rows s0 .. s0+63 of the sample, columns c0 .. c0+CH: thread i
             // copies elements i, i+256, ... of the 64 x CH block (row-major;
-            // consecutive threads read consecutive columns of one row)
-            for (int e = tid; e < 64 * CH; e += 256) {
-                const int r = e >> CH_LOG, c = e & (CH - 1);
-                const uint32_t tr = srow[r];
-                rows[r][c] = (tr != kSentinelIdx && c < cw) ? X[(int64_t)tr * d + c0 + c] : T(0);
-            }
-            for (int e = tid; e < kSeedQpb * CH; e += 256) {
-                const int j = e >> CH_LOG, c = e & (CH - 1);
-                const int64_t qg = (qb0 + j < nq) ? qb0 + j : nq - 1;
-                qch[j][c] = (c < cw) ? Q[qg * d + c0 + c] : T(0);
+            // consecutive threads read consecutive columns of one row), 16
+            // bytes at a time where rows are 16-byte aligned (cw is then a
+            // multiple of V), all of a thread's loads issued together
+            if (vec) {
+                constexpr int CV = CH / V;  // 16-byte pieces per chunk row (32)
+#pragma unroll
+                for (int i = 0; i < 64 * CV / 256; ++i) {
+                    const int e = tid + 256 * i;
+                    const int r = e / CV, c = (e % CV) * V;
+                    const uint32_t tr = srow[r];
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (tr != kSentinelIdx && c < cw)
+                        v = *reinterpret_cast<const float4*>(X + (int64_t)tr * d + c0 + c);
+                    *reinterpret_cast<float4*>(&rows[r][c]) = v;
+                }
+#pragma unroll
+                for (int i = 0; i < (kSeedQpb * CV + 255) / 256; ++i) {
+                    const int e = tid + 256 * i;
+                    if (e < kSeedQpb * CV) {
+                        const int j = e / CV, c = (e % CV) * V;
+                        const int64_t qg = (qb0 + j < nq) ? qb0 + j : nq - 1;
+                        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (c < cw) v = *reinterpret_cast<const float4*>(Q + qg * d + c0 + c);
+                        *reinterpret_cast<float4*>(&qch[j][c]) = v;
+                    }
+                }
+            } else {
+                for (int e = tid; e < 64 * CH; e += 256) {
+                    const int r = e >> CH_LOG, c = e & (CH - 1);
+                    const uint32_t tr = srow[r];
+                    rows[r][c] = (tr != kSentinelIdx && c < cw) ? X[(int64_t)tr * d + c0 + c] : T(0);
+                }
+                for (int e = tid; e < kSeedQpb * CH; e += 256) {
+                    const int j = e >> CH_LOG, c = e & (CH - 1);
+                    const int64_t qg = (qb0 + j < nq) ? qb0 + j : nq - 1;
+                    qch[j][c] = (c < cw) ? Q[qg * d + c0 + c] : T(0);
+                }
             }
             __syncthreads();
             // V columns per step, in ascending order (the arm's operation
@@ -686,7 +716,35 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
             for (int b = 1; b < SB; ++b)
                 if (((k - 1) >> 6) == b) kth = lv[j][b];
             kth = bcast_f(kth, (k - 1) & 63);
-            if (!__builtin_amdgcn_ballot_w64(e < kth)) continue;
+            const uint64_t cand = __builtin_amdgcn_ballot_w64(e < kth);
+            if (!cand) continue;
+            if (SB == 1 && __builtin_popcountll(cand) <= kSeedInsertMax) {
+                // A few rows below the k-th (later batches): each goes into
+                // its place in the list, which is sorted by (value, index)
+                // across the lanes, instead of sorting the batch and merging.
+                // Entries past the k-th may then differ from a full merge's;
+                // the k-th value does not.
+                uint64_t cm = cand;
+                while (cm) {
+                    const int l = __builtin_ctzll(cm);
+                    cm &= cm - 1;
+                    const T ce = bcast_f(e, l);
+                    const uint32_t ct = bcast_u(tj, l);
+                    if (!(ce < bcast_f(lv[j][0], (k - 1) & 63))) continue;
+                    const int p = __builtin_popcountll(
+                        __builtin_amdgcn_ballot_w64(pair_less<T>(lv[j][0], li[j][0], ce, ct)));
+                    const T uv = __shfl_up(lv[j][0], 1, 64);
+                    const uint32_t ui = (uint32_t)__shfl_up((int)li[j][0], 1, 64);
+                    if (lane > p) {
+                        lv[j][0] = uv;
+                        li[j][0] = ui;
+                    } else if (lane == p) {
+                        lv[j][0] = ce;
+                        li[j][0] = ct;
+                    }
+                }
+                continue;
+            }
             wave_sort64<T>(e, tj, lane);
             if (SB == 1)
                 wave_merge64<T>(lv[j][0], li[j][0], e, tj, lane);
