@@ -254,7 +254,10 @@ __global__ __launch_bounds__(256) void km_changed_kernel(const uint32_t* __restr
     if ((threadIdx.x & 63) == 0 && local) atomicAdd(count, local);
 }
 
-template <typename T>
+// VEC: rows 16-byte aligned (d a multiple of 16 / sizeof(T)): the row and its
+// centre are read 16 bytes at a time, eight pieces in flight; the sum is the
+// same ascending acc + diff * diff either way.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restrict__ x, const T* __restrict__ c,
                                                               const uint32_t* __restrict__ labels, int64_t n,
                                                               int64_t d, T* __restrict__ out) {
@@ -263,11 +266,82 @@ __global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restric
     const T* xr = x + i * d;
     const T* cr = c + (int64_t)labels[i] * d;
     T acc = T(0);
-    for (int64_t j = 0; j < d; ++j) {
-        const T diff = xr[j] - cr[j];
-        acc = acc + diff * diff;
+    if constexpr (VEC) {
+        constexpr int V = 16 / (int)sizeof(T);
+        constexpr int U = 8;
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        const float4* c4 = reinterpret_cast<const float4*>(cr);
+        const int64_t n4 = d / V;
+        int64_t p = 0;
+        for (; p + U <= n4; p += U) {
+            float4 a[U], b[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                a[u] = x4[p + u];
+                b[u] = c4[p + u];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const T* av = reinterpret_cast<const T*>(&a[u]);
+                const T* bv = reinterpret_cast<const T*>(&b[u]);
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const T diff = av[e] - bv[e];
+                    acc = acc + diff * diff;
+                }
+            }
+        }
+        for (; p < n4; ++p) {
+            const float4 a = x4[p], b = c4[p];
+            const T* av = reinterpret_cast<const T*>(&a);
+            const T* bv = reinterpret_cast<const T*>(&b);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const T diff = av[e] - bv[e];
+                acc = acc + diff * diff;
+            }
+        }
+    } else {
+        for (int64_t j = 0; j < d; ++j) {
+            const T diff = xr[j] - cr[j];
+            acc = acc + diff * diff;
+        }
     }
     out[i] = acc;
+}
+
+// acc + p[0] + p[1] + ... in order over contiguous values: single values up
+// to a 16-byte boundary, then 16-byte pieces sixteen at a time (one thread
+// walks a whole block of the layout, so the loads in flight set its speed).
+template <typename T>
+__device__ __forceinline__ T ordered_sum_contig(const T* __restrict__ p, int64_t count) {
+    constexpr int V = 16 / (int)sizeof(T);
+    T acc = T(0);
+    if (count <= 0) return acc;
+    int64_t i = 0;
+    while (i < count && (reinterpret_cast<uintptr_t>(p + i) & 15) != 0) acc = acc + p[i++];
+    const float4* p4 = reinterpret_cast<const float4*>(p + i);
+    const int64_t n4 = (count - i) / V;
+    int64_t b = 0;
+    for (; b + 16 <= n4; b += 16) {
+        float4 w[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) w[u] = p4[b + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const T* e = reinterpret_cast<const T*>(&w[u]);
+#pragma unroll
+            for (int j = 0; j < V; ++j) acc = acc + e[j];
+        }
+    }
+    for (; b < n4; ++b) {
+        const float4 w = p4[b];
+        const T* e = reinterpret_cast<const T*>(&w);
+#pragma unroll
+        for (int j = 0; j < V; ++j) acc = acc + e[j];
+    }
+    for (i += n4 * V; i < count; ++i) acc = acc + p[i];
+    return acc;
 }
 
 template <typename T>
@@ -277,7 +351,7 @@ __global__ __launch_bounds__(256) void km_block_sum_kernel(const T* __restrict__
     if (b >= nb) return;
     const int64_t start = b * rpb;
     const int64_t end = (start + rpb) < n ? start + rpb : n;
-    out[b] = ordered_sum<T>(v + start, end - start, 1);
+    out[b] = ordered_sum_contig<T>(v + start, end - start);
 }
 
 template <typename T>
@@ -385,8 +459,14 @@ hipError_t launch_km_changed(const uint32_t* a, const uint32_t* b, int64_t n, un
 template <typename T>
 hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int64_t n, int64_t d, T* rows,
                              int64_t nb, int64_t rpb, T* parts, hipStream_t s) {
-    hipLaunchKernelGGL((km_inertia_rows_kernel<T>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, c, labels, n, d,
-                       rows);
+    const bool vec = (d % (16 / (int64_t)sizeof(T)) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+                     ((reinterpret_cast<uintptr_t>(c) & 15) == 0);
+    if (vec)
+        hipLaunchKernelGGL((km_inertia_rows_kernel<T, true>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, c,
+                           labels, n, d, rows);
+    else
+        hipLaunchKernelGGL((km_inertia_rows_kernel<T, false>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, c,
+                           labels, n, d, rows);
     hipLaunchKernelGGL((km_block_sum_kernel<T>), dim3(blocks_for(nb, 1 << 20)), dim3(256), 0, s, rows, n, nb, rpb,
                        parts);
     return hipGetLastError();
