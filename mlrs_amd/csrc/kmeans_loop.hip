@@ -244,27 +244,43 @@ __global__ __launch_bounds__(256) void km_reduce_kernel(const T* __restrict__ ps
     sums[t] = ordered_sum<T>(psum + t, nb, kd);
 }
 
+// Labels that differ: 16 bytes (four labels) per load where both arrays are
+// 16-byte aligned, the workgroup's count summed in LDS and added to `count`
+// with one atomic per workgroup (one per wave made 5M labels cost 0.14 ms:
+// the atomics on one word serialise).
 __global__ __launch_bounds__(256) void km_changed_kernel(const uint32_t* __restrict__ a,
                                                          const uint32_t* __restrict__ b, int64_t n,
                                                          unsigned int* __restrict__ count) {
+    __shared__ unsigned int part[4];
     const int64_t stride = (int64_t)gridDim.x * 256;
+    const int64_t first = (int64_t)blockIdx.x * 256 + threadIdx.x;
     unsigned int local = 0;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) local += (a[i] != b[i]) ? 1u : 0u;
+    int64_t tail = 0;
+    if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) {
+        const uint4* a4 = reinterpret_cast<const uint4*>(a);
+        const uint4* b4 = reinterpret_cast<const uint4*>(b);
+        const int64_t n4 = n / 4;
+        for (int64_t i = first; i < n4; i += stride) {
+            const uint4 x = a4[i], y = b4[i];
+            local += (x.x != y.x ? 1u : 0u) + (x.y != y.y ? 1u : 0u) + (x.z != y.z ? 1u : 0u) + (x.w != y.w ? 1u : 0u);
+        }
+        tail = 4 * n4;
+    }
+    for (int64_t i = tail + first; i < n; i += stride) local += (a[i] != b[i]) ? 1u : 0u;
     for (int o = 32; o > 0; o >>= 1) local += (unsigned int)__shfl_xor((int)local, o, 64);
-    if ((threadIdx.x & 63) == 0 && local) atomicAdd(count, local);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = local;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int sum = part[0] + part[1] + part[2] + part[3];
+        if (sum) atomicAdd(count, sum);
+    }
 }
 
-// VEC: rows 16-byte aligned (d a multiple of 16 / sizeof(T)): the row and its
-// centre are read 16 bytes at a time, eight pieces in flight; the sum is the
-// same ascending acc + diff * diff either way.
+// sum over j of (x[j] - c[j])^2 as acc + diff * diff in ascending j.  VEC:
+// both rows 16-byte aligned and d a multiple of 16 / sizeof(T), so they are
+// read 16 bytes at a time, eight pieces in flight.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restrict__ x, const T* __restrict__ c,
-                                                              const uint32_t* __restrict__ labels, int64_t n,
-                                                              int64_t d, T* __restrict__ out) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const T* xr = x + i * d;
-    const T* cr = c + (int64_t)labels[i] * d;
+__device__ __forceinline__ T row_sqdist(const T* __restrict__ xr, const T* __restrict__ cr, int64_t d) {
     T acc = T(0);
     if constexpr (VEC) {
         constexpr int V = 16 / (int)sizeof(T);
@@ -307,7 +323,22 @@ __global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restric
             acc = acc + diff * diff;
         }
     }
-    out[i] = acc;
+    return acc;
+}
+
+template <typename T>
+bool rows_vec(const T* x, const T* c, int64_t d) {
+    return (d % (16 / (int64_t)sizeof(T)) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+           ((reinterpret_cast<uintptr_t>(c) & 15) == 0);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restrict__ x, const T* __restrict__ c,
+                                                              const uint32_t* __restrict__ labels, int64_t n,
+                                                              int64_t d, T* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    out[i] = row_sqdist<T, VEC>(x + i * d, c + (int64_t)labels[i] * d, d);
 }
 
 // acc + p[0] + p[1] + ... in order over contiguous values: single values up
@@ -378,18 +409,12 @@ __global__ __launch_bounds__(256) void km_col_sum_kernel(const T* __restrict__ x
     }
 }
 
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void km_mind2_kernel(const T* __restrict__ x, int64_t n, int64_t d, int64_t cidx,
                                                        int first, T* __restrict__ mind2) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const T* xr = x + i * d;
-    const T* cr = x + cidx * d;
-    T acc = T(0);
-    for (int64_t j = 0; j < d; ++j) {
-        const T diff = xr[j] - cr[j];
-        acc = acc + diff * diff;
-    }
+    const T acc = row_sqdist<T, VEC>(x + i * d, x + cidx * d, d);
     if (first || acc < mind2[i]) mind2[i] = acc;
 }
 
@@ -452,16 +477,14 @@ hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n
 hipError_t launch_km_changed(const uint32_t* a, const uint32_t* b, int64_t n, unsigned int* count, hipStream_t s) {
     hipError_t e = launch_fill_u32(count, 1, 0u, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(km_changed_kernel, dim3(blocks_for(n, 4096)), dim3(256), 0, s, a, b, n, count);
+    hipLaunchKernelGGL(km_changed_kernel, dim3(blocks_for((n + 3) / 4, 1024)), dim3(256), 0, s, a, b, n, count);
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int64_t n, int64_t d, T* rows,
                              int64_t nb, int64_t rpb, T* parts, hipStream_t s) {
-    const bool vec = (d % (16 / (int64_t)sizeof(T)) == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
-                     ((reinterpret_cast<uintptr_t>(c) & 15) == 0);
-    if (vec)
+    if (rows_vec(x, c, d))
         hipLaunchKernelGGL((km_inertia_rows_kernel<T, true>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, c,
                            labels, n, d, rows);
     else
@@ -482,8 +505,12 @@ hipError_t launch_km_col_sums(const T* x, int64_t n, int64_t d, int64_t nb, int6
 
 template <typename T>
 hipError_t launch_km_mind2(const T* x, int64_t n, int64_t d, int64_t cidx, int first, T* mind2, hipStream_t s) {
-    hipLaunchKernelGGL((km_mind2_kernel<T>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, n, d, cidx, first,
-                       mind2);
+    if (rows_vec(x, x, d))
+        hipLaunchKernelGGL((km_mind2_kernel<T, true>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, n, d, cidx,
+                           first, mind2);
+    else
+        hipLaunchKernelGGL((km_mind2_kernel<T, false>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, n, d, cidx,
+                           first, mind2);
     return hipGetLastError();
 }
 
