@@ -127,15 +127,17 @@ __host__ __device__ inline int gram_list_cap(int k) {
 inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64 * 2; }
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
-// Index rows the seed launch samples for k > 1 (evenly spaced): 32 k, at
+// Index rows the seed launch samples for k > 1 (evenly spaced): 64 k, at
 // most 2048 and at most nt / 512 (the seed's exact vector work stays near
 // 0.2% of the scan's), but at least 512, so the k-th of the sample sits near
 // the same quantile for every k (at k = 128, 512 rows left the bound near the
-// 25% quantile).  Measured: c2 (1M rows, k = 32) steps fastest with 1024 rows,
-// k = 128 with 2048 (4096: the seed launch costs more than the scan saves),
-// d256 (200k rows) with 512; never more than the index.
+// 25% quantile).  Measured: c2 (1M rows, k = 32) steps fastest with the
+// 1953-row cap (1024 rows: +0.1 ms; 4096: the kernel gains 0.1 ms more but
+// the seed launch costs more), k = 128 likewise (4096 and 8192 rows cut the
+// scan by 0.6 and 1.1 ms and cost more in the seed), d256 (200k rows) with
+// 512; never more than the index.
 inline int64_t gram_seed_rows(int64_t nt, int k) {
-    int64_t n = 32 * (int64_t)k;
+    int64_t n = 64 * (int64_t)k;
     if (n > 2048) n = 2048;
     if (n > nt / 512) n = nt / 512;
     if (n < 512) n = 512;

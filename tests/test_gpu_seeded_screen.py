@@ -1,6 +1,6 @@
 """GPU parity of the Gram kernels' seeded screen on a large index: for k > 1
 the seed launch takes the k-th exact value over an evenly spaced sample of
-the index (row s * n / m, m = 32 k, at most 2048 and n / 512, at least 512) and starts every
+the index (row s * n / m, m = 64 k, at most 2048 and n / 512, at least 512) and starts every
 query's screen there.  The bound only prunes, so the answer must stay the
 reference's own top-k, bit for bit against the CPU oracle -- checked with
 exact ties between a sampled row and unsampled copies of it (the seed's k-th
@@ -21,7 +21,7 @@ NT = 140_000
 
 def _nsamp(k):
     """The seed launch's sample size (gram_seed_rows in knn_kernels.hpp)."""
-    return min(NT, max(512, min(2048, NT // 512, 32 * k)))
+    return min(NT, max(512, min(2048, NT // 512, 64 * k)))
 
 
 def _t(a):
