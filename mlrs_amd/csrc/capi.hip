@@ -471,8 +471,10 @@ static int pick_path(bool lowd_ok, bool gram_ok) {
     return MLRS_PATH_AUTO;
 }
 
+// qsq_pre: the queries' row_sumsq when the caller already holds them (the
+// k-means loop assigns the same rows every iteration); Euclidean arms only.
 int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
-                   int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
+                   int mode, float* out_v, uint32_t* out_i, hipStream_t s, const float* qsq_pre = nullptr) {
     const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
     const bool host_cos = arm == ARM_COS_HOST;
     // sizes that do not depend on the strip count
@@ -505,7 +507,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     float* xinv = cv.take<float>(nt);
     float* xscale = cv.take<float>(nt);
     NormStats* stats = cv.take<NormStats>(1);
-    hipError_t e = launch_row_norms<float>(xq, nq, d, qsq, host_cos ? qinv : nullptr, nullptr, nullptr, s);
+    hipError_t e = hipSuccess;
+    if (qsq_pre && !cos)
+        qsq = const_cast<float*>(qsq_pre);  // only read
+    else
+        e = launch_row_norms<float>(xq, nq, d, qsq, host_cos ? qinv : nullptr, nullptr, nullptr, s);
     if (e == hipSuccess)
         e = launch_row_norms<float>(xt, nt, d, xsq, host_cos ? xinv : nullptr, cos ? xscale : nullptr, stats, s);
     if (e != hipSuccess) return hip_err(e, "row_norms");
@@ -556,7 +562,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
 }
 
 int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, int64_t d, int k, int arm,
-                   int mode, double* out_v, uint32_t* out_i, hipStream_t s) {
+                   int mode, double* out_v, uint32_t* out_i, hipStream_t s, const double* qsq_pre = nullptr) {
     const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
     size_t fixed = 2 * aligned_bytes(sizeof(double) * nq) + 3 * aligned_bytes(sizeof(double) * nt) +
                    aligned_bytes(sizeof(NormStats)) + 1024;
@@ -582,7 +588,11 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     double* xinv = cv.take<double>(nt);
     double* xscale = cv.take<double>(nt);
     NormStats* stats = cv.take<NormStats>(1);
-    hipError_t e = launch_row_norms<double>(xq, nq, d, qsq, qinv, nullptr, nullptr, s);
+    hipError_t e = hipSuccess;
+    if (qsq_pre && !cos)
+        qsq = const_cast<double*>(qsq_pre);  // only read; qinv serves cosine only
+    else
+        e = launch_row_norms<double>(xq, nq, d, qsq, qinv, nullptr, nullptr, s);
     if (e == hipSuccess) e = launch_row_norms<double>(xt, nt, d, xsq, xinv, xscale, stats, s);
     if (e != hipSuccess) return hip_err(e, "row_norms");
     a.q = xq;
@@ -1717,15 +1727,15 @@ int32_t mlrs_hdbscan_core_distances_f64(const double* x, int64_t x_len, int64_t 
 // ---------------------------------------------------------------------------
 extern "C++" {
 static int32_t km_assign(const float* x, int64_t n, const float* c, int64_t k, int64_t d, uint32_t* labels,
-                         float* dist, hipStream_t s) {
+                         float* dist, hipStream_t s, const float* xsq = nullptr) {
     if (d <= gram_f32_max_d() && pick_path(false, true) != MLRS_PATH_GENERIC)
-        return knn_gram32(x, n, c, k, d, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, dist, labels, s);
+        return knn_gram32(x, n, c, k, d, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, dist, labels, s, xsq);
     return kmeans_generic<float>(x, n, c, k, d, labels, dist, s);
 }
 static int32_t km_assign(const double* x, int64_t n, const double* c, int64_t k, int64_t d, uint32_t* labels,
-                         double* dist, hipStream_t s) {
+                         double* dist, hipStream_t s, const double* xsq = nullptr) {
     if (d <= gram_f64_max_d() && pick_path(false, true) != MLRS_PATH_GENERIC)
-        return knn_gram64(x, n, c, k, d, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, dist, labels, s);
+        return knn_gram64(x, n, c, k, d, 1, ARM_EUCLID_MULADD, EMIT_KMEANS, dist, labels, s, xsq);
     return kmeans_generic<double>(x, n, c, k, d, labels, dist, s);
 }
 
@@ -1864,7 +1874,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     km_layout(n, 256, &nbi, &rpbi);                                            // sum_device
 
     const int64_t nsub = km_sub_blocks(nb, rpb, k);
-    size_t bytes = 4 * aligned_bytes(sizeof(uint32_t) * (size_t)n) + 2 * aligned_bytes(sizeof(T) * (size_t)n) +
+    size_t bytes = 4 * aligned_bytes(sizeof(uint32_t) * (size_t)n) + 3 * aligned_bytes(sizeof(T) * (size_t)n) +
                    2 * aligned_bytes(sizeof(uint32_t) * (size_t)(nb * k)) +
                    aligned_bytes(sizeof(uint32_t) * (size_t)(nb * nsub * k)) + 2 * aligned_bytes(sizeof(uint32_t) * k) +
                    aligned_bytes(sizeof(T) * (size_t)(nb * kd)) + 2 * aligned_bytes(sizeof(T) * (size_t)kd) +
@@ -1893,10 +1903,14 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     T* means_dev = cv.take<T>(d);
     int64_t* idx_dev = cv.take<int64_t>(k);
     unsigned int* changed_dev = reinterpret_cast<unsigned int*>(cv.take<uint32_t>(1));
+    // the rows' row_sumsq, which every assignment of this fit reads: computed once
+    T* xsq = cv.take<T>(n);
+    hipError_t e = launch_row_norms<T>(x, n, d, xsq, nullptr, nullptr, nullptr, s);
+    if (e != hipSuccess) return hip_err(e, "kmeans row norms");
 
     // ---- tol_scaled = tol * mean(var(X, axis=0)) (feature_mean_var) ----
     std::vector<T> hp((size_t)std::max(nbi, nbv * d));
-    hipError_t e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, nullptr, parts, s);
+    e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, nullptr, parts, s);
     if (e != hipSuccess) return hip_err(e, "kmeans col sums");
     rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)(nbv * d), s);
     if (rc) return rc;
@@ -2057,7 +2071,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
 
         // ---- single_run ----
         int cur = 0;
-        rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s);
+        rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s, xsq);
         if (rc) return rc;
         int64_t iters = 0;
         for (int64_t it = 0; it < max_iter; ++it) {
@@ -2197,7 +2211,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
             e = hipMemcpyAsync(cdev, ct.data(), sizeof(T) * (size_t)kd, hipMemcpyHostToDevice, s);
             if (e != hipSuccess) return hip_err(e, "kmeans centres upload");
             cur ^= 1;
-            rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s);
+            rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s, xsq);
             if (rc) return rc;
             e = launch_km_changed(lab[cur], lab[cur ^ 1], n, changed_dev, s);
             if (e != hipSuccess) return hip_err(e, "kmeans labels_changed");
