@@ -496,6 +496,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
                    aligned_bytes(qvals * sizeof(float)) + aligned_bytes(summs * sizeof(float4)) +
                    aligned_bytes(sizeof(unsigned int) * nq);
+    // the seed's screen values on the matrix cores, where served and where
+    // the workspace allows (otherwise the exact seed, which needs none)
+    size_t seed_bytes = gram_f32_seed_screen_bytes(nq, nt, d, k, arm, vec4);
+    if (seed_bytes && bytes + aligned_bytes(seed_bytes) > workspace_limit()) seed_bytes = 0;
+    if (seed_bytes) bytes += aligned_bytes(seed_bytes);
     rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
@@ -549,9 +554,10 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     if (qvals) a.qval = cv.take<float>(qvals);
     if (summs) a.summ = cv.take<float4>(summs);
     if (nslots > 1 || k > 1) a.shared_r = cv.take<unsigned int>(nq);
+    void* seed_buf = seed_bytes ? static_cast<void*>(cv.take<char>(seed_bytes)) : nullptr;
     a.out_val = out_v;
     a.out_idx = out_i;
-    e = launch_gram_f32_prep(a, arm, s);
+    e = launch_gram_f32_prep(a, arm, s, seed_buf);
     if (e == hipSuccess) {
         KernelTimer timer(s, "knn_gram_f32_kernel");
         e = launch_gram_f32(a, arm, s);

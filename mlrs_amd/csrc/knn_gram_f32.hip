@@ -1319,6 +1319,113 @@ __global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
     emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, 1, qg, 0, lv, li, a.out_val, a.out_idx);
 }
 
+// Seed on the matrix cores (Euclidean, d <= 128, 16-byte rows): the screen
+// value of every (query, sampled row) pair, as the main kernel forms it
+// (acc = ||x||^2, then v_mfma_f32_32x32x2f32 over -2 q in the same operand
+// layout), turned into an upper bound u = max(round_up(acc + ||q||^2), 0) of
+// the pair's distance less eps, and written to S[q][s] (NaN for a NaN
+// screen value, which the selection never admits).  The k-th smallest u then
+// bounds the query's k-th exact value once eps is added (k sampled rows have
+// exact <= u + eps <= u_k + eps).  A workgroup takes 128 queries and one
+// contiguous range of the sample's 32-row tiles (blockIdx.y: the tiles are
+// split so that the launch fills the chip); sampled row s is index row
+// s * n / m.
+template <int NG>
+__global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, int64_t nsamp,
+                                                                  float* __restrict__ S, int64_t ld) {
+    constexpr int DP = NG * 8;
+    constexpr int STRIDE = DP + 4;
+    __shared__ __attribute__((aligned(16))) float tile[kBn * STRIDE];
+    __shared__ __attribute__((aligned(16))) float tn[kBn];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, jl = lane & 31;
+    const int64_t nq = a.nq, nt = a.nt, d = a.d;
+    const float inf = __builtin_huge_valf();
+    const int64_t q = (int64_t)blockIdx.x * kQpbNarrow + (int64_t)w * 32 + jl;
+    const bool qvalid = q < nq;
+    const int64_t qrow = qvalid ? q : nq - 1;
+    const float qs = a.qsq[qrow];
+    float4 qreg[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int64_t c = 8 * g + 4 * h;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < d) v = *reinterpret_cast<const float4*>(a.q + qrow * d + c);
+        qreg[g] = make_float4(-2.0f * v.x, -2.0f * v.y, -2.0f * v.z, -2.0f * v.w);
+    }
+    const int64_t ntiles = (nsamp + kBn - 1) / kBn;
+    const int64_t per = (ntiles + gridDim.y - 1) / gridDim.y;
+    const int64_t s_lo = (int64_t)blockIdx.y * per * kBn;
+    int64_t s_hi = s_lo + per * kBn;
+    if (s_hi > nsamp) s_hi = nsamp;
+    for (int64_t s0 = s_lo; s0 < s_hi; s0 += kBn) {
+        __syncthreads();  // the previous tile is no longer read
+        for (int f = tid; f < kBn * DP / 4; f += 256) {
+            const int r = f / (DP / 4), c4 = f % (DP / 4);
+            const int64_t sr = s0 + r;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (sr < nsamp && 4 * c4 < d)
+                v = *reinterpret_cast<const float4*>(a.x + ((sr * nt) / nsamp) * d + 4 * c4);
+            *reinterpret_cast<float4*>(&tile[r * STRIDE + 4 * c4]) = v;
+        }
+        if (tid < kBn) {
+            const int64_t sr = s0 + tid;
+            tn[tid] = (sr < nsamp) ? a.xsq[(sr * nt) / nsamp] : inf;
+        }
+        __syncthreads();
+        f32x16 acc;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const float4 n4 = *reinterpret_cast<const float4*>(&tn[8 * g4 + 4 * h]);
+            acc[4 * g4 + 0] = n4.x;
+            acc[4 * g4 + 1] = n4.y;
+            acc[4 * g4 + 2] = n4.z;
+            acc[4 * g4 + 3] = n4.w;
+        }
+        const float* arow = &tile[jl * STRIDE + 4 * h];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const float4 av = *reinterpret_cast<const float4*>(arow + 8 * g);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, qreg[g].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, qreg[g].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, qreg[g].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
+        }
+        if (qvalid) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t sr = s0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (sr < nsamp) {
+                    const float v = acc[r];
+                    float u = __builtin_nanf("");
+                    if (v == v) {
+                        u = round_up_f((double)v + (double)qs);
+                        u = u < 0.0f ? 0.0f : u;
+                    }
+                    S[q * ld + sr] = u;
+                }
+            }
+        }
+    }
+}
+
+// The seed bound from each query's k-th smallest u (out_val[q][k - 1]):
+// round_up(u_k + eps), for queries in screen-value mode (norms well inside
+// the float range); +inf otherwise.
+__global__ void seed_screen_finalize_kernel(GramArgs32 a, const float* __restrict__ kv, int k) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= a.nq) return;
+    const float inf = __builtin_huge_valf();
+    const double qsq = (double)a.qsq[q], xmax = (double)a.stats->xsq_max;
+    const double eps = a.eps_rel * (qsq + xmax) + a.eps_abs;
+    const float vk = kv[q * k + (k - 1)];
+    float R = inf;
+    if (qsq + xmax <= 0x1p124 && eps < 0x1p120 && vk < inf) R = round_up_f((double)vk + eps);
+    a.shared_r[q] = __float_as_uint(R);
+}
+
 // The shared per-query threshold words start at +inf (as float bits).
 __global__ void fill_inf_bits_kernel(unsigned int* p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1393,7 +1500,29 @@ int gram_f32_max_k() { return kKcap; }
 int gram_f32_max_d() { return 256; }
 int gram_f32_rows_per_tile() { return kBn; }
 
-hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
+// Rows the matrix-core seed samples: 64 k, at most 8192 and nt / 128, at
+// least 512 -- four times the exact seed's cap, since a sampled pair costs a
+// few MFMA cycles here instead of a d-long FMA chain.  c2 with k = 128: 7812
+// rows, step 27.2 -> 26.6 ms against the exact seed's 1953 (kernel 26.3 ->
+// 25.2 ms); k = 32 takes 2048 (no change against 1953).
+static int64_t seed_screen_rows(int64_t nt, int k) {
+    int64_t n = 64 * (int64_t)k;
+    if (n > 8192) n = 8192;
+    if (n > nt / 128) n = nt / 128;
+    if (n < 512) n = 512;
+    return nt < n ? nt : n;
+}
+
+size_t gram_f32_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4) {
+    if (k <= 1 || k > kKcap || d > 128 || !vec4 || (arm != ARM_EUCLID_FMA && arm != ARM_EUCLID_MULADD)) return 0;
+    const int64_t nsamp = seed_screen_rows(nt, k);
+    if (nsamp < k) return 0;
+    const int64_t ld = (nsamp + 3) / 4 * 4;
+    const size_t bytes = (size_t)nq * (size_t)ld * 4 + 2 * (((size_t)nq * (size_t)k * 4 + 255) & ~(size_t)255) + 512;
+    return bytes <= ((size_t)512 << 20) ? bytes : 0;  // larger searches keep the exact seed
+}
+
+hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s, void* seed_buf) {
     if (!a.shared_r) return hipSuccess;
     if (a.summ) {
         const int64_t n = (int64_t)a.nslots * a.nq * 4;
@@ -1403,7 +1532,39 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s) {
         if (e != hipSuccess) return e;
     }
     if (a.k > 1) {
-        const int64_t nsamp = gram_seed_rows(a.nt, a.k);
+        const int64_t nsamp = seed_buf ? seed_screen_rows(a.nt, a.k) : gram_seed_rows(a.nt, a.k);
+        if (seed_buf) {
+            const int64_t ld = (nsamp + 3) / 4 * 4;
+            float* S = static_cast<float*>(seed_buf);
+            char* p = reinterpret_cast<char*>(S + (size_t)a.nq * (size_t)ld);
+            p = reinterpret_cast<char*>(((uintptr_t)p + 255) & ~(uintptr_t)255);
+            float* kv = reinterpret_cast<float*>(p);
+            p += ((size_t)a.nq * (size_t)a.k * 4 + 255) & ~(size_t)255;
+            uint32_t* ki = reinterpret_cast<uint32_t*>(p);
+            // about four workgroups per CU: the sample's tiles split over blockIdx.y
+            const int64_t nqb = (a.nq + kQpbNarrow - 1) / kQpbNarrow;
+            const int64_t ntiles = (nsamp + kBn - 1) / kBn;
+            int64_t ys = (1024 + nqb - 1) / nqb;
+            if (ys > ntiles) ys = ntiles;
+            if (ys > 65535) ys = 65535;
+            if (ys < 1) ys = 1;
+            const dim3 grid((unsigned)nqb, (unsigned)ys);
+            const int ng = (int)((a.d + 7) / 8);
+            if (ng <= 4)
+                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<4>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            else if (ng <= 8)
+                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<8>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            else if (ng <= 12)
+                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<12>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            else
+                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<16>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            hipError_t e = hipGetLastError();
+            if (e == hipSuccess) e = launch_select_rows<float>(S, a.nq, nsamp, ld, a.k, EMIT_IDENTITY, kv, ki, nullptr, s);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL(seed_screen_finalize_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a,
+                               kv, a.k);
+            return hipGetLastError();
+        }
         if (arm == ARM_EUCLID_FMA) return launch_seed<ARM_EUCLID_FMA>(a, nsamp, s);
         if (arm == ARM_EUCLID_MULADD) return launch_seed<ARM_EUCLID_MULADD>(a, nsamp, s);
         if (arm == ARM_COS_FOLD) return launch_seed<ARM_COS_FOLD>(a, nsamp, s);

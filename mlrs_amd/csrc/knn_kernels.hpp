@@ -152,7 +152,10 @@ void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, bool vec4
 // Three launches per search: prep (the shared per-query bound: seeded from a
 // row sample for k > 1, else reset), the Gram kernel, the strip merge +
 // output transform.
-hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s);
+// seed_buf: gram_f32_seed_screen_bytes(...) bytes of workspace when that is
+// nonzero (the seed then runs on the matrix cores), else null.
+hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s, void* seed_buf);
+size_t gram_f32_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4);
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
 hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s);
 int gram_f32_max_k();

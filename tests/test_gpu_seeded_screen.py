@@ -1,12 +1,15 @@
 """GPU parity of the Gram kernels' seeded screen on a large index: for k > 1
-the seed launch takes the k-th exact value over an evenly spaced sample of
-the index (row s * n / m, m = 64 k, at most 2048 and n / 512, at least 512) and starts every
-query's screen there.  The bound only prunes, so the answer must stay the
-reference's own top-k, bit for bit against the CPU oracle -- checked with
-exact ties between a sampled row and unsampled copies of it (the seed's k-th
-value can then equal the final one), a query on that point, and a NaN row,
-for both register shapes (d <= 128 and 128 < d <= 256) and the Euclidean and
-cosine arms."""
+the seed launch bounds each query's k-th value over an evenly spaced sample
+of the index (row s * n / m) and starts every query's screen there.  Two
+seeds exist: the exact one (the k-th exact value; m = 64 k, at most 2048 and
+n / 512, at least 512) and, for Euclidean f32 at d <= 128, the matrix-core
+one (the k-th smallest screen value plus its error bound; m = 64 k, at most
+8192 and n / 128, at least 512).  The bound only prunes, so the answer must
+stay the reference's own top-k, bit for bit against the CPU oracle --
+checked with exact ties between a sampled row of either sample and
+unsampled copies of it (the seed's k-th value can then equal the final one),
+queries on those points, and a NaN row, for both register shapes (d <= 128
+and 128 < d <= 256) and the Euclidean and cosine arms."""
 import numpy as np
 import pytest
 import torch
@@ -20,8 +23,13 @@ NT = 140_000
 
 
 def _nsamp(k):
-    """The seed launch's sample size (gram_seed_rows in knn_kernels.hpp)."""
+    """The exact seed's sample size (gram_seed_rows in knn_kernels.hpp)."""
     return min(NT, max(512, min(2048, NT // 512, 64 * k)))
+
+
+def _nsamp_screen(k):
+    """The matrix-core seed's sample size (seed_screen_rows in knn_gram_f32.hip)."""
+    return min(NT, max(512, min(8192, NT // 128, 64 * k)))
 
 
 def _t(a):
@@ -34,12 +42,17 @@ def _data(seed, nq, d, metric, k):
         xq, xt = rng.random((nq, d), dtype=np.float32), rng.random((NT, d), dtype=np.float32)
     else:
         xq, xt = rng.standard_normal((nq, d), dtype=np.float32), rng.standard_normal((NT, d), dtype=np.float32)
-    s1 = 1 * NT // _nsamp(k)               # a sampled row
-    for r in (5, 6, 7, NT - 2):            # unsampled exact copies of it
+    s1 = 1 * NT // _nsamp(k)               # a row of the exact seed's sample
+    s2 = 3 * NT // _nsamp_screen(k)        # a row of the matrix-core seed's sample
+    for r in (5, 6, 7, NT - 2):            # unsampled exact copies of them
         xt[r] = xt[s1]
+    for r in (11, 12, NT - 5):
+        xt[r] = xt[s2]
     xt[9, 0] = np.nan                      # never admitted
-    xq[0] = xt[s1]                         # a query on the tied point
-    xq[1] = xt[s1] * 1.0000001             # and one next to it
+    xq[0] = xt[s1]                         # queries on the tied points
+    xq[1] = xt[s1] * 1.0000001             # and next to them
+    xq[2] = xt[s2]
+    xq[3] = xt[s2] * 1.0000001
     return xq, xt
 
 
