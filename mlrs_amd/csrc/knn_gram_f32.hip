@@ -1319,10 +1319,11 @@ __global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
     emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, 1, qg, 0, lv, li, a.out_val, a.out_idx);
 }
 
-// Seed on the matrix cores (Euclidean, d <= 128, 16-byte rows): the screen
-// value of every (query, sampled row) pair, as the main kernel forms it
-// (acc = ||x||^2, then v_mfma_f32_32x32x2f32 over -2 q in the same operand
-// layout), turned into an upper bound u = max(round_up(acc + ||q||^2), 0) of
+// Seed on the matrix cores (Euclidean, d <= 256, 16-byte rows): the screen
+// value of every (query, sampled row) pair, formed as the narrow main kernel
+// forms it (acc = ||x||^2, then v_mfma_f32_32x32x2f32 over -2 q; above
+// d = 128 too, where the main kernel contracts on 16x16x4 tiles: the screen
+// bound holds for any summation order), turned into an upper bound u = max(round_up(acc + ||q||^2), 0) of
 // the pair's distance less eps, and written to S[q][s] (NaN for a NaN
 // screen value, which the selection never admits).  The k-th smallest u then
 // bounds the query's k-th exact value once eps is added (k sampled rows have
@@ -1514,7 +1515,7 @@ static int64_t seed_screen_rows(int64_t nt, int k) {
 }
 
 size_t gram_f32_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4) {
-    if (k <= 1 || k > kKcap || d > 128 || !vec4 || (arm != ARM_EUCLID_FMA && arm != ARM_EUCLID_MULADD)) return 0;
+    if (k <= 1 || k > kKcap || d > 256 || !vec4 || (arm != ARM_EUCLID_FMA && arm != ARM_EUCLID_MULADD)) return 0;
     const int64_t nsamp = seed_screen_rows(nt, k);
     if (nsamp < k) return 0;
     const int64_t ld = (nsamp + 3) / 4 * 4;
@@ -1556,8 +1557,12 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s, voi
                 hipLaunchKernelGGL((knn_seed_screen_f32_kernel<8>), grid, dim3(256), 0, s, a, nsamp, S, ld);
             else if (ng <= 12)
                 hipLaunchKernelGGL((knn_seed_screen_f32_kernel<12>), grid, dim3(256), 0, s, a, nsamp, S, ld);
-            else
+            else if (ng <= 16)
                 hipLaunchKernelGGL((knn_seed_screen_f32_kernel<16>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            else if (ng <= 24)
+                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<24>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            else
+                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<32>), grid, dim3(256), 0, s, a, nsamp, S, ld);
             hipError_t e = hipGetLastError();
             if (e == hipSuccess) e = launch_select_rows<float>(S, a.nq, nsamp, ld, a.k, EMIT_IDENTITY, kv, ki, nullptr, s);
             if (e != hipSuccess) return e;
