@@ -583,6 +583,12 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     size_t qvals = gram_f64_qval_elems(grid_wgs);
     size_t bytes = fixed + aligned_bytes(parts * sizeof(double)) + aligned_bytes(parts * sizeof(uint32_t)) +
                    aligned_bytes(qvals * sizeof(double)) + aligned_bytes(sizeof(unsigned long long) * nq);
+    // the seed's screen values on the matrix cores where the workspace allows
+    const bool vec2 = (d % 2 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(xt) & 15) == 0);
+    size_t seed_bytes = gram_f64_seed_screen_bytes(nq, nt, d, k, vec2);
+    if (seed_bytes && bytes + aligned_bytes(seed_bytes) > workspace_limit()) seed_bytes = 0;
+    if (seed_bytes) bytes += aligned_bytes(seed_bytes);
     rc = workspace(bytes, s, &ws, &cus);
     if (rc) return rc;
     Carver cv(ws);
@@ -631,9 +637,10 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     a.part_idx = cv.take<uint32_t>(parts);
     a.qval = cv.take<double>(qvals);
     a.shared_r = cv.take<unsigned long long>(nq);
+    void* seed_buf = seed_bytes ? static_cast<void*>(cv.take<char>(seed_bytes)) : nullptr;
     a.out_val = out_v;
     a.out_idx = out_i;
-    e = launch_gram_f64_prep(a, arm, s);
+    e = launch_gram_f64_prep(a, arm, s, seed_buf);
     if (e == hipSuccess) {
         KernelTimer timer(s, "knn_gram_f64_kernel");
         e = launch_gram_f64(a, arm, s);

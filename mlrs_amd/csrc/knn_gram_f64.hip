@@ -846,6 +846,121 @@ void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nsl
 int gram_f64_max_k() { return kKcap; }
 int gram_f64_max_d() { return kMaxD; }
 
+// Seed on the matrix cores (16-byte rows): the screen value of every
+// (query, sampled row) pair on v_mfma_f64_16x16x4f64 (Euclidean: acc =
+// ||x||^2 - 2 x.q; cosine: acc = -(x.q)/||x||), turned into the distance it
+// stands for, u = max(acc + ||q||^2, 0) or clamp(1 + acc/||q||, 0, 2) (NaN
+// kept), written to S[q][s].  The screen bound eps holds for any summation
+// order, so k sampled rows have exact <= u + eps <= u_k + eps.  A wave takes
+// 16 queries (lane l: query l % 16, k-slot g = l / 16 supplies feature
+// 4 s + g at k-step s), a workgroup 64 queries and a slice of the sample's
+// 16-row tiles (blockIdx.y); sampled row s is index row s * n / m.
+template <int KS, bool COS>
+__global__ __launch_bounds__(256) void knn_seed_screen_f64_kernel(GramArgs64 a, int64_t nsamp,
+                                                                  double* __restrict__ S, int64_t ld) {
+    constexpr int DP = 4 * KS;
+    constexpr int STR = DP + 1;
+    __shared__ double tile[kBn * STR];
+    __shared__ double tn[kBn];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, j = lane & 15;
+    const int64_t nq = a.nq, nt = a.nt, d = a.d;
+    const double inf = __builtin_huge_val();
+    const int64_t q = (int64_t)blockIdx.x * kQpb + (int64_t)w * kQpw + j;
+    const bool qvalid = q < nq;
+    const int64_t qrow = qvalid ? q : nq - 1;
+    const double qsq = a.qsq[qrow];
+    const double qs = COS ? __builtin_sqrt(qsq) : qsq;
+    double qreg[KS];
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+        const int64_t c = 4 * st + g;
+        qreg[st] = (c < d) ? a.q[qrow * d + c] * (COS ? 1.0 : -2.0) : 0.0;
+    }
+    const int64_t ntiles = (nsamp + kBn - 1) / kBn;
+    const int64_t per = (ntiles + gridDim.y - 1) / gridDim.y;
+    const int64_t s_lo = (int64_t)blockIdx.y * per * kBn;
+    int64_t s_hi = s_lo + per * kBn;
+    if (s_hi > nsamp) s_hi = nsamp;
+    for (int64_t s0 = s_lo; s0 < s_hi; s0 += kBn) {
+        __syncthreads();  // the previous tile is no longer read
+        for (int e = tid; e < kBn * DP; e += 256) {
+            const int r = e / DP, c = e % DP;
+            const int64_t sr = s0 + r;
+            tile[r * STR + c] = (sr < nsamp && c < d) ? a.x[((sr * nt) / nsamp) * d + c] : 0.0;
+        }
+        if (tid < kBn) {
+            const int64_t sr = s0 + tid;
+            const int64_t t = (sr < nsamp) ? (sr * nt) / nsamp : 0;
+            tn[tid] = (sr < nsamp) ? (COS ? a.xscale[t] : a.xsq[t]) : (COS ? 0.0 : inf);
+        }
+        __syncthreads();
+        f64x4 acc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = COS ? 0.0 : tn[g + 4 * r];
+        const double* arow = &tile[j * STR + g];
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(arow[4 * st], qreg[st], acc, 0, 0, 0);
+        if (qvalid) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t sr = s0 + g + 4 * r;
+                if (sr < nsamp) {
+                    const double v = COS ? acc[r] * tn[g + 4 * r] : acc[r];
+                    double u = __builtin_nan("");
+                    if (v == v) {
+                        if (COS) {
+                            u = 1.0 + v / qs;
+                            u = u < 0.0 ? 0.0 : (u > 2.0 ? 2.0 : u);
+                        } else {
+                            u = v + qsq;
+                            u = u < 0.0 ? 0.0 : u;
+                        }
+                    }
+                    S[q * ld + sr] = u;
+                }
+            }
+        }
+    }
+}
+
+// The seed bound from each query's k-th smallest u: (u_k + eps) rounded
+// up by a relative 2^-50, for queries in screen-value mode; +inf otherwise.
+__global__ void seed_screen_finalize64_kernel(GramArgs64 a, const double* __restrict__ kv, int k, int cos) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= a.nq) return;
+    const double inf = __builtin_huge_val();
+    const double qsq = a.qsq[q], xmax = a.stats->xsq_max64;
+    const double eps = cos ? a.eps_abs : a.eps_rel * (qsq + xmax) + a.eps_abs;
+    const bool sv = (qsq + xmax <= 0x1p1020) && (eps < inf) && (!cos || qsq > 0.0);
+    const double vk = kv[q * k + (k - 1)];
+    double R = inf;
+    if (sv && vk < inf) R = (vk + eps) * (1.0 + 0x1p-50);
+    a.shared_r[q] = (unsigned long long)__double_as_longlong(R);
+}
+
+// Rows the matrix-core seed samples: the exact seed's (gram_seed_rows).
+static int64_t seed_screen_rows64(int64_t nt, int k) { return gram_seed_rows(nt, k); }
+
+size_t gram_f64_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, bool vec2) {
+    if (k <= 1 || k > kKcap || d > kMaxD || !vec2) return 0;
+    const int64_t nsamp = seed_screen_rows64(nt, k);
+    if (nsamp < k) return 0;
+    const int64_t ld = (nsamp + 1) / 2 * 2;
+    const size_t bytes = (size_t)nq * (size_t)ld * 8 + (((size_t)nq * (size_t)k * 8 + 255) & ~(size_t)255) +
+                         (((size_t)nq * (size_t)k * 4 + 255) & ~(size_t)255) + 512;
+    return bytes <= ((size_t)512 << 20) ? bytes : 0;
+}
+
+template <int KS, bool COS>
+static void launch_seed_screen64_ks(const GramArgs64& a, int64_t nsamp, double* S, int64_t ld, dim3 grid,
+                                    hipStream_t s) {
+    hipLaunchKernelGGL((knn_seed_screen_f64_kernel<KS, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+}
+
 template <int ARM>
 hipError_t launch_seed64(const GramArgs64& a, int64_t nsamp, hipStream_t s) {
     const dim3 grid((unsigned)((a.nq + kSeedQpb - 1) / kSeedQpb));
@@ -856,8 +971,45 @@ hipError_t launch_seed64(const GramArgs64& a, int64_t nsamp, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s) {
+hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s, void* seed_buf) {
     if (!a.shared_r) return hipSuccess;
+    if (seed_buf && a.k > 1) {
+        const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
+        const int64_t nsamp = seed_screen_rows64(a.nt, a.k);
+        const int64_t ld = (nsamp + 1) / 2 * 2;
+        double* S = static_cast<double*>(seed_buf);
+        char* p = reinterpret_cast<char*>(S + (size_t)a.nq * (size_t)ld);
+        p = reinterpret_cast<char*>(((uintptr_t)p + 255) & ~(uintptr_t)255);
+        double* kv = reinterpret_cast<double*>(p);
+        p += ((size_t)a.nq * (size_t)a.k * 8 + 255) & ~(size_t)255;
+        uint32_t* ki = reinterpret_cast<uint32_t*>(p);
+        // about four workgroups per CU: the sample's tiles split over blockIdx.y
+        const int64_t nqb = (a.nq + kQpb - 1) / kQpb;
+        const int64_t ntiles = (nsamp + kBn - 1) / kBn;
+        int64_t ys = (1024 + nqb - 1) / nqb;
+        if (ys > ntiles) ys = ntiles;
+        if (ys > 65535) ys = 65535;
+        if (ys < 1) ys = 1;
+        const dim3 grid((unsigned)nqb, (unsigned)ys);
+        const int64_t ks = (a.d + 3) / 4;
+        if (cos) {
+            if (ks <= 16) launch_seed_screen64_ks<16, true>(a, nsamp, S, ld, grid, s);
+            else if (ks <= 32) launch_seed_screen64_ks<32, true>(a, nsamp, S, ld, grid, s);
+            else if (ks <= 48) launch_seed_screen64_ks<48, true>(a, nsamp, S, ld, grid, s);
+            else launch_seed_screen64_ks<64, true>(a, nsamp, S, ld, grid, s);
+        } else {
+            if (ks <= 16) launch_seed_screen64_ks<16, false>(a, nsamp, S, ld, grid, s);
+            else if (ks <= 32) launch_seed_screen64_ks<32, false>(a, nsamp, S, ld, grid, s);
+            else if (ks <= 48) launch_seed_screen64_ks<48, false>(a, nsamp, S, ld, grid, s);
+            else launch_seed_screen64_ks<64, false>(a, nsamp, S, ld, grid, s);
+        }
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = launch_select_rows<double>(S, a.nq, nsamp, ld, a.k, EMIT_IDENTITY, kv, ki, nullptr, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(seed_screen_finalize64_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a,
+                           kv, a.k, cos ? 1 : 0);
+        return hipGetLastError();
+    }
     const int64_t nsamp = gram_seed_rows(a.nt, a.k);
     if (nsamp >= a.k) {
         if (arm == ARM_EUCLID_FMA) return launch_seed64<ARM_EUCLID_FMA>(a, nsamp, s);

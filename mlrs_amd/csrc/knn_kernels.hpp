@@ -193,7 +193,10 @@ struct GramArgs64 {
 void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
 // prep: the shared per-query bound, seeded with the k-th exact value over a
 // row sample (arm: the exact arithmetic)
-hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s);
+// seed_buf: gram_f64_seed_screen_bytes(...) bytes when that is nonzero (the
+// seed then runs on the matrix cores), else null.
+hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s, void* seed_buf);
+size_t gram_f64_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, bool vec2);
 hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s);
 hipError_t launch_gram_f64_merge(const GramArgs64& a, int arm, hipStream_t s);
 int gram_f64_max_k();
