@@ -1319,19 +1319,20 @@ __global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
     emit_pair(a.mode, a.q, a.x, a.qsq, a.xsq, a.d, 1, qg, 0, lv, li, a.out_val, a.out_idx);
 }
 
-// Seed on the matrix cores (Euclidean, d <= 256, 16-byte rows): the screen
-// value of every (query, sampled row) pair, formed as the narrow main kernel
-// forms it (acc = ||x||^2, then v_mfma_f32_32x32x2f32 over -2 q; above
-// d = 128 too, where the main kernel contracts on 16x16x4 tiles: the screen
-// bound holds for any summation order), turned into an upper bound u = max(round_up(acc + ||q||^2), 0) of
-// the pair's distance less eps, and written to S[q][s] (NaN for a NaN
-// screen value, which the selection never admits).  The k-th smallest u then
-// bounds the query's k-th exact value once eps is added (k sampled rows have
-// exact <= u + eps <= u_k + eps).  A workgroup takes 128 queries and one
-// contiguous range of the sample's 32-row tiles (blockIdx.y: the tiles are
-// split so that the launch fills the chip); sampled row s is index row
-// s * n / m.
-template <int NG>
+// Seed on the matrix cores (d <= 256, 16-byte rows): the screen value of
+// every (query, sampled row) pair, formed as the narrow main kernel forms it
+// (Euclidean: acc = ||x||^2, then v_mfma_f32_32x32x2f32 over -2 q; cosine:
+// the contraction over q scaled by -1/||x|| afterwards; above d = 128 too,
+// where the main kernel contracts on 16x16x4 tiles: the screen bound holds
+// for any summation order), turned into the distance it stands for, rounded
+// up -- u = max(acc + ||q||^2, 0) or clamp(1 + acc/||q||, 0, 2) -- and
+// written to S[q][s] (NaN for a NaN screen value, which the selection never
+// admits).  The k-th smallest u then bounds the query's k-th exact value
+// once eps is added (k sampled rows have exact <= u + eps <= u_k + eps).  A
+// workgroup takes 128 queries and one contiguous range of the sample's
+// 32-row tiles (blockIdx.y: the tiles are split so that the launch fills the
+// chip); sampled row s is index row s * n / m.
+template <int NG, bool COS>
 __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, int64_t nsamp,
                                                                   float* __restrict__ S, int64_t ld) {
     constexpr int DP = NG * 8;
@@ -1347,14 +1348,16 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
     const int64_t q = (int64_t)blockIdx.x * kQpbNarrow + (int64_t)w * 32 + jl;
     const bool qvalid = q < nq;
     const int64_t qrow = qvalid ? q : nq - 1;
-    const float qs = a.qsq[qrow];
+    const float qsq = a.qsq[qrow];
+    const float qs = COS ? __builtin_sqrtf(qsq) : qsq;  // the main kernel's screen operand
+    const float scale = COS ? 1.0f : -2.0f;
     float4 qreg[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
         const int64_t c = 8 * g + 4 * h;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < d) v = *reinterpret_cast<const float4*>(a.q + qrow * d + c);
-        qreg[g] = make_float4(-2.0f * v.x, -2.0f * v.y, -2.0f * v.z, -2.0f * v.w);
+        qreg[g] = make_float4(scale * v.x, scale * v.y, scale * v.z, scale * v.w);
     }
     const int64_t ntiles = (nsamp + kBn - 1) / kBn;
     const int64_t per = (ntiles + gridDim.y - 1) / gridDim.y;
@@ -1373,17 +1376,18 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
         }
         if (tid < kBn) {
             const int64_t sr = s0 + tid;
-            tn[tid] = (sr < nsamp) ? a.xsq[(sr * nt) / nsamp] : inf;
+            const int64_t t = (sr < nsamp) ? (sr * nt) / nsamp : 0;
+            tn[tid] = (sr < nsamp) ? (COS ? a.xscale[t] : a.xsq[t]) : (COS ? 0.0f : inf);
         }
         __syncthreads();
         f32x16 acc;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
             const float4 n4 = *reinterpret_cast<const float4*>(&tn[8 * g4 + 4 * h]);
-            acc[4 * g4 + 0] = n4.x;
-            acc[4 * g4 + 1] = n4.y;
-            acc[4 * g4 + 2] = n4.z;
-            acc[4 * g4 + 3] = n4.w;
+            acc[4 * g4 + 0] = COS ? 0.0f : n4.x;
+            acc[4 * g4 + 1] = COS ? 0.0f : n4.y;
+            acc[4 * g4 + 2] = COS ? 0.0f : n4.z;
+            acc[4 * g4 + 3] = COS ? 0.0f : n4.w;
         }
         const float* arow = &tile[jl * STRIDE + 4 * h];
 #pragma unroll
@@ -1399,11 +1403,18 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
             for (int r = 0; r < 16; ++r) {
                 const int64_t sr = s0 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (sr < nsamp) {
-                    const float v = acc[r];
+                    // cosine: the contraction scaled by -1/||x|| afterwards, as
+                    // in the main kernel
+                    const float v = COS ? acc[r] * tn[8 * (r >> 2) + 4 * h + (r & 3)] : acc[r];
                     float u = __builtin_nanf("");
                     if (v == v) {
-                        u = round_up_f((double)v + (double)qs);
-                        u = u < 0.0f ? 0.0f : u;
+                        if (COS) {
+                            u = round_up_f(1.0 + (double)v / (double)qs);
+                            u = u < 0.0f ? 0.0f : (u > 2.0f ? 2.0f : u);
+                        } else {
+                            u = round_up_f((double)v + (double)qs);
+                            u = u < 0.0f ? 0.0f : u;
+                        }
                     }
                     S[q * ld + sr] = u;
                 }
@@ -1415,15 +1426,17 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
 // The seed bound from each query's k-th smallest u (out_val[q][k - 1]):
 // round_up(u_k + eps), for queries in screen-value mode (norms well inside
 // the float range); +inf otherwise.
-__global__ void seed_screen_finalize_kernel(GramArgs32 a, const float* __restrict__ kv, int k) {
+__global__ void seed_screen_finalize_kernel(GramArgs32 a, const float* __restrict__ kv, int k, int cos) {
     const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (q >= a.nq) return;
     const float inf = __builtin_huge_valf();
     const double qsq = (double)a.qsq[q], xmax = (double)a.stats->xsq_max;
-    const double eps = a.eps_rel * (qsq + xmax) + a.eps_abs;
+    const double eps = cos ? a.eps_abs : a.eps_rel * (qsq + xmax) + a.eps_abs;
     const float vk = kv[q * k + (k - 1)];
     float R = inf;
-    if (qsq + xmax <= 0x1p124 && eps < 0x1p120 && vk < inf) R = round_up_f((double)vk + eps);
+    // cosine: a zero query ties every row and is never screened
+    if (qsq + xmax <= 0x1p124 && eps < 0x1p120 && vk < inf && (!cos || qsq > 0.0))
+        R = round_up_f((double)vk + eps);
     a.shared_r[q] = __float_as_uint(R);
 }
 
@@ -1514,8 +1527,25 @@ static int64_t seed_screen_rows(int64_t nt, int k) {
     return nt < n ? nt : n;
 }
 
+template <bool COS>
+static void launch_seed_screen_ng(const GramArgs32& a, int64_t nsamp, float* S, int64_t ld, dim3 grid, int ng,
+                                  hipStream_t s) {
+    if (ng <= 4)
+        hipLaunchKernelGGL((knn_seed_screen_f32_kernel<4, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+    else if (ng <= 8)
+        hipLaunchKernelGGL((knn_seed_screen_f32_kernel<8, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+    else if (ng <= 12)
+        hipLaunchKernelGGL((knn_seed_screen_f32_kernel<12, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+    else if (ng <= 16)
+        hipLaunchKernelGGL((knn_seed_screen_f32_kernel<16, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+    else if (ng <= 24)
+        hipLaunchKernelGGL((knn_seed_screen_f32_kernel<24, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+    else
+        hipLaunchKernelGGL((knn_seed_screen_f32_kernel<32, COS>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+}
+
 size_t gram_f32_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4) {
-    if (k <= 1 || k > kKcap || d > 256 || !vec4 || (arm != ARM_EUCLID_FMA && arm != ARM_EUCLID_MULADD)) return 0;
+    if (k <= 1 || k > kKcap || d > 256 || !vec4) return 0;
     const int64_t nsamp = seed_screen_rows(nt, k);
     if (nsamp < k) return 0;
     const int64_t ld = (nsamp + 3) / 4 * 4;
@@ -1551,23 +1581,16 @@ hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s, voi
             if (ys < 1) ys = 1;
             const dim3 grid((unsigned)nqb, (unsigned)ys);
             const int ng = (int)((a.d + 7) / 8);
-            if (ng <= 4)
-                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<4>), grid, dim3(256), 0, s, a, nsamp, S, ld);
-            else if (ng <= 8)
-                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<8>), grid, dim3(256), 0, s, a, nsamp, S, ld);
-            else if (ng <= 12)
-                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<12>), grid, dim3(256), 0, s, a, nsamp, S, ld);
-            else if (ng <= 16)
-                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<16>), grid, dim3(256), 0, s, a, nsamp, S, ld);
-            else if (ng <= 24)
-                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<24>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+            const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
+            if (cos)
+                launch_seed_screen_ng<true>(a, nsamp, S, ld, grid, ng, s);
             else
-                hipLaunchKernelGGL((knn_seed_screen_f32_kernel<32>), grid, dim3(256), 0, s, a, nsamp, S, ld);
+                launch_seed_screen_ng<false>(a, nsamp, S, ld, grid, ng, s);
             hipError_t e = hipGetLastError();
             if (e == hipSuccess) e = launch_select_rows<float>(S, a.nq, nsamp, ld, a.k, EMIT_IDENTITY, kv, ki, nullptr, s);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL(seed_screen_finalize_kernel, dim3((unsigned)((a.nq + 255) / 256)), dim3(256), 0, s, a,
-                               kv, a.k);
+                               kv, a.k, cos ? 1 : 0);
             return hipGetLastError();
         }
         if (arm == ARM_EUCLID_FMA) return launch_seed<ARM_EUCLID_FMA>(a, nsamp, s);
