@@ -75,3 +75,70 @@ def test_seeded_screen_matches_oracle(metric, d, k):
     bad = np.argwhere(gi != wi.astype(np.int64))
     assert bad.size == 0, "%s d=%d k=%d: %d index mismatches, first %s" % (metric, d, k, len(bad), bad[:3].tolist())
     assert np.array_equal(gd, wd), "%s d=%d k=%d: distance bits differ" % (metric, d, k)
+
+
+def _fused(xq, xt, k, metric):
+    prims.force_path("fused")
+    try:
+        gd, gi = prims.knn_topk(_t(xq), _t(xt), k, metric)
+        torch.cuda.synchronize()
+    finally:
+        prims.force_path("auto")
+    return gd.cpu().numpy(), gi.cpu().numpy()
+
+
+def _same(gd, gi, wd, wi, label):
+    bad = np.argwhere(gi != wi.astype(np.int64))
+    assert bad.size == 0, "%s: %d index mismatches, first %s" % (label, len(bad), bad[:3].tolist())
+    same = (gd == wd) | (np.isnan(gd) & np.isnan(wd))
+    assert same.all(), "%s: distance bits differ at %s" % (label, np.argwhere(~same)[:3].tolist())
+
+
+def test_seed_large_norms_unseeded():
+    # squared norms past 2^124: screen values may overflow, so the matrix-core
+    # seed must leave such queries unbounded (their screen is not trusted)
+    rng = np.random.default_rng(3)
+    scale = np.float32(2.0 ** 59)
+    xt = (rng.standard_normal((NT, 64)) * scale).astype(np.float32)
+    xq = (rng.standard_normal((64, 64)) * scale).astype(np.float32)
+    assert float(np.max(np.sum(xt.astype(np.float64) ** 2, axis=1))) > 2.0 ** 124
+    xt[100] = xt[NT // 2]
+    xq[0] = xt[NT // 2]
+    wd, wi = oracle.knn_topk(xq, xt, 16, "euclidean")
+    gd, gi = _fused(xq, xt, 16, "euclidean")
+    _same(gd, gi, wd, wi, "large norms")
+
+
+def test_seed_cosine_zero_query_and_rows():
+    # a zero query ties every row at distance 1 (lowest indices win) and is
+    # never seeded; zero rows score 1 against every query
+    rng = np.random.default_rng(4)
+    xt = rng.random((NT, 64), dtype=np.float32)
+    xq = rng.random((64, 64), dtype=np.float32)
+    xq[0] = 0.0
+    xt[7] = 0.0
+    xt[NT - 3] = 0.0
+    wd, wi = oracle.knn_topk(xq, xt, 16, "cosine")
+    gd, gi = _fused(xq, xt, 16, "cosine")
+    _same(gd, gi, wd, wi, "cosine zeros")
+
+
+@pytest.mark.parametrize("metric,d", [("euclidean", 256), ("cosine", 256), ("euclidean", 40), ("cosine", 130)])
+def test_seed_f64_matches_oracle(metric, d):
+    # the f64 kernel's matrix-core seed, with ties to a sampled row and NaN rows
+    nt = 60_000
+    rng = np.random.default_rng(d + (7 if metric == "cosine" else 0))
+    if metric == "cosine":
+        xq, xt = rng.random((96, d)), rng.random((nt, d))
+    else:
+        xq, xt = rng.standard_normal((96, d)), rng.standard_normal((nt, d))
+    m = min(nt, max(512, min(2048, nt // 512, 64 * 16)))
+    s1 = 2 * nt // m
+    for r in (3, 4, nt - 1):
+        xt[r] = xt[s1]
+    xt[11, 5] = np.nan
+    xq[0] = xt[s1]
+    xq[1] = xt[s1] * (1.0 + 1e-15)
+    wd, wi = oracle.knn_topk(xq, xt, 16, metric)
+    gd, gi = _fused(xq, xt, 16, metric)
+    _same(gd, gi, wd, wi, "f64 %s d=%d" % (metric, d))
