@@ -1399,13 +1399,17 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, qreg[g].w, acc, 0, 0, 0);
         }
         if (qvalid) {
+            // values r = 4 g4 .. 4 g4 + 3 are four consecutive sampled rows:
+            // one 16-byte store (ld and s0 are multiples of 4)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t sr = s0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (sr < nsamp) {
+            for (int g4 = 0; g4 < 4; ++g4) {
+                float u4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g4 + e;
                     // cosine: the contraction scaled by -1/||x|| afterwards, as
                     // in the main kernel
-                    const float v = COS ? acc[r] * tn[8 * (r >> 2) + 4 * h + (r & 3)] : acc[r];
+                    const float v = COS ? acc[r] * tn[8 * g4 + 4 * h + e] : acc[r];
                     float u = __builtin_nanf("");
                     if (v == v) {
                         if (COS) {
@@ -1416,7 +1420,15 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
                             u = u < 0.0f ? 0.0f : u;
                         }
                     }
-                    S[q * ld + sr] = u;
+                    u4[e] = u;
+                }
+                const int64_t sr0 = s0 + 8 * g4 + 4 * h;
+                if (sr0 + 3 < nsamp) {
+                    *reinterpret_cast<float4*>(S + q * ld + sr0) = make_float4(u4[0], u4[1], u4[2], u4[3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (sr0 + e < nsamp) S[q * ld + sr0 + e] = u4[e];
                 }
             }
         }
