@@ -127,8 +127,12 @@ int32_t mlrs_knn_max_k(int32_t dtype_bytes, int64_t n_features, int32_t metric);
  * tiles) lives: in a static device array of MLRS_NOALLOC_SCRATCH_BYTES per
  * GPU, held until the process ends, instead of the library's cached
  * workspace.  The call makes no hipMalloc / hipFree / allocating library
- * call; its first call on a device looks the array's device address up once
- * (hipGetSymbolAddress).  A search whose scratch would exceed the array
+ * call; its first call on a device looks the array's device address
+ * (hipGetSymbolAddress) and the CU count up once: make that first call, which
+ * may have n_query = 0, outside a graph capture.  After it, calls can be
+ * captured into a HIP graph (every step is a kernel launch: no memset, no
+ * copy, no event) and replayed with new data in the same buffers.  A search
+ * whose scratch would exceed the array
  * returns MLRS_ERR_UNSUPPORTED, operand "scratch" {rows = bytes needed,
  * len = MLRS_NOALLOC_SCRATCH_BYTES}, before any launch (the exact-tile path
  * sizes its tiles to fit; the Gram path at n_train = 1M, d = 128, k = 32
@@ -324,10 +328,10 @@ int32_t mlrs_radius_neighbors_f64(const double *xq, int64_t xq_len, int64_t n_qu
  *   pow(sum pow(|diff|, p), 1/p).  out_idx / out_dist (n x k, device): per row
  *   ascending (distance, index); include_self = 0 leaves out the row's own
  *   index (by identity, not by distance: a duplicate point stays); an entry
- *   the scan cannot fill is (0, 0.0).  One difference of order: candidates are
- *   ranked by the aggregate before the root, where the host scan ranks the
- *   rooted value -- two aggregates one rounding apart that root to the same
- *   double may come out in the other order.
+ *   the scan cannot fill is (0, 0.0).  As in the host scan's KNearest
+ *   (umap_host_knn.rs:171-198, pushing the final distance at :494), the lists
+ *   are ranked by the final distance, not by the aggregate before the root:
+ *   two aggregates that root to the same double are ordered by index.
  * Errors (knn_graph.rs:475-539): ShapeMismatch "x" {n, d, len} (or a
  *   dimension above u32::MAX), "k" {1, k, max_k} with max_k = n - 1 (n with
  *   include_self), "p" {1, 0, 1} (Minkowski p < 1), "out"; Unsupported

@@ -88,6 +88,7 @@ struct Arena {
     char* base = nullptr;
     size_t cap = 0;
     int cus = 0;
+    bool pooled = false;  // base came from hipMallocAsync
 };
 Arena g_arena[kMaxDevices];
 
@@ -117,7 +118,6 @@ static size_t aligned_bytes(size_t n) { return (n + 255) & ~(size_t)255; }
 // reference's single stream (crates/mlrs-backend/src/stream_cap.rs:69).
 struct DevOrder {
     hipEvent_t ev = nullptr;
-    hipStream_t last = nullptr;
     bool have = false;
 };
 DevOrder g_order[kMaxDevices];
@@ -143,10 +143,7 @@ struct CallGuard {
     ~CallGuard() {
         if (st.armed) {
             DevOrder& O = g_order[st.dev];
-            if (hipEventRecord(O.ev, st.s) == hipSuccess) {
-                O.last = st.s;
-                O.have = true;
-            }
+            if (hipEventRecord(O.ev, st.s) == hipSuccess) O.have = true;
         }
         g_call = nullptr;
     }
@@ -166,7 +163,10 @@ int32_t order_after_last_call(int dev, hipStream_t s) {
             return hip_err(e, "hipEventCreateWithFlags");
         }
     }
-    if (O.have && O.last != s) {
+    // Waited for even when the stream handle equals the last call's: a
+    // destroyed stream's handle can be handed out again while its work is
+    // pending, and waiting on an event the stream itself recorded is free.
+    if (O.have) {
         e = hipStreamWaitEvent(s, O.ev, 0);
         if (e != hipSuccess) return hip_err(e, "hipStreamWaitEvent");
     }
@@ -213,9 +213,65 @@ void note_read_back() {
 // allocation-free variant, else unbounded).
 size_t workspace_limit() { return g_noalloc ? (size_t)MLRS_NOALLOC_SCRATCH_BYTES : SIZE_MAX; }
 
-// Growing a cached buffer synchronizes the whole device (the old buffer may
-// still be read by earlier work on any stream, and hipFree synchronizes the
-// device anyway).
+// 1 where the device has stream-ordered memory pools, 0 where not, -1 unknown.
+int g_mempools[kMaxDevices];
+bool g_mempools_init = [] {
+    for (int& v : g_mempools) v = -1;
+    return true;
+}();
+
+// Replace a cached buffer (*base, *pooled) by one of `want` bytes.  The old
+// buffer is read only by the library's own earlier work on this device, and
+// the call ordering (order_after_last_call, which every grower runs first)
+// has already put stream `s` after all of it.  With memory pools the old
+// buffer is therefore returned and the new one taken in stream order on `s`
+// (hipFreeAsync, hipMallocAsync): neither waits for other streams, nor for
+// the host.  Without them (and for a buffer hipMalloc made) the old buffer
+// goes after a device-wide synchronize, since hipFree waits for the device.
+// On failure *base is null.
+hipError_t buffer_regrow(int dev, char** base, bool* pooled, size_t want, hipStream_t s) {
+    if (g_mempools[dev] < 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMemoryPoolsSupported, dev) != hipSuccess) v = 0;
+        g_mempools[dev] = v ? 1 : 0;
+    }
+    hipError_t e = hipSuccess;
+    if (*base) {
+        if (*pooled) {
+            e = hipFreeAsync(*base, s);
+        } else {
+            e = hipDeviceSynchronize();
+            if (e == hipSuccess) (void)hipFree(*base);
+        }
+        *base = nullptr;
+        if (e != hipSuccess) return e;
+    }
+    if (g_mempools[dev]) {
+        e = hipMallocAsync((void**)base, want, s);
+        *pooled = true;
+    } else {
+        e = hipMalloc((void**)base, want);
+        *pooled = false;
+    }
+    if (e != hipSuccess) *base = nullptr;
+    return e;
+}
+
+// Return a cached buffer at release (the caller has synchronized the device).
+void buffer_free(char** base, bool* pooled) {
+    if (!*base) return;
+    if (*pooled) {
+        (void)hipFreeAsync(*base, nullptr);
+        (void)hipStreamSynchronize(nullptr);
+    } else {
+        (void)hipFree(*base);
+    }
+    *base = nullptr;
+    *pooled = false;
+}
+
+// Growing a cached buffer waits for nothing but the call's own stream order
+// (buffer_regrow).
 int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
     int dev = 0;
     int32_t rc = current_device(&dev);
@@ -242,17 +298,10 @@ int32_t workspace(size_t bytes, hipStream_t s, char** out, int* cus) {
     if (rc) return rc;
     if (A.cap < bytes) {
         const size_t old_cap = A.cap;
-        if (A.base) {
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
-            (void)hipFree(A.base);
-            A.base = nullptr;
-            A.cap = 0;
-        }
         size_t want = std::max(bytes + bytes / 4, (size_t)64 << 20);
-        e = hipMalloc((void**)&A.base, want);
+        e = buffer_regrow(dev, &A.base, &A.pooled, want, s);
         if (e != hipSuccess) {
-            A.base = nullptr;
+            A.cap = 0;
             pool_note_release(dev, old_cap);
             return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)want, 0, 0, (int)e,
                            "device workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
@@ -408,21 +457,27 @@ int32_t knn_generic(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d,
         }
         if (e != hipSuccess) return hip_err(e, "row_norms");
     }
+    const bool minkowski = (arm == ARM_MINKOWSKI_INT || arm == ARM_MINKOWSKI_POW);
+    // EMIT_ROOT_RANKED: the tile holds the roots (sqrt, or pow(v, 1/p) for
+    // Minkowski), so the selection ranks by (root, index)
+    const bool ranked = mode == EMIT_ROOT_RANKED;
+    const int root = ranked ? (minkowski ? 2 : 1) : 0;
     for (int64_t q0 = 0; q0 < nq; q0 += qt) {
         int64_t rows = std::min<int64_t>(qt, nq - q0);
         hipError_t e;
         {
             KernelTimer timer(s, "pairwise_tile_kernel");
             e = launch_pairwise_tile<T>(xq + q0 * d, rows, xt, nt, d, arm, cos ? qa + q0 : nullptr, xa, dist,
-                                        nt, 0, s, (T)p, minkowski_powi(p));
+                                        nt, root, s, (T)p, minkowski_powi(p), (T)(1.0 / p));
         }
         if (e == hipSuccess)
-            e = launch_select_rows<T>(dist, rows, nt, nt, k, mode, out_v + q0 * k, out_i + q0 * k, sel, s);
+            e = launch_select_rows<T>(dist, rows, nt, nt, k, ranked ? EMIT_IDENTITY : mode, out_v + q0 * k,
+                                      out_i + q0 * k, sel, s);
         if (e != hipSuccess) return hip_err(e, "generic kNN");
     }
     // Minkowski's boundary root over the emitted values, exponent
     // f64_to_host(1/p) (prims/knn.rs:882-888)
-    if (arm == ARM_MINKOWSKI_INT || arm == ARM_MINKOWSKI_POW) {
+    if (minkowski && !ranked) {
         hipError_t e = launch_pow_inplace<T>(out_v, nq * k, (T)(1.0 / p), s);
         if (e != hipSuccess) return hip_err(e, "minkowski root");
     }
@@ -581,8 +636,10 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     gram_f64_split(nq, nt, cus, &grid_wgs, &nslots);
     size_t parts = (size_t)nslots * nq * gram_list_cap(k);
     size_t qvals = gram_f64_qval_elems(grid_wgs);
+    const bool ranked = mode == EMIT_ROOT_RANKED;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(double)) + aligned_bytes(parts * sizeof(uint32_t)) +
-                   aligned_bytes(qvals * sizeof(double)) + aligned_bytes(sizeof(unsigned long long) * nq);
+                   aligned_bytes(qvals * sizeof(double)) + aligned_bytes(sizeof(unsigned long long) * nq) +
+                   (ranked ? aligned_bytes(sizeof(uint32_t) * nq) : 0);
     // the seed's screen values on the matrix cores where the workspace allows
     const bool vec2 = (d % 2 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(xt) & 15) == 0);
@@ -637,6 +694,7 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     a.part_idx = cv.take<uint32_t>(parts);
     a.qval = cv.take<double>(qvals);
     a.shared_r = cv.take<unsigned long long>(nq);
+    a.root_flag = ranked ? cv.take<unsigned int>(nq) : nullptr;
     void* seed_buf = seed_bytes ? static_cast<void*>(cv.take<char>(seed_bytes)) : nullptr;
     a.out_val = out_v;
     a.out_idx = out_i;
@@ -646,6 +704,7 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
         e = launch_gram_f64(a, arm, s);
     }
     if (e == hipSuccess) e = launch_gram_f64_merge(a, arm, s);
+    if (e == hipSuccess && ranked) e = launch_gram_f64_root_fill(a, arm, s);
     if (e != hipSuccess) return hip_err(e, "knn_gram_f64");
     return ok();
 }
@@ -825,6 +884,31 @@ int32_t mlrs_knn_topk_f32(const float* xq, int64_t xq_len, int64_t n_query, int6
                                  (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+// The allocation-free entry point's set-up on the current device, once: the
+// scratch array's device address and the CU count the split reads.  Done by
+// the first call on the device, which may have n_query = 0, so that calls
+// captured into a graph afterwards make no such query.
+static int32_t noalloc_setup(int* dev) {
+    int32_t rc = current_device(dev);
+    if (rc) return rc;
+    if (g_scratch_dev[*dev]) return MLRS_OK;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_err(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress");
+    if (g_arena[*dev].cus == 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, *dev);
+        if (e != hipSuccess) return hip_err(e, "hipDeviceGetAttribute");
+        g_arena[*dev].cus = n > 0 ? n : 1;
+    }
+    g_scratch_dev[*dev] = static_cast<char*>(ptr);
+    return MLRS_OK;
+}
+
+extern "C" {
+
 int32_t mlrs_knn_topk_f32_noalloc(const float* xq, int64_t xq_len, int64_t n_query, int64_t n_features,
                                   const float* x_train, int64_t xt_len, int64_t n_train, int32_t k, int32_t metric,
                                   double p, float* out_dist, uint32_t* out_idx, int64_t out_len, void* stream) {
@@ -832,16 +916,15 @@ int32_t mlrs_knn_topk_f32_noalloc(const float* xq, int64_t xq_len, int64_t n_que
     int32_t rc = knn_topk_f32_validate(xq, xq_len, n_query, n_features, x_train, xt_len, n_train, k, metric, p,
                                        out_dist, out_idx, out_len);
     if (rc) return rc;
-    if (n_query == 0) return MLRS_OK;
     int dev = 0;
-    rc = current_device(&dev);
-    if (rc) return rc;
-    if (!g_scratch_dev[dev]) {
-        void* ptr = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !ptr) return hip_err(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress");
-        g_scratch_dev[dev] = static_cast<char*>(ptr);
+    if (n_query == 0) {
+        // nothing to search: the device's set-up only, where there is a
+        // device (a failure is reported by the first call with queries)
+        (void)noalloc_setup(&dev);
+        return MLRS_OK;
     }
+    rc = noalloc_setup(&dev);
+    if (rc) return rc;
     NoAllocScope scope(g_scratch_dev[dev]);
     return knn_topk_f32_dispatch(xq, n_query, n_features, x_train, n_train, k, metric, p, out_dist, out_idx,
                                  (hipStream_t)stream);
@@ -1167,6 +1250,7 @@ struct RadiusPlan {
     unsigned long long total = 0;
     char* base = nullptr;
     size_t cap = 0;
+    bool pooled = false;  // base came from hipMallocAsync
 };
 RadiusPlan g_rplan[kMaxDevices];
 
@@ -1219,7 +1303,8 @@ static size_t radius_carve(char* base, int64_t nq, int64_t nt, int64_t d, int ns
     return cv.off + 256;
 }
 
-static int32_t radius_plan_memory(RadiusPlan& P, size_t bytes) {
+// (The call has run order_after_last_call on `s` through workspace().)
+static int32_t radius_plan_memory(RadiusPlan& P, size_t bytes, hipStream_t s) {
     const int dev = (int)(&P - g_rplan);
     if (P.cap >= bytes) {
         g_pool[dev].reuses += 1;
@@ -1227,17 +1312,10 @@ static int32_t radius_plan_memory(RadiusPlan& P, size_t bytes) {
     }
     const size_t old_cap = P.cap;
     P.valid = false;
-    if (P.base) {
-        hipError_t e = hipDeviceSynchronize();
-        if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
-        (void)hipFree(P.base);
-        P.base = nullptr;
-        P.cap = 0;
-    }
     size_t want = std::max(bytes + bytes / 4, (size_t)16 << 20);
-    hipError_t e = hipMalloc((void**)&P.base, want);
+    hipError_t e = buffer_regrow(dev, &P.base, &P.pooled, want, s);
     if (e != hipSuccess) {
-        P.base = nullptr;
+        P.cap = 0;
         pool_note_release(dev, old_cap);
         return set_err(MLRS_ERR_ALLOC, "radius", (int64_t)want, 0, 0, (int)e,
                        "device allocation of %zu bytes for the radius scan failed: %s", want, hipGetErrorString(e));
@@ -1360,7 +1438,7 @@ static int32_t radius_impl(const T* xq, int64_t xq_len, int64_t nq, int64_t d, c
     const size_t need = radius_carve<T>(nullptr, nq, nt, d, nstrips, stage_cap, &B);
     if (!same) {
         P.valid = false;
-        rc = radius_plan_memory(P, need);
+        rc = radius_plan_memory(P, need, s);
         if (rc) return rc;
     }
     (void)radius_carve<T>(P.base, nq, nt, d, nstrips, stage_cap, &B);
@@ -1562,17 +1640,10 @@ static int32_t aux_workspace(size_t bytes, hipStream_t s, char** out) {
     Arena& A = g_aux[dev];
     if (A.cap < bytes) {
         const size_t old_cap = A.cap;
-        if (A.base) {
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
-            (void)hipFree(A.base);
-            A.base = nullptr;
-            A.cap = 0;
-        }
         size_t want = std::max(bytes + bytes / 4, (size_t)16 << 20);
-        e = hipMalloc((void**)&A.base, want);
+        e = buffer_regrow(dev, &A.base, &A.pooled, want, s);
         if (e != hipSuccess) {
-            A.base = nullptr;
+            A.cap = 0;
             pool_note_release(dev, old_cap);
             return set_err(MLRS_ERR_ALLOC, "workspace", (int64_t)want, 0, 0, (int)e,
                            "device allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
@@ -1615,14 +1686,19 @@ static int32_t validate_graph(const void* x, int64_t x_len, int64_t n, int64_t d
 
 // The host scans' per-metric arithmetic as engine arms (umap_host_knn.rs:318-411):
 // Euclidean and cosine accumulate diff*diff with separate rounding (cosine over
-// normalised rows), Minkowski always through pow.
+// normalised rows), Minkowski always through pow.  The scans push the final
+// distance, `(ops.fin)(a)` (:494), into a list ordered by (distance, index)
+// (KNearest::push, :171-198): Euclidean and Minkowski are ranked by their root
+// (EMIT_ROOT_RANKED), so aggregates that root to the same value are ordered
+// by index; the other finals (identity, the exact halving of cosine) keep the
+// aggregate's order.
 static void graph_arm(int32_t metric, int* arm, int* mode) {
     switch (metric) {
-    case MLRS_METRIC_EUCLIDEAN: *arm = ARM_EUCLID_MULADD; *mode = EMIT_SQRT; break;
+    case MLRS_METRIC_EUCLIDEAN: *arm = ARM_EUCLID_MULADD; *mode = EMIT_ROOT_RANKED; break;
     case MLRS_METRIC_COSINE: *arm = ARM_EUCLID_MULADD; *mode = EMIT_IDENTITY; break;
     case MLRS_METRIC_MANHATTAN: *arm = ARM_MANHATTAN; *mode = EMIT_IDENTITY; break;
     case MLRS_METRIC_CHEBYSHEV: *arm = ARM_CHEBYSHEV; *mode = EMIT_IDENTITY; break;
-    default: *arm = ARM_MINKOWSKI_POW; *mode = EMIT_IDENTITY; break;
+    default: *arm = ARM_MINKOWSKI_POW; *mode = EMIT_ROOT_RANKED; break;
     }
 }
 
@@ -2413,21 +2489,18 @@ int32_t mlrs_release_workspace(void) {
         if (e != hipSuccess) return hip_err(e, "hipDeviceSynchronize");
     }
     if (A.base) {
-        (void)hipFree(A.base);
+        buffer_free(&A.base, &A.pooled);
         pool_note_release(dev, A.cap);
-        A.base = nullptr;
         A.cap = 0;
     }
     if (X.base) {
-        (void)hipFree(X.base);
+        buffer_free(&X.base, &X.pooled);
         pool_note_release(dev, X.cap);
-        X.base = nullptr;
         X.cap = 0;
     }
     if (P.base) {
-        (void)hipFree(P.base);
+        buffer_free(&P.base, &P.pooled);
         pool_note_release(dev, P.cap);
-        P.base = nullptr;
         P.cap = 0;
         P.valid = false;
     }

@@ -57,7 +57,10 @@ template <bool COS>
 __device__ __forceinline__ double screen_threshold64(double R, double qs, double eps) {
     const double inf = __builtin_huge_val();
     if (!(R < inf)) return inf;
-    if (!COS) return (R - qs) + eps;
+    // Euclidean: R widened by a relative 2^-48, so that every pair whose root
+    // equals the root of a value <= R passes too (the X-vs-X graph ranks by
+    // the root, and sqrt maps at most a few consecutive doubles to one)
+    if (!COS) return ((R + __builtin_fabs(R) * 0x1p-48) - qs) + eps;
     if (qs == 0.0) return inf;  // a zero query ties every row: never screened
     return ((R + eps) - 1.0) * qs;
 }
@@ -328,6 +331,8 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
         else                                                                                 \
             dm_ = wave_merge_blocks_drop<double, KL>(lv_, li_, e_, t_, lane);                \
         double R_ = list_value_at<double, KL>(lv_, k - 1);                                   \
+        /* the smallest exact value the list drops (exact lists only) */                     \
+        double dx_ = exact_ ? ((K2 < 64 * KL) ? list_value_at<double, KL>(lv_, K2) : dm_) : inf; \
         if (!exact_) {                                                                       \
             const double dr_ = (K2 < 64 * KL) ? list_value_at<double, KL>(lv_, K2) : dm_;    \
             double w_ = R_ + 2.0 * L.eps[j_];                                                \
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
                 if (x2_ != x2_) { x2_ = inf; i2_ = kSentinelIdx; }                           \
                 wave_sort64<double>(x1_, i1_, lane);                                         \
                 wave_sort64<double>(x2_, i2_, lane);                                         \
-                wave_merge64<double>(x1_, i1_, x2_, i2_, lane);                              \
+                dx_ = wave_merge64_drop<double>(x1_, i1_, x2_, i2_, lane);                   \
                 lv_[0] = x1_;                                                                \
                 li_[0] = i1_;                                                                \
               } else {                                                                       \
@@ -363,9 +368,10 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
                     if (i_ != kSentinelIdx) x_ = MLRS_EXACT64_AT(i_);                        \
                     if (x_ != x_) { x_ = inf; i_ = kSentinelIdx; }                           \
                     wave_sort64<double>(x_, i_, lane);                                       \
-                    wave_merge_blocks<double, KL>(lv_, li_, x_, i_, lane);                   \
+                    dx_ = fmin(dx_, wave_merge_blocks_drop<double, KL>(lv_, li_, x_, i_, lane)); \
                 }                                                                            \
               }                                                                              \
+                if (K2 < 64 * KL) dx_ = fmin(dx_, list_value_at<double, KL>(lv_, K2));       \
                 R_ = list_value_at<double, KL>(lv_, k - 1);                                  \
                 if (lane == 0) L.mode[j_] = 1u;                                              \
             } else if (R_ < inf) {                                                           \
@@ -379,6 +385,10 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
                 LI[qg_ * K2 + p_] = li_[r_];                                                 \
             }                                                                                \
         }                                                                                    \
+        /* a dropped exact value whose root may equal the k-th's: the merge */               \
+        /* cannot rank that root's ties by index, the root fill will */                      \
+        if (a.root_flag && lane == 0 && dx_ < inf && dx_ <= R_ + __builtin_fabs(R_) * 0x1p-48) \
+            a.root_flag[qg_] = 1u;                                                           \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf && R_ >= 0.0) {                                         \
                 const unsigned long long old_ =                                              \
@@ -591,6 +601,10 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
 // k-th smallest value over all lists a pair can be among the k best only if
 // its value is <= V + 2 eps: exactly those pairs are evaluated in the arm's
 // operation order and ranked by (exact value, index), NaN never admitted.
+// EMIT_ROOT_RANKED ranks by (sqrt(exact value), index) instead: every pair
+// whose root equals the k-th root lies within V + 2 eps too (its aggregate
+// exceeds the k-th by a relative 2^-50 at most), and the kernel's screen and
+// drops keep all of them listed unless root_flag says otherwise.
 template <int ARM, bool VEC2>
 __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
     __shared__ uint32_t cand[4][128];
@@ -635,6 +649,8 @@ __global__ __launch_bounds__(256) void knn_merge_f64_kernel(GramArgs64 a) {
             if (e != e) {
                 e = inf;
                 t = kSentinelIdx;
+            } else if (a.mode == EMIT_ROOT_RANKED) {
+                e = __builtin_sqrt(e);  // ranked by (root, index)
             }
         }
         wave_sort64<double>(e, t, lane);
@@ -744,6 +760,8 @@ __global__ __launch_bounds__(256) void knn_merge_blocks_f64_kernel(GramArgs64 a)
             if (e != e) {
                 e = inf;
                 t = kSentinelIdx;
+            } else if (a.mode == EMIT_ROOT_RANKED) {
+                e = __builtin_sqrt(e);  // ranked by (root, index)
             }
         }
         wave_sort64<double>(e, t, lane);
@@ -782,6 +800,48 @@ __global__ __launch_bounds__(256) void knn_merge_blocks_f64_kernel(GramArgs64 a)
             a.out_val[o] = (a.mode == EMIT_SQRT) ? __builtin_sqrt(lv[r]) : lv[r];
             a.out_idx[o] = (li[r] == kSentinelIdx) ? 0u : li[r];
         }
+    }
+}
+
+// EMIT_ROOT_RANKED, queries with root_flag set (an exact list dropped a pair
+// whose root may equal the k-th root, so ties of that root may be missing
+// from the merge): the emitted row keeps its m entries below the k-th root
+// r (all pairs with a smaller root: their aggregates are below the k-th, so
+// the merge saw them) and slots m..k-1 get r with the lowest-index rows whose
+// root is r, found by evaluating every index row in ascending order, 64 at a
+// time (one wave per query; unflagged queries return at once).  This is the
+// host scan's KNearest order (crates/mlrs-algos/src/manifold/
+// umap_host_knn.rs:171-198): (root, index).
+template <int ARM, bool VEC2>
+__global__ __launch_bounds__(256) void knn_root_fill_f64_kernel(GramArgs64 a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t qg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (qg >= a.nq || a.root_flag[qg] == 0u) return;
+    const int k = a.k;
+    double* ov = a.out_val + qg * k;
+    uint32_t* oi = a.out_idx + qg * k;
+    const double r = ov[k - 1];
+    if (!(r < __builtin_huge_val())) return;
+    uint32_t m = 0;
+    for (int j0 = 0; j0 < k; j0 += 64)
+        m += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(j0 + lane < k && ov[j0 + lane] < r));
+    const uint32_t need = (uint32_t)k - m;
+    const int64_t d = a.d;
+    uint32_t found = 0;
+    for (int64_t t0 = 0; t0 < a.nt && found < need; t0 += 64) {
+        const int64_t t = t0 + lane;
+        bool hit = false;
+        if (t < a.nt) {
+            const double e = exact_f64<ARM, VEC2, 8>(a.q + qg * d, a.x + t * d, d, 0.0, 0.0);
+            hit = (e == e) && __builtin_sqrt(e) == r;
+        }
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(hit);
+        const uint32_t pos = found + (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull));
+        if (hit && pos < need) {
+            ov[m + pos] = r;
+            oi[m + pos] = (uint32_t)t;
+        }
+        found += (uint32_t)__builtin_popcountll(bal);
     }
 }
 
@@ -972,6 +1032,10 @@ hipError_t launch_seed64(const GramArgs64& a, int64_t nsamp, hipStream_t s) {
 }
 
 hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s, void* seed_buf) {
+    if (a.root_flag) {
+        const hipError_t e = launch_fill_u32(a.root_flag, a.nq, 0u, s);
+        if (e != hipSuccess) return e;
+    }
     if (!a.shared_r) return hipSuccess;
     if (seed_buf && a.k > 1) {
         const bool cos = (arm == ARM_COS_FOLD || arm == ARM_COS_HOST);
@@ -1057,6 +1121,28 @@ hipError_t launch_gram_f64_merge(const GramArgs64& a, int arm, hipStream_t s) {
     if (arm == ARM_COS_FOLD) return launch_merge64<ARM_COS_FOLD>(a, vec2, s);
     if (arm == ARM_COS_HOST) return launch_merge64<ARM_COS_HOST>(a, vec2, s);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_gram_f64_root_fill(const GramArgs64& a, int arm, hipStream_t s) {
+    if (!a.root_flag || a.mode != EMIT_ROOT_RANKED) return hipSuccess;
+    const bool vec2 = (a.d % 2 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    const dim3 grid((unsigned)((a.nq + 3) / 4));
+    if (arm == ARM_EUCLID_MULADD) {
+        if (vec2)
+            hipLaunchKernelGGL((knn_root_fill_f64_kernel<ARM_EUCLID_MULADD, true>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((knn_root_fill_f64_kernel<ARM_EUCLID_MULADD, false>), grid, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    if (arm == ARM_EUCLID_FMA) {
+        if (vec2)
+            hipLaunchKernelGGL((knn_root_fill_f64_kernel<ARM_EUCLID_FMA, true>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((knn_root_fill_f64_kernel<ARM_EUCLID_FMA, false>), grid, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;  // the roots are sqrt: Euclidean arms only
 }
 
 }  // namespace mlrs

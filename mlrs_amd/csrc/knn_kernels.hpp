@@ -10,6 +10,11 @@ enum EmitMode : int {
     EMIT_SQRT = 0,      // Euclidean kNN: boundary sqrt of the k kept squared values
     EMIT_IDENTITY = 1,  // cosine kNN: values as kept
     EMIT_KMEANS = 2,    // k-means assignment: squared value + argmin centre-0 rule
+    // X-vs-X graph (the host scans' KNearest): the values are the roots
+    // (sqrt for the Euclidean arms, pow(v, 1/p) for Minkowski) and the lists
+    // are ranked by (root, index), so two aggregates that root to the same
+    // value are ordered by index
+    EMIT_ROOT_RANKED = 3,
 };
 
 // Device-resident summary of the index rows' squared norms, written by the
@@ -188,6 +193,10 @@ struct GramArgs64 {
     double* out_val;      // [nq][k]
     uint32_t* out_idx;
     unsigned long long* shared_r;  // [nq] best known exact k-th value per query (double bits)
+    // EMIT_ROOT_RANKED only, else null: [nq], set to 1 where an exact list
+    // dropped a pair whose root may equal the k-th root (the merge cannot
+    // then rank that root's ties by index; launch_gram_f64_root_fill does)
+    unsigned int* root_flag;
 };
 
 void gram_f64_split(int64_t nq, int64_t nt, int cus, int64_t* grid_wgs, int* nslots);
@@ -199,6 +208,9 @@ hipError_t launch_gram_f64_prep(const GramArgs64& a, int arm, hipStream_t s, voi
 size_t gram_f64_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, bool vec2);
 hipError_t launch_gram_f64(const GramArgs64& a, int arm, hipStream_t s);
 hipError_t launch_gram_f64_merge(const GramArgs64& a, int arm, hipStream_t s);
+// EMIT_ROOT_RANKED (Euclidean arms): the queries root_flag marks get the
+// rows whose root equals their k-th root in ascending index order
+hipError_t launch_gram_f64_root_fill(const GramArgs64& a, int arm, hipStream_t s);
 int gram_f64_max_k();
 int gram_f64_max_d();
 

@@ -11,11 +11,17 @@
 * An f64 brute force that sorts every row's distances, for the graph and for
   the HDBSCAN core distances (column k-1 of the self-inclusive lists), on
   inputs with ties, duplicate rows and a NaN row.
+* The ranking by the final distance (KNearest::push of `(ops.fin)(a)`,
+  crates/mlrs-algos/src/manifold/umap_host_knn.rs:171-198, 494): on rows
+  whose aggregates differ by one ulp but root to the same double
+  (tests/rooted_ties.py), the oracle's lists are the (root, index) order of
+  a numpy brute force and differ from the (aggregate, index) order.
 """
 import numpy as np
 import pytest
 
 import oracle
+import rooted_ties
 from conftest import load_golden
 
 METRICS = ["euclidean", "manhattan", "chebyshev", "minkowski", "cosine"]
@@ -136,3 +142,19 @@ def test_nan_row_and_errors():
         oracle.knn_graph(x, 40, "euclidean")      # k > n - 1
     with pytest.raises(ValueError):
         oracle.core_distances(x, 3, "cosine")
+
+
+@pytest.mark.parametrize("metric", ["euclidean", "minkowski"])
+@pytest.mark.parametrize("k", [6, 10, 20, 32])
+@pytest.mark.parametrize("include_self", [False, True])
+def test_graph_ranks_by_root(metric, k, include_self):
+    x, p = rooted_ties.build(metric, k)
+    want_i, want_d = rooted_ties.brute_graph(x, k, metric, p, by_root=True, include_self=include_self)
+    agg_i, _ = rooted_ties.brute_graph(x, k, metric, p, by_root=False, include_self=include_self)
+    assert not np.array_equal(want_i, agg_i)   # the data separates the two orders
+    got_i, got_d = oracle.knn_graph(x, k, metric, p=p, include_self=include_self)
+    np.testing.assert_array_equal(got_i, want_i)
+    # the groups' query rows: every value an exact root
+    cen = [i for i in range(x.shape[0]) if x[i, 0] % 100.0 == 0.0]
+    np.testing.assert_array_equal(got_d[cen], want_d[cen])
+    np.testing.assert_allclose(got_d, want_d, rtol=4 * np.finfo(np.float64).eps, atol=0)

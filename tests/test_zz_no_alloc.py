@@ -3,9 +3,13 @@ the allocating one (mlrs_knn_topk_f32), bit for bit, through the C ABI.
 
 Each case makes two calls in a row, the second with a smaller input, so the
 static scratch is reused with the first call's contents still in it.  The
-three kernel families (fused Gram, low-d, exact tiles) are each reached.  A
+three kernel families (fused Gram, low-d, exact tiles) are each reached, and
+the library's buffer counters (allocations, reuses, live bytes) must not move
+across an allocation-free call: the cached buffers are never touched.  A
 search whose scratch would exceed MLRS_NOALLOC_SCRATCH_BYTES is rejected
-before any launch.
+before any launch.  Calls captured into a HIP graph (torch.cuda.CUDAGraph,
+after a first call with n_query = 0 outside the capture) replay with new data
+in place, each replay bit-equal to the allocating entry point.
 """
 import ctypes
 
@@ -30,11 +34,18 @@ def _call(name, xq, xt, k, metric=0):
     return rc, dist, idx
 
 
+def _counters():
+    st = prims.pool_stats()
+    return st["allocations"], st["reuses"], st["live_bytes"]
+
+
 def _both(xq, xt, k, metric=0):
     rc, d0, i0 = _call("mlrs_knn_topk_f32", xq, xt, k, metric)
     _lib.check(rc)
+    before = _counters()
     rc, d1, i1 = _call("mlrs_knn_topk_f32_noalloc", xq, xt, k, metric)
     _lib.check(rc)
+    assert _counters() == before, "the allocation-free call touched the cached buffers"
     torch.cuda.synchronize()
     assert torch.equal(i0, i1), "indices differ"
     assert torch.equal(d0.view(torch.int32), d1.view(torch.int32)), "distance bits differ"
@@ -87,3 +98,47 @@ def test_noalloc_rejects_scratch_beyond_its_size():
     # the device is untouched and usable afterwards
     xq2, xt2 = _rand(1, 300, 128), _rand(2, 30000, 128)
     _both(xq2, xt2, 32)
+
+
+@pytest.mark.parametrize("family,shape", [("fused", (1200, 60000, 128, 32)), ("fused", (1000, 40000, 64, 1)),
+                                          ("lowd", (4000, 50000, 3, 8)), ("generic", (300, 5000, 64, 10))])
+def test_noalloc_graph_capture_replays(family, shape):
+    nq, nt, d, k = shape
+    prims.force_path(family)
+    try:
+        xq, xt = _rand(nq + d, nq, d), _rand(nt + d, nt, d)
+        dist = torch.full((nq, k), -1.0, dtype=torch.float32, device=DEV)
+        idx = torch.full((nq, k), -1, dtype=torch.int32, device=DEV)
+        lib = _lib.load()
+
+        def call():
+            s = torch.cuda.current_stream(DEV).cuda_stream
+            return lib.mlrs_knn_topk_f32_noalloc(xq.data_ptr(), xq.numel(), nq, d, xt.data_ptr(), xt.numel(), nt,
+                                                 k, 0, 2.0, dist.data_ptr(), idx.data_ptr(), dist.numel(), s)
+
+        # set-up outside the capture: a call with no queries
+        _lib.check(lib.mlrs_knn_topk_f32_noalloc(xq.data_ptr(), 0, 0, d, xt.data_ptr(), xt.numel(), nt, k, 0, 2.0,
+                                                  dist.data_ptr(), idx.data_ptr(), 0,
+                                                  torch.cuda.current_stream(DEV).cuda_stream))
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        rcs = []
+        with torch.cuda.graph(g):
+            rcs.append(call())
+        assert rcs == [0]
+        for rep in range(3):
+            # new data in the captured buffers, written by eager work
+            xq.copy_(_rand(1000 + rep, nq, d))
+            xt.copy_(_rand(2000 + rep, nt, d))
+            xt[7] = xt[3]  # a tie
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            rc, d0, i0 = _call("mlrs_knn_topk_f32", xq, xt, k)
+            _lib.check(rc)
+            torch.cuda.synchronize()
+            assert torch.equal(i0, idx), "indices differ on replay %d" % rep
+            assert torch.equal(d0.view(torch.int32), dist.view(torch.int32)), "distance bits differ on replay %d" % rep
+        del g
+    finally:
+        prims.force_path("auto")
