@@ -63,6 +63,11 @@ def main():
                     help="measure radius_neighbors with this radius instead of the k-nearest search")
     ap.add_argument("--fit", action="store_true", help="k-means fit at c5 scale (with --config c5)")
     ap.add_argument("--fit-iters", type=int, default=10, help="Lloyd iterations per fit step (--fit)")
+    ap.add_argument("--fit-algorithm", choices=("lloyd", "elkan"), default="lloyd",
+                    help="assignment of the fit (--fit): every row each iteration, or the bound-pruned one")
+    ap.add_argument("--fit-init", choices=("random", "centroids"), default="random",
+                    help="initial centres of the fit (--fit): a seeded random draw of points, or c5's 1,024 "
+                         "centroids (one per mixture component)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel "
                          "of known traffic, the scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -103,7 +108,12 @@ def main():
         if radius is not None:
             return prims.radius_neighbors(ta, tb, radius, metric)
         if args.fit:
-            r = prims.kmeans_fit(ta, n_index, "random", seed=7, max_iter=args.fit_iters, tol=0.0)
+            if args.fit_init == "centroids":
+                r = prims.kmeans_fit(ta, n_index, "array", tb, max_iter=args.fit_iters, tol=0.0,
+                                     algorithm=args.fit_algorithm)
+            else:
+                r = prims.kmeans_fit(ta, n_index, "random", seed=7, max_iter=args.fit_iters, tol=0.0,
+                                     algorithm=args.fit_algorithm)
             fit_iters.append(r[3])
             return r
         if kmeans:
@@ -153,8 +163,14 @@ def main():
         import oracle
         fc, fl, finert, fit_n = out
         npre = 200_000
-        wc, wl, wi, wn = oracle.kmeans_fit(a[:npre], n_index, "random", seed=7, max_iter=3, tol=0.0)
-        gc, gl, gi, gn = prims.kmeans_fit(ta[:npre].contiguous(), n_index, "random", seed=7, max_iter=3, tol=0.0)
+        if args.fit_init == "centroids":
+            wc, wl, wi, wn = oracle.kmeans_fit(a[:npre], n_index, "array", b, max_iter=3, tol=0.0)
+            gc, gl, gi, gn = prims.kmeans_fit(ta[:npre].contiguous(), n_index, "array", tb, max_iter=3, tol=0.0,
+                                              algorithm=args.fit_algorithm)
+        else:
+            wc, wl, wi, wn = oracle.kmeans_fit(a[:npre], n_index, "random", seed=7, max_iter=3, tol=0.0)
+            gc, gl, gi, gn = prims.kmeans_fit(ta[:npre].contiguous(), n_index, "random", seed=7, max_iter=3,
+                                              tol=0.0, algorithm=args.fit_algorithm)
         ok = (np.array_equal(gl.cpu().numpy(), wl.astype(np.int64)) and np.array_equal(gc.cpu().numpy(), wc)
               and gi == wi and gn == wn)
         sub = np.arange(npre)
@@ -223,6 +239,10 @@ def main():
         # units without packed math (an FMA counts two flops)
         bound, peak, unit = "valu", PEAKS["valu_f64" if f64 else "valu_f32"], "TFLOP/s"
     achieved = flops / (kern_ms_step / 1000.0) / 1e12
+    if args.fit and args.fit_algorithm == "elkan":
+        # the bound-pruned fit searches only the rows its bounds leave: the
+        # Lloyd fit's flops over its kernel time would overstate the rate
+        achieved = None
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "traffic_%s%s.json" % ("radius_" if radius is not None else "",
                                                                    args.config))
@@ -284,8 +304,10 @@ def main():
           "d256": "d256: 200k index x 5k queries, d=256, k=32, f32, 100-comp GMM",
           "c2k128": "c2k128: c2's data (1M index x 10k queries, d=128) with k=128, f32"}[args.config]
     if args.fit:
-        wl = ("k-means fit at c5 scale: 5M points into 1024 clusters, d=64, f32, seeded random init, tol 0, "
-              "at most %d Lloyd iterations per step" % args.fit_iters)
+        wl = ("k-means fit at c5 scale: 5M points into 1024 clusters, d=64, f32, %s init, tol 0, "
+              "at most %d Lloyd iterations per step, algorithm=%s"
+              % ("seeded random" if args.fit_init == "random" else "the c5 centroids' (explicit)", args.fit_iters,
+                 args.fit_algorithm))
     if radius is not None:
         wl = "radius_neighbors, radius %g, on %s (%d matches, %.1f per query)" % (radius, wl, matches,
                                                                                  matches / n_query)
@@ -313,7 +335,8 @@ def main():
                    "queries_per_s": n_query / (ms_per_step / 1000.0), "parity": parity},
         "fit": ({"iterations": float(np.mean(fit_iters[-args.steps:])), "ms_per_iteration": ms_per_iter}
                 if args.fit else None),
-        "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
+        "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                     "frac": achieved / peak if achieved is not None else None,
                      "traffic": traffic, "kernel": name.value.decode(), "kernel_ms": kern_ms,
                      "kernel_launches_per_step": launches.value / args.steps, "kernel_ms_per_step": kern_ms_step,
                      "basis": {"mfma": "dense MFMA peak, 2*d flops per distance evaluation",

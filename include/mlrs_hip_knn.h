@@ -72,7 +72,7 @@ int32_t mlrs_last_error(mlrs_error_info *out);
 const char *mlrs_status_string(int32_t code);
 /* ABI version of this header (bumped on any signature change). */
 int32_t mlrs_abi_version(void);
-#define MLRS_ABI_VERSION 4
+#define MLRS_ABI_VERSION 5
 
 /*
  * Brute-force k nearest training rows of every query row.
@@ -374,25 +374,35 @@ int32_t mlrs_hdbscan_core_distances_f64(const double *x, int64_t x_len, int64_t 
  *   relocate_empty_clusters, the f64 mean update, the strict label-equality
  *   break then the tol break, inertia_rows + sum_device, and the restart rule
  *   (strictly lower inertia on a partition that is not a relabelling).
- *   algorithm = 'elkan' returns the same fit in the reference, so this loop
- *   serves both.
+ * algorithm: MLRS_KMEANS_LLOYD runs the fused k = 1 assignment over every row
+ *   each iteration (assign_min); MLRS_KMEANS_ELKAN the bound-pruned one
+ *   (elkan_init_bounds / elkan_assign_device / elkan_relax_bounds,
+ *   prims/kmeans.rs:1523-1717), without the reference's n x k lower bounds:
+ *   per row an upper bound on its centre distance, the sorted k x k half
+ *   centre distances, and the fused search for the rows those cannot settle.
+ *   Both return the same fit, bit for bit (labels, centres, inertia, n_iter),
+ *   as the reference pins for its two arms; 'elkan' serves k <= 4096 with
+ *   finite rows and runs Lloyd otherwise.
  * init_kind: 0 explicit centres (init, device, k x n_features; one run), 1
  *   k-means++, 2 random.  out_centers (k x n_features, device, F),
  *   out_labels (n, device), *out_inertia and *out_n_iter (host) of the
  *   winning restart.  Synchronous.
  * Errors: InvalidParam "k" (AlgoError::InvalidK text), "n_init", "max_iter",
- *   "tol"; ShapeMismatch "x", "init", "centers", "labels", and "labels"
+ *   "tol", "algorithm"; ShapeMismatch "x", "init", "centers", "labels", and "labels"
  *   {n, k, empty clusters} when an empty cluster finds no donor row;
  *   Unsupported "init".
  */
+#define MLRS_KMEANS_LLOYD 0
+#define MLRS_KMEANS_ELKAN 1
 int32_t mlrs_kmeans_fit_f32(const float *x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
                             int32_t init_kind, const float *init, int64_t init_len, uint64_t seed, int64_t n_init,
-                            int64_t max_iter, double tol, float *out_centers, int64_t centers_len,
+                            int64_t max_iter, double tol, int32_t algorithm, float *out_centers, int64_t centers_len,
                             uint32_t *out_labels, int64_t labels_len, double *out_inertia, int64_t *out_n_iter,
                             void *stream);
 int32_t mlrs_kmeans_fit_f64(const double *x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
                             int32_t init_kind, const double *init, int64_t init_len, uint64_t seed, int64_t n_init,
-                            int64_t max_iter, double tol, double *out_centers, int64_t centers_len,
+                            int64_t max_iter, double tol, int32_t algorithm, double *out_centers,
+                            int64_t centers_len,
                             uint32_t *out_labels, int64_t labels_len, double *out_inertia, int64_t *out_n_iter,
                             void *stream);
 

@@ -119,9 +119,9 @@ SIGNATURES = {
     "mlrs_hdbscan_core_distances_f32": (_i32, [_vp, _i64, _i64, _i64, _i32, _f64, _i64, _vp, _i64, _vp]),
     "mlrs_hdbscan_core_distances_f64": (_i32, [_vp, _i64, _i64, _i64, _i32, _f64, _i64, _vp, _i64, _vp]),
     "mlrs_kmeans_fit_f32": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, ctypes.c_uint64, _i64, _i64, _f64,
-                                   _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
+                                   _i32, _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
     "mlrs_kmeans_fit_f64": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _i64, ctypes.c_uint64, _i64, _i64, _f64,
-                                   _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
+                                   _i32, _vp, _i64, _vp, _i64, ctypes.POINTER(_f64), ctypes.POINTER(_i64), _vp]),
     "mlrs_release_workspace": (_i32, []),
     "mlrs_device_copy_f32": (_i32, [_vp, _i64, _vp, _i64, _vp]),
     "mlrs_device_copy_f64": (_i32, [_vp, _i64, _vp, _i64, _vp]),

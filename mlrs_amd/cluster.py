@@ -30,8 +30,8 @@ class KMeans:
     or a callable ``init(X, k, random_state=...)`` (evaluated once at ``fit``
     and used as an explicit init).  ``n_init="auto"`` resolves to 1 for
     k-means++ and explicit inits, 10 for "random".  ``algorithm`` "lloyd" or
-    "elkan" -- the reference's Elkan returns the same fit as Lloyd, and this
-    engine runs the Lloyd loop for both.  ``random_state=None`` is seed 0.
+    "elkan" -- the bound-pruned assignment, which returns the same fit as
+    Lloyd (as the reference's Elkan does).  ``random_state=None`` is seed 0.
     ``verbose`` / ``copy_x`` are accepted and have no effect.
     ``cluster_centers=`` sets fitted centres directly (``predict`` without ``fit``).
     """
@@ -106,8 +106,10 @@ class KMeans:
         n_init = self._resolve_n_init(init_kind)
         ini = torch.from_numpy(arr).to(device=x.device, dtype=x.dtype) if arr is not None else None
         seed = 0 if self.random_state is None else int(self.random_state)
+        algorithm = "lloyd" if k == 1 else self.algorithm
         centers, labels, inertia, n_iter = prims.kmeans_fit(x, k, init_kind, ini, seed=seed, n_init=n_init,
-                                                            max_iter=int(self.max_iter), tol=float(self.tol))
+                                                            max_iter=int(self.max_iter), tol=float(self.tol),
+                                                            algorithm=algorithm)
         self._centers_dev = centers
         self.cluster_centers_ = centers.cpu().numpy()
         self.labels_ = labels.to(torch.int32).cpu().numpy()
@@ -116,7 +118,7 @@ class KMeans:
         self.n_iter_ = n_iter
         self.n_features_in_ = d
         self._n_init = n_init
-        self._algorithm = "lloyd" if k == 1 else self.algorithm
+        self._algorithm = algorithm
         return self
 
     def fit_predict(self, X, y=None):

@@ -1933,8 +1933,9 @@ static int32_t km_rank_device(const T* dist, const uint32_t* labels, int64_t n, 
 template <typename T>
 static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, int64_t k, int32_t init_kind,
                                const T* init, int64_t init_len, uint64_t seed, int64_t n_init, int64_t max_iter,
-                               double tol, T* out_centers, int64_t centers_len, uint32_t* out_labels,
-                               int64_t labels_len, double* out_inertia, int64_t* out_n_iter, void* stream) {
+                               double tol, int32_t algorithm, T* out_centers, int64_t centers_len,
+                               uint32_t* out_labels, int64_t labels_len, double* out_inertia, int64_t* out_n_iter,
+                               void* stream) {
     CallGuard cg;
     if (k < 1 || k > n)
         return set_err(MLRS_ERR_INVALID_PARAM, "k", 1, k, n, 0,
@@ -1949,6 +1950,9 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     if (n_init < 1) return set_err(MLRS_ERR_INVALID_PARAM, "n_init", n_init, 0, 0, 0, "n_init must be >= 1");
     if (max_iter < 0) return set_err(MLRS_ERR_INVALID_PARAM, "max_iter", max_iter, 0, 0, 0, "max_iter must be >= 0");
     if (!(tol >= 0.0)) return set_err(MLRS_ERR_INVALID_PARAM, "tol", 0, 0, 0, 0, "tol must be >= 0");
+    if (algorithm != MLRS_KMEANS_LLOYD && algorithm != MLRS_KMEANS_ELKAN)
+        return set_err(MLRS_ERR_INVALID_PARAM, "algorithm", algorithm, 0, 0, 0,
+                       "algorithm %d is neither lloyd (0) nor elkan (1)", algorithm);
     if (centers_len != k * d) return shape_err("centers", k, d, centers_len);
     if (labels_len != n) return shape_err("labels", n, 1, labels_len);
     if (!x || !out_centers || !out_labels || !out_inertia || !out_n_iter || (init_kind == 0 && !init))
@@ -1969,6 +1973,21 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                    aligned_bytes(sizeof(T) * (size_t)(nb * kd)) + 2 * aligned_bytes(sizeof(T) * (size_t)kd) +
                    aligned_bytes(sizeof(T) * (size_t)std::max(nbi, nbv * d)) + aligned_bytes(sizeof(T) * d) +
                    aligned_bytes(sizeof(int64_t) * k) + 1024;
+    // algorithm = 'elkan': the bound-pruned assignment (launch_km_elkan) for
+    // k <= 4096 (its k x k half-distance tables), k > 1 and finite rows: per
+    // row an f64 upper bound and a slot of the fused-search list; the k x k
+    // tables (sorted rows); and dense buffers for up to prune_chunk rows (1 GB)
+    // of one fused search of the rows it cannot settle itself.
+    bool prune = algorithm == MLRS_KMEANS_ELKAN && k > 1 && k <= 4096;
+    const int64_t prune_chunk =
+        std::max<int64_t>(64, std::min<int64_t>(n, ((int64_t)1 << 30) / (d * (int64_t)sizeof(T))));
+    const size_t psel = prune ? select_rows_scratch_bytes(k, (int)k, (int)sizeof(double)) : 0;
+    if (prune)
+        bytes += aligned_bytes(sizeof(double) * (size_t)n) + aligned_bytes(sizeof(uint32_t) * (size_t)n) +
+                 2 * aligned_bytes(sizeof(double) * (size_t)(k * k)) + aligned_bytes(sizeof(uint32_t) * (size_t)(k * k)) +
+                 2 * aligned_bytes(sizeof(double) * (size_t)k) + aligned_bytes(sizeof(uint32_t)) + aligned_bytes(psel) +
+                 aligned_bytes(sizeof(T) * (size_t)(prune_chunk * d)) + 2 * aligned_bytes(sizeof(T) * (size_t)prune_chunk) +
+                 aligned_bytes(sizeof(uint32_t) * (size_t)prune_chunk) + 1024;
     char* aux;
     int32_t rc = aux_workspace(bytes, s, &aux);
     if (rc) return rc;
@@ -1996,6 +2015,84 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     T* xsq = cv.take<T>(n);
     hipError_t e = launch_row_norms<T>(x, n, d, xsq, nullptr, nullptr, nullptr, s);
     if (e != hipSuccess) return hip_err(e, "kmeans row norms");
+    KmPruneConsts pc{};
+    double* pU = nullptr;
+    uint32_t* pfb = nullptr;
+    double *phcd = nullptr, *psv = nullptr, *pdnc = nullptr, *pdelta = nullptr;
+    uint32_t* psi = nullptr;
+    unsigned int* pfbn = nullptr;
+    void* pscratch = nullptr;
+    T *pxs = nullptr, *pxsq = nullptr, *pdist = nullptr;
+    uint32_t* plab = nullptr;
+    if (prune) {
+        pU = cv.take<double>(n);
+        pfb = cv.take<uint32_t>(n);
+        phcd = cv.take<double>(k * k);
+        psv = cv.take<double>(k * k);
+        psi = cv.take<uint32_t>(k * k);
+        pdnc = cv.take<double>(k);
+        pdelta = cv.take<double>(k);
+        pfbn = reinterpret_cast<unsigned int*>(cv.take<uint32_t>(1));
+        pscratch = psel ? static_cast<void*>(cv.take<char>(psel)) : nullptr;
+        pxs = cv.take<T>(prune_chunk * d);
+        pxsq = cv.take<T>(prune_chunk);
+        pdist = cv.take<T>(prune_chunk);
+        plab = cv.take<uint32_t>(prune_chunk);
+        // the computed squared distance sum (x_j - c_j)^2 (F, ascending j)
+        // lies within gamma (relative) and eta (absolute, underflow) of the
+        // true one
+        const double uF = sizeof(T) == 4 ? std::ldexp(1.0, -24) : std::ldexp(1.0, -53);
+        const double tinyF = sizeof(T) == 4 ? std::ldexp(1.0, -126) : std::ldexp(1.0, -1022);
+        pc.gamma = 2.0 * (double)(d + 3) * uF;
+        pc.eta = (double)(d + 3) * tinyF;
+        pc.K = (1.0 + pc.gamma) / (1.0 - pc.gamma) * (1.0 + std::ldexp(1.0, -30));
+        pc.umin = std::sqrt(std::ldexp(pc.eta, 30));
+        pc.maxcand = 32;
+        // finite rows only (the fused search's NaN rules stay its own)
+        unsigned int bad = 0;
+        e = launch_km_count_nonfinite<T>(xsq, n, pfbn, s);
+        if (e != hipSuccess) return hip_err(e, "kmeans finite check");
+        rc = km_d2h<T>(&bad, pfbn, sizeof(bad), s);
+        if (rc) return rc;
+        prune = bad == 0;
+    }
+    // Settles the assignment into lab_new from lab_old under the centres in
+    // cdev, which moved by at most pdelta since lab_old's assignment: the
+    // bound-pruned assignment plus fused searches of the rows it leaves
+    // (all rows when they are most of them).  *fresh: every row's distance
+    // was computed.
+    auto prune_assign = [&](const uint32_t* lab_old, uint32_t* lab_new, bool* fresh) -> int32_t {
+        hipError_t e2 = launch_km_half_dist<T>(cdev, k, d, phcd, pdnc, s);
+        if (e2 == hipSuccess)
+            e2 = launch_select_rows<double>(phcd, k, k, k, (int)k, EMIT_IDENTITY, psv, psi, pscratch, s);
+        if (e2 == hipSuccess) e2 = launch_fill_u32(pfbn, 1, 0u, s);
+        if (e2 == hipSuccess)
+            e2 = launch_km_elkan<T>(x, n, d, cdev, k, w.perm, lab_old, lab_new, dist, pU, pdelta, pdnc, psv, psi, pc,
+                                    pfb, pfbn, s);
+        if (e2 != hipSuccess) return hip_err(e2, "kmeans pruned assignment");
+        unsigned int m = 0;
+        int32_t rc2 = km_d2h<T>(&m, pfbn, sizeof(m), s);
+        if (rc2) return rc2;
+        if ((int64_t)m * 5 > n * 3) {  // most rows left: one fused search of all of them
+            rc2 = km_assign(x, n, cdev, k, d, lab_new, dist, s, xsq);
+            if (rc2) return rc2;
+            e2 = launch_km_bound_init<T>(dist, n, pc.gamma, pc.eta, pU, s);
+            if (e2 != hipSuccess) return hip_err(e2, "kmeans bounds");
+            *fresh = true;
+            return MLRS_OK;
+        }
+        for (int64_t o = 0; o < (int64_t)m; o += prune_chunk) {
+            const int64_t cm = std::min<int64_t>(prune_chunk, (int64_t)m - o);
+            e2 = launch_km_gather_list<T>(x, xsq, pfb + o, cm, d, pxs, pxsq, s);
+            if (e2 != hipSuccess) return hip_err(e2, "kmeans pruned gather");
+            rc2 = km_assign(pxs, cm, cdev, k, d, plab, pdist, s, pxsq);
+            if (rc2) return rc2;
+            e2 = launch_km_scatter_list<T>(pfb + o, cm, plab, pdist, pc.gamma, pc.eta, lab_new, dist, pU, s);
+            if (e2 != hipSuccess) return hip_err(e2, "kmeans pruned scatter");
+        }
+        *fresh = false;
+        return MLRS_OK;
+    };
 
     // ---- tol_scaled = tol * mean(var(X, axis=0)) (feature_mean_var) ----
     std::vector<T> hp((size_t)std::max(nbi, nbv * d));
@@ -2021,7 +2118,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     for (int64_t q = 0; q < nbv * d; ++q) var_sum += (double)hp[q];
     const double tol_scaled = tol * ((var_sum * inv_n) / (double)d);
 
-    std::vector<double> cen((size_t)kd), best_cen((size_t)kd), nc((size_t)kd);
+    std::vector<double> cen((size_t)kd), best_cen((size_t)kd), nc((size_t)kd), delta_h((size_t)k);
     std::vector<T> ct((size_t)kd), sums_h((size_t)kd);
     std::vector<uint32_t> counts_h((size_t)k), lab_h, best_lab_h, lab_rel;
     std::vector<T> dist_h;
@@ -2162,6 +2259,11 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
         int cur = 0;
         rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s, xsq);
         if (rc) return rc;
+        bool dist_fresh = true;  // dist holds every row's distance to its centre
+        if (prune) {
+            e = launch_km_bound_init<T>(dist, n, pc.gamma, pc.eta, pU, s);
+            if (e != hipSuccess) return hip_err(e, "kmeans bounds");
+        }
         int64_t iters = 0;
         for (int64_t it = 0; it < max_iter; ++it) {
             ++iters;
@@ -2181,6 +2283,15 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
             for (int64_t q = 0; q < kd; ++q) nc[q] = (double)sums_h[q];
             int64_t empties = 0;
             for (int64_t c = 0; c < k; ++c) empties += cnt[c] == 0;
+            if (empties && !dist_fresh) {
+                // the ranking reads every row's distance: the pruned
+                // assignment left some untouched (same centres, same labels)
+                rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s, xsq);
+                if (rc) return rc;
+                e = launch_km_bound_init<T>(dist, n, pc.gamma, pc.eta, pU, s);
+                if (e != hipSuccess) return hip_err(e, "kmeans bounds");
+                dist_fresh = true;
+            }
             if (empties) {
                 // relocate_empty_clusters (prims/kmeans.rs:1323-1410): the
                 // farthest rows by (distance desc, index asc) into the empty
@@ -2296,11 +2407,29 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                 shift += diff * diff;
             }
             cen.swap(nc);
+            if (prune) {
+                // an upper bound of each centre's move (F centres, f64 sums)
+                for (int64_t c = 0; c < k; ++c) {
+                    double acc = 0.0;
+                    for (int64_t j = 0; j < d; ++j) {
+                        const double diff = (double)(T)cen[c * d + j] - (double)ct[c * d + j];
+                        acc += diff * diff;
+                    }
+                    delta_h[c] = std::sqrt(acc) * (1.0 + std::ldexp(1.0, -40));
+                }
+                e = hipMemcpyAsync(pdelta, delta_h.data(), sizeof(double) * (size_t)k, hipMemcpyHostToDevice, s);
+                if (e != hipSuccess) return hip_err(e, "kmeans centre moves upload");
+            }
             for (int64_t q = 0; q < kd; ++q) ct[q] = (T)cen[q];
             e = hipMemcpyAsync(cdev, ct.data(), sizeof(T) * (size_t)kd, hipMemcpyHostToDevice, s);
             if (e != hipSuccess) return hip_err(e, "kmeans centres upload");
             cur ^= 1;
-            rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s, xsq);
+            if (prune) {
+                rc = prune_assign(lab[cur ^ 1], lab[cur], &dist_fresh);
+            } else {
+                rc = km_assign(x, n, cdev, k, d, lab[cur], dist, s, xsq);
+                dist_fresh = true;
+            }
             if (rc) return rc;
             e = launch_km_changed(lab[cur], lab[cur ^ 1], n, changed_dev, s);
             if (e != hipSuccess) return hip_err(e, "kmeans labels_changed");
@@ -2364,20 +2493,20 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
 
 int32_t mlrs_kmeans_fit_f32(const float* x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
                             int32_t init_kind, const float* init, int64_t init_len, uint64_t seed, int64_t n_init,
-                            int64_t max_iter, double tol, float* out_centers, int64_t centers_len,
+                            int64_t max_iter, double tol, int32_t algorithm, float* out_centers, int64_t centers_len,
                             uint32_t* out_labels, int64_t labels_len, double* out_inertia, int64_t* out_n_iter,
                             void* stream) {
     return kmeans_fit_impl<float>(x, x_len, n, n_features, n_clusters, init_kind, init, init_len, seed, n_init,
-                                  max_iter, tol, out_centers, centers_len, out_labels, labels_len, out_inertia,
+                                  max_iter, tol, algorithm, out_centers, centers_len, out_labels, labels_len, out_inertia,
                                   out_n_iter, stream);
 }
 int32_t mlrs_kmeans_fit_f64(const double* x, int64_t x_len, int64_t n, int64_t n_features, int64_t n_clusters,
                             int32_t init_kind, const double* init, int64_t init_len, uint64_t seed, int64_t n_init,
-                            int64_t max_iter, double tol, double* out_centers, int64_t centers_len,
+                            int64_t max_iter, double tol, int32_t algorithm, double* out_centers, int64_t centers_len,
                             uint32_t* out_labels, int64_t labels_len, double* out_inertia, int64_t* out_n_iter,
                             void* stream) {
     return kmeans_fit_impl<double>(x, x_len, n, n_features, n_clusters, init_kind, init, init_len, seed, n_init,
-                                   max_iter, tol, out_centers, centers_len, out_labels, labels_len, out_inertia,
+                                   max_iter, tol, algorithm, out_centers, centers_len, out_labels, labels_len, out_inertia,
                                    out_n_iter, stream);
 }
 

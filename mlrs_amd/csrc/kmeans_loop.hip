@@ -580,6 +580,360 @@ hipError_t launch_km_take_u32(const uint32_t* src, int64_t n_src, const uint32_t
     return hipGetLastError();
 }
 
+namespace {
+
+// ---------------------------------------------------------------------------
+// Bound-pruned assignment (algorithm = 'elkan'; the reference's
+// elkan_init_bounds / elkan_assign_device / elkan_relax_bounds,
+// crates/mlrs-backend/src/prims/kmeans.rs:1523-1717, carry an n x k lower-bound
+// matrix, 20 GB and as many bytes of traffic per iteration at 5M x 1,024).
+// Here: one upper bound U[i] >= |x_i - c_a| per row (a its label), the k x k
+// half centre distances h(a, c) = |c_a - c_c| / 2 (lower bounds) with each
+// centre's row sorted, and dnc[a] = min over c != a of h(a, c).  By the
+// triangle inequality |x_i - c_c| >= 2 h(a, c) - U, so every centre with
+// h(a, c) >= K U lies strictly farther than c_a -- strictly also for the
+// COMPUTED distances (F arithmetic, the assignment's operation order): with
+// gamma bounding their relative error and eta the absolute error of
+// underflowing terms, K = (1 + gamma) / (1 - gamma) (1 + 2^-30) and U >= umin =
+// sqrt(2^30 eta) leave a margin U^2 (1 + gamma) 2^-29 > 2 eta.  A row with
+// dnc[a] >= K U keeps its label without a distance; else its own distance
+// tightens U, and the centres with h(a, c) < K U (a prefix of a's sorted row)
+// are evaluated exactly and ranked by (distance, index) with c_a; a row with
+// more than maxcand such centres goes to the fused k = 1 search instead
+// (compacted into fb_list).  Labels are therefore the assignment's own.
+// Bounds are kept in f64: after a centre update U += delta[a] (an upper
+// bound of the centre's move), and every fresh distance v resets
+// U = sqrt((v + eta) / (1 - gamma)).
+template <typename T>
+__global__ __launch_bounds__(256) void km_half_dist_kernel(const T* __restrict__ c, int64_t k, int64_t d,
+                                                           double* __restrict__ hcd, double* __restrict__ dnc) {
+    const int64_t a = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (a >= k) return;
+    const double inf = __builtin_huge_val();
+    double best = inf;
+    for (int64_t c0 = 0; c0 < k; c0 += 64) {
+        const int64_t cc = c0 + lane;
+        if (cc < k) {
+            double acc = 0.0;
+            for (int64_t j = 0; j < d; ++j) {
+                const double diff = (double)c[a * d + j] - (double)c[cc * d + j];
+                acc += diff * diff;
+            }
+            // a lower bound: the f64 sum's relative error is far below 2^-40
+            const double h = 0.5 * __builtin_sqrt(acc) * (1.0 - 0x1p-40);
+            hcd[a * k + cc] = (cc == a) ? 0.0 : h;
+            if (cc != a) best = fmin(best, h);
+        }
+    }
+    for (int m = 32; m > 0; m >>= 1) best = fmin(best, __shfl_xor(best, m, 64));
+    if (lane == 0) dnc[a] = best;
+}
+
+__device__ __forceinline__ double km_upper(double v, double gamma, double eta) {
+    // |x - c|^2 <= (v + eta) / (1 - gamma); NaN or inf gives +inf
+    const double u = __builtin_sqrt((v + eta) / (1.0 - gamma)) * (1.0 + 0x1p-50);
+    return (u == u && u < __builtin_huge_val()) ? u : __builtin_huge_val();
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_bound_init_kernel(const T* __restrict__ dist, int64_t n, double gamma,
+                                                            double eta, double* __restrict__ U) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) U[i] = km_upper((double)dist[i], gamma, eta);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void km_elkan_kernel(const T* __restrict__ x, int64_t n, int64_t d,
+                                                       const T* __restrict__ c, int64_t k,
+                                                       const uint32_t* __restrict__ lab_old,
+                                                       uint32_t* __restrict__ lab_new, T* __restrict__ dist,
+                                                       double* __restrict__ U, const double* __restrict__ delta,
+                                                       const double* __restrict__ dnc,
+                                                       const double* __restrict__ sv,
+                                                       const uint32_t* __restrict__ si, KmPruneConsts pc,
+                                                       uint32_t* __restrict__ fb_list,
+                                                       unsigned int* __restrict__ fb_count) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    bool fallback = false;
+    if (i < n) {
+        uint32_t a = lab_old[i];
+        double u = (U[i] + delta[a]) * (1.0 + 0x1p-50);
+        if (!(u == u)) u = __builtin_huge_val();
+        if (!(u >= pc.umin && dnc[a] >= pc.K * u)) {
+            const T* xr = x + i * d;
+            const T da = row_sqdist<T, VEC>(xr, c + (int64_t)a * d, d);
+            const double ut = km_upper((double)da, pc.gamma, pc.eta);
+            if (ut < u) u = ut;
+            T bv = da;
+            uint32_t bi = a;
+            if (!(u >= pc.umin && dnc[a] >= pc.K * u)) {
+                // the centres that may lie nearer: a prefix of a's sorted row
+                const double lim = (u >= pc.umin) ? pc.K * u : __builtin_huge_val();
+                const double* hrow = sv + (int64_t)a * k;
+                const uint32_t* crow = si + (int64_t)a * k;
+                int cnt = 0;
+                for (int64_t j = 0; j < k; ++j) {
+                    if (!(hrow[j] < lim)) break;
+                    const uint32_t cc = crow[j];
+                    if (cc == a) continue;
+                    if (++cnt > pc.maxcand) {
+                        fallback = true;
+                        break;
+                    }
+                    const T dc = row_sqdist<T, VEC>(xr, c + (int64_t)cc * d, d);
+                    if (dc < bv || (dc == bv && cc < bi)) {
+                        bv = dc;
+                        bi = cc;
+                    }
+                }
+            }
+            if (!fallback) {
+                a = bi;
+                dist[i] = bv;
+                u = km_upper((double)bv, pc.gamma, pc.eta);
+            }
+        }
+        if (!fallback) {
+            lab_new[i] = a;
+            U[i] = u;
+        }
+    }
+    // rows for the fused search: one atomic per wave
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(fallback);
+    if (bal) {
+        const int first = __builtin_ctzll(bal);
+        unsigned int base = 0;
+        if (lane == first) base = atomicAdd(fb_count, (unsigned int)__builtin_popcountll(bal));
+        base = (unsigned int)__shfl((int)base, first, 64);
+        if (fallback) fb_list[base + (unsigned int)__builtin_popcountll(bal & ((1ull << lane) - 1ull))] = (uint32_t)i;
+    }
+}
+
+// The same assignment over rows taken in the label-major order of the
+// centroid sums' permutation (perm, for the labels lab_old), with the rows
+// staged through LDS: a workgroup takes 256 consecutive perm entries, so its
+// rows arrive with coalesced 16-byte loads (16-byte rows of at most 512
+// bytes: RC chunks, row stride RC + 1 chunks so that the threads' 16-byte
+// reads of one chunk column hit distinct bank groups) and its threads mostly
+// share one centre, whose row and sorted half-distance row they read
+// together.  Each row's distances are still one thread's ascending sum.
+template <typename T, int RC>
+__global__ __launch_bounds__(256) void km_elkan_lds_kernel(const T* __restrict__ x, int64_t n, int64_t d,
+                                                           const T* __restrict__ c, int64_t k,
+                                                           const uint32_t* __restrict__ perm,
+                                                           const uint32_t* __restrict__ lab_old,
+                                                           uint32_t* __restrict__ lab_new, T* __restrict__ dist,
+                                                           double* __restrict__ U, const double* __restrict__ delta,
+                                                           const double* __restrict__ dnc,
+                                                           const double* __restrict__ sv,
+                                                           const uint32_t* __restrict__ si, KmPruneConsts pc,
+                                                           uint32_t* __restrict__ fb_list,
+                                                           unsigned int* __restrict__ fb_count) {
+    constexpr int V = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+    constexpr int RS = (RC + 1) * V;        // row stride (elements)
+    __shared__ __attribute__((aligned(16))) T xs[256 * RS];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int64_t p0 = (int64_t)blockIdx.x * 256;
+    const int64_t pos = p0 + tid;
+    const bool valid = pos < n;
+    const uint32_t i = valid ? perm[pos] : 0u;
+    uint32_t a = valid ? lab_old[i] : 0u;
+    double u = 0.0;
+    bool need = false;
+    if (valid) {
+        u = (U[i] + delta[a]) * (1.0 + 0x1p-50);
+        if (!(u == u)) u = __builtin_huge_val();
+        need = !(u >= pc.umin && dnc[a] >= pc.K * u);
+    }
+    bool fallback = false;
+    if (__syncthreads_or(need)) {
+        const int cpr = (int)(d / V);  // 16-byte chunks per row (<= RC)
+        for (int e = tid; e < 256 * cpr; e += 256) {
+            const int r = e / cpr, ch = e - r * cpr;
+            if (p0 + r < n) {
+                const float4 v = *reinterpret_cast<const float4*>(x + (int64_t)perm[p0 + r] * d + (int64_t)ch * V);
+                *reinterpret_cast<float4*>(&xs[r * RS + ch * V]) = v;
+            }
+        }
+        __syncthreads();
+        if (need) {
+            const T* xr = &xs[tid * RS];
+            auto sqd = [&](uint32_t cc) -> T {
+                const T* cr = c + (int64_t)cc * d;
+                T acc = T(0);
+                for (int ch = 0; ch < cpr; ++ch) {
+                    const float4 xv = *reinterpret_cast<const float4*>(xr + ch * V);
+                    const float4 cv = *reinterpret_cast<const float4*>(cr + ch * V);
+                    const T* xa = reinterpret_cast<const T*>(&xv);
+                    const T* ca = reinterpret_cast<const T*>(&cv);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        const T diff = xa[e] - ca[e];
+                        acc = acc + diff * diff;
+                    }
+                }
+                return acc;
+            };
+            const T da = sqd(a);
+            const double ut = km_upper((double)da, pc.gamma, pc.eta);
+            if (ut < u) u = ut;
+            T bv = da;
+            uint32_t bi = a;
+            if (!(u >= pc.umin && dnc[a] >= pc.K * u)) {
+                const double lim = (u >= pc.umin) ? pc.K * u : __builtin_huge_val();
+                const double* hrow = sv + (int64_t)a * k;
+                const uint32_t* crow = si + (int64_t)a * k;
+                int cnt = 0;
+                for (int64_t j = 0; j < k; ++j) {
+                    if (!(hrow[j] < lim)) break;
+                    const uint32_t cc = crow[j];
+                    if (cc == a) continue;
+                    if (++cnt > pc.maxcand) {
+                        fallback = true;
+                        break;
+                    }
+                    const T dc = sqd(cc);
+                    if (dc < bv || (dc == bv && cc < bi)) {
+                        bv = dc;
+                        bi = cc;
+                    }
+                }
+            }
+            if (!fallback) {
+                a = bi;
+                dist[i] = bv;
+                u = km_upper((double)bv, pc.gamma, pc.eta);
+            }
+        }
+    }
+    if (valid && !fallback) {
+        lab_new[i] = a;
+        U[i] = u;
+    }
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(fallback);
+    if (bal) {
+        const int first = __builtin_ctzll(bal);
+        unsigned int base = 0;
+        if (lane == first) base = atomicAdd(fb_count, (unsigned int)__builtin_popcountll(bal));
+        base = (unsigned int)__shfl((int)base, first, 64);
+        if (fallback) fb_list[base + (unsigned int)__builtin_popcountll(bal & ((1ull << lane) - 1ull))] = i;
+    }
+}
+
+// The rows (and their row_sumsq) of fb_list[0..m) into dense buffers.
+template <typename T>
+__global__ __launch_bounds__(256) void km_gather_list_kernel(const T* __restrict__ x, const T* __restrict__ xsq,
+                                                             const uint32_t* __restrict__ list, int64_t m,
+                                                             int64_t d, T* __restrict__ out,
+                                                             T* __restrict__ out_sq) {
+    const int64_t total = m * d;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += stride) {
+        const int64_t r = e / d;
+        out[e] = x[(int64_t)list[r] * d + (e - r * d)];
+        if (e - r * d == 0) out_sq[r] = xsq[list[r]];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void km_scatter_list_kernel(const uint32_t* __restrict__ list, int64_t m,
+                                                              const uint32_t* __restrict__ lab_sub,
+                                                              const T* __restrict__ dist_sub, double gamma,
+                                                              double eta, uint32_t* __restrict__ lab_new,
+                                                              T* __restrict__ dist, double* __restrict__ U) {
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= m) return;
+    const uint32_t i = list[j];
+    lab_new[i] = lab_sub[j];
+    dist[i] = dist_sub[j];
+    U[i] = km_upper((double)dist_sub[j], gamma, eta);
+}
+
+// Rows whose row_sumsq is not finite (inf or NaN entries, or an overflowing
+// sum): the pruned assignment serves finite data only.
+template <typename T>
+__global__ __launch_bounds__(256) void km_count_nonfinite_kernel(const T* __restrict__ v, int64_t n,
+                                                                 unsigned int* __restrict__ count) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool bad = i < n && !(v[i] == v[i] && v[i] < (T)__builtin_huge_val() && v[i] > -(T)__builtin_huge_val());
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(bad);
+    if (bal && (threadIdx.x & 63) == __builtin_ctzll(bal)) atomicAdd(count, (unsigned int)__builtin_popcountll(bal));
+}
+
+}  // namespace
+
+template <typename T>
+hipError_t launch_km_half_dist(const T* c, int64_t k, int64_t d, double* hcd, double* dnc, hipStream_t s) {
+    hipLaunchKernelGGL((km_half_dist_kernel<T>), dim3((unsigned)((k + 3) / 4)), dim3(256), 0, s, c, k, d, hcd, dnc);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_bound_init(const T* dist, int64_t n, double gamma, double eta, double* U, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL((km_bound_init_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dist, n, gamma,
+                       eta, U);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_elkan(const T* x, int64_t n, int64_t d, const T* c, int64_t k, const uint32_t* perm,
+                           const uint32_t* lab_old, uint32_t* lab_new, T* dist, double* U, const double* delta,
+                           const double* dnc, const double* sv, const uint32_t* si, const KmPruneConsts& pc,
+                           uint32_t* fb_list, unsigned int* fb_count, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    const int64_t chunks = d * (int64_t)sizeof(T) / 16;  // 16-byte chunks per row
+    if (perm && rows_vec<T>(x, c, d) && chunks <= 32) {
+        if (chunks <= 16)
+            hipLaunchKernelGGL((km_elkan_lds_kernel<T, 16>), grid, dim3(256), 0, s, x, n, d, c, k, perm, lab_old,
+                               lab_new, dist, U, delta, dnc, sv, si, pc, fb_list, fb_count);
+        else
+            hipLaunchKernelGGL((km_elkan_lds_kernel<T, 32>), grid, dim3(256), 0, s, x, n, d, c, k, perm, lab_old,
+                               lab_new, dist, U, delta, dnc, sv, si, pc, fb_list, fb_count);
+        return hipGetLastError();
+    }
+    if (rows_vec<T>(x, c, d))
+        hipLaunchKernelGGL((km_elkan_kernel<T, true>), grid, dim3(256), 0, s, x, n, d, c, k, lab_old, lab_new, dist,
+                           U, delta, dnc, sv, si, pc, fb_list, fb_count);
+    else
+        hipLaunchKernelGGL((km_elkan_kernel<T, false>), grid, dim3(256), 0, s, x, n, d, c, k, lab_old, lab_new,
+                           dist, U, delta, dnc, sv, si, pc, fb_list, fb_count);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_gather_list(const T* x, const T* xsq, const uint32_t* list, int64_t m, int64_t d, T* out,
+                                 T* out_sq, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    int64_t b = (m * d + 255) / 256;
+    if (b > 65536) b = 65536;
+    hipLaunchKernelGGL((km_gather_list_kernel<T>), dim3((unsigned)b), dim3(256), 0, s, x, xsq, list, m, d, out,
+                       out_sq);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_scatter_list(const uint32_t* list, int64_t m, const uint32_t* lab_sub, const T* dist_sub,
+                                  double gamma, double eta, uint32_t* lab_new, T* dist, double* U, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    hipLaunchKernelGGL((km_scatter_list_kernel<T>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, list, m,
+                       lab_sub, dist_sub, gamma, eta, lab_new, dist, U);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_count_nonfinite(const T* v, int64_t n, unsigned int* count, hipStream_t s) {
+    hipError_t e = launch_fill_u32(count, 1, 0u, s);
+    if (e != hipSuccess || n <= 0) return e;
+    hipLaunchKernelGGL((km_count_nonfinite_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, v, n,
+                       count);
+    return hipGetLastError();
+}
+
 #define MLRS_KM_INST(T)                                                                                            \
     template hipError_t launch_km_centroid_sums<T>(const T*, const uint32_t*, int64_t, int64_t, int64_t, int64_t,   \
                                                    int64_t, const KmScratch<T>&, hipStream_t);                     \
@@ -589,7 +943,19 @@ hipError_t launch_km_take_u32(const uint32_t* src, int64_t n_src, const uint32_t
                                               hipStream_t);                                                        \
     template hipError_t launch_km_mind2<T>(const T*, int64_t, int64_t, int64_t, int, T*, hipStream_t);              \
     template hipError_t launch_km_gather<T>(const T*, const int64_t*, int64_t, int64_t, T*, hipStream_t);        \
-    template hipError_t launch_km_neg<T>(const T*, int64_t, int64_t, T*, unsigned int*, hipStream_t);
+    template hipError_t launch_km_neg<T>(const T*, int64_t, int64_t, T*, unsigned int*, hipStream_t);                \
+    template hipError_t launch_km_half_dist<T>(const T*, int64_t, int64_t, double*, double*, hipStream_t);       \
+    template hipError_t launch_km_bound_init<T>(const T*, int64_t, double, double, double*, hipStream_t);        \
+    template hipError_t launch_km_elkan<T>(const T*, int64_t, int64_t, const T*, int64_t, const uint32_t*,         \
+                                           const uint32_t*, uint32_t*, T*, double*, const double*, const double*, \
+                                           const double*,                                                        \
+                                           const uint32_t*, const KmPruneConsts&, uint32_t*, unsigned int*,      \
+                                           hipStream_t);                                                          \
+    template hipError_t launch_km_gather_list<T>(const T*, const T*, const uint32_t*, int64_t, int64_t, T*, T*,   \
+                                                 hipStream_t);                                                    \
+    template hipError_t launch_km_scatter_list<T>(const uint32_t*, int64_t, const uint32_t*, const T*, double,   \
+                                                  double, uint32_t*, T*, double*, hipStream_t);                   \
+    template hipError_t launch_km_count_nonfinite<T>(const T*, int64_t, unsigned int*, hipStream_t);
 MLRS_KM_INST(float)
 MLRS_KM_INST(double)
 #undef MLRS_KM_INST

@@ -778,6 +778,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     __syncthreads();  // per-wave LDS init visible to the wave
 
     float thr = L.thr[jl];
+    const float eps2 = 2.0f * L.eps[jl];  // k = 1 tightening (exact doubling)
     // k = 1: a lower bound on the screen values of the rows in query jl's
     // queue.  A NaN screen value can hide a finite exact value only where a
     // sum may overflow, so queries without screen-value mode (L.mode) keep
@@ -919,7 +920,12 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             for (int r = 0; r < SH::vals; ++r) m = fminf(m, val(r));  // NaN ignored; past-end rows are +inf
             if (W16) m = fminf(m, shfl_xor_f(m, 16));
             m = fminf(m, shfl_xor_f(m, 32));
-            if (m < inf) thr = fminf(thr, round_up_f((double)m + 2.0 * (double)L.eps[jl]));
+            if (m < inf) {
+                // m + 2 eps rounded to nearest, then stepped up by at least one
+                // ulp (2^-126 near zero): an upper bound of the exact sum
+                const float s_ = m + eps2;
+                thr = fminf(thr, s_ + (__builtin_fabsf(s_) * 0x1p-23f + 0x1p-126f));
+            }
             if constexpr (K1) {
                 // Rows queued on earlier tiles whose screen values all exceed
                 // the tightened threshold cannot be the nearest row (nor tie

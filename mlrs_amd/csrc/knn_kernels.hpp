@@ -387,6 +387,34 @@ template <typename T>
 hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n, int64_t d, int64_t k, int64_t nb,
                                    int64_t rpb, const KmScratch<T>& w, hipStream_t s);
 hipError_t launch_km_changed(const uint32_t* a, const uint32_t* b, int64_t n, unsigned int* count, hipStream_t s);
+
+// Bound-pruned assignment (the fit's algorithm = 'elkan'): see kmeans_loop.hip.
+struct KmPruneConsts {
+    double gamma;  // relative error bound of a computed squared distance
+    double eta;    // its absolute error bound (underflowing terms)
+    double K;      // (1 + gamma) / (1 - gamma) (1 + 2^-30)
+    double umin;   // sqrt(2^30 eta): below it no centre is excluded
+    int maxcand;   // centres a row evaluates itself before it goes to the fused search
+};
+template <typename T>
+hipError_t launch_km_half_dist(const T* c, int64_t k, int64_t d, double* hcd, double* dnc, hipStream_t s);
+template <typename T>
+hipError_t launch_km_bound_init(const T* dist, int64_t n, double gamma, double eta, double* U, hipStream_t s);
+template <typename T>
+// perm: the rows in the label-major order of lab_old (the centroid sums'
+// permutation), or null (rows in index order)
+hipError_t launch_km_elkan(const T* x, int64_t n, int64_t d, const T* c, int64_t k, const uint32_t* perm,
+                           const uint32_t* lab_old, uint32_t* lab_new, T* dist, double* U, const double* delta,
+                           const double* dnc, const double* sv, const uint32_t* si, const KmPruneConsts& pc,
+                           uint32_t* fb_list, unsigned int* fb_count, hipStream_t s);
+template <typename T>
+hipError_t launch_km_gather_list(const T* x, const T* xsq, const uint32_t* list, int64_t m, int64_t d, T* out,
+                                 T* out_sq, hipStream_t s);
+template <typename T>
+hipError_t launch_km_scatter_list(const uint32_t* list, int64_t m, const uint32_t* lab_sub, const T* dist_sub,
+                                  double gamma, double eta, uint32_t* lab_new, T* dist, double* U, hipStream_t s);
+template <typename T>
+hipError_t launch_km_count_nonfinite(const T* v, int64_t n, unsigned int* count, hipStream_t s);
 template <typename T>
 hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int64_t n, int64_t d, T* rows,
                              int64_t nb, int64_t rpb, T* parts, hipStream_t s);

@@ -324,11 +324,19 @@ def core_distances(x, min_samples, metric="euclidean", p=2.0):
 _KMEANS_INIT = {"array": 0, "k-means++": 1, "random": 2}
 
 
-def kmeans_fit(x, n_clusters, init="k-means++", init_centers=None, seed=0, n_init=1, max_iter=300, tol=1e-4):
+_KMEANS_ALGORITHM = {"lloyd": 0, "elkan": 1}
+
+
+def kmeans_fit(x, n_clusters, init="k-means++", init_centers=None, seed=0, n_init=1, max_iter=300, tol=1e-4,
+               algorithm="lloyd"):
     """k-means fit on the device (mlrs_kmeans_fit_*): ``(centers (k, d) in
     x's dtype, labels int64 (n,), inertia float, n_iter int)`` of the winning
     restart.  ``init`` is "k-means++", "random" or "array" (then
-    ``init_centers`` is a (k, d) device tensor of x's dtype)."""
+    ``init_centers`` is a (k, d) device tensor of x's dtype).  ``algorithm``
+    "lloyd" (every row assigned each iteration) or "elkan" (the bound-pruned
+    assignment): the same fit either way."""
+    if algorithm not in _KMEANS_ALGORITHM:
+        raise ValueError("algorithm should be 'lloyd' or 'elkan', got %r" % (algorithm,))
     _dev_check(x)
     s = _suffix(x)
     n, d = x.shape
@@ -342,7 +350,8 @@ def kmeans_fit(x, n_clusters, init="k-means++", init_centers=None, seed=0, n_ini
     n_iter = ctypes.c_int64()
     rc = getattr(_lib.load(), "mlrs_kmeans_fit_" + s)(
         _ptr(x), x.numel(), n, d, k, _KMEANS_INIT[init], _ptr(ini), ini.numel() if ini is not None else 0,
-        int(seed) & 0xFFFFFFFFFFFFFFFF, int(n_init), int(max_iter), float(tol), _ptr(centers), centers.numel(),
+        int(seed) & 0xFFFFFFFFFFFFFFFF, int(n_init), int(max_iter), float(tol), _KMEANS_ALGORITHM[algorithm],
+        _ptr(centers), centers.numel(),
         _ptr(labels), labels.numel(), ctypes.byref(inertia), ctypes.byref(n_iter), _stream(x.device))
     _lib.check(rc)
     return centers, labels.to(torch.int64), inertia.value, int(n_iter.value)

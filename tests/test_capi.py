@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib.load()
-    assert lib.mlrs_abi_version() == 4
+    assert lib.mlrs_abi_version() == 5
     assert lib.mlrs_status_string(0) == b"ok"
     assert lib.mlrs_status_string(-7) == b"invalid parameter value"
     assert lib.mlrs_status_string(-1) == b"shape mismatch"
@@ -226,8 +226,8 @@ def test_kmeans_fit_validation():
     inertia, n_iter = ctypes.c_double(), ctypes.c_int64()
 
     def call(n=10, d=3, k=3, kind=1, init_len=0, n_init=1, max_iter=10, tol=1e-4, x_len=None, c_len=None,
-             l_len=None):
-        return f(P, n * d if x_len is None else x_len, n, d, k, kind, P, init_len, 0, n_init, max_iter, tol, P,
+             l_len=None, algorithm=0):
+        return f(P, n * d if x_len is None else x_len, n, d, k, kind, P, init_len, 0, n_init, max_iter, tol, algorithm, P,
                  k * d if c_len is None else c_len, P, n if l_len is None else l_len, ctypes.byref(inertia),
                  ctypes.byref(n_iter), None)
     assert call(k=11) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"k"
@@ -238,6 +238,7 @@ def test_kmeans_fit_validation():
     assert call(kind=5) == _lib.MLRS_ERR_UNSUPPORTED
     assert call(n_init=0) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"n_init"
     assert call(tol=-1.0) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"tol"
+    assert call(algorithm=2) == _lib.MLRS_ERR_INVALID_PARAM and _info().operand == b"algorithm"
     assert call(c_len=8) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"centers"
     assert call(l_len=9) == _lib.MLRS_ERR_SHAPE_MISMATCH and _info().operand == b"labels"
 
