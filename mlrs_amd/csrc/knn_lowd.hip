@@ -24,7 +24,6 @@ namespace mlrs {
 
 namespace {
 
-constexpr int kRt = 512;        // index rows per LDS tile
 constexpr int kMaxD = 16;
 constexpr int kMaxK = 32;
 
@@ -35,7 +34,8 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
 #define MLRS_LOWD_RU4 8
 #endif
     constexpr int RU = DPN <= 4 ? MLRS_LOWD_RU4 : (DPN <= 8 ? 4 : 2);  // rows per screening step
-    __shared__ __attribute__((aligned(16))) float tile[kRt * DPN];
+    constexpr int RT = 64 * RU;            // index rows per LDS tile: 64 steps
+    __shared__ __attribute__((aligned(16))) float tile[RT * DPN];
 
     const int tid = threadIdx.x;
     const int64_t qbase = (int64_t)blockIdx.x * (256 * QL) + tid;
@@ -84,10 +84,17 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
         }
     }
 
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += kRt) {
-        const int nrows = (int)((t_end - t0) < kRt ? (t_end - t0) : kRt);
+    // The tile's rows are screened first, each step of RU rows recording one
+    // bit when any value of the lane passes; the recorded steps are rescored
+    // at the tile's end (the rows still in LDS), against the thresholds as
+    // they tighten.  A wave enters rescoring once per tile instead of at every
+    // step where one of its lanes passes (about one step in five at c4),
+    // and the screen loop carries no rescoring code.
+    constexpr int STEPS = RT / RU;            // steps per tile (64)
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += RT) {
+        const int nrows = (int)((t_end - t0) < RT ? (t_end - t0) : RT);
         __syncthreads();
-        for (int e = tid; e < kRt * DPN; e += 256) {
+        for (int e = tid; e < RT * DPN; e += 256) {
             const int r = e / DPN, c = e % DPN;
             float v = 0.0f;
             if (r < nrows) {
@@ -99,9 +106,20 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
             tile[e] = v;
         }
         __syncthreads();
-        // RU rows per step: their LDS reads are issued together, so one
-        // LDS latency is paid per RU rows, not per row.
-        for (int r0 = 0; r0 < nrows; r0 += RU) {
+        // screen: acc = ||x||^2 - 2 x.q, the group's smallest against the
+        // threshold (one min per pair instead of a compare).  fminf drops
+        // a NaN value unless the whole group is NaN (which then passes);
+        // a NaN screen value means a NaN or infinite input, whose exact
+        // value is NaN (never admitted) or +inf (admitted only while the
+        // list is not full, when thr is +inf and every finite value
+        // passes too), so dropping it here never loses a pair.  The
+        // padding rows of a partial tile are zeros: they may pass, and
+        // rescoring skips them.
+        uint64_t pend = 0;
+        for (int st = 0; st < STEPS && st * RU < nrows; ++st) {
+            const int r0 = st * RU;
+            // RU rows per step: their LDS reads are issued together, so one
+            // LDS latency is paid per RU rows, not per row
             float row[RU][DPN];
 #pragma unroll
             for (int rr = 0; rr < RU; ++rr)
@@ -113,13 +131,6 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
                     row[rr][4 * c4 + 2] = v.z;
                     row[rr][4 * c4 + 3] = v.w;
                 }
-            // screen: acc = ||x||^2 - 2 x.q, the group's smallest against the
-            // threshold (one min per pair instead of a compare).  fminf drops
-            // a NaN value unless the whole group is NaN (which then passes);
-            // a NaN screen value means a NaN or infinite input, whose exact
-            // value is NaN (never admitted) or +inf (admitted only while the
-            // list is not full, when thr is +inf and every finite value
-            // passes too), so dropping it here never loses a pair.
             bool any = false;
 #pragma unroll
             for (int i = 0; i < QL; ++i) {
@@ -133,19 +144,26 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
                 }
                 any |= !(mn > thr[i]);
             }
-            if (!any) continue;
-            // exact rescoring of the passing pairs (rare after the lists fill):
-            // the screen is redone from the row registers into a bit mask,
-            // and only the passing rows are read back from LDS
+            pend |= (uint64_t)any << st;
+        }
+        // rescoring of the recorded steps: the screen again, now against the
+        // current thresholds, and an exact evaluation of each passing pair
+        // in the reference's order, offered to the list with insert_lane's
+        // rule (value, index), NaN never admitted
+        while (pend) {
+            const int st = __builtin_ctzll(pend);
+            pend &= pend - 1;
+            const int r0 = st * RU;
             const int rmax = (nrows - r0) < RU ? (nrows - r0) : RU;  // padding rows of the last step
 #pragma unroll
             for (int i = 0; i < QL; ++i) {
                 uint32_t m = 0;
 #pragma unroll
                 for (int rr = 0; rr < RU; ++rr) {
-                    float s_ = row[rr][D];
+                    const float* yr = &tile[(r0 + rr) * DPN];
+                    float s_ = yr[D];
 #pragma unroll
-                    for (int c = 0; c < D; ++c) s_ = __builtin_fmaf(qm2[i][c], row[rr][c], s_);
+                    for (int c = 0; c < D; ++c) s_ = __builtin_fmaf(qm2[i][c], yr[c], s_);
                     m |= (uint32_t)!(s_ > thr[i]) << rr;
                 }
                 m &= (rmax >= 32) ? 0xFFFFFFFFu : ((1u << rmax) - 1u);
@@ -185,9 +203,14 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs32 a) {
                             worst[i] = lv[i][j];
                             worst_i[i] = li[i][j];
                         }
-                    // exact <= R  =>  ||x||^2 - 2 x.q <= R - ||q||^2 + eps
-                    if (worst[i] < inf)
-                        thr[i] = round_up_f((double)worst[i] - (double)qsq[i] + (double)eps[i]);
+                    // exact <= R  =>  ||x||^2 - 2 x.q <= R - ||q||^2 + eps:
+                    // (R + eps) - ||q||^2 in f32, raised by four times its
+                    // rounding bound (2^-126 near zero) -- an upper bound
+                    if (worst[i] < inf) {
+                        const float we_ = worst[i] + eps[i];
+                        const float s_ = we_ - qsq[i];
+                        thr[i] = s_ + ((we_ + __builtin_fabsf(s_)) * 0x1p-22f + 0x1p-126f);
+                    }
                 }
             }
         }
