@@ -461,6 +461,20 @@ int32_t mlrs_timing_enable(int32_t on);
 int32_t mlrs_timing_read(double *total_ms, int64_t *launches, char *kernel_name, int32_t name_len);
 
 /*
+ * Peak probe (no counterpart in the reference; the basis of the roofline
+ * fractions the benchmark reports).  Runs register-only chains on every CU
+ * with `waves_per_simd` waves on each SIMD (1..8) and returns the achieved
+ * TFLOP/s (an FMA counts two flops) of the second of two launches, timed with
+ * HIP events on `stream`:
+ *   kind 0: v_fma_f32 (eight independent chains per lane, no packed math)
+ *   kind 1: v_fma_f64 (likewise)
+ *   kind 2: v_mfma_f32_32x32x2f32 (two independent accumulator chains)
+ *   kind 3: v_mfma_f64_16x16x4f64 (four independent accumulator chains)
+ * Synchronous.  Errors: Unsupported "kind" / "waves_per_simd".
+ */
+int32_t mlrs_probe_peak(int32_t kind, int32_t waves_per_simd, double *tflops, void *stream);
+
+/*
  * Kernel-family override (no counterpart in the reference; for tests and
  * benchmarks).  Every family returns the same bits, so this only changes
  * speed: 0 = automatic choice (default); 1 = the fused Gram-MFMA kernels

@@ -128,6 +128,7 @@ SIGNATURES = {
     "mlrs_pool_stats_get": (_i32, [ctypes.POINTER(PoolStats)]),
     "mlrs_pool_stats_reset": (_i32, []),
     "mlrs_timing_enable": (_i32, [_i32]),
+    "mlrs_probe_peak": (_i32, [_i32, _i32, ctypes.POINTER(_f64), _vp]),
     "mlrs_force_path": (_i32, [_i32]),
     "mlrs_timing_read": (_i32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, _i32]),
 }

@@ -2557,6 +2557,42 @@ int32_t mlrs_timing_read(double* total_ms, int64_t* launches, char* kernel_name,
     return MLRS_OK;
 }
 
+int32_t mlrs_probe_peak(int32_t kind, int32_t waves_per_simd, double* tflops, void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (kind < 0 || kind > 3) return set_err(MLRS_ERR_UNSUPPORTED, "kind", kind, 0, 0, 0, "probe kind %d", kind);
+    if (waves_per_simd < 1 || waves_per_simd > 8)
+        return set_err(MLRS_ERR_UNSUPPORTED, "waves_per_simd", waves_per_simd, 0, 0, 0,
+                       "waves per SIMD must be 1..8, got %d", waves_per_simd);
+    if (!tflops) return set_err(MLRS_ERR_NULL_POINTER, "tflops", 0, 0, 0, 0, "null pointer");
+    int dev = 0, cus = 0;
+    int32_t rc = current_device(&dev);
+    if (rc) return rc;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_err(e, "hipDeviceGetAttribute");
+    // a workgroup is four waves, one per SIMD
+    const int64_t blocks = (int64_t)cus * waves_per_simd;
+    const int iters = kind <= 1 ? 4096 : 1024;
+    hipStream_t s = (hipStream_t)stream;
+    void* out = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    e = hipMalloc(&out, (size_t)blocks * 256 * 8);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = launch_probe(kind, blocks, iters, out, s);  // warm-up
+    if (e == hipSuccess) e = hipEventRecord(a, s);
+    if (e == hipSuccess) e = launch_probe(kind, blocks, iters, out, s);
+    if (e == hipSuccess) e = hipEventRecord(b, s);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (out) (void)hipFree(out);
+    if (e != hipSuccess) return hip_err(e, "peak probe");
+    *tflops = probe_flops(kind, blocks, iters) / ((double)ms * 1e-3) / 1e12;
+    return MLRS_OK;
+}
+
 }  // extern "C"
 
 namespace {

@@ -388,6 +388,12 @@ hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n
                                    int64_t rpb, const KmScratch<T>& w, hipStream_t s);
 hipError_t launch_km_changed(const uint32_t* a, const uint32_t* b, int64_t n, unsigned int* count, hipStream_t s);
 
+// Peak probe (probe.hip): kind 0 FMA f32, 1 FMA f64, 2 MFMA f32, 3 MFMA f64;
+// `blocks` workgroups of 256 threads, iters loop trips; out holds one value
+// per thread (8 bytes).
+hipError_t launch_probe(int kind, int64_t blocks, int iters, void* out, hipStream_t s);
+double probe_flops(int kind, int64_t blocks, int iters);
+
 // Bound-pruned assignment (the fit's algorithm = 'elkan'): see kmeans_loop.hip.
 struct KmPruneConsts {
     double gamma;  // relative error bound of a computed squared distance
