@@ -89,7 +89,6 @@ def main():
     from mlrs_amd import _lib, prims, synthetic
 
     if args.probe_peak:
-        import ctypes
         lib = _lib.load()
         res = {}
         for kind, label, peak in ((0, "valu_fma_f32", PEAKS["valu_f32"]), (1, "valu_fma_f64", PEAKS["valu_f64"]),
