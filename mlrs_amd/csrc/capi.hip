@@ -1657,6 +1657,32 @@ static int32_t aux_workspace(size_t bytes, hipStream_t s, char** out) {
     return MLRS_OK;
 }
 
+// Pinned host memory for the k-means fit's read-backs and uploads (grown on
+// demand and kept; used under the call lock).  Copies to and from it are DMA
+// transfers queued behind the kernels, where pageable memory would be staged
+// by the runtime on the host's time.  Every fit waits for its own copies
+// before it returns, so growing may free the old block.
+char* g_pinned = nullptr;
+size_t g_pinned_cap = 0;
+
+static int32_t pinned_staging(size_t bytes, char** out) {
+    if (g_pinned_cap < bytes) {
+        if (g_pinned) (void)hipHostFree(g_pinned);
+        g_pinned = nullptr;
+        g_pinned_cap = 0;
+        const size_t want = std::max(bytes + bytes / 4, (size_t)1 << 20);
+        void* p = nullptr;
+        hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+        if (e != hipSuccess)
+            return set_err(MLRS_ERR_ALLOC, "pinned", (int64_t)want, 0, 0, (int)e,
+                           "pinned host allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+        g_pinned = static_cast<char*>(p);
+        g_pinned_cap = want;
+    }
+    *out = g_pinned;
+    return MLRS_OK;
+}
+
 // The f64 search under an explicit arm: the Gram-MFMA kernel where it serves
 // the arm and shape, else exact tiles + selection.
 static int32_t search_f64(const double* xq, int64_t nq, const double* xt, int64_t nt, int64_t d, int k, int arm,
@@ -1970,7 +1996,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     size_t bytes = 4 * aligned_bytes(sizeof(uint32_t) * (size_t)n) + 3 * aligned_bytes(sizeof(T) * (size_t)n) +
                    2 * aligned_bytes(sizeof(uint32_t) * (size_t)(nb * k)) +
                    aligned_bytes(sizeof(uint32_t) * (size_t)(nb * nsub * k)) + 2 * aligned_bytes(sizeof(uint32_t) * k) +
-                   aligned_bytes(sizeof(T) * (size_t)(nb * kd)) + 2 * aligned_bytes(sizeof(T) * (size_t)kd) +
+                   aligned_bytes(sizeof(T) * (size_t)(nb * kd)) + 3 * aligned_bytes(sizeof(T) * (size_t)kd) +
                    aligned_bytes(sizeof(T) * (size_t)std::max(nbi, nbv * d)) + aligned_bytes(sizeof(T) * d) +
                    aligned_bytes(sizeof(int64_t) * k) + 1024;
     // algorithm = 'elkan': the bound-pruned assignment (launch_km_elkan) for
@@ -2007,6 +2033,7 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
     w.psum = cv.take<T>(nb * kd);
     w.sums = cv.take<T>(kd);
     T* cdev = cv.take<T>(kd);
+    T* cnext = cv.take<T>(kd);
     T* parts = cv.take<T>(std::max(nbi, nbv * d));
     T* means_dev = cv.take<T>(d);
     int64_t* idx_dev = cv.take<int64_t>(k);
@@ -2094,46 +2121,135 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
         return MLRS_OK;
     };
 
-    // ---- tol_scaled = tol * mean(var(X, axis=0)) (feature_mean_var) ----
-    std::vector<T> hp((size_t)std::max(nbi, nbv * d));
-    e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, nullptr, parts, s);
-    if (e != hipSuccess) return hip_err(e, "kmeans col sums");
-    rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)(nbv * d), s);
+    // ---- pipeline: every read-back lands in pinned memory and is waited for
+    //      through an event, so the device keeps the next kernels queued while
+    //      the host works.  Per iteration the host waits twice: for the
+    //      counts (it decides on relocation before the assignment), and, with
+    //      the next iteration's sums already queued, for the changed flag. ----
+    const size_t st_bytes = aligned_bytes(sizeof(T) * (size_t)std::max(nbi, nbv * d)) +
+                            2 * aligned_bytes(sizeof(T) * (size_t)kd) + aligned_bytes(sizeof(uint32_t) * (size_t)k) +
+                            aligned_bytes(sizeof(int64_t) * (size_t)k) + aligned_bytes(sizeof(double) * (size_t)k) +
+                            aligned_bytes(sizeof(T) * (size_t)d) + aligned_bytes(sizeof(unsigned int)) + 256;
+    char* stage;
+    rc = pinned_staging(st_bytes, &stage);
     if (rc) return rc;
-    const double inv_n = 1.0 / (double)n;
-    std::vector<double> means((size_t)d, 0.0);
-    for (int64_t b = 0; b < nbv; ++b)
-        for (int64_t j = 0; j < d; ++j) means[j] += (double)hp[b * d + j];
-    std::vector<T> means_t((size_t)d);
-    for (int64_t j = 0; j < d; ++j) {
-        means[j] *= inv_n;
-        means_t[j] = (T)means[j];
+    Carver sc(stage);
+    T* h_parts = sc.take<T>((size_t)std::max(nbi, nbv * d));
+    T* h_sums = sc.take<T>((size_t)kd);
+    T* h_ct = sc.take<T>((size_t)kd);
+    uint32_t* h_counts = sc.take<uint32_t>((size_t)k);
+    int64_t* h_idx = sc.take<int64_t>((size_t)k);
+    double* h_delta = sc.take<double>((size_t)k);
+    T* h_means = sc.take<T>((size_t)d);
+    unsigned int* h_changed = sc.take<unsigned int>(1);
+    // the copies into pinned memory end before the call does, on every path
+    struct Drain {
+        hipStream_t s;
+        bool on = false;
+        hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+        ~Drain() {
+            if (on) (void)hipStreamSynchronize(s);
+            for (hipEvent_t x : ev)
+                if (x) (void)hipEventDestroy(x);
+        }
+    } drain{s};
+    for (hipEvent_t& x : drain.ev) {
+        e = hipEventCreateWithFlags(&x, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            x = nullptr;
+            return hip_err(e, "hipEventCreateWithFlags");
+        }
     }
-    e = hipMemcpyAsync(means_dev, means_t.data(), sizeof(T) * (size_t)d, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, means_dev, parts, s);
-    if (e != hipSuccess) return hip_err(e, "kmeans col sqdiff");
-    rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)(nbv * d), s);
-    if (rc) return rc;
-    double var_sum = 0.0;
-    for (int64_t q = 0; q < nbv * d; ++q) var_sum += (double)hp[q];
-    const double tol_scaled = tol * ((var_sum * inv_n) / (double)d);
+    hipEvent_t evA = drain.ev[0], evB = drain.ev[1], evP = drain.ev[2];
+    auto d2h_async = [&](void* dst, const void* src, size_t len) -> hipError_t {
+        note_read_back();
+        drain.on = true;
+        return hipMemcpyAsync(dst, src, len, hipMemcpyDeviceToHost, s);
+    };
+    auto h2d_async = [&](void* dst, const void* src, size_t len) -> hipError_t {
+        drain.on = true;
+        return hipMemcpyAsync(dst, src, len, hipMemcpyHostToDevice, s);
+    };
+    auto wait_ev = [&](hipEvent_t ev, const char* what) -> int32_t {
+        const hipError_t r = hipEventSynchronize(ev);
+        return r == hipSuccess ? MLRS_OK : hip_err(r, what);
+    };
 
-    std::vector<double> cen((size_t)kd), best_cen((size_t)kd), nc((size_t)kd), delta_h((size_t)k);
-    std::vector<T> ct((size_t)kd), sums_h((size_t)kd);
-    std::vector<uint32_t> counts_h((size_t)k), lab_h, best_lab_h, lab_rel;
+    // ---- tol_scaled = tol * mean(var(X, axis=0)) (feature_mean_var).  The
+    //      two passes' block partials come back asynchronously and the host
+    //      sums them (f64, block order) while the first assignment runs. ----
+    const double inv_n = 1.0 / (double)n;
+    double tol_scaled = 0.0;
+    int tol_stage = 0;  // 0: first pass queued; 1: second pass queued; 2: done
+    e = launch_km_col_sums<T>(x, n, d, nbv, rpbv, nullptr, parts, s);
+    if (e == hipSuccess) e = d2h_async(h_parts, parts, sizeof(T) * (size_t)(nbv * d));
+    if (e == hipSuccess) e = hipEventRecord(evP, s);
+    if (e != hipSuccess) return hip_err(e, "kmeans col sums");
+    auto tol_step = [&]() -> int32_t {
+        int32_t r = wait_ev(evP, "kmeans col sums");
+        if (r) return r;
+        if (tol_stage == 0) {
+            std::vector<double> means((size_t)d, 0.0);
+            for (int64_t b = 0; b < nbv; ++b)
+                for (int64_t j = 0; j < d; ++j) means[j] += (double)h_parts[b * d + j];
+            for (int64_t j = 0; j < d; ++j) {
+                means[j] *= inv_n;
+                h_means[j] = (T)means[j];
+            }
+            hipError_t e2 = h2d_async(means_dev, h_means, sizeof(T) * (size_t)d);
+            if (e2 == hipSuccess) e2 = launch_km_col_sums<T>(x, n, d, nbv, rpbv, means_dev, parts, s);
+            if (e2 == hipSuccess) e2 = d2h_async(h_parts, parts, sizeof(T) * (size_t)(nbv * d));
+            if (e2 == hipSuccess) e2 = hipEventRecord(evP, s);
+            if (e2 != hipSuccess) return hip_err(e2, "kmeans col sqdiff");
+            tol_stage = 1;
+        } else if (tol_stage == 1) {
+            double var_sum = 0.0;
+            for (int64_t q = 0; q < nbv * d; ++q) var_sum += (double)h_parts[q];
+            tol_scaled = tol * ((var_sum * inv_n) / (double)d);
+            tol_stage = 2;
+        }
+        return MLRS_OK;
+    };
+
+    // Two device centre buffers: the assignment reads one while the next
+    // iteration's mean divide (queued before the loop knows whether it goes
+    // on) writes the other.
+    T* cbuf[2] = {cdev, cnext};
+    int cb = 0;
+    cdev = cbuf[cb];
+    // This iteration's centroid sums under labv, the mean divide into cout,
+    // the counts read back (the sums too where the host needs them before
+    // the assignment: the pruned fit's centre moves); evA follows them.
+    auto enqueue_sums = [&](const uint32_t* labv, T* cout) -> int32_t {
+        hipError_t e2;
+        {
+            KernelTimer kt(s, "km_centroid_sums");
+            e2 = launch_km_centroid_sums<T>(x, labv, n, d, k, nb, rpb, w, s);
+        }
+        if (e2 == hipSuccess) e2 = launch_km_mean<T>(w.sums, w.counts, k, d, cout, s);
+        if (e2 == hipSuccess) e2 = d2h_async(h_counts, w.counts, sizeof(uint32_t) * (size_t)k);
+        if (e2 == hipSuccess && prune) e2 = d2h_async(h_sums, w.sums, sizeof(T) * (size_t)kd);
+        if (e2 == hipSuccess) e2 = hipEventRecord(evA, s);
+        return e2 == hipSuccess ? MLRS_OK : hip_err(e2, "kmeans centroid sums");
+    };
+
+    std::vector<double> cen((size_t)kd), best_cen((size_t)kd), nc((size_t)kd);
+    std::vector<T> ct((size_t)kd);
+    std::vector<uint32_t> lab_h, best_lab_h;
     std::vector<T> dist_h;
     bool have = false;
     double best_inertia = 0.0;
     int64_t best_iter = 0;
-    std::vector<int64_t> chosen;  // outlives the asynchronous upload of the picks
     for (int64_t restart = 0; restart < runs; ++restart) {
         // ---- initial centres (init_centers, cluster/kmeans.rs:893-920) ----
+        cb = 0;
+        cdev = cbuf[cb];
         if (init_kind == 0) {
             e = hipMemcpyAsync(cdev, init, sizeof(T) * (size_t)kd, hipMemcpyDeviceToDevice, s);
             if (e != hipSuccess) return hip_err(e, "kmeans init");
         } else {
             KmRng rng{seed + (uint64_t)restart};
-            chosen.clear();
+            std::vector<int64_t> chosen;
             chosen.reserve((size_t)k);
             if (init_kind == 2) {  // random_sample (prims/kmeans.rs:1769-1786)
                 // the partial Fisher-Yates shuffle of 0..n over the positions
@@ -2247,13 +2363,15 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                     cur = next;
                 }
             }
-            e = hipMemcpyAsync(idx_dev, chosen.data(), sizeof(int64_t) * (size_t)k, hipMemcpyHostToDevice, s);
+            for (int64_t i = 0; i < k; ++i) h_idx[i] = chosen[i];
+            e = h2d_async(idx_dev, h_idx, sizeof(int64_t) * (size_t)k);
             if (e == hipSuccess) e = launch_km_gather<T>(x, idx_dev, k, d, cdev, s);
             if (e != hipSuccess) return hip_err(e, "kmeans init gather");
         }
-        rc = km_d2h<T>(ct.data(), cdev, sizeof(T) * (size_t)kd, s);
-        if (rc) return rc;
-        for (int64_t q = 0; q < kd; ++q) cen[q] = (double)ct[q];
+        // the initial centres read back, waited for once the first assignment is queued
+        e = d2h_async(h_ct, cdev, sizeof(T) * (size_t)kd);
+        if (e == hipSuccess) e = hipEventRecord(evB, s);
+        if (e != hipSuccess) return hip_err(e, "kmeans init read-back");
 
         // ---- single_run ----
         int cur = 0;
@@ -2264,25 +2382,43 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
             e = launch_km_bound_init<T>(dist, n, pc.gamma, pc.eta, pU, s);
             if (e != hipSuccess) return hip_err(e, "kmeans bounds");
         }
+        if (tol_stage == 0) {
+            rc = tol_step();  // the means, summed while the assignment runs
+            if (rc) return rc;
+        }
+        if (max_iter > 0) {
+            rc = enqueue_sums(lab[cur], cbuf[cb ^ 1]);
+            if (rc) return rc;
+        }
+        rc = wait_ev(evB, "kmeans init read-back");
+        if (rc) return rc;
+        for (int64_t q = 0; q < kd; ++q) {
+            ct[q] = h_ct[q];
+            cen[q] = (double)ct[q];
+        }
         int64_t iters = 0;
         for (int64_t it = 0; it < max_iter; ++it) {
             ++iters;
-            {
-                KernelTimer kt(s, "km_centroid_sums");
-                e = launch_km_centroid_sums<T>(x, lab[cur], n, d, k, nb, rpb, w, s);
-            }
-            note_read_back();
-            if (e == hipSuccess) e = hipMemcpyAsync(sums_h.data(), w.sums, sizeof(T) * (size_t)kd,
-                                                    hipMemcpyDeviceToHost, s);
-            if (e == hipSuccess) e = hipMemcpyAsync(counts_h.data(), w.counts, sizeof(uint32_t) * (size_t)k,
-                                                    hipMemcpyDeviceToHost, s);
-            if (e == hipSuccess) e = hipStreamSynchronize(s);
-            if (e != hipSuccess) return hip_err(e, "kmeans centroid sums");
+            rc = wait_ev(evA, "kmeans centroid sums");
+            if (rc) return rc;
             std::vector<int64_t> cnt((size_t)k);
-            for (int64_t c = 0; c < k; ++c) cnt[c] = counts_h[c];
-            for (int64_t q = 0; q < kd; ++q) nc[q] = (double)sums_h[q];
             int64_t empties = 0;
-            for (int64_t c = 0; c < k; ++c) empties += cnt[c] == 0;
+            for (int64_t c = 0; c < k; ++c) {
+                cnt[c] = h_counts[c];
+                empties += cnt[c] == 0;
+            }
+            // The sums on the host: the pruned fit has them already (its
+            // centre moves); a relocation needs them now; else they come back
+            // with the changed flag, for the centre shift.
+            bool have_sums = prune;
+            if (empties && !have_sums) {
+                e = d2h_async(h_sums, w.sums, sizeof(T) * (size_t)kd);
+                if (e == hipSuccess) e = hipStreamSynchronize(s);
+                if (e != hipSuccess) return hip_err(e, "kmeans centroid sums");
+                have_sums = true;
+            }
+            if (have_sums)
+                for (int64_t q = 0; q < kd; ++q) nc[q] = (double)h_sums[q];
             if (empties && !dist_fresh) {
                 // the ranking reads every row's distance: the pruned
                 // assignment left some untouched (same centres, same labels)
@@ -2396,33 +2532,39 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
                 }
                 cnt = cnt_w;
             }
-            // mean divide in f64 and the centre shift (single_run :1010-1030)
-            for (int64_t c = 0; c < k; ++c) {
-                const double inv = 1.0 / (double)cnt[c];
-                for (int64_t j = 0; j < d; ++j) nc[c * d + j] = nc[c * d + j] * inv;
-            }
-            double shift = 0.0;
-            for (int64_t q = 0; q < kd; ++q) {
-                const double diff = nc[q] - cen[q];
-                shift += diff * diff;
-            }
-            cen.swap(nc);
-            if (prune) {
-                // an upper bound of each centre's move (F centres, f64 sums)
+            // mean divide in f64 (single_run :1010-1030); the device's
+            // km_mean_kernel made the same centres from the same operands, and
+            // only a relocation changes them
+            T* cnew = cbuf[cb ^ 1];
+            auto mean_divide = [&]() {
                 for (int64_t c = 0; c < k; ++c) {
-                    double acc = 0.0;
-                    for (int64_t j = 0; j < d; ++j) {
-                        const double diff = (double)(T)cen[c * d + j] - (double)ct[c * d + j];
-                        acc += diff * diff;
-                    }
-                    delta_h[c] = std::sqrt(acc) * (1.0 + std::ldexp(1.0, -40));
+                    const double inv = 1.0 / (double)cnt[c];
+                    for (int64_t j = 0; j < d; ++j) nc[c * d + j] = nc[c * d + j] * inv;
                 }
-                e = hipMemcpyAsync(pdelta, delta_h.data(), sizeof(double) * (size_t)k, hipMemcpyHostToDevice, s);
-                if (e != hipSuccess) return hip_err(e, "kmeans centre moves upload");
+            };
+            if (have_sums) {
+                mean_divide();
+                if (empties) {
+                    for (int64_t q = 0; q < kd; ++q) h_ct[q] = (T)nc[q];
+                    e = h2d_async(cnew, h_ct, sizeof(T) * (size_t)kd);
+                    if (e != hipSuccess) return hip_err(e, "kmeans centres upload");
+                }
+                if (prune) {
+                    // an upper bound of each centre's move (F centres, f64 sums)
+                    for (int64_t c = 0; c < k; ++c) {
+                        double acc = 0.0;
+                        for (int64_t j = 0; j < d; ++j) {
+                            const double diff = (double)(T)nc[c * d + j] - (double)ct[c * d + j];
+                            acc += diff * diff;
+                        }
+                        h_delta[c] = std::sqrt(acc) * (1.0 + std::ldexp(1.0, -40));
+                    }
+                    e = h2d_async(pdelta, h_delta, sizeof(double) * (size_t)k);
+                    if (e != hipSuccess) return hip_err(e, "kmeans centre moves upload");
+                }
             }
-            for (int64_t q = 0; q < kd; ++q) ct[q] = (T)cen[q];
-            e = hipMemcpyAsync(cdev, ct.data(), sizeof(T) * (size_t)kd, hipMemcpyHostToDevice, s);
-            if (e != hipSuccess) return hip_err(e, "kmeans centres upload");
+            cb ^= 1;
+            cdev = cnew;
             cur ^= 1;
             if (prune) {
                 rc = prune_assign(lab[cur ^ 1], lab[cur], &dist_fresh);
@@ -2432,21 +2574,49 @@ static int32_t kmeans_fit_impl(const T* x, int64_t x_len, int64_t n, int64_t d, 
             }
             if (rc) return rc;
             e = launch_km_changed(lab[cur], lab[cur ^ 1], n, changed_dev, s);
+            if (e == hipSuccess) e = d2h_async(h_changed, changed_dev, sizeof(unsigned int));
+            if (e == hipSuccess && !have_sums) e = d2h_async(h_sums, w.sums, sizeof(T) * (size_t)kd);
+            if (e == hipSuccess) e = hipEventRecord(evB, s);
             if (e != hipSuccess) return hip_err(e, "kmeans labels_changed");
-            unsigned int changed = 0;
-            rc = km_d2h<T>(&changed, changed_dev, sizeof(changed), s);
+            // the next iteration's sums, queued before this one's outcome is
+            // known (unused when the loop stops here)
+            if (it + 1 < max_iter) {
+                rc = enqueue_sums(lab[cur], cbuf[cb ^ 1]);
+                if (rc) return rc;
+            }
+            if (tol_stage == 1) {
+                rc = tol_step();  // the variance, summed while the assignment runs
+                if (rc) return rc;
+            }
+            rc = wait_ev(evB, "kmeans labels_changed");
             if (rc) return rc;
-            if (changed == 0) break;       // strict convergence first
+            if (!have_sums) {
+                for (int64_t q = 0; q < kd; ++q) nc[q] = (double)h_sums[q];
+                mean_divide();
+            }
+            double shift = 0.0;
+            for (int64_t q = 0; q < kd; ++q) {
+                const double diff = nc[q] - cen[q];
+                shift += diff * diff;
+            }
+            cen.swap(nc);
+            for (int64_t q = 0; q < kd; ++q) ct[q] = (T)cen[q];
+            if (*h_changed == 0) break;    // strict convergence first
             if (shift <= tol_scaled) break;
         }
         // ---- inertia_ = sum of the per-row squared distances (inertia_rows +
-        //      sum_device) ----
-        e = launch_km_inertia<T>(x, cdev, lab[cur], n, d, dist, nbi, rpbi, parts, s);
+        //      sum_device).  After a full assignment dist holds exactly those
+        //      values (the assignment's exact value is inertia_rows' sum, in
+        //      its order, under the final centres), so only the block sums run. ----
+        if (dist_fresh)
+            e = launch_km_block_sum<T>(dist, n, nbi, rpbi, parts, s);
+        else
+            e = launch_km_inertia<T>(x, cdev, lab[cur], n, d, dist, nbi, rpbi, parts, s);
         if (e != hipSuccess) return hip_err(e, "kmeans inertia");
-        rc = km_d2h<T>(hp.data(), parts, sizeof(T) * (size_t)nbi, s);
+        rc = km_d2h<T>(h_parts, parts, sizeof(T) * (size_t)nbi, s);
         if (rc) return rc;
         double inertia = 0.0;
-        for (int64_t b = 0; b < nbi; ++b) inertia += (double)hp[b];
+        for (int64_t b = 0; b < nbi; ++b) inertia += (double)h_parts[b];
         // ---- keep the restart? strictly lower inertia on a different partition ----
         bool keep = !have;
         if (have && inertia < best_inertia) {

@@ -28,7 +28,7 @@
 //
 // Also: km_changed_kernel (labels that differ), km_inertia_rows_kernel and
 // km_block_sum_kernel (inertia_rows + block_sum_f, kernels/kmeans.rs:123-145,
-// 523-545), km_col_sum_kernel (col_sum_blocked and, given the means,
+// 523-545), km_mean_kernel (the mean divide), km_col_sum_kernel (col_sum_blocked and, given the means,
 // col_sqdiff_blocked, :704-762), km_mind2_kernel (kmeanspp_mind2, :576-603) and
 // km_gather_kernel (gather_rows_idx, :552-570).  Every sum is the reference's
 // element type and order.
@@ -341,48 +341,73 @@ __global__ __launch_bounds__(256) void km_inertia_rows_kernel(const T* __restric
     out[i] = row_sqdist<T, VEC>(x + i * d, c + (int64_t)labels[i] * d, d);
 }
 
-// acc + p[0] + p[1] + ... in order over contiguous values: single values up
-// to a 16-byte boundary, then 16-byte pieces sixteen at a time (one thread
-// walks a whole block of the layout, so the loads in flight set its speed).
+// block_sum_f: out[b] = ((v[b rpb] + v[b rpb + 1]) + ...) in order, one
+// dependent chain per block (a few hundred blocks of ~20,000 rows at the
+// reference's sum_device layout).  A workgroup per block stages its values
+// through LDS in 16 KB chunks, double-buffered: lane 0 adds one chunk while
+// waves 1-3 load the next, so the chain runs at the add latency rather than
+// behind one thread's loads.
 template <typename T>
-__device__ __forceinline__ T ordered_sum_contig(const T* __restrict__ p, int64_t count) {
+__global__ __launch_bounds__(256) void km_block_sum_kernel(const T* __restrict__ v, int64_t n, int64_t rpb,
+                                                           T* __restrict__ out) {
+    constexpr int CH = 16384 / (int)sizeof(T);
     constexpr int V = 16 / (int)sizeof(T);
+    __shared__ __attribute__((aligned(16))) T buf[2][CH];
+    const int64_t start = (int64_t)blockIdx.x * rpb;
+    const int64_t len = ((start + rpb) < n ? start + rpb : n) - start;
+    const int nch = (int)((len + CH - 1) / CH);
+    const int tid = threadIdx.x;
+    auto chunk_len = [&](int c) -> int {
+        const int64_t left = len - (int64_t)c * CH;
+        return left < CH ? (int)left : CH;
+    };
+    auto load = [&](int c, T* dst, int first, int step) {
+        const T* src = v + start + (int64_t)c * CH;
+        const int cnt = chunk_len(c);
+        for (int i = first; i < cnt; i += step) dst[i] = src[i];
+    };
+    if (nch > 0) load(0, buf[0], tid, 256);
+    __syncthreads();
     T acc = T(0);
-    if (count <= 0) return acc;
-    int64_t i = 0;
-    while (i < count && (reinterpret_cast<uintptr_t>(p + i) & 15) != 0) acc = acc + p[i++];
-    const float4* p4 = reinterpret_cast<const float4*>(p + i);
-    const int64_t n4 = (count - i) / V;
-    int64_t b = 0;
-    for (; b + 16 <= n4; b += 16) {
-        float4 w[16];
+    for (int c = 0; c < nch; ++c) {
+        if (tid >= 64 && c + 1 < nch) load(c + 1, buf[(c + 1) & 1], tid - 64, 192);
+        if (tid == 0) {
+            const T* p = buf[c & 1];
+            const int cnt = chunk_len(c);
+            const int nv = cnt / V;
+            int i = 0;
+            // 16-byte reads eight ahead of the adds (they are independent of them)
+            for (; i + 8 <= nv; i += 8) {
+                float4 w[8];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) w[u] = p4[b + u];
+                for (int u = 0; u < 8; ++u) w[u] = reinterpret_cast<const float4*>(p)[i + u];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const T* e = reinterpret_cast<const T*>(&w[u]);
+                for (int u = 0; u < 8; ++u) {
+                    const T* e = reinterpret_cast<const T*>(&w[u]);
 #pragma unroll
-            for (int j = 0; j < V; ++j) acc = acc + e[j];
+                    for (int j = 0; j < V; ++j) acc = acc + e[j];
+                }
+            }
+            for (int j = i * V; j < cnt; ++j) acc = acc + p[j];
         }
+        __syncthreads();  // chunk c read; chunk c + 1 stored
     }
-    for (; b < n4; ++b) {
-        const float4 w = p4[b];
-        const T* e = reinterpret_cast<const T*>(&w);
-#pragma unroll
-        for (int j = 0; j < V; ++j) acc = acc + e[j];
-    }
-    for (i += n4 * V; i < count; ++i) acc = acc + p[i];
-    return acc;
+    if (tid == 0) out[blockIdx.x] = acc;
 }
 
+// The new centres from the sums and counts: (T)((double)sums * (1.0 /
+// (double)count)), the host's mean divide (single_run, cluster/kmeans.rs
+// :1010-1030) operation for operation; every step is correctly rounded on the
+// device as on the host, so the centres are the same bits.  A label without
+// rows gives NaN or inf here; the host then relocates and uploads its own.
 template <typename T>
-__global__ __launch_bounds__(256) void km_block_sum_kernel(const T* __restrict__ v, int64_t n, int64_t nb,
-                                                           int64_t rpb, T* __restrict__ out) {
-    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (b >= nb) return;
-    const int64_t start = b * rpb;
-    const int64_t end = (start + rpb) < n ? start + rpb : n;
-    out[b] = ordered_sum_contig<T>(v + start, end - start);
+__global__ __launch_bounds__(256) void km_mean_kernel(const T* __restrict__ sums, const uint32_t* __restrict__ counts,
+                                                      int64_t k, int64_t d, T* __restrict__ out) {
+    const int64_t total = k * d;
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < total; q += (int64_t)gridDim.x * 256) {
+        const double inv = 1.0 / (double)counts[q / d];
+        out[q] = (T)((double)sums[q] * inv);
+    }
 }
 
 template <typename T>
@@ -490,8 +515,21 @@ hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int
     else
         hipLaunchKernelGGL((km_inertia_rows_kernel<T, false>), dim3(blocks_for(n, 1 << 30)), dim3(256), 0, s, x, c,
                            labels, n, d, rows);
-    hipLaunchKernelGGL((km_block_sum_kernel<T>), dim3(blocks_for(nb, 1 << 20)), dim3(256), 0, s, rows, n, nb, rpb,
-                       parts);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? launch_km_block_sum<T>(rows, n, nb, rpb, parts, s) : e;
+}
+
+template <typename T>
+hipError_t launch_km_block_sum(const T* v, int64_t n, int64_t nb, int64_t rpb, T* parts, hipStream_t s) {
+    if (nb <= 0) return hipSuccess;
+    hipLaunchKernelGGL((km_block_sum_kernel<T>), dim3((unsigned)nb), dim3(256), 0, s, v, n, rpb, parts);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_km_mean(const T* sums, const uint32_t* counts, int64_t k, int64_t d, T* out, hipStream_t s) {
+    if (k * d <= 0) return hipSuccess;
+    hipLaunchKernelGGL((km_mean_kernel<T>), dim3(blocks_for(k * d, 4096)), dim3(256), 0, s, sums, counts, k, d, out);
     return hipGetLastError();
 }
 
@@ -939,6 +977,8 @@ hipError_t launch_km_count_nonfinite(const T* v, int64_t n, unsigned int* count,
                                                    int64_t, const KmScratch<T>&, hipStream_t);                     \
     template hipError_t launch_km_inertia<T>(const T*, const T*, const uint32_t*, int64_t, int64_t, T*, int64_t,    \
                                              int64_t, T*, hipStream_t);                                            \
+    template hipError_t launch_km_block_sum<T>(const T*, int64_t, int64_t, int64_t, T*, hipStream_t);              \
+    template hipError_t launch_km_mean<T>(const T*, const uint32_t*, int64_t, int64_t, T*, hipStream_t);          \
     template hipError_t launch_km_col_sums<T>(const T*, int64_t, int64_t, int64_t, int64_t, const T*, T*,           \
                                               hipStream_t);                                                        \
     template hipError_t launch_km_mind2<T>(const T*, int64_t, int64_t, int64_t, int, T*, hipStream_t);              \

@@ -421,6 +421,12 @@ hipError_t launch_km_scatter_list(const uint32_t* list, int64_t m, const uint32_
                                   double gamma, double eta, uint32_t* lab_new, T* dist, double* U, hipStream_t s);
 template <typename T>
 hipError_t launch_km_count_nonfinite(const T* v, int64_t n, unsigned int* count, hipStream_t s);
+// block_sum_f over v: parts[b] = the ordered sum of rows [b rpb, (b + 1) rpb).
+template <typename T>
+hipError_t launch_km_block_sum(const T* v, int64_t n, int64_t nb, int64_t rpb, T* parts, hipStream_t s);
+// out = (T)((double)sums * (1.0 / (double)counts[c])), element by element.
+template <typename T>
+hipError_t launch_km_mean(const T* sums, const uint32_t* counts, int64_t k, int64_t d, T* out, hipStream_t s);
 template <typename T>
 hipError_t launch_km_inertia(const T* x, const T* c, const uint32_t* labels, int64_t n, int64_t d, T* rows,
                              int64_t nb, int64_t rpb, T* parts, hipStream_t s);
