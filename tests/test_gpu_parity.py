@@ -139,6 +139,21 @@ def test_quantized_data_many_ties(d, k):
     check_knn(xq, xt, k, "cosine", "quantized cosine")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("k", [1, 100])
+def test_nan_rows_sign_screen(d, k):
+    """The k = 1 and three-block-list kernels screen by the sign of
+    (threshold - value) in waves whose queries all have finite screen sums:
+    NaN index rows give NaN screen values, which that screen drops (their exact
+    values are NaN, never kept), and the waves holding a NaN query keep the
+    compare screen.  Both must give the reference's lists."""
+    xq, xt = _data(15, 150, 3000, d)
+    xt[[5, 1200, 2999]] = np.nan
+    xt[40, 3] = np.nan
+    xq[[1, 90]] = np.nan
+    check_knn(xq, xt, k, "euclidean", "nan sign screen k=%d" % k)
+
+
 @pytest.mark.parametrize("d", [4, 64, 200])
 def test_nan_rows(d):
     xq, xt = _data(8, 200, 1500, d)
@@ -232,12 +247,13 @@ def test_f64_nonaligned_pointer():
 
 
 @pytest.mark.parametrize("d", [64, 240])
-def test_huge_values_overflow_norms(d):
+@pytest.mark.parametrize("k", [1, 6, 100])
+def test_huge_values_overflow_norms(d, k):
     """Squared norms overflow f32: the screen bound becomes infinite and every
     row is evaluated exactly; results still match the reference arithmetic."""
     xq, xt = _data(10, 40, 500, d, scale=1e18)
     xt[:5] *= 1e2
-    check_knn(xq, xt, 6, "euclidean", "huge")
+    check_knn(xq, xt, k, "euclidean", "huge")
 
 
 def test_k_equals_n_train_and_tiny_index():
