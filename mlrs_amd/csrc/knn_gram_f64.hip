@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     const int K2 = gram_list_cap(k);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile rows and LDS slots in SGPRs
     const int g = lane >> 4;   // lane group: K quarter / first tile row of the lane
     const int jl = lane & 15;  // query of the lane within the wave
     WaveLds64& L = wl[w];
@@ -417,15 +417,28 @@ __global__ __launch_bounds__(256, 2) void knn_gram_f64_kernel(GramArgs64 a) {
     // staged path.
     auto direct_load = [&](double (&dst)[kBn][STRIDE], uint32_t t0) {
         if constexpr (DIRECT) {
+            // the row (and kilobyte) of each load is wave-uniform: a scalar
+            // base plus the lane's 16-byte offset.  A whole tile of rows
+            // without padded columns loads unconditionally (t0 + kBn could
+            // wrap, so the rows left are compared).
+            if (t_end32 - t0 >= (uint32_t)kBn && d == DP) {
 #pragma unroll
-        for (int i = 0; i < LOADS_PER_WAVE; ++i) {
-            const int kb = w * LOADS_PER_WAVE + i;
-            const int r = kb / KB_PER_ROW, half = kb % KB_PER_ROW;
-            const uint32_t t = t0 + (uint32_t)r;
-            const int c = half * 128 + 2 * lane;
-            if (t < t_end32 && c < d)
-                global_to_lds16(X + (int64_t)t * d + c, &dst[r][half * 128]);
-        }
+                for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+                    const int kb = w * LOADS_PER_WAVE + i;
+                    const int r = kb / KB_PER_ROW, half = kb % KB_PER_ROW;
+                    const double* row = X + ((int64_t)(t0 + (uint32_t)r) * d + half * 128);
+                    global_to_lds16(row + 2 * lane, &dst[r][half * 128]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+                    const int kb = w * LOADS_PER_WAVE + i;
+                    const int r = kb / KB_PER_ROW, half = kb % KB_PER_ROW;
+                    const double* row = X + ((int64_t)(t0 + (uint32_t)r) * d + half * 128);
+                    if (t0 + (uint32_t)r < t_end32 && half * 128 + 2 * lane < d)
+                        global_to_lds16(row + 2 * lane, &dst[r][half * 128]);
+                }
+            }
         }
         if (tid < kBn) {
             const uint32_t t = t0 + (uint32_t)tid;
