@@ -236,6 +236,52 @@ __global__ __launch_bounds__(256) void km_psum_kernel(const T* __restrict__ x, i
     }
 }
 
+// The same sums with one wave per (bucket, 64-feature chunk), for d a
+// multiple of 64: the bucket is wave-uniform, so its row numbers come through
+// scalar loads, eight at a time with the next eight requested while this
+// eight's row loads are in flight, and lane j adds feature chunk * 64 + j of
+// each row in ascending order (the same order and operations as
+// km_psum_kernel).
+template <typename T>
+__global__ __launch_bounds__(256) void km_psum_wave_kernel(const T* __restrict__ x, int64_t d, int64_t nb,
+                                                           int64_t k, const uint32_t* __restrict__ pcount,
+                                                           const uint32_t* __restrict__ seg,
+                                                           const uint32_t* __restrict__ perm,
+                                                           T* __restrict__ psum) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nch = d >> 6;
+    const int64_t total = nb * k * nch;
+    const int64_t step = (int64_t)gridDim.x * 4;
+    for (int64_t wv = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); wv < total;
+         wv += step) {
+        const int64_t bc = wv / nch;
+        const int64_t j = (wv - bc * nch) * 64 + lane;
+        const uint32_t s0 = seg[bc], m = pcount[bc];
+        const uint32_t* __restrict__ pp = perm + s0;
+        const T* __restrict__ xj = x + j;
+        T acc = T(0);
+        uint32_t p = 0;
+        uint32_t r[8];
+        if (m >= 8) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) r[u] = pp[u];
+        }
+        for (; p + 8 <= m; p += 8) {
+            T v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = xj[(int64_t)r[u] * d];
+            if (p + 16 <= m) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) r[u] = pp[p + 8 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = acc + v[u];
+        }
+        for (; p < m; ++p) acc = acc + xj[(int64_t)pp[p] * d];
+        psum[bc * d + j] = acc;
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void km_reduce_kernel(const T* __restrict__ psum, int64_t nb, int64_t kd,
                                                         T* __restrict__ sums) {
@@ -492,8 +538,12 @@ hipError_t launch_km_centroid_sums(const T* x, const uint32_t* labels, int64_t n
     hipLaunchKernelGGL(km_add_starts_kernel, dim3(blocks_for(nb * k, 4096)), dim3(256), 0, s, w.seg, nb, k, w.starts);
     hipLaunchKernelGGL(km_scatter_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, labels, n, rpb, k, nsub,
                        srows, nbits, w.seg, w.cursor, w.perm);
-    hipLaunchKernelGGL((km_psum_kernel<T>), dim3(blocks_for(nb * k * d, 65536)), dim3(256), 0, s, x, d, nb, k,
-                       w.pcount, w.seg, w.perm, w.psum);
+    if (d % 64 == 0)
+        hipLaunchKernelGGL((km_psum_wave_kernel<T>), dim3(blocks_for(nb * k * (d / 64) * 64, 65536)), dim3(256), 0, s,
+                           x, d, nb, k, w.pcount, w.seg, w.perm, w.psum);
+    else
+        hipLaunchKernelGGL((km_psum_kernel<T>), dim3(blocks_for(nb * k * d, 65536)), dim3(256), 0, s, x, d, nb, k,
+                           w.pcount, w.seg, w.perm, w.psum);
     hipLaunchKernelGGL((km_reduce_kernel<T>), dim3(blocks_for(k * d, 1 << 20)), dim3(256), 0, s, w.psum, nb, k * d,
                        w.sums);
     return hipGetLastError();
