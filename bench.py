@@ -254,7 +254,7 @@ def main():
         bound, peak, unit = "valu", PEAKS["valu_f64" if f64 else "valu_f32"], "TFLOP/s"
     elif kname.startswith("knn_gram_f64"):
         bound, peak, unit = "mfma", PEAKS["mfma_f64"], "TFLOP/s"
-    elif kname.startswith("knn_gram_f32"):
+    elif kname.startswith("knn_gram_f32") or kname.startswith("knn_k1_resident_f32"):
         bound, peak, unit = "mfma", PEAKS["mfma_f32"], "TFLOP/s"
     else:
         # the low-d ALU kernel and the exact tiles of small searches: vector

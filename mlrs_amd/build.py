@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libmlrs_hip_knn.so")
 SOURCES = ["capi.hip", "knn_exact.hip", "knn_gram_f32.hip", "knn_gram_f64.hip", "knn_lowd.hip",
            "knn_consumers.hip", "knn_radius.hip", "knn_radius_gram.hip", "knn_graph.hip",
-           "kmeans_loop.hip", "probe.hip"]
+           "kmeans_loop.hip", "probe.hip", "knn_k1_resident.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",

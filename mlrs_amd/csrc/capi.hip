@@ -544,8 +544,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     const bool vec4 = (d % 4 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(xt) & 15) == 0);
     gram_f32_split(nq, nt, d, k, cus, vec4, &grid_wgs, &nslots);
+    // k = 1 over an index that a few workgroups' LDS holds: the resident
+    // search (knn_k1_resident.hip), one list slot per chunk
+    const int res_chunks = gram_f32_k1_resident_chunks(nq, nt, d, k, arm, vec4);
     // per-(segment slot, query) lists: the kernel's top-k state, merged at the end
-    size_t parts = (size_t)nslots * nq * gram_list_cap(k);
+    size_t parts = (size_t)std::max<int64_t>(nslots, res_chunks) * nq * gram_list_cap(k);
     size_t qvals = (k > 1) ? gram_f32_qval_elems(grid_wgs) : 0;
     size_t summs = (k > 1) ? (size_t)nslots * nq : 0;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +
@@ -612,6 +615,15 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     void* seed_buf = seed_bytes ? static_cast<void*>(cv.take<char>(seed_bytes)) : nullptr;
     a.out_val = out_v;
     a.out_idx = out_i;
+    if (res_chunks) {
+        {
+            KernelTimer timer(s, "knn_k1_resident_f32_kernel");
+            e = launch_gram_f32_k1_resident(a, arm, cus, s);
+        }
+        if (e == hipSuccess) e = launch_gram_f32_k1_resident_merge(a, res_chunks, s);
+        if (e != hipSuccess) return hip_err(e, "knn_k1_resident_f32");
+        return ok();
+    }
     e = launch_gram_f32_prep(a, arm, s, seed_buf);
     if (e == hipSuccess) {
         KernelTimer timer(s, "knn_gram_f32_kernel");

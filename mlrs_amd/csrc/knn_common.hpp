@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "knn_kernels.hpp"  // EmitMode
+
 namespace mlrs {
 
 // Arithmetic arms of the reference cpu backend (the ones results are compared
@@ -766,6 +768,33 @@ __device__ __forceinline__ void seed_kth_block(const T* __restrict__ Q, const T*
                 shared_r[q0 + j] = (Bits)__double_as_longlong((double)kv);
         }
     }
+}
+
+// Output transform: the boundary root of prims/knn.rs:877-883 (Euclidean),
+// identity (cosine), or the k-means (label, squared distance) pair with
+// argmin_dist_rows' centre-0 seeding (crates/mlrs-kernels/src/kmeans.rs:284-310).
+__device__ __forceinline__ void emit_pair(int mode, const float* __restrict__ Q, const float* __restrict__ X,
+                                          const float* __restrict__ qsq, const float* __restrict__ xsq, int64_t d,
+                                          int k, int64_t qg, int slot, float v, uint32_t ix,
+                                          float* __restrict__ out_val, uint32_t* __restrict__ out_idx) {
+    const int64_t o = qg * k + slot;
+    if (mode == EMIT_KMEANS) {
+        // argmin_dist_rows seeds `best` from centre 0 unconditionally, so a NaN
+        // distance to centre 0 wins with label 0.  That distance can only be
+        // NaN when a norm is non-finite; check those rows exactly.
+        const float inf = __builtin_huge_valf();
+        if (!(qsq[qg] < inf) || !(xsq[0] < inf)) {
+            float e0 = exact_pair<float, ARM_EUCLID_MULADD>(Q + qg * d, X, d, 0.0f, 0.0f);
+            if (e0 != e0) {
+                v = e0;
+                ix = 0;
+            }
+        }
+        out_val[o] = v;
+    } else {
+        out_val[o] = (mode == EMIT_SQRT) ? __builtin_sqrtf(v) : v;
+    }
+    out_idx[o] = (ix == kSentinelIdx) ? 0u : ix;
 }
 
 }  // namespace mlrs

@@ -162,6 +162,14 @@ void gram_f32_split(int64_t nq, int64_t nt, int64_t d, int k, int cus, bool vec4
 hipError_t launch_gram_f32_prep(const GramArgs32& a, int arm, hipStream_t s, void* seed_buf);
 size_t gram_f32_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4);
 hipError_t launch_gram_f32(const GramArgs32& a, int arm, hipStream_t s);
+// k = 1 Euclidean searches whose index fits a few workgroups' LDS
+// (knn_k1_resident.hip): the chunk count the launch uses (each chunk one
+// (chunk, query) list slot), or 0 where it does not serve the shape.
+int gram_f32_k1_resident_chunks(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4);
+// The resident search (part_val / part_idx: one slot per chunk), then the
+// merge of the chunks' lists with the output transform.
+hipError_t launch_gram_f32_k1_resident(const GramArgs32& a, int arm, int cus, hipStream_t s);
+hipError_t launch_gram_f32_k1_resident_merge(const GramArgs32& a, int nchunks, hipStream_t s);
 hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s);
 int gram_f32_max_k();
 int gram_f32_max_d();
