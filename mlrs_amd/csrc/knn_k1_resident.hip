@@ -16,8 +16,9 @@
 //  * Per tile, the k = 1 steps of the fused kernel: the threshold tightened
 //    with the tile's smallest expansion value + 2 eps, the screen (the sign
 //    of threshold - value where the wave's screen sums cannot overflow, the
-//    compare elsewhere), passing rows queued per query in LDS (16-bit chunk
-//    rows), a queue whose rows all screen above the tightened threshold
+//    compare elsewhere), passing rows queued per query (16-bit chunk rows, in
+//    global memory: admissions are rare at k = 1, and the LDS goes to the
+//    chunk), a queue whose rows all screen above the tightened threshold
 //    emptied before the tile's rows join it.
 //  * The queued rows are evaluated exactly, in the reference arm's operation
 //    order, with the query row from global memory and the index row from the
@@ -42,7 +43,6 @@ constexpr int kResQcap = 48;              // queued rows per query (flushed abov
 constexpr int kResLdsBytes = 163840;      // gfx950's LDS per workgroup
 
 struct ResWave {
-    uint16_t qidx[kResQpw][kResQcap];   // queued chunk rows
     float thr[kResQpw];
     float qs[kResQpw];
     float eps[kResQpw];
@@ -61,7 +61,8 @@ __host__ __device__ constexpr int res_rows_max(int dp) {
 
 template <int NG, int ARM>
 __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramArgs32 a, int chunk_rows,
-                                                                          int nchunks) {
+                                                                          int nchunks,
+                                                                          uint16_t* __restrict__ queues) {
     constexpr int DP = NG * 8;
     constexpr int STRIDE = DP + 4;  // an odd number of 16-byte chunks: 16 consecutive rows on distinct bank groups
     constexpr int RMAX = res_rows_max(DP);
@@ -82,6 +83,8 @@ __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramAr
     const int jl = lane & 31;
     const float inf = __builtin_huge_valf();
     ResWave& L = wl[w];
+    // this wave's queues in global memory, [query][position]: chunk rows
+    uint16_t* __restrict__ QI = queues + ((int64_t)blockIdx.x * kResWaves + w) * (kResQpw * kResQcap);
 
     // ---- the chunk: rows [row0, row0 + rows), zero columns past d, padded
     //      to whole tiles with zero rows of norm +inf ----
@@ -155,6 +158,9 @@ __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramAr
             }
             const uint32_t total = (uint32_t)__shfl((int)incl, kResQpw - 1, 64);
             if (lane < kResQpw) L.off[lane] = incl - c_;
+            // the queued rows were stored by other lanes of this wave
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             for (uint32_t base = 0; base < total; base += 64) {
                 const uint32_t e_ = base + (uint32_t)lane;
                 if (e_ < total) {
@@ -162,7 +168,7 @@ __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramAr
 #pragma unroll
                     for (int m_ = kResQpw / 2; m_ >= 1; m_ >>= 1)
                         if (L.off[j_ + m_] <= e_) j_ += m_;
-                    const uint32_t t_ = L.qidx[j_][e_ - L.off[j_]];
+                    const uint32_t t_ = QI[j_ * kResQcap + (e_ - L.off[j_])];
                     const float* qp = Q + (qwave + j_) * d;
                     const float* yp = &chunk[(int)t_ * STRIDE];
                     float acc = 0.0f;
@@ -270,7 +276,7 @@ __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramAr
                 while (msk) {
                     const int r = __builtin_ctz(msk);
                     msk &= msk - 1;
-                    L.qidx[jl][pos++] = (uint16_t)(tb + 8 * (r >> 2) + 4 * h + (r & 3));
+                    QI[jl * kResQcap + pos++] = (uint16_t)(tb + 8 * (r >> 2) + 4 * h + (r & 3));
                 }
                 cntr += c + co;
             }
@@ -319,11 +325,15 @@ hipError_t launch_res_ng(const GramArgs32& a, int cus, hipStream_t s) {
     const int64_t need = (nqb + kResWaves - 1) / kResWaves;  // groups that still get a block per wave
     if (ngrp > need) ngrp = need;
     hipLaunchKernelGGL((knn_k1_resident_f32_kernel<NG, ARM>), dim3((unsigned)(ngrp * nchunks)), dim3(kResThreads), 0,
-                       s, a, chunk_rows, nchunks);
+                       s, a, chunk_rows, nchunks, reinterpret_cast<uint16_t*>(a.qval));
     return hipGetLastError();
 }
 
 }  // namespace
+
+size_t gram_f32_k1_resident_queue_bytes(int cus) {
+    return (size_t)(cus > 0 ? cus : 1) * kResWaves * kResQpw * kResQcap * sizeof(uint16_t);
+}
 
 int gram_f32_k1_resident_chunks(int64_t nq, int64_t nt, int64_t d, int k, int arm, bool vec4) {
     if (k != 1 || !vec4 || d > 64 || nq < 1 || nt < 1) return 0;
