@@ -572,9 +572,11 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     float* xscale = cv.take<float>(nt);
     NormStats* stats = cv.take<NormStats>(1);
     hipError_t e = hipSuccess;
+    // the resident k = 1 search forms the query norms from its operand
+    const bool res_qsq = res_chunks && !qsq_pre;
     if (qsq_pre && !cos)
         qsq = const_cast<float*>(qsq_pre);  // only read
-    else
+    else if (!res_qsq)
         e = launch_row_norms<float>(xq, nq, d, qsq, host_cos ? qinv : nullptr, nullptr, nullptr, s);
     if (e == hipSuccess)
         e = launch_row_norms<float>(xt, nt, d, xsq, host_cos ? xinv : nullptr, cos ? xscale : nullptr, stats, s);
@@ -619,7 +621,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     if (res_chunks) {
         {
             KernelTimer timer(s, "knn_k1_resident_f32_kernel");
-            e = launch_gram_f32_k1_resident(a, arm, cus, s);
+            e = launch_gram_f32_k1_resident(a, arm, cus, res_qsq ? qsq : nullptr, s);
         }
         if (e == hipSuccess) e = launch_gram_f32_k1_resident_merge(a, res_chunks, s);
         if (e != hipSuccess) return hip_err(e, "knn_k1_resident_f32");

@@ -62,7 +62,8 @@ __host__ __device__ constexpr int res_rows_max(int dp) {
 template <int NG, int ARM>
 __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramArgs32 a, int chunk_rows,
                                                                           int nchunks,
-                                                                          uint16_t* __restrict__ queues) {
+                                                                          uint16_t* __restrict__ queues,
+                                                                          float* __restrict__ qsq_out) {
     constexpr int DP = NG * 8;
     constexpr int STRIDE = DP + 4;  // an odd number of 16-byte chunks: 16 consecutive rows on distinct bank groups
     constexpr int RMAX = res_rows_max(DP);
@@ -113,7 +114,6 @@ __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramAr
         const int64_t qrow = qvalid ? qmine : nq - 1;
 
         // ---- per-query state (lanes 0..31 of the wave) ----
-        const float qsq_l = QSQ[qrow];
         float4 qreg[NG];
         {
             const float* qp = Q + qrow * d;
@@ -124,6 +124,22 @@ __global__ __launch_bounds__(kResThreads) void knn_k1_resident_f32_kernel(GramAr
                 qreg[g] = (qvalid && c < d) ? make_float4(-2.0f * v.x, -2.0f * v.y, -2.0f * v.z, -2.0f * v.w)
                                             : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+        }
+        float qsq_l;
+        if (qsq_out) {
+            // ||q||^2 from the operand: qreg = -2 q exactly, so the sum of its
+            // squares is 4 ||q||^2 in some order (within the screen bound's
+            // allowance for the norm's rounding, as a sum in any order is);
+            // chunk 0 keeps it for the merge's k-means rule
+            float s2 = 0.0f;
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                s2 = s2 + qreg[g].x * qreg[g].x + qreg[g].y * qreg[g].y + qreg[g].z * qreg[g].z +
+                     qreg[g].w * qreg[g].w;
+            qsq_l = (s2 + shfl_xor_f(s2, 32)) * 0.25f;
+            if (cidx == 0 && h == 0 && qvalid) qsq_out[qmine] = qsq_l;
+        } else {
+            qsq_l = QSQ[qrow];
         }
         if (lane < kResQpw) {
             const float qsq = qvalid ? qsq_l : 0.0f;
@@ -313,7 +329,7 @@ __global__ __launch_bounds__(256) void knn_merge1_chunks_f32_kernel(GramArgs32 a
 }
 
 template <int NG, int ARM>
-hipError_t launch_res_ng(const GramArgs32& a, int cus, hipStream_t s) {
+hipError_t launch_res_ng(const GramArgs32& a, int cus, float* qsq_out, hipStream_t s) {
     const int rmax = res_rows_max(NG * 8);
     const int nchunks = (int)((a.nt + rmax - 1) / rmax);
     // balanced chunks in whole tiles
@@ -325,7 +341,7 @@ hipError_t launch_res_ng(const GramArgs32& a, int cus, hipStream_t s) {
     const int64_t need = (nqb + kResWaves - 1) / kResWaves;  // groups that still get a block per wave
     if (ngrp > need) ngrp = need;
     hipLaunchKernelGGL((knn_k1_resident_f32_kernel<NG, ARM>), dim3((unsigned)(ngrp * nchunks)), dim3(kResThreads), 0,
-                       s, a, chunk_rows, nchunks, reinterpret_cast<uint16_t*>(a.qval));
+                       s, a, chunk_rows, nchunks, reinterpret_cast<uint16_t*>(a.qval), qsq_out);
     return hipGetLastError();
 }
 
@@ -350,13 +366,13 @@ hipError_t launch_gram_f32_k1_resident_merge(const GramArgs32& a, int nchunks, h
     return hipGetLastError();
 }
 
-hipError_t launch_gram_f32_k1_resident(const GramArgs32& a, int arm, int cus, hipStream_t s) {
+hipError_t launch_gram_f32_k1_resident(const GramArgs32& a, int arm, int cus, float* qsq_out, hipStream_t s) {
     if (!gram_f32_k1_resident_chunks(a.nq, a.nt, a.d, a.k, arm, true)) return hipErrorInvalidValue;
     if (a.d <= 32)
-        return arm == ARM_EUCLID_FMA ? launch_res_ng<4, ARM_EUCLID_FMA>(a, cus, s)
-                                     : launch_res_ng<4, ARM_EUCLID_MULADD>(a, cus, s);
-    return arm == ARM_EUCLID_FMA ? launch_res_ng<8, ARM_EUCLID_FMA>(a, cus, s)
-                                 : launch_res_ng<8, ARM_EUCLID_MULADD>(a, cus, s);
+        return arm == ARM_EUCLID_FMA ? launch_res_ng<4, ARM_EUCLID_FMA>(a, cus, qsq_out, s)
+                                     : launch_res_ng<4, ARM_EUCLID_MULADD>(a, cus, qsq_out, s);
+    return arm == ARM_EUCLID_FMA ? launch_res_ng<8, ARM_EUCLID_FMA>(a, cus, qsq_out, s)
+                                 : launch_res_ng<8, ARM_EUCLID_MULADD>(a, cus, qsq_out, s);
 }
 
 }  // namespace mlrs

@@ -169,7 +169,9 @@ int gram_f32_k1_resident_chunks(int64_t nq, int64_t nt, int64_t d, int k, int ar
 // The resident search (part_val / part_idx: one slot per chunk), then the
 // merge of the chunks' lists with the output transform.
 // a.qval must hold gram_f32_k1_resident_queue_bytes(cus) (the waves' queues).
-hipError_t launch_gram_f32_k1_resident(const GramArgs32& a, int arm, int cus, hipStream_t s);
+// qsq_out non-null: the kernel forms the queries' squared norms itself and
+// writes them there (a.qsq must then point at the same array, for the merge).
+hipError_t launch_gram_f32_k1_resident(const GramArgs32& a, int arm, int cus, float* qsq_out, hipStream_t s);
 size_t gram_f32_k1_resident_queue_bytes(int cus);
 hipError_t launch_gram_f32_k1_resident_merge(const GramArgs32& a, int nchunks, hipStream_t s);
 hipError_t launch_gram_f32_merge(const GramArgs32& a, int arm, hipStream_t s);
