@@ -60,6 +60,7 @@ def _rand(seed, n, d):
 CASES = [
     ("fused", (3000, 200000, 128, 32, 0), (700, 50000, 96, 10, 0)),
     ("fused", (2048, 120000, 64, 1, 0), (100, 9000, 64, 1, 0)),
+    ("fused", (5000, 3000, 64, 1, 0), (700, 1000, 32, 1, 0)),  # k = 1 with the index resident in LDS
     ("fused", (1500, 80000, 100, 20, 1), (300, 20000, 100, 5, 1)),
     ("lowd", (20000, 200000, 3, 8, 0), (5000, 40000, 3, 8, 0)),
     ("generic", (1000, 10000, 64, 10, 0), (200, 3000, 64, 10, 0)),
@@ -101,6 +102,7 @@ def test_noalloc_rejects_scratch_beyond_its_size():
 
 
 @pytest.mark.parametrize("family,shape", [("fused", (1200, 60000, 128, 32)), ("fused", (1000, 40000, 64, 1)),
+                                          ("fused", (4000, 1500, 64, 1)),
                                           ("lowd", (4000, 50000, 3, 8)), ("generic", (300, 5000, 64, 10))])
 def test_noalloc_graph_capture_replays(family, shape):
     nq, nt, d, k = shape
