@@ -516,6 +516,18 @@ static bool small_search(int64_t nq, int64_t nt, int64_t d) {
     return (double)nq * (double)nt * (double)d <= 4294967296.0;
 }
 
+// f32 Euclidean searches the low-d ALU kernel serves faster than the Gram
+// kernel (timed on 500,000-row self-searches: the ALU kernel's cost grows with
+// d and, past list capacity 16, with one query per lane instead of two; the
+// Gram kernel's is nearly flat for d <= 16): every d at k <= 8, d <= 11 at
+// k <= 16, d <= 3 at k <= 32.  f64 always takes the ALU kernel (its Gram
+// kernel runs 2.4-12x slower there).
+static bool lowd_f32_faster(int64_t d, int64_t k) {
+    if (k <= 8) return true;
+    if (k <= 16) return d <= 11;
+    return d <= 3;
+}
+
 // Process-wide kernel-family override (mlrs_force_path); a family that does
 // not serve the shape yields the automatic choice.
 static int g_force_path = MLRS_PATH_AUTO;
@@ -724,32 +736,41 @@ int32_t knn_gram64(const double* xq, int64_t nq, const double* xt, int64_t nt, i
     return ok();
 }
 
-int32_t knn_lowd32(const float* xq, int64_t nq, const float* xt, int64_t nt, int64_t d, int k, int arm,
-                   int mode, float* out_v, uint32_t* out_i, hipStream_t s) {
-    const size_t fixed = aligned_bytes(sizeof(float) * nq) + aligned_bytes(sizeof(float) * nt) +
+// The low-d ALU path (knn_lowd.hip), f32 and f64.
+static hipError_t launch_lowd_t(const LowdArgs32& a, int arm, hipStream_t s) { return launch_lowd_f32(a, arm, s); }
+static hipError_t launch_lowd_t(const LowdArgs64& a, int arm, hipStream_t s) { return launch_lowd_f64(a, arm, s); }
+
+template <typename T>
+int32_t knn_lowd(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, int k, int arm, int mode,
+                 T* out_v, uint32_t* out_i, hipStream_t s) {
+    typedef typename LowdBits<T>::type B;
+    const size_t fixed = aligned_bytes(sizeof(T) * nq) + aligned_bytes(sizeof(T) * nt) +
                          aligned_bytes(sizeof(NormStats)) + 1024;
     char* ws;
     int cus;
     int32_t rc = workspace(fixed, s, &ws, &cus);
     if (rc) return rc;
-    const int64_t nblocks = (nq + lowd_queries_per_block(k) - 1) / lowd_queries_per_block(k);
+    const int qpb = lowd_queries_per_block(k, d, (int)sizeof(T));
+    const int64_t nblocks = (nq + qpb - 1) / qpb;
     // ~3 resident 256-lane workgroups per CU (the k <= 8 kernel holds ~150 VGPRs)
     int nstrips = pick_strips(nblocks, nt, (int64_t)cus * 3, 4096, 64);
     int64_t rps = (nt + nstrips - 1) / nstrips;
     nstrips = (int)((nt + rps - 1) / rps);
     size_t parts = nstrips > 1 ? (size_t)nstrips * nq * k : 0;
     if (parts) {
-        rc = workspace(fixed + aligned_bytes(parts * 4) * 2 + aligned_bytes(sizeof(unsigned int) * nq), s, &ws, &cus);
+        rc = workspace(fixed + aligned_bytes(parts * sizeof(T)) + aligned_bytes(parts * sizeof(uint32_t)) +
+                           aligned_bytes(sizeof(B) * nq),
+                       s, &ws, &cus);
         if (rc) return rc;
     }
     Carver cv(ws);
-    LowdArgs32 a;
+    LowdArgs<T> a;
     std::memset(&a, 0, sizeof(a));
-    float* qsq = cv.take<float>(nq);
-    float* xsq = cv.take<float>(nt);
+    T* qsq = cv.take<T>(nq);
+    T* xsq = cv.take<T>(nt);
     NormStats* stats = cv.take<NormStats>(1);
-    hipError_t e = launch_row_norms<float>(xq, nq, d, qsq, nullptr, nullptr, nullptr, s);
-    if (e == hipSuccess) e = launch_row_norms<float>(xt, nt, d, xsq, nullptr, nullptr, stats, s);
+    hipError_t e = launch_row_norms<T>(xq, nq, d, qsq, nullptr, nullptr, nullptr, s);
+    if (e == hipSuccess) e = launch_row_norms<T>(xt, nt, d, xsq, nullptr, nullptr, stats, s);
     if (e != hipSuccess) return hip_err(e, "row_norms");
     a.q = xq;
     a.nq = nq;
@@ -761,24 +782,27 @@ int32_t knn_lowd32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     a.qsq = qsq;
     a.xsq = xsq;
     a.stats = stats;
-    // the Gram kernels' Euclidean screen bound (knn_gram32)
-    const double u = std::ldexp(1.0, -23);
+    // the Gram kernels' Euclidean screen bound (knn_gram32 / knn_gram64) with
+    // the element type's unit: 2^-23 (f32) or 2^-52 (f64); the threshold
+    // arithmetic carries its own rounding margin
+    const bool f64 = sizeof(T) == 8;
+    const double u = std::ldexp(1.0, f64 ? -52 : -23);
     a.eps_rel = 8.0 * (double)(d + 4) * u;
-    a.eps_abs = (double)(d + 4) * std::ldexp(1.0, -120);
+    a.eps_abs = (double)(d + 4) * std::ldexp(1.0, f64 ? -1000 : -120);
     a.rows_per_strip = rps;
     a.nstrips = nstrips;
     if (parts) {
-        a.part_val = cv.take<float>(parts);
+        a.part_val = cv.take<T>(parts);
         a.part_idx = cv.take<uint32_t>(parts);
-        a.shared_r = cv.take<unsigned int>(nq);
+        a.shared_r = cv.take<B>(nq);
     }
     a.out_val = out_v;
     a.out_idx = out_i;
     {
         KernelTimer timer(s, "knn_lowd_kernel");
-        e = launch_lowd_f32(a, arm, s);
+        e = launch_lowd_t(a, arm, s);
     }
-    if (e != hipSuccess) return hip_err(e, "knn_lowd_f32");
+    if (e != hipSuccess) return hip_err(e, f64 ? "knn_lowd_f64" : "knn_lowd_f32");
     return ok();
 }
 
@@ -847,12 +871,14 @@ int32_t knn_topk_f32_dispatch(const float* xq, int64_t n_query, int64_t n_featur
     const bool gram_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD || arm == ARM_COS_FOLD ||
                           (arm == ARM_COS_HOST && n_features > 128)) &&
                          n_features <= gram_f32_max_d() && k <= gram_f32_max_k();
+    const bool small = small_search(n_query, n_train, n_features);
     int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)
-        path = lowd_ok ? MLRS_PATH_LOWD
-                       : (gram_ok && !small_search(n_query, n_train, n_features)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+        path = (lowd_ok && (small || !gram_ok || lowd_f32_faster(n_features, k))) ? MLRS_PATH_LOWD
+               : (gram_ok && !small)                                             ? MLRS_PATH_FUSED
+                                                                                 : MLRS_PATH_GENERIC;
     if (path == MLRS_PATH_LOWD)
-        return knn_lowd32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
+        return knn_lowd<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     if (path == MLRS_PATH_FUSED)
         return knn_gram32(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     return knn_generic<float>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s, p);
@@ -958,10 +984,14 @@ int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int
     hipStream_t s = (hipStream_t)stream;
     const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
+    const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
     const bool gram_ok = arm <= ARM_COS_HOST && n_features <= gram_f64_max_d() && k <= gram_f64_max_k();
-    int path = pick_path(false, gram_ok);
+    int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)
-        path = (gram_ok && !small_search(n_query, n_train, n_features)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+        path = lowd_ok ? MLRS_PATH_LOWD
+                       : (gram_ok && !small_search(n_query, n_train, n_features)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+    if (path == MLRS_PATH_LOWD)
+        return knn_lowd<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     if (path == MLRS_PATH_FUSED)
         return knn_gram64(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s);
     return knn_generic<double>(xq, n_query, x_train, n_train, n_features, k, arm, mode, out_dist, out_idx, s, p);
@@ -1698,13 +1728,18 @@ static int32_t pinned_staging(size_t bytes, char** out) {
     return MLRS_OK;
 }
 
-// The f64 search under an explicit arm: the Gram-MFMA kernel where it serves
-// the arm and shape, else exact tiles + selection.
+// The f64 search under an explicit arm: the low-d ALU kernel for Euclidean
+// arms ranked by the aggregate (d <= 16, k <= 32), the Gram-MFMA kernel where
+// it serves the arm and shape, else exact tiles + selection.
 static int32_t search_f64(const double* xq, int64_t nq, const double* xt, int64_t nt, int64_t d, int k, int arm,
                           int mode, double p, double* ov, uint32_t* oi, hipStream_t s) {
+    const bool lowd_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD) && mode != EMIT_ROOT_RANKED &&
+                         d <= lowd_max_d() && k <= lowd_max_k();
     const bool gram_ok = arm <= ARM_COS_HOST && d <= gram_f64_max_d() && k <= gram_f64_max_k();
-    int path = pick_path(false, gram_ok);
-    if (path == MLRS_PATH_AUTO) path = (gram_ok && !small_search(nq, nt, d)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+    int path = pick_path(lowd_ok, gram_ok);
+    if (path == MLRS_PATH_AUTO)
+        path = lowd_ok ? MLRS_PATH_LOWD : (gram_ok && !small_search(nq, nt, d)) ? MLRS_PATH_FUSED : MLRS_PATH_GENERIC;
+    if (path == MLRS_PATH_LOWD) return knn_lowd<double>(xq, nq, xt, nt, d, k, arm, mode, ov, oi, s);
     if (path == MLRS_PATH_FUSED) return knn_gram64(xq, nq, xt, nt, d, k, arm, mode, ov, oi, s);
     return knn_generic<double>(xq, nq, xt, nt, d, k, arm, mode, ov, oi, s, p);
 }

@@ -260,35 +260,56 @@ template <typename T>
 hipError_t launch_argmin_rows(const T* dist, int64_t rows, int64_t cols, int64_t ld, uint32_t* labels,
                               T* best, hipStream_t s);
 
-// Low-dimension ALU path (exact, lane per query).
-struct LowdArgs32 {
-    const float* q;
+// Low-dimension ALU path (exact, lane per query), f32 and f64.  The shared
+// per-query bound holds the k-th value's bits (non-negative values order as
+// their bits): 32-bit words for f32, 64-bit for f64.
+template <typename T>
+struct LowdBits;
+template <>
+struct LowdBits<float> {
+    typedef unsigned int type;
+};
+template <>
+struct LowdBits<double> {
+    typedef unsigned long long type;
+};
+template <typename T>
+struct LowdArgs {
+    const T* q;
     int64_t nq;
-    const float* x;
+    const T* x;
     int64_t nt;
     int64_t d;
     int k;
     int mode;
-    const float* qsq;       // query row_sumsq
-    const float* xsq;       // index row_sumsq
+    const T* qsq;           // query row_sumsq
+    const T* xsq;           // index row_sumsq
     const NormStats* stats; // max index row_sumsq (screen bound)
     double eps_rel;         // screen bound eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
     double eps_abs;
     int64_t rows_per_strip;
     int nstrips;
-    unsigned int* shared_r;  // [nq] k-th value reached by finished strips (float bits), or null
-    float* part_val;
+    typename LowdBits<T>::type* shared_r;  // [nq] k-th value reached by finished strips (bits), or null
+    T* part_val;
     uint32_t* part_idx;
-    float* out_val;
+    T* out_val;
     uint32_t* out_idx;
 };
-// Queries per lane of the low-d kernel for a list capacity K.
+typedef LowdArgs<float> LowdArgs32;
+typedef LowdArgs<double> LowdArgs64;
+// Queries per lane of the low-d kernel for a list capacity K and row width D
+// (f64 lanes hold twice the registers per value: two queries only up to
+// D = 8).
 #ifndef MLRS_LOWD_QL_SMALL_K
 #define MLRS_LOWD_QL_SMALL_K 2
 #endif
-constexpr int lowd_queries_per_lane(int K) { return K <= 8 ? MLRS_LOWD_QL_SMALL_K : (K <= 16 ? 2 : 1); }
-int lowd_queries_per_block(int k);
+template <typename T>
+constexpr int lowd_queries_per_lane(int K, int D) {
+    return sizeof(T) == 8 ? ((K <= 16 && D <= 8) ? 2 : 1) : (K <= 8 ? MLRS_LOWD_QL_SMALL_K : (K <= 16 ? 2 : 1));
+}
+int lowd_queries_per_block(int k, int64_t d, int elem_bytes);
 hipError_t launch_lowd_f32(const LowdArgs32& a, int arm, hipStream_t s);
+hipError_t launch_lowd_f64(const LowdArgs64& a, int arm, hipStream_t s);
 int lowd_max_d();
 int lowd_max_k();
 
