@@ -14,6 +14,7 @@ arithmetic) timed on a bounded sample of the same workload on this host.
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
   python bench.py --radius R [--config c2]    # radius_neighbors on the same data
   python bench.py --config c5 --fit [--fit-iters N]   # k-means fit at c5 scale
+  python bench.py --config c4 --dtype f64     # a k-NN configuration in the other element type
 
 With --radius a step is one radius_neighbors call (count pass, row offsets,
 fill pass, boundary transform) of all queries against the index; its parity
@@ -74,6 +75,9 @@ def main():
     ap.add_argument("--probe-peak", action="store_true",
                     help="only measure the peaks the roofline fractions are stated against (mlrs_probe_peak: "
                          "FMA f32/f64 and MFMA f32/f64 chains at 1..8 waves per SIMD) and print them as one JSON line")
+    ap.add_argument("--dtype", choices=("f32", "f64"), default=None,
+                    help="k-NN configurations (c1-c4, d256, c2k128): run the same data in this element type "
+                         "(parity then against the CPU oracle on sampled rows)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel "
                          "of known traffic, the scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -104,12 +108,22 @@ def main():
                           "device": torch.cuda.get_device_name(0)}))
         return
 
-    cfg = synthetic.CONFIGS[args.config]
+    cfg = dict(synthetic.CONFIGS[args.config])
     dev = torch.device("cuda:0")
     log("generating %s %s" % (args.config, cfg))
     t = time.time()
     a, b = synthetic.generate(args.config)
     log("generated in %.1fs" % (time.time() - t))
+    retyped = args.dtype is not None and args.dtype != cfg["dtype"]
+    if args.dtype is not None and (args.config == "c5" or args.fit):
+        print("--dtype applies to the k-NN configurations", file=sys.stderr)
+        sys.exit(2)
+    if retyped:
+        # the same values in the other element type (f32 -> f64 is exact)
+        npt = np.float64 if args.dtype == "f64" else np.float32
+        a, b = a.astype(npt), b.astype(npt)
+        cfg["dtype"] = args.dtype
+        log("element type %s" % args.dtype)
     ta = torch.from_numpy(a).to(dev)
     tb = torch.from_numpy(b).to(dev)
     torch.cuda.synchronize()
@@ -179,7 +193,7 @@ def main():
 
     # ---- parity of the measured run against the committed golden subset ----
     gpath = os.path.join(ROOT, "tests", "golden", "%s_golden.npz" % args.config)
-    g = np.load(gpath) if os.path.exists(gpath) else None
+    g = np.load(gpath) if (os.path.exists(gpath) and not retyped) else None
     sub = g["subset"] if g is not None else np.unique(np.linspace(0, n_query - 1, 64).astype(np.int64))
     if args.fit:
         import oracle
@@ -266,8 +280,8 @@ def main():
         # Lloyd fit's flops over its kernel time would overstate the rate
         achieved = None
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "traffic_%s%s.json" % ("radius_" if radius is not None else "",
-                                                                   args.config))
+    tfile = os.path.join(ROOT, "profiles", "traffic_%s%s%s.json" % ("radius_" if radius is not None else "",
+                                                                     args.config, "_" + args.dtype if retyped else ""))
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
 
@@ -325,6 +339,8 @@ def main():
           "c5": "c5: k-means assign, 5M points x 1024 centroids, d=64, f32",
           "d256": "d256: 200k index x 5k queries, d=256, k=32, f32, 100-comp GMM",
           "c2k128": "c2k128: c2's data (1M index x 10k queries, d=128) with k=128, f32"}[args.config]
+    if retyped:
+        wl = "%s; run in %s" % (wl, args.dtype)
     if args.fit:
         wl = ("k-means fit at c5 scale: 5M points into 1024 clusters, d=64, f32, %s init, tol 0, "
               "at most %d Lloyd iterations per step, algorithm=%s"
@@ -362,12 +378,14 @@ def main():
                      "traffic": traffic, "kernel": name.value.decode(), "kernel_ms": kern_ms,
                      "kernel_launches_per_step": launches.value / args.steps, "kernel_ms_per_step": kern_ms_step,
                      "frac_nonpacked": (achieved / VALU_F32_NONPACKED
-                                        if bound == "valu" and achieved is not None else None),
+                                        if bound == "valu" and not f64 and achieved is not None else None),
                      "basis": {"mfma": "dense MFMA peak, 2*d flops per distance evaluation",
-                               "valu": "published vector FP32 peak 157.3 TFLOP/s, which counts packed FP32 "
-                                       "math; the kernel is built without packed ops, whose ceiling is "
-                                       "78.6 TFLOP/s (frac_nonpacked); 2*d flops per distance "
-                                       "evaluation"}[bound]},
+                               "valu": ("published vector FP64 peak 78.6 TFLOP/s; 2*d flops per distance "
+                                        "evaluation" if f64 else
+                                        "published vector FP32 peak 157.3 TFLOP/s, which counts packed FP32 "
+                                        "math; the kernel is built without packed ops, whose ceiling is "
+                                        "78.6 TFLOP/s (frac_nonpacked); 2*d flops per distance "
+                                        "evaluation")}[bound]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
