@@ -1332,10 +1332,11 @@ __global__ __launch_bounds__(256) void knn_merge1_f32_kernel(GramArgs32 a) {
 // once eps is added (k sampled rows have exact <= u + eps <= u_k + eps).  A
 // workgroup takes 128 queries and one contiguous range of the sample's
 // 32-row tiles (blockIdx.y: the tiles are split so that the launch fills the
-// chip); sampled row s is index row s * n / m.
+// chip); sampled row s is index row s * n / m.  The next tile's rows are
+// loaded into registers while the current tile's MFMA chain runs.
 template <int NG, bool COS>
-__global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, int64_t nsamp,
-                                                                  float* __restrict__ S, int64_t ld) {
+__global__ __launch_bounds__(256, 2) void knn_seed_screen_f32_kernel(GramArgs32 a, int64_t nsamp,
+                                                                     float* __restrict__ S, int64_t ld) {
     constexpr int DP = NG * 8;
     constexpr int STRIDE = DP + 4;
     __shared__ __attribute__((aligned(16))) float tile[kBn * STRIDE];
@@ -1365,22 +1366,40 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f32_kernel(GramArgs32 a, 
     const int64_t s_lo = (int64_t)blockIdx.y * per * kBn;
     int64_t s_hi = s_lo + per * kBn;
     if (s_hi > nsamp) s_hi = nsamp;
-    for (int64_t s0 = s_lo; s0 < s_hi; s0 += kBn) {
-        __syncthreads();  // the previous tile is no longer read
-        for (int f = tid; f < kBn * DP / 4; f += 256) {
+    // staging: chunk f = tid + 256 p is column chunk f % (DP / 4) of tile row
+    // f / (DP / 4); the next tile is loaded into registers under the chain
+    constexpr int PF = (kBn * DP / 4 + 255) / 256;
+    float4 pf[PF];
+    float pfn = 0.0f;
+    auto load_tile = [&](int64_t s0) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int f = tid + 256 * p;
             const int r = f / (DP / 4), c4 = f % (DP / 4);
             const int64_t sr = s0 + r;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (sr < nsamp && 4 * c4 < d)
+            if (f < kBn * DP / 4 && sr < nsamp && 4 * c4 < d)
                 v = *reinterpret_cast<const float4*>(a.x + ((sr * nt) / nsamp) * d + 4 * c4);
-            *reinterpret_cast<float4*>(&tile[r * STRIDE + 4 * c4]) = v;
+            pf[p] = v;
         }
         if (tid < kBn) {
             const int64_t sr = s0 + tid;
             const int64_t t = (sr < nsamp) ? (sr * nt) / nsamp : 0;
-            tn[tid] = (sr < nsamp) ? (COS ? a.xscale[t] : a.xsq[t]) : (COS ? 0.0f : inf);
+            pfn = (sr < nsamp) ? (COS ? a.xscale[t] : a.xsq[t]) : (COS ? 0.0f : inf);
         }
+    };
+    if (s_lo < s_hi) load_tile(s_lo);
+    for (int64_t s0 = s_lo; s0 < s_hi; s0 += kBn) {
+        __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int f = tid + 256 * p;
+            if (f < kBn * DP / 4)
+                *reinterpret_cast<float4*>(&tile[(f / (DP / 4)) * STRIDE + 4 * (f % (DP / 4))]) = pf[p];
+        }
+        if (tid < kBn) tn[tid] = pfn;
         __syncthreads();
+        if (s0 + kBn < s_hi) load_tile(s0 + kBn);  // in flight under the chain
         f32x16 acc;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
@@ -1527,13 +1546,14 @@ int gram_f32_max_k() { return kKcap; }
 int gram_f32_max_d() { return 256; }
 int gram_f32_rows_per_tile() { return kBn; }
 
-// Rows the matrix-core seed samples: 64 k, at most 8192 and nt / 128, at
-// least 512 -- four times the exact seed's cap, since a sampled pair costs a
+// Rows the matrix-core seed samples: 128 k, at most 8192 and nt / 128, at
+// least 512 -- more than the exact seed's cap, since a sampled pair costs a
 // few MFMA cycles here instead of a d-long FMA chain.  c2 with k = 128: 7812
 // rows, step 27.2 -> 26.6 ms against the exact seed's 1953 (kernel 26.3 ->
-// 25.2 ms); k = 32 takes 2048 (no change against 1953).
+// 25.2 ms); k = 32 takes 4096: kernel 20.76 -> 20.68 ms against 2048 at the
+// same step (8192 rows at k = 32: kernel 20.59 ms, step +0.1 ms).
 static int64_t seed_screen_rows(int64_t nt, int k) {
-    int64_t n = 64 * (int64_t)k;
+    int64_t n = 128 * (int64_t)k;
     if (n > 8192) n = 8192;
     if (n > nt / 128) n = nt / 128;
     if (n < 512) n = 512;

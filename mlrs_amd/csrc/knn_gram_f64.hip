@@ -925,15 +925,23 @@ int gram_f64_max_d() { return kMaxD; }
 // stands for, u = max(acc + ||q||^2, 0) or clamp(1 + acc/||q||, 0, 2) (NaN
 // kept), written to S[q][s].  The screen bound eps holds for any summation
 // order, so k sampled rows have exact <= u + eps <= u_k + eps.  A wave takes
-// 16 queries (lane l: query l % 16, k-slot g = l / 16 supplies feature
-// 4 s + g at k-step s), a workgroup 64 queries and a slice of the sample's
-// 16-row tiles (blockIdx.y); sampled row s is index row s * n / m.
+// 16 queries (lane l: query l % 16; k-slot g = l / 16 supplies feature
+// g KS + s at k-step s, so each lane's query operand and tile reads are
+// contiguous runs, loaded 16 bytes at a time), a workgroup 64 queries and a
+// slice of the sample's 16-row tiles (blockIdx.y); sampled row s is index row
+// s * n / m.  The next tile's rows are loaded into registers while the
+// current tile's MFMA chain runs (two accumulator chains: the even and odd
+// k-steps), and stored into the one LDS tile between two barriers.
 template <int KS, bool COS>
-__global__ __launch_bounds__(256) void knn_seed_screen_f64_kernel(GramArgs64 a, int64_t nsamp,
-                                                                  double* __restrict__ S, int64_t ld) {
+__global__ __launch_bounds__(256, 2) void knn_seed_screen_f64_kernel(GramArgs64 a, int64_t nsamp,
+                                                                     double* __restrict__ S, int64_t ld) {
+    static_assert(KS % 2 == 0, "k-steps come in 16-byte pairs");
     constexpr int DP = 4 * KS;
-    constexpr int STR = DP + 1;
-    __shared__ double tile[kBn * STR];
+    constexpr int STR = DP + 2;               // rows 16 bytes apart in the banks
+    constexpr int CPR = DP / 2;               // 16-byte chunks per tile row
+    constexpr int PF = kBn * CPR / 256;       // chunks each thread stages per tile
+    static_assert(kBn * CPR % 256 == 0, "whole chunks per thread");
+    __shared__ __attribute__((aligned(16))) double tile[kBn * STR];
     __shared__ double tn[kBn];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -948,41 +956,69 @@ __global__ __launch_bounds__(256) void knn_seed_screen_f64_kernel(GramArgs64 a, 
     const double qs = COS ? __builtin_sqrt(qsq) : qsq;
     double qreg[KS];
 #pragma unroll
-    for (int st = 0; st < KS; ++st) {
-        const int64_t c = 4 * st + g;
-        qreg[st] = (c < d) ? a.q[qrow * d + c] * (COS ? 1.0 : -2.0) : 0.0;
+    for (int st = 0; st < KS; st += 2) {
+        const int64_t c = (int64_t)g * KS + st;  // c and d even: c < d covers c + 1
+        double2 v = make_double2(0.0, 0.0);
+        if (c < d) v = *reinterpret_cast<const double2*>(a.q + qrow * d + c);
+        qreg[st] = v.x * (COS ? 1.0 : -2.0);
+        qreg[st + 1] = v.y * (COS ? 1.0 : -2.0);
     }
     const int64_t ntiles = (nsamp + kBn - 1) / kBn;
     const int64_t per = (ntiles + gridDim.y - 1) / gridDim.y;
     const int64_t s_lo = (int64_t)blockIdx.y * per * kBn;
     int64_t s_hi = s_lo + per * kBn;
     if (s_hi > nsamp) s_hi = nsamp;
-    for (int64_t s0 = s_lo; s0 < s_hi; s0 += kBn) {
-        __syncthreads();  // the previous tile is no longer read
-        for (int e = tid; e < kBn * DP; e += 256) {
-            const int r = e / DP, c = e % DP;
+    // staging: chunk f = tid + 256 p is column pair f % CPR of tile row f / CPR
+    double2 pf[PF];
+    double pfn = 0.0;
+    auto load_tile = [&](int64_t s0) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int f = tid + 256 * p;
+            const int r = f / CPR, c2 = f % CPR;
             const int64_t sr = s0 + r;
-            tile[r * STR + c] = (sr < nsamp && c < d) ? a.x[((sr * nt) / nsamp) * d + c] : 0.0;
+            double2 v = make_double2(0.0, 0.0);
+            if (sr < nsamp && 2 * c2 < d)
+                v = *reinterpret_cast<const double2*>(a.x + ((sr * nt) / nsamp) * d + 2 * c2);
+            pf[p] = v;
         }
         if (tid < kBn) {
             const int64_t sr = s0 + tid;
             const int64_t t = (sr < nsamp) ? (sr * nt) / nsamp : 0;
-            tn[tid] = (sr < nsamp) ? (COS ? a.xscale[t] : a.xsq[t]) : (COS ? 0.0 : inf);
+            pfn = (sr < nsamp) ? (COS ? a.xscale[t] : a.xsq[t]) : (COS ? 0.0 : inf);
         }
+    };
+    if (s_lo < s_hi) load_tile(s_lo);
+    for (int64_t s0 = s_lo; s0 < s_hi; s0 += kBn) {
+        __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int f = tid + 256 * p;
+            *reinterpret_cast<double2*>(&tile[(f / CPR) * STR + 2 * (f % CPR)]) = pf[p];
+        }
+        if (tid < kBn) tn[tid] = pfn;
         __syncthreads();
-        f64x4 acc;
+        if (s0 + kBn < s_hi) load_tile(s0 + kBn);  // in flight under the chain
+        f64x4 acc0, acc1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = COS ? 0.0 : tn[g + 4 * r];
-        const double* arow = &tile[j * STR + g];
+        for (int r = 0; r < 4; ++r) {
+            acc0[r] = COS ? 0.0 : tn[g + 4 * r];
+            acc1[r] = 0.0;
+        }
+        const double* arow = &tile[j * STR + g * KS];
 #pragma unroll
-        for (int st = 0; st < KS; ++st)
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(arow[4 * st], qreg[st], acc, 0, 0, 0);
+        for (int st = 0; st < KS; st += 2) {
+            const double2 av = *reinterpret_cast<const double2*>(arow + st);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(av.x, qreg[st], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(av.y, qreg[st + 1], acc1, 0, 0, 0);
+        }
         if (qvalid) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t sr = s0 + g + 4 * r;
                 if (sr < nsamp) {
-                    const double v = COS ? acc[r] * tn[g + 4 * r] : acc[r];
+                    const double acc = acc0[r] + acc1[r];
+                    const double v = COS ? acc * tn[g + 4 * r] : acc;
                     double u = __builtin_nan("");
                     if (v == v) {
                         if (COS) {
@@ -1015,8 +1051,18 @@ __global__ void seed_screen_finalize64_kernel(GramArgs64 a, const double* __rest
     a.shared_r[q] = (unsigned long long)__double_as_longlong(R);
 }
 
-// Rows the matrix-core seed samples: the exact seed's (gram_seed_rows).
-static int64_t seed_screen_rows64(int64_t nt, int k) { return gram_seed_rows(nt, k); }
+// Rows the matrix-core seed samples: 128 k, at most 8192 and nt / 64, at
+// least 512.  With the tile loads under the MFMA chain the launch is cheap
+// enough for four times the exact seed's sample at c3 (k = 16, 2048 rows):
+// kernel 9.15 -> 9.01 ms and step 9.43 -> 9.41 ms against 512 rows (A/B of
+// two builds on one box; 4096 rows: kernel 8.96 ms, step 9.53 ms).
+static int64_t seed_screen_rows64(int64_t nt, int k) {
+    int64_t n = 128 * (int64_t)k;
+    if (n > 8192) n = 8192;
+    if (n > nt / 64) n = nt / 64;
+    if (n < 512) n = 512;
+    return nt < n ? nt : n;
+}
 
 size_t gram_f64_seed_screen_bytes(int64_t nq, int64_t nt, int64_t d, int k, bool vec2) {
     if (k <= 1 || k > kKcap || d > kMaxD || !vec2) return 0;
