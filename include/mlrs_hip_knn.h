@@ -481,8 +481,8 @@ int32_t mlrs_probe_peak(int32_t kind, int32_t waves_per_simd, double *tflops, vo
  * wherever they serve the shape (d <= 256, k <= 128; the f32 knn_host
  * cosine arm only at d > 128; k-means: d <= 256);
  * 2 = the
- * low-d ALU kernel wherever it serves the shape (f32 and f64 Euclidean,
- * d <= 16, k <= 32); 3 = the generic exact-tile path.  A family that does not serve
+ * low-d ALU kernel wherever it serves the shape (f32 and f64, Euclidean
+ * and cosine, d <= 16, k <= 32); 3 = the generic exact-tile path.  A family that does not serve
  * a shape falls back to the automatic choice.  radius_neighbors: 1 = the
  * matrix-core screen wherever it serves (f32 Euclidean / cosine, d <= 128),
  * 3 = the host-scan kernel.  Process-wide.

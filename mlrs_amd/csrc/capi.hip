@@ -516,16 +516,17 @@ static bool small_search(int64_t nq, int64_t nt, int64_t d) {
     return (double)nq * (double)nt * (double)d <= 4294967296.0;
 }
 
-// f32 Euclidean searches the low-d ALU kernel serves faster than the Gram
-// kernel (timed on 500,000-row self-searches: the ALU kernel's cost grows with
-// d and, past list capacity 16, with one query per lane instead of two; the
+// f32 searches the low-d ALU kernel serves faster than the Gram kernel
+// (timed on 500,000-row self-searches: the ALU kernel's cost grows with d
+// and, past list capacity 16, with one query per lane instead of two; the
 // Gram kernel's is nearly flat for d <= 16): every d at k <= 8, d <= 11 at
-// k <= 16, d <= 3 at k <= 32.  f64 always takes the ALU kernel (its Gram
-// kernel runs 2.4-12x slower there).
-static bool lowd_f32_faster(int64_t d, int64_t k) {
+// k <= 16, and for Euclidean d <= 3 at k <= 32 (cosine at d = 3, k = 32:
+// 176 ms against the Gram kernel's 149).  f64 always takes the ALU kernel
+// (its Gram kernel runs 2.4-12x slower there).
+static bool lowd_f32_faster(int64_t d, int64_t k, bool cos) {
     if (k <= 8) return true;
     if (k <= 16) return d <= 11;
-    return d <= 3;
+    return !cos && d <= 3;
 }
 
 // Process-wide kernel-family override (mlrs_force_path); a family that does
@@ -744,7 +745,8 @@ template <typename T>
 int32_t knn_lowd(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, int k, int arm, int mode,
                  T* out_v, uint32_t* out_i, hipStream_t s) {
     typedef typename LowdBits<T>::type B;
-    const size_t fixed = aligned_bytes(sizeof(T) * nq) + aligned_bytes(sizeof(T) * nt) +
+    const bool cos = arm == ARM_COS_FOLD;
+    const size_t fixed = aligned_bytes(sizeof(T) * nq) + (cos ? 2 : 1) * aligned_bytes(sizeof(T) * nt) +
                          aligned_bytes(sizeof(NormStats)) + 1024;
     char* ws;
     int cus;
@@ -768,9 +770,10 @@ int32_t knn_lowd(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, in
     std::memset(&a, 0, sizeof(a));
     T* qsq = cv.take<T>(nq);
     T* xsq = cv.take<T>(nt);
+    T* xscale = cos ? cv.take<T>(nt) : nullptr;
     NormStats* stats = cv.take<NormStats>(1);
     hipError_t e = launch_row_norms<T>(xq, nq, d, qsq, nullptr, nullptr, nullptr, s);
-    if (e == hipSuccess) e = launch_row_norms<T>(xt, nt, d, xsq, nullptr, nullptr, stats, s);
+    if (e == hipSuccess) e = launch_row_norms<T>(xt, nt, d, xsq, nullptr, xscale, stats, s);
     if (e != hipSuccess) return hip_err(e, "row_norms");
     a.q = xq;
     a.nq = nq;
@@ -781,14 +784,21 @@ int32_t knn_lowd(const T* xq, int64_t nq, const T* xt, int64_t nt, int64_t d, in
     a.mode = mode;
     a.qsq = qsq;
     a.xsq = xsq;
+    a.xscale = xscale;
     a.stats = stats;
-    // the Gram kernels' Euclidean screen bound (knn_gram32 / knn_gram64) with
-    // the element type's unit: 2^-23 (f32) or 2^-52 (f64); the threshold
-    // arithmetic carries its own rounding margin
+    // the Gram kernels' screen bounds (knn_gram32 / knn_gram64) with the
+    // element type's unit: 2^-23 (f32) or 2^-52 (f64).  Euclidean: the
+    // threshold arithmetic carries its own rounding margin; cosine: f32 rounds
+    // the threshold up from double, f64 folds its rounding into eps (+16 u).
     const bool f64 = sizeof(T) == 8;
     const double u = std::ldexp(1.0, f64 ? -52 : -23);
-    a.eps_rel = 8.0 * (double)(d + 4) * u;
-    a.eps_abs = (double)(d + 4) * std::ldexp(1.0, f64 ? -1000 : -120);
+    if (cos) {
+        a.eps_rel = 0.0;
+        a.eps_abs = (8.0 * (double)d + (f64 ? 48.0 : 32.0)) * u;
+    } else {
+        a.eps_rel = 8.0 * (double)(d + 4) * u;
+        a.eps_abs = (double)(d + 4) * std::ldexp(1.0, f64 ? -1000 : -120);
+    }
     a.rows_per_strip = rps;
     a.nstrips = nstrips;
     if (parts) {
@@ -865,7 +875,8 @@ int32_t knn_topk_f32_dispatch(const float* xq, int64_t n_query, int64_t n_featur
                               uint32_t* out_idx, hipStream_t s) {
     const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
-    const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
+    const bool lowd_ok = (metric == MLRS_METRIC_EUCLIDEAN || (metric == MLRS_METRIC_COSINE && arm == ARM_COS_FOLD)) &&
+                         n_features <= lowd_max_d() && k <= lowd_max_k();
     // the knn_host cosine arm on the matrix cores in the wide shape only (it
     // serves d > 128, where the wide shape runs)
     const bool gram_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD || arm == ARM_COS_FOLD ||
@@ -874,7 +885,7 @@ int32_t knn_topk_f32_dispatch(const float* xq, int64_t n_query, int64_t n_featur
     const bool small = small_search(n_query, n_train, n_features);
     int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)
-        path = (lowd_ok && (small || !gram_ok || lowd_f32_faster(n_features, k))) ? MLRS_PATH_LOWD
+        path = (lowd_ok && (small || !gram_ok || lowd_f32_faster(n_features, k, metric == MLRS_METRIC_COSINE))) ? MLRS_PATH_LOWD
                : (gram_ok && !small)                                             ? MLRS_PATH_FUSED
                                                                                  : MLRS_PATH_GENERIC;
     if (path == MLRS_PATH_LOWD)
@@ -984,7 +995,8 @@ int32_t mlrs_knn_topk_f64(const double* xq, int64_t xq_len, int64_t n_query, int
     hipStream_t s = (hipStream_t)stream;
     const int arm = knn_arm(n_features, k, metric, p);
     const int mode = (metric == MLRS_METRIC_EUCLIDEAN) ? EMIT_SQRT : EMIT_IDENTITY;
-    const bool lowd_ok = metric == MLRS_METRIC_EUCLIDEAN && n_features <= lowd_max_d() && k <= lowd_max_k();
+    const bool lowd_ok = (metric == MLRS_METRIC_EUCLIDEAN || (metric == MLRS_METRIC_COSINE && arm == ARM_COS_FOLD)) &&
+                         n_features <= lowd_max_d() && k <= lowd_max_k();
     const bool gram_ok = arm <= ARM_COS_HOST && n_features <= gram_f64_max_d() && k <= gram_f64_max_k();
     int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)
@@ -1733,8 +1745,8 @@ static int32_t pinned_staging(size_t bytes, char** out) {
 // it serves the arm and shape, else exact tiles + selection.
 static int32_t search_f64(const double* xq, int64_t nq, const double* xt, int64_t nt, int64_t d, int k, int arm,
                           int mode, double p, double* ov, uint32_t* oi, hipStream_t s) {
-    const bool lowd_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD) && mode != EMIT_ROOT_RANKED &&
-                         d <= lowd_max_d() && k <= lowd_max_k();
+    const bool lowd_ok = (arm == ARM_EUCLID_FMA || arm == ARM_EUCLID_MULADD || arm == ARM_COS_FOLD) &&
+                         mode != EMIT_ROOT_RANKED && d <= lowd_max_d() && k <= lowd_max_k();
     const bool gram_ok = arm <= ARM_COS_HOST && d <= gram_f64_max_d() && k <= gram_f64_max_k();
     int path = pick_path(lowd_ok, gram_ok);
     if (path == MLRS_PATH_AUTO)

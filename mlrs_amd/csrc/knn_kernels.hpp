@@ -284,6 +284,7 @@ struct LowdArgs {
     int mode;
     const T* qsq;           // query row_sumsq
     const T* xsq;           // index row_sumsq
+    const T* xscale;        // cosine: -1/||x|| (0 for zero rows); null for Euclidean
     const NormStats* stats; // max index row_sumsq (screen bound)
     double eps_rel;         // screen bound eps = eps_rel*(||q||^2 + max||x||^2) + eps_abs
     double eps_abs;

@@ -1,4 +1,5 @@
-// Low-dimension kNN on the vector ALUs (d <= 16), no MFMA, f32 and f64.
+// Low-dimension kNN on the vector ALUs (d <= 16), no MFMA, f32 and f64,
+// Euclidean and cosine.
 //
 // The MI355X counterpart of euclidean_topk_rows_cpu_direct
 // (crates/mlrs-kernels/src/knn.rs:2968-3227).  Each lane owns QL query rows
@@ -16,7 +17,16 @@
 //
 // Index rows are staged through LDS with their norm appended ((d+1) values
 // padded to 16 bytes); every lane of a wave reads the same row at the same
-// time, so the reads are LDS broadcasts.  f64 runs the same code in double:
+// time, so the reads are LDS broadcasts.
+//
+// Cosine (the metric arm, ARM_COS_FOLD: d <= 128, k <= 128 always holds
+// here) screens by the Gram kernels' cosine screen, the dot product scaled
+// by the row's -1/||x|| (staged after the row, then its squared norm),
+// against ((R + eps) - 1) ||q||, eps the absolute cosine bound; a passing
+// pair is evaluated as the arm does (fma dot product over ascending
+// columns, sqrt(||q||^2 ||x||^2), divide, clamp to [0, 2]).  Zero queries
+// and queries whose norm sums may overflow are never screened (every row is
+// evaluated exactly), as in the Gram kernels.  f64 runs the same code in double:
 // MI355X issues v_fma_f64 at the rate of a non-packed v_fma_f32, so the f64
 // screen costs what the f32 one does, and only the LDS reads double.
 #include "knn_common.hpp"
@@ -80,16 +90,29 @@ struct LowdNum<double> {
     }
 };
 
-// Row + norm, padded to whole 16-byte reads.
-template <typename T, int D>
+// NV staged values per row (the row, then its norm operands), padded to
+// whole 16-byte reads.
+template <typename T, int NV>
 constexpr int lowd_row_width() {
-    return (D + 1 + LowdNum<T>::kVec - 1) / LowdNum<T>::kVec * LowdNum<T>::kVec;
+    return (NV + LowdNum<T>::kVec - 1) / LowdNum<T>::kVec * LowdNum<T>::kVec;
+}
+
+// Cosine screen threshold: exact <= R  =>  1 + acc/||q|| <= R + eps  =>
+// acc <= (R + eps - 1) ||q||; f32 rounded up from double, f64 in double with
+// its rounding inside eps (the Gram kernels' forms).
+__device__ __forceinline__ float lowd_cos_threshold(float R, float qs, float eps) {
+    return round_up_f(((double)R + (double)eps - 1.0) * (double)qs);
+}
+__device__ __forceinline__ double lowd_cos_threshold(double R, double qs, double eps) {
+    return ((R + eps) - 1.0) * qs;
 }
 
 template <typename T, int D, int K, int QL, int ARM>
 __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
     typedef LowdNum<T> N;
-    constexpr int DPN = lowd_row_width<T, D>();
+    constexpr bool COS = ARM == ARM_COS_FOLD;
+    // staged per row: Euclidean ||x||^2; cosine -1/||x||, then ||x||^2
+    constexpr int DPN = lowd_row_width<T, D + (COS ? 2 : 1)>();
 #ifndef MLRS_LOWD_RU4
 #define MLRS_LOWD_RU4 8
 #endif
@@ -111,10 +134,13 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
     const T inf = N::inf();
     const T* __restrict__ X = a.x;
     const T* __restrict__ XSQ = a.xsq;
+    const T* __restrict__ XSCALE = a.xscale;
 
     T qv[QL][D];    // the queries
-    T qm2[QL][D];   // -2 * the queries (exact scaling) for the screen
+    T qm2[QL][D];   // Euclidean: -2 * the queries (exact scaling) for the screen
     T qsq[QL], eps[QL], thr[QL], worst[QL];
+    T qs[QL];       // cosine: ||q||, the screen's scale
+    bool screened[QL];  // cosine: the screen bound holds for this query
     uint32_t worst_i[QL];
     T lv[QL][K];
     uint32_t li[QL][K];
@@ -130,6 +156,10 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
         }
         qsq[i] = ok ? a.qsq[q] : T(0);
         eps[i] = (T)(a.eps_rel * ((double)qsq[i] + xmax) + a.eps_abs);
+        qs[i] = N::sqrt_(qsq[i]);
+        // cosine: a zero query ties every row (never screened), and the
+        // bound needs norm sums well inside the range
+        screened[i] = !COS || (qs[i] > T(0) && (double)qsq[i] + xmax <= (sizeof(T) == 4 ? 0x1p124 : 0x1p1020));
         // An inactive lane can never admit (prefill_lists' -inf bound, knn.rs:2875-2905).
         worst[i] = ok ? inf : -inf;
         thr[i] = ok ? inf : -inf;
@@ -139,8 +169,10 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
         // have usually finished by then); any k real rows bound the answer.
         if (ok && a.shared_r && blockIdx.y > 0) {
             const T R0 = N::from_bits(__hip_atomic_load(&a.shared_r[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            if (R0 < inf) {
-                if constexpr (sizeof(T) == 4) {
+            if (R0 < inf && screened[i]) {
+                if constexpr (COS) {
+                    thr[i] = lowd_cos_threshold(R0, qs[i], eps[i]);
+                } else if constexpr (sizeof(T) == 4) {
                     thr[i] = round_up_f((double)R0 - (double)qsq[i] + (double)eps[i]);
                 } else {
                     const T we_ = R0 + eps[i];
@@ -173,6 +205,8 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
                 if (c < D)
                     v = X[(t0 + r) * D + c];
                 else if (c == D)
+                    v = COS ? XSCALE[t0 + r] : XSQ[t0 + r];
+                else if (COS && c == D + 1)
                     v = XSQ[t0 + r];
             }
             tile[e] = v;
@@ -207,9 +241,17 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
                 T mn = inf;
 #pragma unroll
                 for (int rr = 0; rr < RU; ++rr) {
-                    T s_ = row[rr][D];
+                    T s_;
+                    if constexpr (COS) {
+                        s_ = T(0);
 #pragma unroll
-                    for (int c = 0; c < D; ++c) s_ = N::fma_(qm2[i][c], row[rr][c], s_);
+                        for (int c = 0; c < D; ++c) s_ = N::fma_(qv[i][c], row[rr][c], s_);
+                        s_ = s_ * row[rr][D];
+                    } else {
+                        s_ = row[rr][D];
+#pragma unroll
+                        for (int c = 0; c < D; ++c) s_ = N::fma_(qm2[i][c], row[rr][c], s_);
+                    }
                     mn = (rr == 0) ? s_ : N::min_(mn, s_);
                 }
                 any |= !(mn > thr[i]);
@@ -231,9 +273,17 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
 #pragma unroll
                 for (int rr = 0; rr < RU; ++rr) {
                     const T* yr = &tile[(r0 + rr) * DPN];
-                    T s_ = yr[D];
+                    T s_;
+                    if constexpr (COS) {
+                        s_ = T(0);
 #pragma unroll
-                    for (int c = 0; c < D; ++c) s_ = N::fma_(qm2[i][c], yr[c], s_);
+                        for (int c = 0; c < D; ++c) s_ = N::fma_(qv[i][c], yr[c], s_);
+                        s_ = s_ * yr[D];
+                    } else {
+                        s_ = yr[D];
+#pragma unroll
+                        for (int c = 0; c < D; ++c) s_ = N::fma_(qm2[i][c], yr[c], s_);
+                    }
                     m |= (uint32_t)!(s_ > thr[i]) << rr;
                 }
                 m &= (rmax >= 32) ? 0xFFFFFFFFu : ((1u << rmax) - 1u);
@@ -243,13 +293,23 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
                     const T* yr = &tile[(r0 + rr) * DPN];
                     const uint32_t t = (uint32_t)(t0 + r0 + rr);
                     T e = T(0);
+                    if constexpr (COS) {
+                        // the metric arm's cosine (exact_pair, ARM_COS_FOLD)
+                        T dot = T(0);
 #pragma unroll
-                    for (int c = 0; c < D; ++c) {
-                        const T diff = qv[i][c] - yr[c];
-                        if (ARM == ARM_EUCLID_FMA)
-                            e = N::fma_(diff, diff, e);
-                        else
-                            e = e + diff * diff;
+                        for (int c = 0; c < D; ++c) dot = N::fma_(qv[i][c], yr[c], dot);
+                        const T denom = N::sqrt_(qsq[i] * yr[D + 1]);
+                        const T sim = (denom > T(0)) ? dot / denom : T(0);
+                        e = clamp02<T>(T(1) - sim);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < D; ++c) {
+                            const T diff = qv[i][c] - yr[c];
+                            if (ARM == ARM_EUCLID_FMA)
+                                e = N::fma_(diff, diff, e);
+                            else
+                                e = e + diff * diff;
+                        }
                     }
                     if (!(e <= worst[i]) || (e == worst[i] && t > worst_i[i])) continue;
                     T cav = e;
@@ -277,10 +337,14 @@ __global__ __launch_bounds__(256) void knn_lowd_kernel(LowdArgs<T> a) {
                     // (R + eps) - ||q||^2 in the element type, raised by four
                     // times its rounding bound (the smallest normal near
                     // zero) -- an upper bound
-                    if (worst[i] < inf) {
-                        const T we_ = worst[i] + eps[i];
-                        const T s_ = we_ - qsq[i];
-                        thr[i] = s_ + N::margin(we_, s_);
+                    if (worst[i] < inf && screened[i]) {
+                        if constexpr (COS) {
+                            thr[i] = lowd_cos_threshold(worst[i], qs[i], eps[i]);
+                        } else {
+                            const T we_ = worst[i] + eps[i];
+                            const T s_ = we_ - qsq[i];
+                            thr[i] = s_ + N::margin(we_, s_);
+                        }
                     }
                 }
             }
@@ -436,6 +500,8 @@ hipError_t launch_lowd(const LowdArgs<T>& a, int arm, hipStream_t s) {
         e = launch_d<T, ARM_EUCLID_FMA>(a, s);
     else if (arm == ARM_EUCLID_MULADD)
         e = launch_d<T, ARM_EUCLID_MULADD>(a, s);
+    else if (arm == ARM_COS_FOLD && a.xscale)
+        e = launch_d<T, ARM_COS_FOLD>(a, s);
     else
         return hipErrorInvalidValue;
     if (e != hipSuccess || a.nstrips <= 1) return e;

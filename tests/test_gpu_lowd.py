@@ -2,7 +2,8 @@
 bit against the CPU oracle (euclidean_topk_rows_cpu_direct,
 crates/mlrs-kernels/src/knn.rs:2968-3227: the exact value fma(q-x, q-x, acc)
 over ascending columns, lists ranked by (value, index) with insert_lane's
-rule, knn.rs:2655-2706, NaN never admitted).
+rule, knn.rs:2655-2706, NaN never admitted; cosine by the metric arm's
+fold: fma dot product, sqrt(||q||^2 ||x||^2), divide, clamp to [0, 2]).
 
 Every d from 1 to 16 and every list capacity (k = 1, 4, 8, 16, 32 and values
 between) is reached; index sizes that split the rows into several strips
@@ -32,13 +33,13 @@ def _t(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
 
 
-def _knn_served(xq, xt, k):
+def _knn_served(xq, xt, k, metric):
     """The engine's (distances, indices) and the name of the kernel it timed."""
     lib = _lib.load()
     _lib.check(lib.mlrs_timing_enable(1))
     prims.force_path("lowd")
     try:
-        gd, gi = prims.knn_topk(_t(xq), _t(xt), k, "euclidean")
+        gd, gi = prims.knn_topk(_t(xq), _t(xt), k, metric)
         torch.cuda.synchronize()
         tot, n = ctypes.c_double(), ctypes.c_int64()
         name = ctypes.create_string_buffer(64)
@@ -49,10 +50,10 @@ def _knn_served(xq, xt, k):
     return gd.cpu().numpy(), gi.cpu().numpy(), name.value.decode()
 
 
-def check_lowd(xq, xt, k, label=""):
-    gd, gi, kern = _knn_served(xq, xt, k)
+def check_lowd(xq, xt, k, label="", metric="euclidean"):
+    gd, gi, kern = _knn_served(xq, xt, k, metric)
     assert kern == "knn_lowd_kernel", "%s: served by %s" % (label, kern)
-    wd, wi = oracle.knn_topk(xq, xt, k, "euclidean")
+    wd, wi = oracle.knn_topk(xq, xt, k, metric)
     bad = np.argwhere(gi != wi.astype(np.int64))
     assert bad.size == 0, "%s: %d index mismatches, first %s" % (label, len(bad), bad[:3].tolist())
     same = (gd == wd) | (np.isnan(gd) & np.isnan(wd))
@@ -151,3 +152,49 @@ def test_zero_rows_and_k_equals_n_train(dtype):
     xq[:3] = 0
     check_lowd(xq, xt, 32, "k = n_train")
     check_lowd(xq, xt, 1, "k = 1 on quantised rows")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [1, 2, 3, 5, 8, 11, 16])
+@pytest.mark.parametrize("k", [1, 8, 16, 32])
+def test_cosine(dtype, d, k):
+    rng = np.random.default_rng(700 + d + k)
+    xt = (rng.standard_normal((3000, d)) + 0.3).astype(dtype)
+    xq = (rng.standard_normal((600, d)) + 0.3).astype(dtype)
+    check_lowd(xq, xt, k, "cosine d=%d k=%d" % (d, k), "cosine")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cosine_strips_ties_zero_and_nan(dtype):
+    """Rows that are positive multiples of one direction lead the list of a
+    query along it (the ties among them go by index, across strips); zero rows
+    score exactly 1; a zero query scores 1 against every row (its norm
+    product is 0 or NaN, so the arm's similarity is 0) and is never screened;
+    NaN and inf rows are otherwise never admitted; a NaN query admits
+    nothing."""
+    rng = np.random.default_rng(23)
+    xt = rng.standard_normal((80000, 3)).astype(dtype)
+    base = xt[17].copy()
+    same = np.array([17, 300, 301, 40000, 79999])
+    xt[same] = base * np.array([1, 2, 3, 0.5, 7], dtype=dtype)[:, None]
+    xt[[5, 60000]] = 0
+    xt[[6, 70000]] = np.nan
+    xt[7, 1] = np.inf
+    xq = rng.standard_normal((300, 3)).astype(dtype)
+    xq[0] = base
+    xq[1] = 0
+    xq[2] = np.nan
+    gd, gi = check_lowd(xq, xt, 8, "cosine ties", "cosine")
+    assert set(same.tolist()) <= set(gi[0].tolist())
+    assert (gd[1] == 1).all()  # the zero query scores 1 against every row
+
+
+@pytest.mark.parametrize("dtype,scale", [(np.float32, 1e20), (np.float64, 1e160), (np.float32, 1e-20),
+                                         (np.float64, 1e-160)])
+def test_cosine_extreme_norms(dtype, scale):
+    """Norm sums that overflow (the query is evaluated exactly against every
+    row) or underflow."""
+    rng = np.random.default_rng(29)
+    xt = (rng.standard_normal((3000, 4)) * scale).astype(dtype)
+    xq = (rng.standard_normal((200, 4)) * scale).astype(dtype)
+    check_lowd(xq, xt, 8, "cosine scale %g" % scale, "cosine")
