@@ -355,6 +355,8 @@ def main():
         metric_name = "radius_neighbors dist-evals/s (%s)" % args.config
     else:
         metric_name = METRIC if args.config == "c2" else "dist-evals/s (%s)" % args.config
+        if retyped:
+            metric_name = "dist-evals/s (%s in %s)" % (args.config, args.dtype)
     line = {
         "metric": metric_name,
         "value": value,
