@@ -697,20 +697,34 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     // of row f / CPR, which holds the row's column chunk position ^ (row & 15).
     // Rows past the segment are not loaded (their values are masked out of the
     // screen); the row norms go through a register as in the staged path.
+    // pair layout: lane l loads chunk l % 32 of slot row 16 (l / 32)
+    const uint32_t pair_off = (uint32_t)(16 * (lane >> 5) * DP + 4 * (lane & 31));
     auto direct_load = [&](float (&dst)[TILE_FL], uint32_t t0) {
         if constexpr (DIRECT && PAIRS) {
             // slots 4w .. 4w + 3: lane l loads chunk l % 32 of row slot + 16 (l / 32)
-            const int rl = 16 * (lane >> 5);
-            const float* xw = X + (int64_t)(t0 + (uint32_t)(4 * w)) * d + (int64_t)rl * d + 4 * (lane & 31);
-            const int di = (int)d;
-            if (4 * (lane & 31) < di) {
-                if (t_end32 - t0 >= (uint32_t)kBn) {  // whole tile (t0 + kBn could wrap)
+            if (d == DP && t_end32 - t0 >= (uint32_t)kBn) {
+                // unpadded rows, whole tile (t0 + kBn could wrap): a
+                // wave-uniform row base plus the lane's constant offset, so no
+                // per-slot runtime strides are kept (they were scalar
+                // registers spilled to VGPR lanes, read back every tile)
+                const float* base = X + (int64_t)(t0 + (uint32_t)(4 * w)) * DP;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
-                } else {
+                for (int i = 0; i < 4; ++i)
+                    global_to_lds16(base + (uint32_t)(i * DP + pair_off), &dst[(4 * w + i) * SLOT]);
+            } else {
+                const int rl = 16 * (lane >> 5);
+                const float* xw = X + (int64_t)(t0 + (uint32_t)(4 * w)) * d + (int64_t)rl * d + 4 * (lane & 31);
+                const int di = (int)d;
+                if (4 * (lane & 31) < di) {
+                    if (t_end32 - t0 >= (uint32_t)kBn) {  // whole tile (t0 + kBn could wrap)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (t0 + (uint32_t)(4 * w + i + rl) < t_end32) global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
+                        for (int i = 0; i < 4; ++i) global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (t0 + (uint32_t)(4 * w + i + rl) < t_end32)
+                                global_to_lds16(xw + i * di, &dst[(4 * w + i) * SLOT]);
+                    }
                 }
             }
         } else if constexpr (DIRECT) {
@@ -732,8 +746,11 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
                 }
             }
         }
-        if (tid < kBn) {
-            const uint32_t t = t0 + (uint32_t)tid;
+        // the tile's row norms, one per lane of wave 0 (the three-block-list
+        // kernel tests the wave index and the lane, which measured faster
+        // there: c2k128 25.04 -> 24.51 ms; the others test tid)
+        if (KL > 1 ? (w == 0 && lane < kBn) : (tid < kBn)) {
+            const uint32_t t = t0 + (uint32_t)(KL > 1 ? lane : tid);
             if (COS)
                 pfn = (t < t_end32) ? XSCALE[t] : 0.0f;
             else
@@ -789,7 +806,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
                 }
             }
         }
-        if (tid < kBn) tncur[tid] = pfn;
+        if (KL > 1 ? (w == 0 && lane < kBn) : (tid < kBn)) tncur[KL > 1 ? lane : tid] = pfn;
         __syncthreads();
         if (!SINGLE && t_end32 - (uint32_t)t0 > (uint32_t)kBn) load_tile(nxt, t0 + kBn);
 
@@ -896,7 +913,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
         };
 
         // ---- k = 1: tighten with this tile's smallest expansion value ----
-        if (!COS && k == 1) {
+        if (K1 && !COS) {  // the k = 1 kernel (every k = 1 search launches it)
             float m = inf;
 #pragma unroll
             for (int r = 0; r < SH::vals; ++r) m = fminf(m, val(r));  // NaN ignored; past-end rows are +inf
