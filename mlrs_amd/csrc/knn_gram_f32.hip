@@ -247,7 +247,10 @@ struct GramOcc {
 
 // KL: 64-entry blocks of a (segment, query) list in registers during a flush
 // (1 for k <= 64, 3 for k <= 128: k + 32 entries).
-template <int NG, int ARM, bool COS, bool VEC4, bool K1, int KL>
+// FULLW: every row is exactly DP = 8 NG floats wide (d = DP), launched for the
+// paired-row kernels (d = 128) so that their tile loads need no runtime
+// stride.
+template <int NG, int ARM, bool COS, bool VEC4, bool K1, int KL, bool FULLW = false>
 // (__launch_bounds__' second argument is waves per SIMD: workgroups per CU x
 // waves per workgroup / 4.)
 __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
@@ -702,7 +705,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     auto direct_load = [&](float (&dst)[TILE_FL], uint32_t t0) {
         if constexpr (DIRECT && PAIRS) {
             // slots 4w .. 4w + 3: lane l loads chunk l % 32 of row slot + 16 (l / 32)
-            if (d == DP && t_end32 - t0 >= (uint32_t)kBn) {
+            if (FULLW && t_end32 - t0 >= (uint32_t)kBn) {
                 // unpadded rows, whole tile (t0 + kBn could wrap): a
                 // wave-uniform row base plus the lane's constant offset, so no
                 // per-slot runtime strides are kept (they were scalar
@@ -1500,10 +1503,18 @@ hipError_t launch_ng(const GramArgs32& a, int64_t nblocks, hipStream_t s) {
     dim3 grid((unsigned)StreamSplit(a.nq, a.nt, a.qpb, kBn, a.grid_wgs).G);
     const dim3 block(GramShape<(NG > 16)>::threads);
     (void)nblocks;
+    // rows exactly 128 floats wide take the paired-row kernels' fixed-stride
+    // instance (k > 1: the k = 1 kernel stages its tiles)
+    constexpr bool kPairs = NG == 16 && VEC4;
+    const bool fullw = kPairs && a.d == 8 * NG;
     if (a.k == 1)
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, true, 1>), grid, block, 0, s, a);
+    else if (a.k <= 64 && fullw)
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 1, kPairs>), grid, block, 0, s, a);
     else if (a.k <= 64)
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 1>), grid, block, 0, s, a);
+    else if (fullw)
+        hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 3, kPairs>), grid, block, 0, s, a);
     else
         hipLaunchKernelGGL((knn_gram_f32_kernel<NG, ARM, COS, VEC4, false, 3>), grid, block, 0, s, a);
     return hipGetLastError();
