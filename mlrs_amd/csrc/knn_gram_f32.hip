@@ -65,10 +65,13 @@ constexpr int kBn = 32;                  // index rows per tile
 constexpr int kKcap = 128;               // largest k this kernel keeps
 constexpr int kQcapK1 = 48;              // k = 1: the screen tightens every tile, queues stay short
 constexpr int kShareEvery = 64;          // tiles between reads of the shared thresholds
-// k <= 64 lists (k > 1) read them every 128 tiles: c2 kernel 20.38 -> 20.29 ms;
-// the three-block lists keep 64 (at 128: c2k128 +0.1 ms; 96, not a power of
-// two, was slower for both)
-constexpr int share_every(bool k1, int kl) { return (!k1 && kl == 1) ? 2 * kShareEvery : kShareEvery; }
+// The narrow shape's k <= 64 lists (k > 1) read them every 128 tiles: c2
+// kernel 20.38 -> 20.29 ms; the three-block lists and the wide shape keep 64
+// (at 128: c2k128 +0.1 ms, d256 +0.07 ms; 96, not a power of two, was slower
+// for both narrow kernels; 256: c2 +0.15 ms)
+constexpr int share_every(bool k1, int kl, bool w16) {
+    return (!k1 && kl == 1 && !w16) ? 2 * kShareEvery : kShareEvery;
+}
 constexpr int kSumSlots = 16;            // segment summaries read per refresh (k > 1)
 
 // The two register shapes of a wave's block of (row, query) values.
@@ -1033,7 +1036,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
         }
         // ---- pick up thresholds tightened by other strips of these queries ----
         rotate_wave_priority((uint32_t)tiles + 1u, GramOcc<NG, K1, KL, VEC4>::wgs);
-        if (SHARED_R && (++tiles % share_every(K1, KL)) == 0) {
+        if (SHARED_R && (++tiles % share_every(K1, KL, W16)) == 0) {
             if (lane < QPW && qvalid) {
                 float R = __uint_as_float(SHARED_R[qmine]);
                 if (nsum > 0) {
