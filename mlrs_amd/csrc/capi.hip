@@ -562,7 +562,7 @@ int32_t knn_gram32(const float* xq, int64_t nq, const float* xt, int64_t nt, int
     const int res_chunks = gram_f32_k1_resident_chunks(nq, nt, d, k, arm, vec4);
     // per-(segment slot, query) lists: the kernel's top-k state, merged at the end
     size_t parts = (size_t)std::max<int64_t>(nslots, res_chunks) * nq * gram_list_cap(k);
-    size_t qvals = (k > 1) ? gram_f32_qval_elems(grid_wgs)
+    size_t qvals = (k > 1) ? gram_f32_qval_elems(grid_wgs, k)
                  : res_chunks ? (gram_f32_k1_resident_queue_bytes(cus) + sizeof(float) - 1) / sizeof(float) : 0;
     size_t summs = (k > 1) ? (size_t)nslots * nq : 0;
     size_t bytes = fixed + aligned_bytes(parts * sizeof(float)) + aligned_bytes(parts * sizeof(uint32_t)) +

@@ -95,12 +95,16 @@ struct GramShape {
     static constexpr int qpb = waves * qpw;        // queries per workgroup
     static constexpr int vals = W16 ? 8 : 16;      // tile values per lane
     static constexpr int qcap = W16 ? 48 : 64;     // queued candidates per query (k > 1)
+    // three-block lists (k > 64): longer queues, about half as many flushes
+    // (c2k128 kernel 24.5 -> 23.0 ms; 96 entries 24.0, 192 23.4, 256 23.2)
+    static constexpr int qcap3 = W16 ? 48 : 128;
 };
 constexpr int kQpbNarrow = GramShape<false>::qpb;
 constexpr int kQpbWide = GramShape<true>::qpb;
-constexpr int kQvalPerWave = 32 * 64;             // pairs a wave may queue (either shape), k > 1
-// Per wave in a.qval: kQvalPerWave screen values, then their kQvalPerWave
-// index-row numbers, both [queue position][query].
+constexpr int kQvalPerWave = 32 * 128;            // pairs a wave may queue (any shape), k > 1
+// Per wave in a.qval: the kernel's QPW x QCAP screen values, then as many
+// index-row numbers, both [queue position][query] (gram_f32_qval_elems sizes
+// the buffer for the launch's list length).
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -304,7 +308,8 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     __shared__ __attribute__((aligned(16))) float tileB[SINGLE ? 4 : TILE_FL];
     __shared__ __attribute__((aligned(16))) float tnA[kBn];
     __shared__ __attribute__((aligned(16))) float tnB[kBn];
-    constexpr int QCAP = K1 ? kQcapK1 : SH::qcap;
+    constexpr int QCAP = K1 ? kQcapK1 : (KL > 1 ? SH::qcap3 : SH::qcap);
+    constexpr int QB = (QCAP + 63) / 64;  // 64-entry blocks of a flushed queue
     constexpr int kFlushAt = QCAP - kBn;  // flush when a queue may overflow next tile
     __shared__ WaveLds<K1 ? QCAP : 1, QPW> wl[WV];
 
@@ -330,8 +335,9 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     const float inf = __builtin_huge_valf();
     // screen values and index rows of this wave's queued pairs (k > 1),
     // [queue position][query]
-    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * WV + w) * (2 * kQvalPerWave);
-    uint32_t* __restrict__ QIw = K1 ? nullptr : reinterpret_cast<uint32_t*>(QVw + kQvalPerWave);
+    constexpr int QVW = QPW * QCAP;  // this kernel's pairs per wave (<= kQvalPerWave)
+    float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * WV + w) * (2 * QVW);
+    uint32_t* __restrict__ QIw = K1 ? nullptr : reinterpret_cast<uint32_t*>(QVw + QVW);
 
     // Tile row of value r of this lane.
     auto row_of = [&](int r) -> int {
@@ -564,28 +570,54 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             lk_[r_] = kKeyEmpty;                                                             \
             if (p_ < K2) lk_[r_] = pair_key(LV[qg_ * K2 + p_], LI[qg_ * K2 + p_]);           \
         }                                                                                    \
-        float e_ = inf;                                                                      \
-        uint32_t t_ = kSentinelIdx;                                                          \
-        if ((uint32_t)lane < n_) {                                                           \
-            t_ = QIw[lane * QPW + j_];                                                       \
-            const float s_ = exact_ ? 0.0f : QVw[lane * QPW + j_];                           \
-            if (exact_ || s_ != s_)                                                          \
-                e_ = MLRS_EXACT_AT(t_);                                                      \
-            else                                                                             \
-                e_ = COS ? 1.0f + s_ / L.qs[j_] : s_ + L.qs[j_];                             \
-            if (e_ != e_) { /* NaN is never admitted */                                      \
-                e_ = inf;                                                                    \
-                t_ = kSentinelIdx;                                                           \
-            }                                                                                \
-        }                                                                                    \
-        unsigned long long ek_ = pair_key(e_, t_);                                           \
-        wave_sort64_key(ek_, lane);                                                          \
         const unsigned long long ok_ = lk_[0];                                               \
-        unsigned long long dk_;                                                              \
-        if constexpr (KL == 1)                                                               \
-            dk_ = wave_merge64_key_drop(lk_[0], ek_, lane);                                  \
-        else                                                                                 \
-            dk_ = wave_merge_blocks_key_drop<KL>(lk_, ek_, lane);                            \
+        unsigned long long dk_ = kKeyEmpty;                                                  \
+        unsigned long long ek_ = kKeyEmpty;                                                  \
+        if constexpr (QB == 1) {                                                             \
+            float e_ = inf;                                                                  \
+            uint32_t t_ = kSentinelIdx;                                                      \
+            if ((uint32_t)lane < n_) {                                                       \
+                t_ = QIw[lane * QPW + j_];                                                   \
+                const float s_ = exact_ ? 0.0f : QVw[lane * QPW + j_];                       \
+                if (exact_ || s_ != s_)                                                      \
+                    e_ = MLRS_EXACT_AT(t_);                                                  \
+                else                                                                         \
+                    e_ = COS ? 1.0f + s_ / L.qs[j_] : s_ + L.qs[j_];                         \
+                if (e_ != e_) { /* NaN is never admitted */                                  \
+                    e_ = inf;                                                                \
+                    t_ = kSentinelIdx;                                                       \
+                }                                                                            \
+            }                                                                                \
+            ek_ = pair_key(e_, t_);                                                          \
+            wave_sort64_key(ek_, lane);                                                      \
+            if constexpr (KL == 1)                                                           \
+                dk_ = wave_merge64_key_drop(lk_[0], ek_, lane);                              \
+            else                                                                             \
+                dk_ = wave_merge_blocks_key_drop<KL>(lk_, ek_, lane);                        \
+        } else {                                                                             \
+          _Pragma("unroll") for (int b_ = 0; b_ < QB; ++b_) {                                \
+            if (b_ == 0 || n_ > 64u * (uint32_t)b_) {                                        \
+              float e_ = inf;                                                                \
+              uint32_t t_ = kSentinelIdx;                                                    \
+              const uint32_t qi_ = 64u * (uint32_t)b_ + (uint32_t)lane;                      \
+              if (qi_ < n_) {                                                                \
+                  t_ = QIw[qi_ * QPW + j_];                                                  \
+                  const float s_ = exact_ ? 0.0f : QVw[qi_ * QPW + j_];                      \
+                  if (exact_ || s_ != s_)                                                    \
+                      e_ = MLRS_EXACT_AT(t_);                                                \
+                  else                                                                       \
+                      e_ = COS ? 1.0f + s_ / L.qs[j_] : s_ + L.qs[j_];                       \
+                  if (e_ != e_) { /* NaN is never admitted */                                \
+                      e_ = inf;                                                              \
+                      t_ = kSentinelIdx;                                                     \
+                  }                                                                          \
+              }                                                                              \
+              ek_ = pair_key(e_, t_);                                                        \
+              wave_sort64_key(ek_, lane);                                                    \
+              dk_ = wave_merge_blocks_key_drop<KL>(lk_, ek_, lane);                          \
+            }                                                                                \
+          }                                                                                  \
+        }                                                                                    \
         float R_ = f32_from_order_bits(list_hi_at<KL>(lk_, k - 1));                          \
         if (!exact_) {                                                                       \
             const float dr_ = (K2 < 64 * KL) ? f32_from_order_bits(list_hi_at<KL>(lk_, K2))  \
@@ -609,13 +641,13 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
               } else {                                                                       \
                 /* the old list (still in memory) and the queue, exactly */                  \
                 _Pragma("unroll") for (int r_ = 0; r_ < KL; ++r_) lk_[r_] = kKeyEmpty;       \
-                _Pragma("unroll") for (int r_ = 0; r_ <= KL; ++r_) {                         \
+                _Pragma("unroll") for (int r_ = 0; r_ < KL + QB; ++r_) {                     \
                     uint32_t i_ = kSentinelIdx;                                              \
                     if (r_ < KL) {                                                           \
                         const int p_ = 64 * r_ + lane;                                       \
                         if (p_ < K2) i_ = LI[qg_ * K2 + p_];                                 \
-                    } else if ((uint32_t)lane < n_) {                                        \
-                        i_ = QIw[lane * QPW + j_];                                           \
+                    } else if (64u * (uint32_t)(r_ - KL) + (uint32_t)lane < n_) {            \
+                        i_ = QIw[(64u * (uint32_t)(r_ - KL) + (uint32_t)lane) * QPW + j_];   \
                     }                                                                        \
                     float x_ = inf;                                                          \
                     if (i_ != kSentinelIdx) x_ = MLRS_EXACT_AT(i_);                          \
@@ -652,9 +684,9 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
         }                                                                                    \
         if (lane == 0) {                                                                     \
             if (SHARED_R && R_ < inf) {                                                      \
-                /* published without waiting for the old value: other segments' */          \
+                /* published without waiting for the old value: other segments' */           \
                 /* bounds reach this one at its next refresh */                              \
-                __hip_atomic_fetch_min(&SHARED_R[qg_], __float_as_uint(R_), __ATOMIC_RELAXED,  \
+                __hip_atomic_fetch_min(&SHARED_R[qg_], __float_as_uint(R_), __ATOMIC_RELAXED, \
                                        __HIP_MEMORY_SCOPE_AGENT);                            \
             }                                                                                \
             L.thr[j_] = fminf(L.thr[j_], screen_threshold<COS>(R_, L.qs[j_], L.eps[j_]));    \

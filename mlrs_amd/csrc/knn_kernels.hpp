@@ -129,7 +129,12 @@ __host__ __device__ inline int gram_list_cap(int k) {
 
 // Screen values (f32: and their index rows) kept per workgroup while pairs
 // wait in the queues (k > 1): 2 x 2048 per wave, 4 waves per workgroup.
-inline size_t gram_f32_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 32 * 64 * 2; }
+// Queued (screen value, index row) pairs of the f32 Gram kernel: 4 waves x
+// 32 queries x the queue length (64; 128 for the three-block lists, k > 64)
+// x 2 words per workgroup.
+inline size_t gram_f32_qval_elems(int64_t grid_wgs, int k) {
+    return (size_t)grid_wgs * 4 * 32 * (k > 64 ? 128 : 64) * 2;
+}
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
 // Index rows the seed launch samples for k > 1 (evenly spaced): 64 k, at
