@@ -94,10 +94,13 @@ struct GramShape {
     static constexpr int threads = 64 * waves;
     static constexpr int qpb = waves * qpw;        // queries per workgroup
     static constexpr int vals = W16 ? 8 : 16;      // tile values per lane
-    static constexpr int qcap = W16 ? 48 : 64;     // queued candidates per query (k > 1)
+    // queued candidates per query (k > 1): the wide shape 128 (flushed as two
+    // 64-entry blocks: d256 kernel 4.83 -> 4.59 ms against 48; 64: 4.64,
+    // 96: 4.60); the narrow k <= 64 kernel 64 (128 measured slower there)
+    static constexpr int qcap = W16 ? 128 : 64;
     // three-block lists (k > 64): longer queues, about half as many flushes
     // (c2k128 kernel 24.5 -> 23.0 ms; 96 entries 24.0, 192 23.4, 256 23.2)
-    static constexpr int qcap3 = W16 ? 48 : 128;
+    static constexpr int qcap3 = 128;
 };
 constexpr int kQpbNarrow = GramShape<false>::qpb;
 constexpr int kQpbWide = GramShape<true>::qpb;
@@ -336,6 +339,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
     // screen values and index rows of this wave's queued pairs (k > 1),
     // [queue position][query]
     constexpr int QVW = QPW * QCAP;  // this kernel's pairs per wave (<= kQvalPerWave)
+    static_assert(QVW <= (KL > 1 ? 32 * 128 : 32 * 64), "gram_f32_qval_elems sizes the queues");
     float* __restrict__ QVw = K1 ? nullptr : a.qval + ((int64_t)blockIdx.x * WV + w) * (2 * QVW);
     uint32_t* __restrict__ QIw = K1 ? nullptr : reinterpret_cast<uint32_t*>(QVw + QVW);
 
@@ -614,7 +618,8 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
               }                                                                              \
               ek_ = pair_key(e_, t_);                                                        \
               wave_sort64_key(ek_, lane);                                                    \
-              dk_ = wave_merge_blocks_key_drop<KL>(lk_, ek_, lane);                          \
+              const unsigned long long d_ = wave_merge_blocks_key_drop<KL>(lk_, ek_, lane);  \
+              dk_ = (b_ == 0 || d_ < dk_) ? d_ : dk_; /* the smallest dropped */           \
             }                                                                                \
           }                                                                                  \
         }                                                                                    \
@@ -625,7 +630,7 @@ __global__ __launch_bounds__(GramShape<(NG > 16)>::threads,
             double w_ = (double)R_ + 2.0 * (double)L.eps[j_];                                \
             w_ += __builtin_fabs(w_) * 0x1p-40;                                              \
             if (dr_ < inf && (double)dr_ <= w_) {                                            \
-              if constexpr (KL == 1) {                                                       \
+              if constexpr (KL == 1 && QB == 1) {                                            \
                 /* the old list and the queue, exactly */                                    \
                 float x1_ = inf, x2_ = inf;                                                  \
                 uint32_t i1_ = key_index(ok_), i2_ = key_index(ek_);                         \

@@ -127,14 +127,13 @@ __host__ __device__ inline int gram_list_cap(int k) {
     return k == 1 ? 1 : k <= 64 ? (k + 32 < 64 ? k + 32 : 64) : k + 32;
 }
 
-// Screen values (f32: and their index rows) kept per workgroup while pairs
-// wait in the queues (k > 1): 2 x 2048 per wave, 4 waves per workgroup.
-// Queued (screen value, index row) pairs of the f32 Gram kernel: 4 waves x
-// 32 queries x the queue length (64; 128 for the three-block lists, k > 64)
-// x 2 words per workgroup.
+// Queued (screen value, index row) pairs of the f32 Gram kernel, 2 words
+// each, per workgroup of 4 waves: narrow shape 32 queries x 64 (k <= 64) or
+// 128 (k > 64) entries; the wide shape's 16 x 128 fits either.
 inline size_t gram_f32_qval_elems(int64_t grid_wgs, int k) {
     return (size_t)grid_wgs * 4 * 32 * (k > 64 ? 128 : 64) * 2;
 }
+// The f64 kernel's queued screen values: 4 waves x 16 queries x 48 entries.
 inline size_t gram_f64_qval_elems(int64_t grid_wgs) { return (size_t)grid_wgs * 4 * 16 * 48; }
 
 // Index rows the seed launch samples for k > 1 (evenly spaced): 64 k, at
