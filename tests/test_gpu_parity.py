@@ -116,7 +116,7 @@ def test_f64_bitwise(case, metric):
     check_knn(xq, xt, k, metric, str(case))
 
 
-@pytest.mark.parametrize("d", [3, 64, 256])
+@pytest.mark.parametrize("d", [3, 64, 128, 256])
 @pytest.mark.parametrize("k", [32, 100])
 def test_duplicates_and_boundary_ties(d, k):
     """100 identical rows around the k-th slot: membership and order are
@@ -167,7 +167,7 @@ def test_nan_rows(d):
     check_knn(xq[:20], small, 8, "euclidean", "nan sentinel")
 
 
-@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("perturb", [0.0, 1e-4])
 @pytest.mark.parametrize("k", [32, 120])
 def test_near_ties_across_segments(perturb, d, k):
